@@ -1,0 +1,222 @@
+/*
+ * tinygiant.h -- C ABI of libtinygiant.so, the MI355X (gfx950) build of
+ * TinyGiant's MoE expert hot path.
+ *
+ * Two groups of entry points:
+ *
+ *  1. The reference's own ABI (csrc/libtinygiant.c, registered by
+ *     tinygiant/_lib.py:39-74), same names and C signatures, so that
+ *     load_tinygiant_lib() binds this library unchanged.  Pointers are
+ *     caller-owned host pointers and calls are synchronous, as in the
+ *     reference.
+ *
+ *  2. New entry points for the Q4_0/Q8_0 path: an all-experts-resident HBM
+ *     arena (the reference's SSD/page-cache/mlock tiers collapsed into
+ *     device memory with the same per-expert offsets) and whole-layer /
+ *     whole-stack calls.  They return 0 on success and a negative TG_E*
+ *     code on error; tg_last_error() describes the last error of the
+ *     calling thread.  *_dev variants take device pointers and a HIP stream
+ *     (hipStream_t passed as void*, NULL = null stream) and are
+ *     asynchronous; the others take host pointers and synchronise.
+ *
+ * Formats: Q4_0 = {half d; u8 qs[16]} per 32 weights (element j < 16 is the
+ * low nibble of qs[j], element j+16 the high nibble, value d*(q-8)); Q8_0 =
+ * {half d; i8 qs[32]}.  An expert is gate[I x H] | up[I x H] | down[H x I]
+ * and a layer is experts 0..E-1 back to back, exactly the bytes
+ * tinygiant/relayout.py:142-157 writes; expert e starts at e * expert_bytes.
+ */
+#ifndef TINYGIANT_H
+#define TINYGIANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* error channel (new; the reference ABI has none)                      */
+/* ------------------------------------------------------------------ */
+#define TG_OK 0
+#define TG_E_INVALID -1     /* bad argument: NULL, shape, range */
+#define TG_E_NODEVICE -2    /* no HIP device / init failed */
+#define TG_E_NOMEM -3       /* device allocation failed */
+#define TG_E_HIP -4         /* a HIP runtime call failed */
+#define TG_E_UNSUPPORTED -5 /* entry point not available in this build */
+
+/* Message of the calling thread's last error ("" if none). */
+const char *tg_last_error(void);
+/* Select and initialise a HIP device (idempotent per device). */
+int tg_gpu_init(int device);
+/* Wait for all work on the device. */
+int tg_device_sync(void);
+/* Library version string. */
+const char *tg_version(void);
+/* Kernel timing.  While enabled, the MoE entry points bracket every kernel
+ * launch with HIP events recorded on the launching stream; tg_prof_read
+ * waits for them and returns, for one kernel name ("router", "gateup",
+ * "down"), the number of launches and their summed duration in ms.
+ * tg_prof_enable(1) also discards earlier records. */
+int tg_prof_enable(int on);
+int tg_prof_read(const char *kernel, int *launches, double *total_ms);
+
+/* ------------------------------------------------------------------ */
+/* reference ABI (tinygiant/_lib.py:39-74)                              */
+/* ------------------------------------------------------------------ */
+/* csrc/libtinygiant.c:555 */
+void tg_expert_forward(const uint8_t *q4_data, const float *input,
+                       float *output, float weight,
+                       int embed_dim, int inter_dim);
+/* csrc/libtinygiant.c:599 */
+void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *up_q4,
+                             const void *down_data, int down_format,
+                             const float *input, float *output, float weight,
+                             int embed_dim, int inter_dim);
+/* csrc/libtinygiant.c:187 */
+void tg_matmul_q4k(const uint8_t *q4_matrix, const float *input,
+                   float *output, int nrows, int ncols);
+/* csrc/libtinygiant.c:270 */
+void tg_matmul_q6k(const uint8_t *q6_matrix, const float *input,
+                   float *output, int nrows, int ncols);
+/* csrc/libtinygiant.c:322 */
+void tg_rms_norm(const float *x, const float *weight, float *out,
+                 int dim, float eps);
+/* csrc/libtinygiant.c:304 */
+void tg_f32_matvec(const float *A, const float *x, float *out,
+                   int nrows, int ncols);
+/* csrc/libtinygiant.c:297 */
+void tg_f16_matvec(const uint16_t *A, const float *x, float *out,
+                   int nrows, int ncols);
+/* csrc/libtinygiant.c:365 */
+void tg_attention_decode(
+    const float *wq, const float *wk, const float *wv, const float *wo,
+    const float *q_norm_w, const float *k_norm_w,
+    float *kv_k, float *kv_v, int kv_len, int kv_max,
+    const float *rope_cos, const float *rope_sin,
+    const float *input, float *output,
+    int embed_dim, int n_heads, int n_kv_heads, int head_dim, int pos);
+/* csrc/libtinygiant.c:460 */
+void tg_attention_decode_q4(
+    const uint8_t *wq_q4, const uint8_t *wk_q4,
+    const uint16_t *wv_f16, const uint8_t *wo_q4,
+    const float *q_norm_w, const float *k_norm_w,
+    float *kv_k, float *kv_v, int kv_len, int kv_max,
+    const float *rope_cos, const float *rope_sin,
+    const float *input, float *output,
+    int embed_dim, int n_heads, int n_kv_heads, int head_dim, int pos);
+/* csrc/libtinygiant.c:745 */
+void tg_prefetch(const void *addr, size_t len);
+/* csrc/libtinygiant.c:752 */
+void tg_prefetch_batch(const void **addrs, const size_t *lens, int count);
+/* csrc/libtinygiant.c:761 */
+int tg_mlock(const void *addr, size_t len);
+/* csrc/libtinygiant.c:662 */
+void tg_transformer_layer(
+    const float *wq, const float *wk, const float *wv, const float *wo,
+    const float *attn_norm_w, const float *q_norm_w, const float *k_norm_w,
+    const float *ffn_norm_w,
+    float *kv_k, float *kv_v, int kv_len, int kv_max,
+    const float *rope_cos, const float *rope_sin,
+    const uint8_t **gate_ptrs, const uint8_t **up_ptrs,
+    const void **down_ptrs, const int *down_is_f16,
+    const float *expert_weights, int n_active,
+    float *x,
+    int embed_dim, int inter_dim,
+    int n_heads, int n_kv_heads, int head_dim, int pos);
+/* csrc/libtinygiant.c:647 (exported, not registered by _lib.py) */
+void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights,
+                    int n_experts, const float *input, float *output,
+                    int embed_dim, int inter_dim);
+/* csrc/libtinygiant.c:735 (exported, not registered by _lib.py) */
+void tg_matmul_q4k_scalar(const uint8_t *q4_matrix, const float *input,
+                          float *output, int nrows, int ncols);
+
+/* ------------------------------------------------------------------ */
+/* HBM expert arena (replaces tinygiant/cache.py's mmap/mlock tiers)    */
+/* ------------------------------------------------------------------ */
+typedef struct tg_arena tg_arena;
+
+/* Reserve device memory for n_layers layers of n_experts Q4_0 experts
+ * (embed_dim = H, inter_dim = I, both multiples of 32) plus one fp32 router
+ * [n_experts x H] per layer.  Returns NULL on error (see tg_last_error).
+ * Role: tinygiant/cache.py:14-57 (ExpertCache over index.json). */
+tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim,
+                          int inter_dim, int top_k);
+void tg_arena_destroy(tg_arena *a);
+/* Bytes of one expert / one layer in the relayout format. */
+size_t tg_arena_expert_bytes(const tg_arena *a);
+size_t tg_arena_layer_bytes(const tg_arena *a);
+/* Offset and gate/up/down sizes of expert e inside a layer, as recorded in
+ * index.json's expert_offsets (relayout.py:150-156). */
+int tg_arena_expert_offset(const tg_arena *a, int expert, size_t *offset,
+                           size_t *gate_bytes, size_t *up_bytes,
+                           size_t *down_bytes);
+/* Upload one layer file's bytes (relayout layout, host memory). */
+int tg_arena_load_layer(tg_arena *a, int layer, const void *host_bytes,
+                        size_t nbytes);
+/* Upload one layer's fp32 router [n_experts x H] (host memory). */
+int tg_arena_load_router(tg_arena *a, int layer, const float *host_router,
+                         size_t count);
+/* Read one layer back in the relayout layout (host memory). */
+int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes,
+                        size_t nbytes);
+/* Fill one layer (experts and router) with the synthetic workload on the
+ * device: weights N(0, sigma) quantized to Q4_0, router N(0, sigma) fp32,
+ * from SplitMix64 counters keyed by (seed, layer, expert, tensor). */
+int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float sigma);
+
+/* ------------------------------------------------------------------ */
+/* MoE block: norm -> router -> top-k -> experts -> combine             */
+/* (engine.py:229-258 with Q4_0 experts)                                */
+/* ------------------------------------------------------------------ */
+/* For each of n_tokens tokens x[t] (fp32, H): xn = x / rms(x) (eps),
+ * logits = router xn, top-k with renormalised softmax, moe_out[t] =
+ * sum_j w_j * expert_j(Q8_0(xn)).  topk_idx / topk_w ([n_tokens x k],
+ * descending logit) may be NULL. */
+int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x,
+                         float *moe_out, int n_tokens, int32_t *topk_idx,
+                         float *topk_w, float eps, void *stream);
+int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out,
+                     int n_tokens, int32_t *topk_idx, float *topk_w,
+                     float eps);
+/* x <- x + MoE_l(x) for l = layer0 .. layer0+n_layers-1, in place. */
+int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int layer0,
+                         int n_layers, float eps, void *stream);
+int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
+                     int n_layers, float eps);
+
+/* ------------------------------------------------------------------ */
+/* building blocks (device pointers; used by the parity tests)          */
+/* ------------------------------------------------------------------ */
+/* fp32 -> Q8_0 blocks (34 B each); n multiple of 32. */
+int tg_q40_quantize_q8_0_dev(const float *x, void *q8_out, int n,
+                             void *stream);
+/* Relayout (18-byte block) tensor <-> the arena's tensor-planar form. */
+int tg_q40_to_planar_dev(const void *aos, void *planar, int rows, int nb,
+                         void *stream);
+int tg_q40_from_planar_dev(const void *planar, void *aos, int rows, int nb,
+                           void *stream);
+/* Exact int32 block sums S[r][b] = sum (q_w - 8) q_x of a planar Q4_0
+ * matrix [rows x cols] against Q8_0 blocks. */
+int tg_q40_block_sums_dev(const void *w_planar, int rows, int cols,
+                          const void *xq8, int32_t *sums, void *stream);
+/* out[r] = Q4_0 row r . Q8_0 vector (planar matrix). */
+int tg_q40_matvec_dev(const void *w_planar, int rows, int cols,
+                      const void *xq8, float *out, void *stream);
+/* Router logits + top-k + softmax for n_tokens (any pointer but x/Wr may be
+ * NULL). */
+int tg_router_topk_dev(const float *Wr, const float *x, int n_experts,
+                       int embed_dim, int top_k, float eps, int n_tokens,
+                       float *logits, int32_t *topk_idx, float *topk_w,
+                       void *stream);
+/* Synthetic generators (bit-identical to the host definition). */
+int tg_synth_normal_dev(uint64_t seed, uint64_t stream_id, float sigma,
+                        size_t n, float *out, void *stream);
+int tg_synth_q40_dev(uint64_t seed, uint64_t stream_id, float sigma,
+                     int rows, int cols, void *planar_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

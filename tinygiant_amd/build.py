@@ -1,0 +1,68 @@
+"""Builds libtinygiant.so (gfx950) in-tree with hipcc.
+
+Every HIP source is compiled with -ffp-contract=off and correctly rounded
+fp32 division/square root (the kernels round exactly as the host definition
+of each step), and with the packed-FP32 feature disabled.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libtinygiant.so"
+SOURCES = ["tg_kernels.hip", "tg_abi.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = os.environ.get("TG_OFFLOAD_ARCH", "gfx950")
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(str(c) for c in cmd), flush=True)
+    r = subprocess.run([str(c) for c in cmd], capture_output=True, text=True)
+    out = "\n".join(
+        line for line in (r.stdout + r.stderr).splitlines()
+        if "packed-fp32-ops' is not a recognized feature" not in line
+    )
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(map(str, cmd))}\n{out}")
+    if out.strip() and verbose:
+        print(out)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link libtinygiant.so."""
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    for src in SOURCES:
+        obj = BUILD / (Path(src).stem + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-c", CSRC / src, "-o", obj], verbose)
+        objs.append(obj)
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,603 @@
+// tg_abi.hip -- the C ABI of libtinygiant.so (declared in include/tinygiant.h).
+//
+// The reference's own symbols keep their names, signatures and synchronous
+// host-pointer conventions (csrc/libtinygiant.c, tinygiant/_lib.py:39-74).
+// The new Q4_0 entry points run on the GPU only: every one of them checks
+// for a HIP device and returns TG_E_NODEVICE rather than computing anything
+// on the host.
+#include "tg_internal.h"
+#include "../../include/tinygiant.h"
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <sys/mman.h>
+
+#include <atomic>
+#include <mutex>
+#include <string>
+#include <vector>
+
+using tg::Shape;
+
+// ================================================================ errors
+static thread_local std::string g_err;
+
+static int set_err(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return set_err(TG_E_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),       \
+                           __FILE__, __LINE__);                                            \
+    } while (0)
+
+extern "C" const char *tg_last_error(void) { return g_err.c_str(); }
+
+extern "C" const char *tg_version(void) { return "tinygiant-gfx950 0.1"; }
+
+// ================================================================ device
+static std::mutex g_dev_mu;
+static int g_dev = -1;
+
+extern "C" int tg_gpu_init(int device) {
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return set_err(TG_E_NODEVICE, "no HIP device visible");
+    if (device < 0 || device >= n) return set_err(TG_E_INVALID, "device %d out of range (0..%d)", device, n - 1);
+    HIP_TRY(hipSetDevice(device));
+    HIP_TRY(hipFree(nullptr));
+    g_dev = device;
+    return TG_OK;
+}
+
+static int ensure_device() {
+    if (g_dev >= 0) {
+        int cur = -1;
+        if (hipGetDevice(&cur) == hipSuccess && cur == g_dev) return TG_OK;
+        HIP_TRY(hipSetDevice(g_dev));
+        return TG_OK;
+    }
+    return tg_gpu_init(0);
+}
+
+extern "C" int tg_device_sync(void) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    HIP_TRY(hipDeviceSynchronize());
+    return TG_OK;
+}
+
+static hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ================================================================ timing
+struct ProfRec {
+    std::string kernel;
+    hipEvent_t start, stop;
+};
+static std::mutex g_prof_mu;
+static bool g_prof_on = false;
+static std::vector<ProfRec> g_prof;
+static std::vector<hipEvent_t> g_event_pool;
+
+static hipEvent_t pool_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+static void prof_clear() {
+    for (auto &r : g_prof) {
+        g_event_pool.push_back(r.start);
+        g_event_pool.push_back(r.stop);
+    }
+    g_prof.clear();
+}
+
+// Records the start event of one launch; returns its slot (or -1).
+static int prof_begin(const char *kernel, hipStream_t st) {
+    if (!g_prof_on) return -1;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    ProfRec r{kernel, pool_event(), pool_event()};
+    if (!r.start || !r.stop) return -1;
+    (void)hipEventRecord(r.start, st);
+    g_prof.push_back(r);
+    return (int)g_prof.size() - 1;
+}
+
+static void prof_end(int slot, hipStream_t st) {
+    if (slot < 0) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    (void)hipEventRecord(g_prof[(size_t)slot].stop, st);
+}
+
+extern "C" int tg_prof_enable(int on) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (on) prof_clear();
+    g_prof_on = on != 0;
+    return TG_OK;
+}
+
+extern "C" int tg_prof_read(const char *kernel, int *launches, double *total_ms) {
+    if (!kernel) return set_err(TG_E_INVALID, "kernel name is NULL");
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    int n = 0;
+    double ms = 0.0;
+    for (auto &r : g_prof) {
+        if (r.kernel != kernel) continue;
+        HIP_TRY(hipEventSynchronize(r.stop));
+        float t = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&t, r.start, r.stop));
+        ms += t;
+        n++;
+    }
+    if (launches) *launches = n;
+    if (total_ms) *total_ms = ms;
+    return TG_OK;
+}
+
+#define PROFILED(name, st, launch)             \
+    do {                                       \
+        int slot_ = prof_begin(name, st);      \
+        HIP_TRY(launch);                       \
+        prof_end(slot_, st);                   \
+    } while (0)
+
+// ================================================================ arena
+struct tg_arena {
+    Shape s;
+    int L = 0;
+    uint8_t *experts = nullptr;   // L * LB bytes, tensor-planar per tensor
+    float *routers = nullptr;     // L * E * H
+    uint8_t *staging = nullptr;   // LB bytes, relayout form for load/read
+    // per-call scratch, grown on demand
+    int cap_T = 0;
+    float *logits = nullptr;      // T * E
+    float *h = nullptr;           // T * k * I
+    int32_t *idx = nullptr;       // T * k
+    float *w = nullptr;           // T * k
+    float *xbuf = nullptr;        // T * H (host-pointer entry points)
+    float *obuf = nullptr;        // T * H
+};
+
+static int check_shape(int H, int I, int E, int k) {
+    if (H <= 0 || I <= 0 || H % 256 || I % 32)
+        return set_err(TG_E_INVALID, "embed_dim must be a positive multiple of 256 and inter_dim of 32 (got %d, %d)",
+                       H, I);
+    if (H / 32 > tg::MAX_NB || I / 32 > tg::MAX_NB)
+        return set_err(TG_E_INVALID, "embed_dim / inter_dim above %d", tg::MAX_NB * 32);
+    if (E <= 0 || E > tg::MAX_E) return set_err(TG_E_INVALID, "n_experts must be in 1..%d (got %d)", tg::MAX_E, E);
+    if (k <= 0 || k > tg::MAX_K || k > E)
+        return set_err(TG_E_INVALID, "top_k must be in 1..min(%d, n_experts) (got %d)", tg::MAX_K, k);
+    return TG_OK;
+}
+
+static void dfree(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+static void arena_free(tg_arena *a) {
+    if (!a) return;
+    dfree(a->experts);
+    dfree(a->routers);
+    dfree(a->staging);
+    dfree(a->logits);
+    dfree(a->h);
+    dfree(a->idx);
+    dfree(a->w);
+    dfree(a->xbuf);
+    dfree(a->obuf);
+    delete a;
+}
+
+extern "C" tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim, int inter_dim, int top_k) {
+    if (n_layers <= 0) { set_err(TG_E_INVALID, "n_layers must be positive"); return nullptr; }
+    if (check_shape(embed_dim, inter_dim, n_experts, top_k)) return nullptr;
+    if (ensure_device()) return nullptr;
+    tg_arena *a = new tg_arena();
+    a->s = tg::make_shape(embed_dim, inter_dim, n_experts, top_k);
+    a->L = n_layers;
+    size_t eb = a->s.LB * (size_t)n_layers;
+    size_t rb = sizeof(float) * (size_t)n_experts * embed_dim * n_layers;
+    if (hipMalloc(&a->experts, eb) != hipSuccess || hipMalloc(&a->routers, rb) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err(TG_E_NOMEM, "hipMalloc of %.2f GB expert arena failed", (eb + rb) / 1e9);
+        arena_free(a);
+        return nullptr;
+    }
+    return a;
+}
+
+extern "C" void tg_arena_destroy(tg_arena *a) { arena_free(a); }
+
+extern "C" size_t tg_arena_expert_bytes(const tg_arena *a) { return a ? a->s.EB : 0; }
+extern "C" size_t tg_arena_layer_bytes(const tg_arena *a) { return a ? a->s.LB : 0; }
+
+extern "C" int tg_arena_expert_offset(const tg_arena *a, int expert, size_t *offset, size_t *gate_bytes,
+                                      size_t *up_bytes, size_t *down_bytes) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (expert < 0 || expert >= a->s.E) return set_err(TG_E_INVALID, "expert %d out of range", expert);
+    if (offset) *offset = (size_t)expert * a->s.EB;
+    if (gate_bytes) *gate_bytes = a->s.GB;
+    if (up_bytes) *up_bytes = a->s.GB;
+    if (down_bytes) *down_bytes = a->s.DB;
+    return TG_OK;
+}
+
+static int arena_layer_check(tg_arena *a, int layer) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (layer < 0 || layer >= a->L) return set_err(TG_E_INVALID, "layer %d out of range 0..%d", layer, a->L - 1);
+    return ensure_device();
+}
+
+static int arena_staging(tg_arena *a) {
+    if (a->staging) return TG_OK;
+    if (hipMalloc(&a->staging, a->s.LB) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(TG_E_NOMEM, "hipMalloc of %zu-byte staging buffer failed", a->s.LB);
+    }
+    return TG_OK;
+}
+
+extern "C" int tg_arena_load_layer(tg_arena *a, int layer, const void *host_bytes, size_t nbytes) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    if (!host_bytes) return set_err(TG_E_INVALID, "host_bytes is NULL");
+    if (nbytes != a->s.LB) return set_err(TG_E_INVALID, "layer file has %zu bytes, expected %zu", nbytes, a->s.LB);
+    if ((rc = arena_staging(a))) return rc;
+    HIP_TRY(hipMemcpy(a->staging, host_bytes, nbytes, hipMemcpyHostToDevice));
+    HIP_TRY(tg::launch_repack_layer(a->staging, a->experts + (size_t)layer * a->s.LB, a->s, true, nullptr));
+    HIP_TRY(hipStreamSynchronize(nullptr));
+    return TG_OK;
+}
+
+extern "C" int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes, size_t nbytes) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    if (!host_bytes) return set_err(TG_E_INVALID, "host_bytes is NULL");
+    if (nbytes != a->s.LB) return set_err(TG_E_INVALID, "buffer has %zu bytes, expected %zu", nbytes, a->s.LB);
+    if ((rc = arena_staging(a))) return rc;
+    HIP_TRY(tg::launch_repack_layer(a->experts + (size_t)layer * a->s.LB, a->staging, a->s, false, nullptr));
+    HIP_TRY(hipMemcpy(host_bytes, a->staging, nbytes, hipMemcpyDeviceToHost));
+    return TG_OK;
+}
+
+extern "C" int tg_arena_load_router(tg_arena *a, int layer, const float *host_router, size_t count) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    size_t n = (size_t)a->s.E * a->s.H;
+    if (!host_router || count != n) return set_err(TG_E_INVALID, "router needs %zu floats (got %zu)", n, count);
+    HIP_TRY(hipMemcpy(a->routers + (size_t)layer * n, host_router, n * sizeof(float), hipMemcpyHostToDevice));
+    return TG_OK;
+}
+
+extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float sigma) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    HIP_TRY(tg::launch_synth_layer(a->experts + (size_t)layer * a->s.LB,
+                                   a->routers + (size_t)layer * a->s.E * a->s.H, a->s, layer, seed, sigma,
+                                   nullptr));
+    HIP_TRY(hipStreamSynchronize(nullptr));
+    return TG_OK;
+}
+
+static int arena_scratch(tg_arena *a, int T) {
+    if (T <= a->cap_T) return TG_OK;
+    dfree(a->logits); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf);
+    a->logits = nullptr; a->h = nullptr; a->idx = nullptr; a->w = nullptr; a->xbuf = nullptr; a->obuf = nullptr;
+    a->cap_T = 0;
+    const Shape &s = a->s;
+    bool ok = hipMalloc(&a->logits, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
+              hipMalloc(&a->h, sizeof(float) * (size_t)T * s.k * s.I) == hipSuccess &&
+              hipMalloc(&a->idx, sizeof(int32_t) * (size_t)T * s.k) == hipSuccess &&
+              hipMalloc(&a->w, sizeof(float) * (size_t)T * s.k) == hipSuccess &&
+              hipMalloc(&a->xbuf, sizeof(float) * (size_t)T * s.H) == hipSuccess &&
+              hipMalloc(&a->obuf, sizeof(float) * (size_t)T * s.H) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        return set_err(TG_E_NOMEM, "scratch for %d tokens", T);
+    }
+    a->cap_T = T;
+    return TG_OK;
+}
+
+// ================================================================ MoE block
+static int moe_layer_launch(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T,
+                            int32_t *idx_out, float *w_out, float eps, hipStream_t st) {
+    const Shape &s = a->s;
+    const uint8_t *lp = a->experts + (size_t)layer * s.LB;
+    const float *wr = a->routers + (size_t)layer * s.E * s.H;
+    PROFILED("router", st, tg::launch_router(wr, x, T, s.E, s.H, eps, a->logits, st));
+    PROFILED("gateup", st, tg::launch_gateup(lp, s, x, a->logits, T, eps, a->h, a->idx, a->w, st));
+    PROFILED("down", st, tg::launch_down(lp, s, a->h, a->idx, a->w, T, resid, out, st));
+    if (idx_out) HIP_TRY(hipMemcpyAsync(idx_out, a->idx, sizeof(int32_t) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
+    if (w_out) HIP_TRY(hipMemcpyAsync(w_out, a->w, sizeof(float) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
+    return TG_OK;
+}
+
+static int check_tokens(int T) {
+    if (T <= 0 || T > 65535) return set_err(TG_E_INVALID, "n_tokens must be in 1..65535 (got %d)", T);
+    return TG_OK;
+}
+
+extern "C" int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x, float *moe_out, int n_tokens,
+                                    int32_t *topk_idx, float *topk_w, float eps, void *stream) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    if ((rc = check_tokens(n_tokens))) return rc;
+    if (!x || !moe_out) return set_err(TG_E_INVALID, "x / moe_out is NULL");
+    if ((rc = arena_scratch(a, n_tokens))) return rc;
+    return moe_layer_launch(a, layer, x, moe_out, nullptr, n_tokens, topk_idx, topk_w, eps, as_stream(stream));
+}
+
+extern "C" int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out, int n_tokens,
+                                int32_t *topk_idx, float *topk_w, float eps) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    if ((rc = check_tokens(n_tokens))) return rc;
+    if (!x || !moe_out) return set_err(TG_E_INVALID, "x / moe_out is NULL");
+    if ((rc = arena_scratch(a, n_tokens))) return rc;
+    const Shape &s = a->s;
+    size_t nx = (size_t)n_tokens * s.H;
+    HIP_TRY(hipMemcpy(a->xbuf, x, nx * sizeof(float), hipMemcpyHostToDevice));
+    if ((rc = moe_layer_launch(a, layer, a->xbuf, a->obuf, nullptr, n_tokens, nullptr, nullptr, eps, nullptr)))
+        return rc;
+    HIP_TRY(hipMemcpy(moe_out, a->obuf, nx * sizeof(float), hipMemcpyDeviceToHost));
+    if (topk_idx) HIP_TRY(hipMemcpy(topk_idx, a->idx, sizeof(int32_t) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
+    if (topk_w) HIP_TRY(hipMemcpy(topk_w, a->w, sizeof(float) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
+    return TG_OK;
+}
+
+static int stack_check(tg_arena *a, int layer0, int n_layers, int T, const float *x) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (n_layers <= 0 || layer0 < 0 || layer0 + n_layers > a->L)
+        return set_err(TG_E_INVALID, "layers %d..%d outside the arena's %d", layer0, layer0 + n_layers - 1, a->L);
+    int rc = check_tokens(T);
+    if (rc) return rc;
+    if (!x) return set_err(TG_E_INVALID, "x is NULL");
+    if ((rc = ensure_device())) return rc;
+    return arena_scratch(a, T);
+}
+
+extern "C" int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int layer0, int n_layers, float eps,
+                                    void *stream) {
+    int rc = stack_check(a, layer0, n_layers, n_tokens, x);
+    if (rc) return rc;
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        if ((rc = moe_layer_launch(a, l, x, x, x, n_tokens, nullptr, nullptr, eps, as_stream(stream)))) return rc;
+    return TG_OK;
+}
+
+extern "C" int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0, int n_layers, float eps) {
+    int rc = stack_check(a, layer0, n_layers, n_tokens, x);
+    if (rc) return rc;
+    size_t nx = (size_t)n_tokens * a->s.H;
+    HIP_TRY(hipMemcpy(a->xbuf, x, nx * sizeof(float), hipMemcpyHostToDevice));
+    for (int l = layer0; l < layer0 + n_layers; l++)
+        if ((rc = moe_layer_launch(a, l, a->xbuf, a->xbuf, a->xbuf, n_tokens, nullptr, nullptr, eps, nullptr)))
+            return rc;
+    HIP_TRY(hipMemcpy(x, a->xbuf, nx * sizeof(float), hipMemcpyDeviceToHost));
+    return TG_OK;
+}
+
+// ================================================================ building blocks
+extern "C" int tg_q40_quantize_q8_0_dev(const float *x, void *q8_out, int n, void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!x || !q8_out || n <= 0 || n % 32) return set_err(TG_E_INVALID, "n must be a positive multiple of 32");
+    HIP_TRY(tg::launch_quantize_q8_0(x, static_cast<uint8_t *>(q8_out), n, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_q40_to_planar_dev(const void *aos, void *planar, int rows, int nb, void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!aos || !planar || rows <= 0 || nb <= 0) return set_err(TG_E_INVALID, "bad repack arguments");
+    HIP_TRY(tg::launch_repack_tensor(static_cast<const uint8_t *>(aos), static_cast<uint8_t *>(planar),
+                                     (size_t)rows * nb, true, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_q40_from_planar_dev(const void *planar, void *aos, int rows, int nb, void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!aos || !planar || rows <= 0 || nb <= 0) return set_err(TG_E_INVALID, "bad repack arguments");
+    HIP_TRY(tg::launch_repack_tensor(static_cast<const uint8_t *>(planar), static_cast<uint8_t *>(aos),
+                                     (size_t)rows * nb, false, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_q40_block_sums_dev(const void *w_planar, int rows, int cols, const void *xq8, int32_t *sums,
+                                     void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!w_planar || !xq8 || !sums || rows <= 0 || cols <= 0 || cols % 32)
+        return set_err(TG_E_INVALID, "bad block-sum arguments");
+    HIP_TRY(tg::launch_block_sums(static_cast<const uint8_t *>(w_planar), rows, cols / 32,
+                                  static_cast<const uint8_t *>(xq8), sums, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_q40_matvec_dev(const void *w_planar, int rows, int cols, const void *xq8, float *out,
+                                 void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!w_planar || !xq8 || !out || rows <= 0 || cols <= 0 || cols % 32 || cols / 32 > tg::MAX_NB)
+        return set_err(TG_E_INVALID, "bad matvec arguments (cols multiple of 32, <= %d)", tg::MAX_NB * 32);
+    HIP_TRY(tg::launch_matvec(static_cast<const uint8_t *>(w_planar), rows, cols / 32,
+                              static_cast<const uint8_t *>(xq8), out, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_router_topk_dev(const float *Wr, const float *x, int n_experts, int embed_dim, int top_k,
+                                  float eps, int n_tokens, float *logits, int32_t *topk_idx, float *topk_w,
+                                  void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!Wr || !x || !logits) return set_err(TG_E_INVALID, "Wr / x / logits is NULL");
+    if ((rc = check_shape(embed_dim, 32, n_experts, top_k))) return rc;
+    if ((rc = check_tokens(n_tokens))) return rc;
+    hipStream_t st = as_stream(stream);
+    HIP_TRY(tg::launch_router(Wr, x, n_tokens, n_experts, embed_dim, eps, logits, st));
+    if (topk_idx || topk_w) HIP_TRY(tg::launch_topk(logits, n_tokens, n_experts, top_k, topk_idx, topk_w, st));
+    return TG_OK;
+}
+
+extern "C" int tg_synth_normal_dev(uint64_t seed, uint64_t stream_id, float sigma, size_t n, float *out,
+                                   void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!out) return set_err(TG_E_INVALID, "out is NULL");
+    HIP_TRY(tg::launch_synth_normal(out, tg::host_stream_key(seed, stream_id), sigma, n, as_stream(stream)));
+    return TG_OK;
+}
+
+extern "C" int tg_synth_q40_dev(uint64_t seed, uint64_t stream_id, float sigma, int rows, int cols,
+                                void *planar_out, void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!planar_out || rows <= 0 || cols <= 0 || cols % 32) return set_err(TG_E_INVALID, "bad synth arguments");
+    HIP_TRY(tg::launch_synth_q40(static_cast<uint8_t *>(planar_out), tg::host_stream_key(seed, stream_id), sigma,
+                                 rows, cols / 32, as_stream(stream)));
+    return TG_OK;
+}
+
+// ================================================================ reference ABI
+// Residency helpers: the same POSIX calls as csrc/libtinygiant.c:745-766
+// (16 KiB page mask); with every expert resident in HBM they only matter
+// for host buffers the caller still keeps.
+static const uintptr_t kPageMask = ~((uintptr_t)16384 - 1);
+
+extern "C" void tg_prefetch(const void *addr, size_t len) {
+    void *aligned = (void *)((uintptr_t)addr & kPageMask);
+    size_t alen = len + ((uintptr_t)addr - (uintptr_t)aligned);
+    posix_madvise(aligned, alen, POSIX_MADV_WILLNEED);
+}
+
+extern "C" void tg_prefetch_batch(const void **addrs, const size_t *lens, int count) {
+    for (int i = 0; i < count; i++) tg_prefetch(addrs[i], lens[i]);
+}
+
+extern "C" int tg_mlock(const void *addr, size_t len) {
+    void *aligned = (void *)((uintptr_t)addr & kPageMask);
+    size_t alen = len + ((uintptr_t)addr - (uintptr_t)aligned);
+    return mlock(aligned, alen);
+}
+
+// The Q4_K / Q6_K / f16 / attention entry points are not yet on the GPU in
+// this build.  They fail loudly: an error message (once per symbol on
+// stderr, and in tg_last_error), and NaN in every output element whose count
+// the signature gives, so a caller can never mistake the result for data.
+static void legacy_unavailable(const char *name, std::atomic<bool> &warned) {
+    set_err(TG_E_UNSUPPORTED, "%s: Q4_K/Q6_K/f16 legacy path is not available on the GPU in this build", name);
+    if (!warned.exchange(true)) fprintf(stderr, "libtinygiant (gfx950): %s\n", g_err.c_str());
+}
+
+static void fill_nan(float *p, long n) {
+    if (!p) return;
+    for (long i = 0; i < n; i++) p[i] = NAN;
+}
+
+#define LEGACY_FLAG(name) static std::atomic<bool> warned_##name{false}
+
+LEGACY_FLAG(expert_forward);
+LEGACY_FLAG(expert_forward_mixed);
+LEGACY_FLAG(matmul_q4k);
+LEGACY_FLAG(matmul_q6k);
+LEGACY_FLAG(rms_norm);
+LEGACY_FLAG(f32_matvec);
+LEGACY_FLAG(f16_matvec);
+LEGACY_FLAG(attention_decode);
+LEGACY_FLAG(attention_decode_q4);
+LEGACY_FLAG(transformer_layer);
+LEGACY_FLAG(moe_forward);
+LEGACY_FLAG(matmul_q4k_scalar);
+
+extern "C" void tg_expert_forward(const uint8_t *, const float *, float *output, float, int embed_dim, int) {
+    legacy_unavailable("tg_expert_forward", warned_expert_forward);
+    fill_nan(output, embed_dim);
+}
+
+extern "C" void tg_expert_forward_mixed(const uint8_t *, const uint8_t *, const void *, int, const float *,
+                                        float *output, float, int embed_dim, int) {
+    legacy_unavailable("tg_expert_forward_mixed", warned_expert_forward_mixed);
+    fill_nan(output, embed_dim);
+}
+
+extern "C" void tg_matmul_q4k(const uint8_t *, const float *, float *output, int nrows, int) {
+    legacy_unavailable("tg_matmul_q4k", warned_matmul_q4k);
+    fill_nan(output, nrows);
+}
+
+extern "C" void tg_matmul_q6k(const uint8_t *, const float *, float *output, int nrows, int) {
+    legacy_unavailable("tg_matmul_q6k", warned_matmul_q6k);
+    fill_nan(output, nrows);
+}
+
+extern "C" void tg_rms_norm(const float *, const float *, float *out, int dim, float) {
+    legacy_unavailable("tg_rms_norm", warned_rms_norm);
+    fill_nan(out, dim);
+}
+
+extern "C" void tg_f32_matvec(const float *, const float *, float *out, int nrows, int) {
+    legacy_unavailable("tg_f32_matvec", warned_f32_matvec);
+    fill_nan(out, nrows);
+}
+
+extern "C" void tg_f16_matvec(const uint16_t *, const float *, float *out, int nrows, int) {
+    legacy_unavailable("tg_f16_matvec", warned_f16_matvec);
+    fill_nan(out, nrows);
+}
+
+extern "C" void tg_attention_decode(const float *, const float *, const float *, const float *, const float *,
+                                    const float *, float *, float *, int, int, const float *, const float *,
+                                    const float *, float *output, int embed_dim, int, int, int, int) {
+    legacy_unavailable("tg_attention_decode", warned_attention_decode);
+    fill_nan(output, embed_dim);
+}
+
+extern "C" void tg_attention_decode_q4(const uint8_t *, const uint8_t *, const uint16_t *, const uint8_t *,
+                                       const float *, const float *, float *, float *, int, int, const float *,
+                                       const float *, const float *, float *output, int embed_dim, int, int, int,
+                                       int) {
+    legacy_unavailable("tg_attention_decode_q4", warned_attention_decode_q4);
+    fill_nan(output, embed_dim);
+}
+
+extern "C" void tg_transformer_layer(const float *, const float *, const float *, const float *, const float *,
+                                     const float *, const float *, const float *, float *, float *, int, int,
+                                     const float *, const float *, const uint8_t **, const uint8_t **,
+                                     const void **, const int *, const float *, int, float *x, int embed_dim, int,
+                                     int, int, int, int) {
+    legacy_unavailable("tg_transformer_layer", warned_transformer_layer);
+    fill_nan(x, embed_dim);
+}
+
+extern "C" void tg_moe_forward(const uint8_t **, const float *, int, const float *, float *output, int embed_dim,
+                               int) {
+    legacy_unavailable("tg_moe_forward", warned_moe_forward);
+    fill_nan(output, embed_dim);
+}
+
+extern "C" void tg_matmul_q4k_scalar(const uint8_t *, const float *, float *output, int nrows, int) {
+    legacy_unavailable("tg_matmul_q4k_scalar", warned_matmul_q4k_scalar);
+    fill_nan(output, nrows);
+}

@@ -1,0 +1,68 @@
+// tg_internal.h -- shapes and kernel launchers shared by the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tg {
+
+// One layer's geometry: H = embed dim, I = expert intermediate dim, E
+// experts, top-k.  Byte sizes are those of the relayout format (18 bytes
+// per 32 weights), which the planar arena keeps.
+struct Shape {
+    int H, I, E, k;
+    int nbH, nbI;      // blocks per gate/up row, per down row
+    size_t GB;         // bytes of gate (= up)
+    size_t DB;         // bytes of down
+    size_t EB;         // bytes of one expert
+    size_t LB;         // bytes of one layer's experts
+};
+
+inline Shape make_shape(int H, int I, int E, int k) {
+    Shape s;
+    s.H = H; s.I = I; s.E = E; s.k = k;
+    s.nbH = H / 32; s.nbI = I / 32;
+    s.GB = (size_t)I * s.nbH * 18;
+    s.DB = (size_t)H * s.nbI * 18;
+    s.EB = 2 * s.GB + s.DB;
+    s.LB = s.EB * (size_t)E;
+    return s;
+}
+
+// Counter stream of one synthetic tensor: kind 0 gate, 1 up, 2 down,
+// 3 router, 4 activations.
+__host__ __device__ inline uint64_t stream_id(int layer, int expert, int kind) {
+    return ((uint64_t)(layer & 0xFFFF) << 40) | ((uint64_t)(expert & 0xFFFFFF) << 8) | (uint64_t)(kind & 0xFF);
+}
+
+uint64_t host_stream_key(uint64_t seed, uint64_t stream);
+
+// limits of the decode kernels
+constexpr int MAX_K = 32;        // top-k
+constexpr int MAX_E = 512;       // experts per layer
+constexpr int MAX_NB = 256;      // blocks per row (H, I <= 8192)
+
+hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, int layer,
+                              uint64_t seed, float sigma, hipStream_t st);
+hipError_t launch_synth_q40(uint8_t *pl, uint64_t key, float sigma, int rows, int nb, hipStream_t st);
+hipError_t launch_synth_normal(float *out, uint64_t key, float sigma, size_t n, hipStream_t st);
+hipError_t launch_repack_layer(const uint8_t *src, uint8_t *dst, const Shape &s, bool to_planar,
+                               hipStream_t st);
+hipError_t launch_repack_tensor(const uint8_t *src, uint8_t *dst, size_t nblocks, bool to_planar,
+                                hipStream_t st);
+hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int n, hipStream_t st);
+hipError_t launch_block_sums(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, int32_t *sums,
+                             hipStream_t st);
+hipError_t launch_matvec(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, float *out,
+                         hipStream_t st);
+hipError_t launch_router(const float *Wr, const float *x, int T, int E, int H, float eps, float *logits,
+                         hipStream_t st);
+hipError_t launch_topk(const float *logits, int T, int E, int k, int32_t *idx, float *w, hipStream_t st);
+// decode MoE layer pieces
+hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *logits,
+                         int T, float eps, float *h, int32_t *idx, float *w, hipStream_t st);
+hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx,
+                       const float *w, int T, const float *resid, float *out, hipStream_t st);
+
+}  // namespace tg
