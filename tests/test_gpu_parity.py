@@ -77,9 +77,10 @@ def test_planar_repack_roundtrip(O, tglib, rows, nb):
     gpu_note(f"repack {rows}x{nb}")
     rng = np.random.default_rng(rows * 1000 + nb)
     aos = rng.integers(0, 256, rows * nb * 18, dtype=np.uint8)
+    src = dev(aos)
     pl = torch.empty(aos.size, dtype=torch.uint8, device="cuda")
     back = torch.empty(aos.size, dtype=torch.uint8, device="cuda")
-    call("tg_q40_to_planar_dev", dev(aos).data_ptr(), pl.data_ptr(), rows, nb, stream())
+    call("tg_q40_to_planar_dev", src.data_ptr(), pl.data_ptr(), rows, nb, stream())
     call("tg_q40_from_planar_dev", pl.data_ptr(), back.data_ptr(), rows, nb, stream())
     assert np.array_equal(host(pl), O.to_planar(aos, rows, nb))
     assert np.array_equal(host(back), aos)
@@ -99,8 +100,9 @@ def q8_cases():
 def test_quantize_q8_0_bitexact(O, tglib, which):
     x = q8_cases() if which == "cases" else np.random.default_rng(9).standard_normal(2048 * 40).astype(np.float32)
     gpu_note(f"quantize_q8_0 {which} n={x.size}")
+    xd = dev(x)
     out = torch.empty(x.size // 32 * 34, dtype=torch.uint8, device="cuda")
-    call("tg_q40_quantize_q8_0_dev", dev(x).data_ptr(), out.data_ptr(), x.size, stream())
+    call("tg_q40_quantize_q8_0_dev", xd.data_ptr(), out.data_ptr(), x.size, stream())
     assert np.array_equal(host(out), O.quantize_q8_0(x))
 
 
@@ -112,9 +114,9 @@ def test_block_sums_bitexact(O, tglib, rows, cols):
     x = O.synth_normal(7, O.stream_id(0, 0, 4), 1.0, cols)
     xq = O.quantize_q8_0(x)
     ref = O.block_sums(W, rows, cols, xq)
+    wd, xqd = dev(O.to_planar(W, rows, nb)), dev(xq)
     sums = torch.empty((rows, nb), dtype=torch.int32, device="cuda")
-    call("tg_q40_block_sums_dev", dev(O.to_planar(W, rows, nb)).data_ptr(), rows, cols, dev(xq).data_ptr(),
-         sums.data_ptr(), stream())
+    call("tg_q40_block_sums_dev", wd.data_ptr(), rows, cols, xqd.data_ptr(), sums.data_ptr(), stream())
     assert np.array_equal(host(sums), ref)
 
 
@@ -125,9 +127,9 @@ def test_matvec_bitexact(O, tglib, rows, cols):
     W = O.synth_q40(8, O.stream_id(1, 2, 2), 0.02, rows, cols)
     xq = O.quantize_q8_0(O.synth_normal(8, O.stream_id(1, 0, 4), 1.0, cols))
     ref = O.matvec_q40(W, rows, cols, xq)
+    wd, xqd = dev(O.to_planar(W, rows, nb)), dev(xq)
     out = torch.empty(rows, dtype=torch.float32, device="cuda")
-    call("tg_q40_matvec_dev", dev(O.to_planar(W, rows, nb)).data_ptr(), rows, cols, dev(xq).data_ptr(),
-         out.data_ptr(), stream())
+    call("tg_q40_matvec_dev", wd.data_ptr(), rows, cols, xqd.data_ptr(), out.data_ptr(), stream())
     assert_fp32_parity(host(out), ref, f"matvec {rows}x{cols}")
 
 
@@ -141,7 +143,8 @@ def test_router_topk_exact(O, tglib, E, H, k, T):
     logits = torch.empty((T, E), dtype=torch.float32, device="cuda")
     idx = torch.empty((T, k), dtype=torch.int32, device="cuda")
     w = torch.empty((T, k), dtype=torch.float32, device="cuda")
-    call("tg_router_topk_dev", dev(Wr).data_ptr(), dev(x).data_ptr(), E, H, k, 1e-6, T, logits.data_ptr(),
+    wrd, xd = dev(Wr), dev(x)
+    call("tg_router_topk_dev", wrd.data_ptr(), xd.data_ptr(), E, H, k, 1e-6, T, logits.data_ptr(),
          idx.data_ptr(), w.data_ptr(), stream())
     gl, gi, gw = host(logits), host(idx), host(w)
     for t in range(T):
@@ -168,7 +171,8 @@ def test_router_topk_ties(O, tglib):
     idx = torch.empty((1, k), dtype=torch.int32, device="cuda")
     w = torch.empty((1, k), dtype=torch.float32, device="cuda")
     logits = torch.empty((1, E), dtype=torch.float32, device="cuda")
-    call("tg_router_topk_dev", dev(Wr).data_ptr(), dev(x).data_ptr(), E, H, k, 1e-6, 1, logits.data_ptr(),
+    wrd, xd = dev(Wr), dev(x)
+    call("tg_router_topk_dev", wrd.data_ptr(), xd.data_ptr(), E, H, k, 1e-6, 1, logits.data_ptr(),
          idx.data_ptr(), w.data_ptr(), stream())
     assert host(idx)[0].tolist() == [3, 9, 10, 40, 41, 63, 50, 0]
     ri, rw = O.topk_softmax(host(logits)[0], k)
