@@ -153,7 +153,7 @@ def main() -> int:
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     kern = {}
-    for name in ("router", "gateup", "down"):
+    for name in ("route", "gateup", "down"):
         import ctypes
         n = ctypes.c_int()
         ms = ctypes.c_double()

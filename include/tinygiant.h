@@ -55,7 +55,7 @@ int tg_device_sync(void);
 const char *tg_version(void);
 /* Kernel timing.  While enabled, the MoE entry points bracket every kernel
  * launch with HIP events recorded on the launching stream; tg_prof_read
- * waits for them and returns, for one kernel name ("router", "gateup",
+ * waits for them and returns, for one kernel name ("route", "gateup",
  * "down"), the number of launches and their summed duration in ms.
  * tg_prof_enable(1) also discards earlier records. */
 int tg_prof_enable(int on);
@@ -204,8 +204,8 @@ int tg_q40_block_sums_dev(const void *w_planar, int rows, int cols,
 /* out[r] = Q4_0 row r . Q8_0 vector (planar matrix). */
 int tg_q40_matvec_dev(const void *w_planar, int rows, int cols,
                       const void *xq8, float *out, void *stream);
-/* Router logits + top-k + softmax for n_tokens (any pointer but x/Wr may be
- * NULL). */
+/* Router logits (s * (Wr . x), grouped order) + top-k + softmax for
+ * n_tokens; topk_idx / topk_w may be NULL.  Synchronous. */
 int tg_router_topk_dev(const float *Wr, const float *x, int n_experts,
                        int embed_dim, int top_k, float eps, int n_tokens,
                        float *logits, int32_t *topk_idx, float *topk_w,

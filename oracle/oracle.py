@@ -67,7 +67,7 @@ def lib():
             "tgo_sumsq": (_F, [_P, _I]),
             "tgo_rms_scale": (_F, [_P, _I, _F]),
             "tgo_router_dot": (_F, [_P, _P, _I]),
-            "tgo_router_logits": (None, [_P, _I, _I, _P, _P]),
+            "tgo_router_logits": (None, [_P, _I, _I, _P, _F, _P]),
             "tgo_topk_softmax": (None, [_P, _I, _I, _P, _P]),
             "tgo_silu_mul": (_F, [_F, _F]),
             "tgo_expert_q40": (None, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
@@ -227,17 +227,19 @@ def rms_scale(x: np.ndarray, eps: float = 1e-6) -> float:
     return lib().tgo_rms_scale(_p(x), x.size, eps)
 
 
-def router_dot(w: np.ndarray, xn: np.ndarray) -> float:
+def router_dot(w: np.ndarray, x: np.ndarray) -> float:
+    """Un-normalised grouped dot w . x (the logit is this times the norm scale)."""
     w = np.ascontiguousarray(w, dtype=np.float32)
-    xn = np.ascontiguousarray(xn, dtype=np.float32)
-    return lib().tgo_router_dot(_p(w), _p(xn), w.size)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().tgo_router_dot(_p(w), _p(x), w.size)
 
 
-def router_logits(Wr: np.ndarray, xn: np.ndarray) -> np.ndarray:
+def router_logits(Wr: np.ndarray, x: np.ndarray, s: float) -> np.ndarray:
+    """logits = s * (Wr @ x) in the grouped order, x un-normalised."""
     Wr = np.ascontiguousarray(Wr, dtype=np.float32)
     E, H = Wr.shape
     out = np.empty(E, dtype=np.float32)
-    lib().tgo_router_logits(_p(Wr), E, H, _p(np.ascontiguousarray(xn, dtype=np.float32)), _p(out))
+    lib().tgo_router_logits(_p(Wr), E, H, _p(np.ascontiguousarray(x, dtype=np.float32)), float(s), _p(out))
     return out
 
 

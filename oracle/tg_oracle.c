@@ -18,11 +18,10 @@
  *   row dot      acc = fma(round(S_b * dw_b), dx_b, acc), blocks b = 0..nb-1
  *                (S_b = exact int32 block sum; the same sequential per-block
  *                accumulation as libtinygiant.c:109-167 `total += ...`)
- *   sum of x^2   256 partials (lane t takes float4 chunks t, t+256, ...,
- *                fma in chunk/element order), xor-butterfly 32..1 inside each
- *                group of 64, then (g0 + g1) + (g2 + g3)
- *   router dot   64 partials (lane l takes float4 chunks l, l+64, ...),
- *                xor-butterfly 32..1
+ *   sum of x^2   fma chain inside each group of 32 consecutive elements,
+ *                group sums added in ascending order
+ *   router       logit = s * (w . x) with w . x in the same grouped order and
+ *                s = 1/sqrt(mean(x^2) + eps)
  *   softmax sum  numpy's pairwise float32 sum over the top-k in ascending
  *                logit order (engine.py:232-236)
  *   combine      acc = fma(w_j, down_j, acc) in ascending logit order
@@ -389,36 +388,20 @@ void tgo_q40_from_planar(const uint8_t *pl, int rows, int nb, uint8_t *aos) {
 /* norm, router, SwiGLU                                                 */
 /* ------------------------------------------------------------------ */
 
-static float butterfly(float *p, int n) {
-    /* xor butterfly over n (power of two) partials: p[l] <- p[l] + p[l^s]
-     * for s = n/2 .. 1; every lane ends with the same value. */
-    float t[256];
-    for (int s = n / 2; s >= 1; s >>= 1) {
-        for (int l = 0; l < n; l++) t[l] = p[l] + p[l ^ s];
-        memcpy(p, t, sizeof(float) * (size_t)n);
-    }
-    return p[0];
-}
 
-/* Sum of squares in the GPU's tree (file header).  Role of the vfmaq loop in
- * tg_rms_norm, libtinygiant.c:324-331.  Pinned by
- * tests/test_oracle_math.py::test_sumsq_tree (float64 within bound, and an
- * independent numpy restatement of the tree). */
+/* Sum of squares of x[0..n): fma chains over groups of 32 consecutive
+ * elements (the rows one GPU block owns), then the group sums added in
+ * ascending group order.  Role of the vfmaq loop in tg_rms_norm,
+ * libtinygiant.c:324-331.  Pinned by tests/test_oracle_math.py::
+ * test_sumsq_grouped (float64 bound; numpy restatement of the grouping). */
 float tgo_sumsq(const float *x, int n) {
-    float p[256];
-    int nchunk = n / 4;
-    for (int t = 0; t < 256; t++) {
+    float tot = 0.0f;
+    for (int g = 0; g < n / 32; g++) {
         float a = 0.0f;
-        for (int q = t; q < nchunk; q += 256)
-            for (int c = 0; c < 4; c++) {
-                float v = x[4 * q + c];
-                a = fmaf(v, v, a);
-            }
-        p[t] = a;
+        for (int i = 0; i < 32; i++) a = fmaf(x[32 * g + i], x[32 * g + i], a);
+        tot = tot + a;
     }
-    float g[4];
-    for (int k = 0; k < 4; k++) g[k] = butterfly(p + 64 * k, 64);
-    return (g[0] + g[1]) + (g[2] + g[3]);
+    return tot;
 }
 
 /* 1 / sqrt(mean(x^2) + eps) (libtinygiant.c:332; unit norm weight, D7). */
@@ -427,23 +410,25 @@ float tgo_rms_scale(const float *x, int n, float eps) {
     return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-/* One router logit in the GPU's 64-lane tree (role of routers[i] @ normed,
- * engine.py:231).  Pinned by tests/test_oracle_math.py::test_router_dot. */
-float tgo_router_dot(const float *w, const float *xn, int n) {
-    float p[64];
-    int nchunk = n / 4;
-    for (int l = 0; l < 64; l++) {
+/* Un-normalised router dot w . x in the grouped order of tgo_sumsq: fma
+ * chain inside each group of 32, groups added in ascending order.  The
+ * logit is this value times the norm scale s: routers @ (x * s)
+ * (engine.py:229-231) evaluated as s * (routers @ x), which lets the GPU
+ * form the per-group partial sums where x is produced.  Pinned by
+ * tests/test_oracle_math.py::test_router_dot_grouped. */
+float tgo_router_dot(const float *w, const float *x, int n) {
+    float tot = 0.0f;
+    for (int g = 0; g < n / 32; g++) {
         float a = 0.0f;
-        for (int q = l; q < nchunk; q += 64)
-            for (int c = 0; c < 4; c++) a = fmaf(w[4 * q + c], xn[4 * q + c], a);
-        p[l] = a;
+        for (int i = 0; i < 32; i++) a = fmaf(w[32 * g + i], x[32 * g + i], a);
+        tot = tot + a;
     }
-    return butterfly(p, 64);
+    return tot;
 }
 
-void tgo_router_logits(const float *Wr, int E, int H, const float *xn,
+void tgo_router_logits(const float *Wr, int E, int H, const float *x, float s,
                        float *logits) {
-    for (int e = 0; e < E; e++) logits[e] = tgo_router_dot(Wr + (size_t)e * H, xn, H);
+    for (int e = 0; e < E; e++) logits[e] = tgo_router_dot(Wr + (size_t)e * H, x, H) * s;
 }
 
 /* numpy's pairwise float32 sum (np.sum as used at engine.py:236) for the
@@ -479,7 +464,10 @@ void tgo_topk_softmax(const float *logits, int E, int k, int32_t *idx,
         int best = -1;
         for (int e = 0; e < E; e++) {
             if (taken[e]) continue;
-            if (best < 0 || logits[e] > logits[best]) best = e;
+            /* a NaN logit ranks below every number (as -inf) */
+            float ve = logits[e] != logits[e] ? -INFINITY : logits[e];
+            float vb = best < 0 ? 0.0f : (logits[best] != logits[best] ? -INFINITY : logits[best]);
+            if (best < 0 || ve > vb) best = e;
         }
         taken[best] = 1;
         idx[r] = best;
@@ -556,7 +544,7 @@ void tgo_moe_layer_q40(const uint8_t *layer, const float *Wr, int H, int I,
         const float *xt = x + (size_t)t * H;
         float s = tgo_rms_scale(xt, H, eps);
         for (int i = 0; i < H; i++) xn[i] = xt[i] * s;
-        tgo_router_logits(Wr, E, H, xn, logits);
+        tgo_router_logits(Wr, E, H, xt, s, logits);
         tgo_topk_softmax(logits, E, k, idx, w);
         tgo_quantize_q8_0(xn, (size_t)H, xq);
         if (idx_out) memcpy(idx_out + (size_t)t * k, idx, sizeof(int32_t) * (size_t)k);

@@ -68,8 +68,8 @@ void    tgo_q40_from_planar(const uint8_t *pl, int rows, int nb, uint8_t *aos);
 float   tgo_sumsq(const float *x, int n);
 float   tgo_rms_scale(const float *x, int n, float eps);
 float   tgo_router_dot(const float *w, const float *xn, int n);
-void    tgo_router_logits(const float *Wr, int E, int H, const float *xn,
-                          float *logits);
+void    tgo_router_logits(const float *Wr, int E, int H, const float *x,
+                          float s, float *logits);
 void    tgo_topk_softmax(const float *logits, int E, int k,
                          int32_t *idx, float *w);
 float   tgo_silu_mul(float g, float u);

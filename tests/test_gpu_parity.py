@@ -148,9 +148,7 @@ def test_router_topk_exact(O, tglib, E, H, k, T):
          idx.data_ptr(), w.data_ptr(), stream())
     gl, gi, gw = host(logits), host(idx), host(w)
     for t in range(T):
-        s = O.rms_scale(x[t])
-        xn = (x[t] * np.float32(s)).astype(np.float32)
-        rl = O.router_logits(Wr, xn)
+        rl = O.router_logits(Wr, x[t], O.rms_scale(x[t]))
         ri, rw = O.topk_softmax(rl, k)
         assert np.array_equal(gl[t].view(np.uint32), rl.view(np.uint32)), f"logits token {t}"
         assert np.array_equal(gi[t], ri), f"top-k token {t}"

@@ -13,6 +13,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <sys/mman.h>
 
@@ -170,13 +171,31 @@ struct tg_arena {
     uint8_t *staging = nullptr;   // LB bytes, relayout form for load/read
     // per-call scratch, grown on demand
     int cap_T = 0;
-    float *logits = nullptr;      // T * E
+    float *raw = nullptr;         // T * E raw router dots
     float *h = nullptr;           // T * k * I
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
     float *xbuf = nullptr;        // T * H (host-pointer entry points)
     float *obuf = nullptr;        // T * H
+    // captured stacks, replayed as HIP graphs
+    struct Graph {
+        const float *x;
+        int T, layer0, n;
+        float eps;
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+    };
+    std::vector<Graph> graphs;
+    hipStream_t capture = nullptr;
 };
+
+static void drop_graphs(tg_arena *a) {
+    for (auto &g : a->graphs) {
+        (void)hipGraphExecDestroy(g.exec);
+        (void)hipGraphDestroy(g.graph);
+    }
+    a->graphs.clear();
+}
 
 static int check_shape(int H, int I, int E, int k) {
     if (H <= 0 || I <= 0 || H % 256 || I % 32)
@@ -184,7 +203,8 @@ static int check_shape(int H, int I, int E, int k) {
                        H, I);
     if (H / 32 > tg::MAX_NB || I / 32 > tg::MAX_NB)
         return set_err(TG_E_INVALID, "embed_dim / inter_dim above %d", tg::MAX_NB * 32);
-    if (E <= 0 || E > tg::MAX_E) return set_err(TG_E_INVALID, "n_experts must be in 1..%d (got %d)", tg::MAX_E, E);
+    if (E <= 0 || E > tg::MAX_E - 4 || E % 4)
+        return set_err(TG_E_INVALID, "n_experts must be a multiple of 4 in 4..%d (got %d)", tg::MAX_E - 4, E);
     if (k <= 0 || k > tg::MAX_K || k > E)
         return set_err(TG_E_INVALID, "top_k must be in 1..min(%d, n_experts) (got %d)", tg::MAX_K, k);
     return TG_OK;
@@ -196,10 +216,12 @@ static void dfree(void *p) {
 
 static void arena_free(tg_arena *a) {
     if (!a) return;
+    drop_graphs(a);
+    if (a->capture) (void)hipStreamDestroy(a->capture);
     dfree(a->experts);
     dfree(a->routers);
     dfree(a->staging);
-    dfree(a->logits);
+    dfree(a->raw);
     dfree(a->h);
     dfree(a->idx);
     dfree(a->w);
@@ -211,9 +233,15 @@ static void arena_free(tg_arena *a) {
 extern "C" tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim, int inter_dim, int top_k) {
     if (n_layers <= 0) { set_err(TG_E_INVALID, "n_layers must be positive"); return nullptr; }
     if (check_shape(embed_dim, inter_dim, n_experts, top_k)) return nullptr;
+    tg::Shape shape = tg::make_shape(embed_dim, inter_dim, n_experts, top_k);
+    if (!tg::decode_shape_ok(shape)) {
+        set_err(TG_E_INVALID, "shape H=%d I=%d E=%d k=%d exceeds the decode kernels' limits", embed_dim, inter_dim,
+                n_experts, top_k);
+        return nullptr;
+    }
     if (ensure_device()) return nullptr;
     tg_arena *a = new tg_arena();
-    a->s = tg::make_shape(embed_dim, inter_dim, n_experts, top_k);
+    a->s = shape;
     a->L = n_layers;
     size_t eb = a->s.LB * (size_t)n_layers;
     size_t rb = sizeof(float) * (size_t)n_experts * embed_dim * n_layers;
@@ -301,11 +329,13 @@ extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float
 
 static int arena_scratch(tg_arena *a, int T) {
     if (T <= a->cap_T) return TG_OK;
-    dfree(a->logits); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf);
-    a->logits = nullptr; a->h = nullptr; a->idx = nullptr; a->w = nullptr; a->xbuf = nullptr; a->obuf = nullptr;
+    drop_graphs(a);  // captured graphs point at the old buffers
+    dfree(a->raw); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf);
+    a->raw = nullptr; a->h = nullptr; a->idx = nullptr; a->w = nullptr;
+    a->xbuf = nullptr; a->obuf = nullptr;
     a->cap_T = 0;
     const Shape &s = a->s;
-    bool ok = hipMalloc(&a->logits, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
+    bool ok = hipMalloc(&a->raw, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
               hipMalloc(&a->h, sizeof(float) * (size_t)T * s.k * s.I) == hipSuccess &&
               hipMalloc(&a->idx, sizeof(int32_t) * (size_t)T * s.k) == hipSuccess &&
               hipMalloc(&a->w, sizeof(float) * (size_t)T * s.k) == hipSuccess &&
@@ -320,16 +350,79 @@ static int arena_scratch(tg_arena *a, int T) {
 }
 
 // ================================================================ MoE block
+static const float *router_of(tg_arena *a, int layer) {
+    return a->routers + (size_t)layer * a->s.E * a->s.H;
+}
+
+// One MoE block: raw router dots, gate/up (norm, routing and Q8_0 fused),
+// down + combine.  out = moe_out (resid NULL) or resid + moe_out.
+static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T, float eps,
+                         hipStream_t st) {
+    const Shape &s = a->s;
+    const uint8_t *lp = a->experts + (size_t)layer * s.LB;
+    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
+    PROFILED("gateup", st, tg::launch_gateup(lp, s, x, a->raw, T, eps, a->h, a->idx, a->w, st));
+    PROFILED("down", st, tg::launch_down(lp, s, a->h, a->idx, a->w, T, resid, out, st));
+    return TG_OK;
+}
+
 static int moe_layer_launch(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T,
                             int32_t *idx_out, float *w_out, float eps, hipStream_t st) {
     const Shape &s = a->s;
-    const uint8_t *lp = a->experts + (size_t)layer * s.LB;
-    const float *wr = a->routers + (size_t)layer * s.E * s.H;
-    PROFILED("router", st, tg::launch_router(wr, x, T, s.E, s.H, eps, a->logits, st));
-    PROFILED("gateup", st, tg::launch_gateup(lp, s, x, a->logits, T, eps, a->h, a->idx, a->w, st));
-    PROFILED("down", st, tg::launch_down(lp, s, a->h, a->idx, a->w, T, resid, out, st));
+    int rc = layer_kernels(a, layer, x, out, resid, T, eps, st);
+    if (rc) return rc;
     if (idx_out) HIP_TRY(hipMemcpyAsync(idx_out, a->idx, sizeof(int32_t) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
     if (w_out) HIP_TRY(hipMemcpyAsync(w_out, a->w, sizeof(float) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
+    return TG_OK;
+}
+
+// x <- x + MoE_l(x) for layers [l0, l0+n), in place.
+static int stack_launch(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
+    for (int l = l0; l < l0 + n; l++) {
+        int rc = layer_kernels(a, l, x, x, x, T, eps, st);
+        if (rc) return rc;
+    }
+    return TG_OK;
+}
+
+static bool graphs_enabled() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("TG_NO_GRAPH");
+        on = (e && e[0] == '1') ? 0 : 1;
+    }
+    return on == 1 && !g_prof_on;
+}
+
+// Replays the stack as a HIP graph captured on first use for this
+// (x, T, layer range, eps); falls back to direct launches while kernel
+// timing is on.
+static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
+    if (!graphs_enabled()) return stack_launch(a, x, T, l0, n, eps, st);
+    for (auto &g : a->graphs)
+        if (g.x == x && g.T == T && g.layer0 == l0 && g.n == n && g.eps == eps) {
+            HIP_TRY(hipGraphLaunch(g.exec, st));
+            return TG_OK;
+        }
+    if (!a->capture) HIP_TRY(hipStreamCreateWithFlags(&a->capture, hipStreamNonBlocking));
+    tg_arena::Graph g{x, T, l0, n, eps, nullptr, nullptr};
+    HIP_TRY(hipStreamBeginCapture(a->capture, hipStreamCaptureModeRelaxed));
+    int rc = stack_launch(a, x, T, l0, n, eps, a->capture);
+    hipError_t ec = hipStreamEndCapture(a->capture, &g.graph);
+    if (rc) return rc;
+    if (ec != hipSuccess) return set_err(TG_E_HIP, "graph capture failed: %s", hipGetErrorString(ec));
+    ec = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+    if (ec != hipSuccess) {
+        (void)hipGraphDestroy(g.graph);
+        return set_err(TG_E_HIP, "graph instantiate failed: %s", hipGetErrorString(ec));
+    }
+    if (a->graphs.size() >= 8) {
+        (void)hipGraphExecDestroy(a->graphs.front().exec);
+        (void)hipGraphDestroy(a->graphs.front().graph);
+        a->graphs.erase(a->graphs.begin());
+    }
+    a->graphs.push_back(g);
+    HIP_TRY(hipGraphLaunch(g.exec, st));
     return TG_OK;
 }
 
@@ -381,9 +474,7 @@ extern "C" int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int lay
                                     void *stream) {
     int rc = stack_check(a, layer0, n_layers, n_tokens, x);
     if (rc) return rc;
-    for (int l = layer0; l < layer0 + n_layers; l++)
-        if ((rc = moe_layer_launch(a, l, x, x, x, n_tokens, nullptr, nullptr, eps, as_stream(stream)))) return rc;
-    return TG_OK;
+    return stack_run(a, x, n_tokens, layer0, n_layers, eps, as_stream(stream));
 }
 
 extern "C" int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0, int n_layers, float eps) {
@@ -391,9 +482,7 @@ extern "C" int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
     if (rc) return rc;
     size_t nx = (size_t)n_tokens * a->s.H;
     HIP_TRY(hipMemcpy(a->xbuf, x, nx * sizeof(float), hipMemcpyHostToDevice));
-    for (int l = layer0; l < layer0 + n_layers; l++)
-        if ((rc = moe_layer_launch(a, l, a->xbuf, a->xbuf, a->xbuf, n_tokens, nullptr, nullptr, eps, nullptr)))
-            return rc;
+    if ((rc = stack_run(a, a->xbuf, n_tokens, layer0, n_layers, eps, nullptr))) return rc;
     HIP_TRY(hipMemcpy(x, a->xbuf, nx * sizeof(float), hipMemcpyDeviceToHost));
     return TG_OK;
 }
@@ -456,8 +545,19 @@ extern "C" int tg_router_topk_dev(const float *Wr, const float *x, int n_experts
     if ((rc = check_shape(embed_dim, 32, n_experts, top_k))) return rc;
     if ((rc = check_tokens(n_tokens))) return rc;
     hipStream_t st = as_stream(stream);
-    HIP_TRY(tg::launch_router(Wr, x, n_tokens, n_experts, embed_dim, eps, logits, st));
-    if (topk_idx || topk_w) HIP_TRY(tg::launch_topk(logits, n_tokens, n_experts, top_k, topk_idx, topk_w, st));
+    float *raw = nullptr;
+    if (hipMalloc(&raw, sizeof(float) * (size_t)n_tokens * n_experts) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(TG_E_NOMEM, "router scratch");
+    }
+    hipError_t e1 = tg::launch_route(Wr, x, n_tokens, n_experts, embed_dim, raw, st);
+    hipError_t e2 = e1 == hipSuccess ? tg::launch_topk(raw, x, n_tokens, n_experts, embed_dim, top_k, eps, logits,
+                                                       topk_idx, topk_w, st)
+                                     : e1;
+    hipError_t e3 = hipStreamSynchronize(st);
+    dfree(raw);
+    HIP_TRY(e2);
+    HIP_TRY(e3);
     return TG_OK;
 }
 

@@ -10,9 +10,25 @@ namespace tg {
 // One layer's geometry: H = embed dim, I = expert intermediate dim, E
 // experts, top-k.  Byte sizes are those of the relayout format (18 bytes
 // per 32 weights), which the planar arena keeps.
+// n / d for n * d < 2^32 by one multiply-high: m = ceil(2^32 / d).
+struct FastDiv {
+    uint32_t d;
+    uint64_t m;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    f.m = ((1ull << 32) + d - 1) / d;
+    return f;
+}
+
+__host__ __device__ inline uint32_t fdiv(uint32_t n, FastDiv f) { return (uint32_t)(((uint64_t)n * f.m) >> 32); }
+
 struct Shape {
     int H, I, E, k;
     int nbH, nbI;      // blocks per gate/up row, per down row
+    FastDiv divH, divI;
     size_t GB;         // bytes of gate (= up)
     size_t DB;         // bytes of down
     size_t EB;         // bytes of one expert
@@ -23,6 +39,8 @@ inline Shape make_shape(int H, int I, int E, int k) {
     Shape s;
     s.H = H; s.I = I; s.E = E; s.k = k;
     s.nbH = H / 32; s.nbI = I / 32;
+    s.divH = make_fastdiv((uint32_t)s.nbH);
+    s.divI = make_fastdiv((uint32_t)s.nbI);
     s.GB = (size_t)I * s.nbH * 18;
     s.DB = (size_t)H * s.nbI * 18;
     s.EB = 2 * s.GB + s.DB;
@@ -40,7 +58,7 @@ uint64_t host_stream_key(uint64_t seed, uint64_t stream);
 
 // limits of the decode kernels
 constexpr int MAX_K = 32;        // top-k
-constexpr int MAX_E = 512;       // experts per layer
+constexpr int MAX_E = 256;       // experts per layer (one thread per expert)
 constexpr int MAX_NB = 256;      // blocks per row (H, I <= 8192)
 
 hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, int layer,
@@ -56,13 +74,15 @@ hipError_t launch_block_sums(const uint8_t *w_pl, int rows, int nb, const uint8_
                              hipStream_t st);
 hipError_t launch_matvec(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, float *out,
                          hipStream_t st);
-hipError_t launch_router(const float *Wr, const float *x, int T, int E, int H, float eps, float *logits,
-                         hipStream_t st);
-hipError_t launch_topk(const float *logits, int T, int E, int k, int32_t *idx, float *w, hipStream_t st);
+// routing: raw router dots (grouped order), then norm scale, logits, top-k
+hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st);
+hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, int k, float eps, float *logits,
+                       int32_t *idx, float *w, hipStream_t st);
 // decode MoE layer pieces
-hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *logits,
-                         int T, float eps, float *h, int32_t *idx, float *w, hipStream_t st);
-hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx,
-                       const float *w, int T, const float *resid, float *out, hipStream_t st);
+bool decode_shape_ok(const Shape &s);
+hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T, float eps,
+                         float *h, int32_t *idx, float *w, hipStream_t st);
+hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
+                       int T, const float *resid, float *out, hipStream_t st);
 
 }  // namespace tg

@@ -164,26 +164,8 @@ __global__ __launch_bounds__(256) void k_repack_tensor(const uint8_t *__restrict
 }
 
 // ========================================================== Q8_0 pieces
-// Quantize n values (n multiple of 32) into the LDS activation form: qs
-// (int8, 32 per block), dsc (float(half d)) and sum (sum of the block's q).
-// Called by every thread of a 256-thread block; 32-lane groups are whole
-// blocks, so a group is on or off as a unit and the shuffles are uniform.
-TG_DEV void q8_to_lds(const float *__restrict__ src, int n, int8_t *qs, float *dsc, int *sum,
-                      float scale, bool apply_scale) {
-    for (int base = 0; base < n; base += 256) {
-        int i = base + (int)threadIdx.x;
-        bool on = i < n;
-        float v = on ? src[i] : 0.0f;
-        if (apply_scale) v = v * scale;
-        float dq; int qsum; uint16_t dh;
-        int q = q8_lane(v, dq, qsum, dh);
-        if (on) {
-            qs[i] = (int8_t)q;
-            if ((i & 31) == 0) { dsc[i >> 5] = dq; sum[i >> 5] = qsum; }
-        }
-    }
-}
-
+// fp32 -> Q8_0 blocks in global memory, one value per thread (32-lane
+// groups are whole blocks, on or off as a unit).
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__ x, uint8_t *__restrict__ out, int n) {
     int i = blockIdx.x * 256 + threadIdx.x;
     bool on = i < n;
@@ -268,205 +250,6 @@ TG_DEV float chain(const float *U, const float *dx, int nb) {
     float acc = 0.0f;
     for (int b = 0; b < nb; b++) acc = __builtin_fmaf(U[b], dx[b], acc);
     return acc;
-}
-
-// ============================================================ top-k
-// Top-k of one token's E logits with renormalised softmax; one full wave.
-// Selection: largest logit, equal logits -> lower expert index.  Softmax over
-// the k values in ascending order with numpy's pairwise sum.  Results to LDS
-// (sidx, sw; slog and sex are scratch).
-TG_DEV void wave_topk(const float *__restrict__ logits, int E, int k, int *sidx, float *sw, float *slog,
-                      float *sex) {
-    const int lane = threadIdx.x & 63;
-    constexpr int M = MAX_E / WAVE;
-    float v[M];
-    unsigned taken = 0;
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        int e = lane + WAVE * m;
-        v[m] = e < E ? logits[e] : 0.0f;
-        if (e >= E) taken |= 1u << m;
-    }
-    for (int r = 0; r < k; r++) {
-        float bv = -__builtin_inff();
-        int bi = INT_MAX;
-        bool have = false;
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            if (!((taken >> m) & 1u) && (!have || v[m] > bv)) {
-                bv = v[m];
-                bi = lane + WAVE * m;
-                have = true;
-            }
-        }
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) {
-            float ov = __shfl_xor(bv, s, WAVE);
-            int oi = __shfl_xor(bi, s, WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((bi & (WAVE - 1)) == lane) taken |= 1u << (bi / WAVE);
-        if (lane == 0) { sidx[r] = bi; slog[r] = bv; }
-    }
-    if (lane == 0) {
-        float lmax = slog[0];
-        for (int i = 0; i < k; i++) sex[i] = expf_tg(slog[k - 1 - i] - lmax);
-        float sum = np_pairwise_sum(sex, k);
-        for (int i = 0; i < k; i++) sw[k - 1 - i] = sex[i] / sum;
-    }
-}
-
-__global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, int E, int k,
-                                             int32_t *__restrict__ idx, float *__restrict__ w) {
-    __shared__ int sidx[MAX_K];
-    __shared__ float sw[MAX_K], slog[MAX_K], sex[MAX_K];
-    const int t = blockIdx.x;
-    wave_topk(logits + (size_t)t * E, E, k, sidx, sw, slog, sex);
-    __syncthreads();
-    if ((int)threadIdx.x < k) {
-        if (idx) idx[(size_t)t * k + threadIdx.x] = sidx[threadIdx.x];
-        if (w) w[(size_t)t * k + threadIdx.x] = sw[threadIdx.x];
-    }
-}
-
-// ============================================================ router
-// logits[t][e] = Wr[e] . (x[t] * s), s = 1/sqrt(mean(x^2) + eps).  Each wave
-// takes one expert row: lane l fma-accumulates float4 chunks l, l+64, ...,
-// then an xor butterfly.  4 rows per 256-thread block.
-__global__ __launch_bounds__(256) void k_router(const float *__restrict__ Wr, const float *__restrict__ x,
-                                                int E, int H, float eps, float *__restrict__ logits) {
-    __shared__ float red[4];
-    const int t = blockIdx.y;
-    const float *xt = x + (size_t)t * H;
-    float sc = rms_scale(block_sumsq(xt, H, red), H, eps);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + wave;
-    if (e >= E) return;
-    const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H);
-    const float4 *x4 = reinterpret_cast<const float4 *>(xt);
-    float acc = 0.0f;
-    for (int q = lane; q < H / 4; q += WAVE) {
-        float4 wv = w4[q], xv = x4[q];
-        acc = __builtin_fmaf(wv.x, xv.x * sc, acc);
-        acc = __builtin_fmaf(wv.y, xv.y * sc, acc);
-        acc = __builtin_fmaf(wv.z, xv.z * sc, acc);
-        acc = __builtin_fmaf(wv.w, xv.w * sc, acc);
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) logits[(size_t)t * E + e] = acc;
-}
-
-// ============================================================ gate / up
-// Grid (I/RT, k, T).  Block (rt, j, t) computes rows [rt*RT, rt*RT+RT) of
-// gate and up of token t's j-th expert, then h = SiLU(gate) * up.  Every
-// block re-derives the token's top-k and Q8_0(x / rms(x)) itself (cheap,
-// identical everywhere), so no block waits on another.
-constexpr int GU_RT = 16;
-
-__global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ layer_pl, Shape s,
-                                                const float *__restrict__ x, const float *__restrict__ logits,
-                                                float eps, float *__restrict__ h, int32_t *__restrict__ idx_out,
-                                                float *__restrict__ w_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RT = GU_RT;
-    const int nb = s.nbH, ust = nb + 1;
-    int8_t *xq = reinterpret_cast<int8_t *>(smem);
-    float *xd = reinterpret_cast<float *>(smem + s.H);
-    int *xs = reinterpret_cast<int *>(xd + nb);
-    float *U = reinterpret_cast<float *>(xs + nb);
-    float *accs = U + 2 * RT * ust;
-    int *sidx = reinterpret_cast<int *>(accs + 2 * RT);
-    float *sw = reinterpret_cast<float *>(sidx + MAX_K);
-    float *slog = sw + MAX_K;
-    float *sex = slog + MAX_K;
-    float *red = sex + MAX_K;
-
-    const int t = blockIdx.z, j = blockIdx.y, r0 = blockIdx.x * RT;
-    const float *xt = x + (size_t)t * s.H;
-    if (threadIdx.x < WAVE) wave_topk(logits + (size_t)t * s.E, s.E, s.k, sidx, sw, slog, sex);
-    float sc = rms_scale(block_sumsq(xt, s.H, red), s.H, eps);
-    q8_to_lds(xt, s.H, xq, xd, xs, sc, true);
-    __syncthreads();
-    if (blockIdx.x == 0 && j == 0 && (int)threadIdx.x < s.k) {
-        if (idx_out) idx_out[(size_t)t * s.k + threadIdx.x] = sidx[threadIdx.x];
-        if (w_out) w_out[(size_t)t * s.k + threadIdx.x] = sw[threadIdx.x];
-    }
-    const uint8_t *ex = layer_pl + (size_t)sidx[j] * s.EB;
-    const size_t ntb = (size_t)s.I * nb;
-    const int I = s.I;
-    tile_terms<8>(2 * RT, nb, U, ust, [&](int rd) {
-        int mat = rd >= RT ? 1 : 0;
-        int row = r0 + (rd - mat * RT);
-        const uint8_t *tb = ex + (size_t)mat * s.GB;
-        RowSrc rs;
-        rs.valid = row < I;
-        size_t ro = (size_t)(row < I ? row : 0) * nb;
-        rs.q = reinterpret_cast<const uint4 *>(tb) + ro;
-        rs.d = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + ro;
-        rs.xq = xq;
-        rs.xs = xs;
-        return rs;
-    });
-    __syncthreads();
-    if ((int)threadIdx.x < 2 * RT) accs[threadIdx.x] = chain(U + threadIdx.x * ust, xd, nb);
-    __syncthreads();
-    if ((int)threadIdx.x < RT && r0 + (int)threadIdx.x < I)
-        h[((size_t)t * s.k + j) * I + r0 + threadIdx.x] = silu_mul(accs[threadIdx.x], accs[RT + threadIdx.x]);
-}
-
-// ============================================================ down
-// Grid (H/RD, T).  Block (rb, t) computes rows [rb*RD, rb*RD+RD) of down
-// for all k experts of token t and combines them: out = sum_j w_j down_j in
-// ascending logit order (j = k-1 .. 0), plus resid when given.
-constexpr int DN_RD = 8;
-
-__global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ layer_pl, Shape s,
-                                              const float *__restrict__ h, const int32_t *__restrict__ idx,
-                                              const float *__restrict__ w, const float *resid, float *out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RD = DN_RD;
-    const int k = s.k, nb = s.nbI, I = s.I, H = s.H, ust = nb + 1;
-    int8_t *hq = reinterpret_cast<int8_t *>(smem);
-    float *hd = reinterpret_cast<float *>(smem + (size_t)k * I);
-    int *hs = reinterpret_cast<int *>(hd + k * nb);
-    float *U = reinterpret_cast<float *>(hs + k * nb);
-    float *D = U + k * RD * ust;
-    int *sidx = reinterpret_cast<int *>(D + k * RD);
-    float *sw = reinterpret_cast<float *>(sidx + MAX_K);
-
-    const int t = blockIdx.y, r0 = blockIdx.x * RD;
-    if ((int)threadIdx.x < k) {
-        sidx[threadIdx.x] = idx[(size_t)t * k + threadIdx.x];
-        sw[threadIdx.x] = w[(size_t)t * k + threadIdx.x];
-    }
-    q8_to_lds(h + (size_t)t * k * I, k * I, hq, hd, hs, 1.0f, false);
-    __syncthreads();
-    const size_t ntb = (size_t)H * nb;
-    tile_terms<6>(k * RD, nb, U, ust, [&](int rd) {
-        int jj = rd / RD;
-        int row = r0 + (rd - jj * RD);
-        const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
-        RowSrc rs;
-        rs.valid = row < H;
-        size_t ro = (size_t)(row < H ? row : 0) * nb;
-        rs.q = reinterpret_cast<const uint4 *>(tb) + ro;
-        rs.d = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + ro;
-        rs.xq = hq + (size_t)jj * I;
-        rs.xs = hs + jj * nb;
-        return rs;
-    });
-    __syncthreads();
-    if ((int)threadIdx.x < k * RD) {
-        int jj = threadIdx.x / RD;
-        D[threadIdx.x] = chain(U + threadIdx.x * ust, hd + jj * nb, nb);
-    }
-    __syncthreads();
-    if ((int)threadIdx.x < RD && r0 + (int)threadIdx.x < H) {
-        float acc = 0.0f;
-        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + threadIdx.x], acc);
-        size_t o = (size_t)t * H + r0 + threadIdx.x;
-        out[o] = resid ? resid[o] + acc : acc;
-    }
 }
 
 // ================================================ stand-alone row dots
@@ -592,35 +375,6 @@ hipError_t launch_block_sums(const uint8_t *w_pl, int rows, int nb, const uint8_
 hipError_t launch_matvec(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, float *out, hipStream_t st) {
     size_t lds = (size_t)nb * QK + 8 * (size_t)nb + 4 * (size_t)MV_RT * (nb + 1);
     hipLaunchKernelGGL(k_matvec, dim3(cdiv((size_t)rows, MV_RT)), dim3(256), lds, st, w_pl, rows, nb, xq8, out);
-    return hipGetLastError();
-}
-
-hipError_t launch_router(const float *Wr, const float *x, int T, int E, int H, float eps, float *logits,
-                         hipStream_t st) {
-    hipLaunchKernelGGL(k_router, dim3(cdiv((size_t)E, 4), T), dim3(256), 0, st, Wr, x, E, H, eps, logits);
-    return hipGetLastError();
-}
-
-hipError_t launch_topk(const float *logits, int T, int E, int k, int32_t *idx, float *w, hipStream_t st) {
-    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, st, logits, E, k, idx, w);
-    return hipGetLastError();
-}
-
-hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *logits, int T,
-                         float eps, float *h, int32_t *idx, float *w, hipStream_t st) {
-    size_t lds = (size_t)s.H + 8 * (size_t)s.nbH + 4 * (size_t)2 * GU_RT * (s.nbH + 1) + 4 * 2 * GU_RT +
-                 4 * 4 * MAX_K + 16;
-    hipLaunchKernelGGL(k_gateup, dim3(cdiv((size_t)s.I, GU_RT), s.k, T), dim3(256), lds, st, layer_pl, s, x,
-                       logits, eps, h, idx, w);
-    return hipGetLastError();
-}
-
-hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
-                       int T, const float *resid, float *out, hipStream_t st) {
-    size_t lds = (size_t)s.k * s.I + 8 * (size_t)s.k * s.nbI + 4 * (size_t)s.k * DN_RD * (s.nbI + 1) +
-                 4 * (size_t)s.k * DN_RD + 8 * MAX_K;
-    hipLaunchKernelGGL(k_down, dim3(cdiv((size_t)s.H, DN_RD), T), dim3(256), lds, st, layer_pl, s, h, idx, w,
-                       resid, out);
     return hipGetLastError();
 }
 

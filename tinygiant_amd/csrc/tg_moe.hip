@@ -1,0 +1,533 @@
+// tg_moe.hip -- the decode MoE block on gfx950: routing, gate/up + SwiGLU,
+// down + weighted combine.
+//
+// Per layer three kernels, separated by kernel boundaries (replayed as a HIP
+// graph, where a boundary costs little):
+//
+//   k_route   grid (E, T)       raw router dot of one expert for one token
+//   k_gateup  grid (I/RT, k, T) norm scale, logits, top-k, then RT rows of
+//                               gate and up of one selected expert and
+//                               h = SiLU(gate) * up
+//   k_down    grid (H/RD, T)    RD rows of down for all k experts, combine,
+//                               residual
+//
+// One CU streams only a few tens of GB/s from HBM, so every weight-streaming
+// kernel spreads its bytes over at least one block per CU (256 CUs).
+//
+// Numerics: see tg_kernels.hip (row dots) and the routing definition below;
+// every result is bit-identical to the host definition.
+#include "tg_device.h"
+#include "tg_internal.h"
+
+namespace tg {
+
+// ================================================================= routing
+// Grouped sums: x is split in groups of RG = 32 consecutive elements.
+//   raw[e] = sum over groups g (ascending) of the fma chain over the group
+//            of W[e][i] * x[i]
+//   ss     = the same grouping over x[i] * x[i]
+//   s      = 1 / sqrt(ss / H + eps),  logit[e] = raw[e] * s
+constexpr int RG = 32;
+constexpr int RT_THREADS = 256;  // groups per k_route block (H <= 8192)
+
+__global__ __launch_bounds__(RT_THREADS) void k_route(const float *__restrict__ Wr, const float *__restrict__ x, int E,
+                                                      int H, float *__restrict__ raw) {
+    __shared__ __align__(16) float gp[RT_THREADS];
+    const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, G = H / RG;
+    float acc = 0.0f;
+    if (tid < G) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + tid * RG);
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * H + tid * RG);
+        float4 wv[RG / 4], xv[RG / 4];
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            wv[q] = w4[q];
+            xv[q] = x4[q];
+        }
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            acc = __builtin_fmaf(wv[q].x, xv[q].x, acc);
+            acc = __builtin_fmaf(wv[q].y, xv[q].y, acc);
+            acc = __builtin_fmaf(wv[q].z, xv[q].z, acc);
+            acc = __builtin_fmaf(wv[q].w, xv[q].w, acc);
+        }
+    }
+    gp[tid] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        float tot = 0.0f;
+        for (int g = 0; g < G; g++) tot = tot + gp[g];
+        raw[(size_t)t * E + e] = tot;
+    }
+}
+
+// NaN logits rank below every number (as -inf) and -0 equals +0, so the
+// 64-bit key orders experts by (logit descending, index ascending) and the
+// ranks always form a permutation.
+TG_DEV uint64_t rank_key(float l, int e) {
+    float v = l != l ? -__builtin_inff() : l;
+    v = v + 0.0f;
+    uint32_t u = __float_as_uint(v);
+    uint32_t mono = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)mono << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+// Routing of one token by a 256-thread block, the first thing k_gateup and
+// k_topk do.  x -> registers xv (8 per thread per pass) and LDS xf; s ->
+// sred[0]; logits -> slog; the top-k expert ids -> sidx[0..k) (descending
+// logit, equal logits lower index first).  Ends with a barrier.
+constexpr int RO_THREADS = 256;
+constexpr int RO_MAXPASS = 4;  // H <= 4 * 8 * 256
+
+TG_DEV void route_token(const float *__restrict__ xt, const float *__restrict__ rawt, int E, int H, int k,
+                        float eps, float (&xv)[RO_MAXPASS][8], float *xf, float *gss, float *slog, uint64_t *keys,
+                        int *sidx, float *sred) {
+    const int tid = threadIdx.x, G = H / RG;
+#pragma unroll
+    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+        int i0 = ps * RO_THREADS * 8 + tid * 8;
+        if (i0 < H) {
+            float4 a = *reinterpret_cast<const float4 *>(xt + i0);
+            float4 b = *reinterpret_cast<const float4 *>(xt + i0 + 4);
+            xv[ps][0] = a.x; xv[ps][1] = a.y; xv[ps][2] = a.z; xv[ps][3] = a.w;
+            xv[ps][4] = b.x; xv[ps][5] = b.y; xv[ps][6] = b.z; xv[ps][7] = b.w;
+            *reinterpret_cast<float4 *>(xf + i0) = a;
+            *reinterpret_cast<float4 *>(xf + i0 + 4) = b;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c++) xv[ps][c] = 0.0f;
+        }
+    }
+    float r = tid < E ? rawt[tid] : 0.0f;
+    if (tid < k) sidx[tid] = 0;
+    __syncthreads();
+    if (tid < G) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xf + tid * RG);
+        float a = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            float4 v = x4[q];
+            a = __builtin_fmaf(v.x, v.x, a);
+            a = __builtin_fmaf(v.y, v.y, a);
+            a = __builtin_fmaf(v.z, v.z, a);
+            a = __builtin_fmaf(v.w, v.w, a);
+        }
+        gss[tid] = a;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float tot = 0.0f;
+        for (int g = 0; g < G; g++) tot = tot + gss[g];
+        sred[0] = rms_scale(tot, H, eps);
+    }
+    __syncthreads();
+    if (tid < E) {
+        float l = r * sred[0];
+        slog[tid] = l;
+        keys[tid] = rank_key(l, tid);
+    }
+    __syncthreads();
+    // rank = number of larger keys; two threads per expert when E <= 128
+    const int tpe = 2 * E <= RO_THREADS ? 2 : 1;
+    const int e = tpe == 2 ? tid >> 1 : tid;
+    if (e < E) {
+        const uint64_t my = keys[e];
+        int half = tpe == 2 ? (tid & 1) : 0;
+        int n = E / tpe, b0 = half * n;
+        int cnt = 0;
+#pragma unroll 8
+        for (int i = 0; i < n; i += 2) {
+            ulonglong2 o = *reinterpret_cast<const ulonglong2 *>(keys + b0 + i);
+            cnt += o.x > my ? 1 : 0;
+            cnt += o.y > my ? 1 : 0;
+        }
+        if (tpe == 2) cnt += __shfl_xor(cnt, 1, WAVE);
+        if (half == 0 && cnt < k) sidx[cnt] = e;
+    }
+    __syncthreads();
+}
+
+// Renormalised softmax over the selected logits (engine.py:233-236): the k
+// values in ascending order, e = exp(l - lmax), numpy's pairwise sum, w = e /
+// sum.  One thread.
+TG_DEV void topk_softmax(const float *slog, const int *sidx, int k, float *sw, float *sex) {
+    float lmax = slog[sidx[0]];
+    for (int i = 0; i < k; i++) sex[i] = expf_tg(slog[sidx[k - 1 - i]] - lmax);
+    float sum = np_pairwise_sum(sex, k);
+    for (int i = 0; i < k; i++) sw[k - 1 - i] = sex[i] / sum;
+}
+
+struct RouteLds {
+    float *xf, *gss, *slog, *sw, *sex, *sred;
+    uint64_t *keys;
+    int *sidx;
+};
+
+// LDS for route_token: xf[H] gss[256] slog[MAX_E] sw/sex[MAX_K] sred[4]
+// keys[MAX_E] sidx[MAX_K], from a 16-byte aligned base.
+__host__ __device__ inline size_t route_lds_bytes(int H) {
+    return 4 * (size_t)H + 4 * 256 + 4 * MAX_E + 8 * MAX_K + 16 + 8 * MAX_E + 4 * MAX_K;
+}
+
+TG_DEV RouteLds route_lds(uint8_t *base, int H) {
+    RouteLds r;
+    r.keys = reinterpret_cast<uint64_t *>(base);
+    r.xf = reinterpret_cast<float *>(r.keys + MAX_E);
+    r.gss = r.xf + H;
+    r.slog = r.gss + 256;
+    r.sw = r.slog + MAX_E;
+    r.sex = r.sw + MAX_K;
+    r.sred = r.sex + MAX_K;
+    r.sidx = reinterpret_cast<int *>(r.sred + 4);
+    return r;
+}
+
+// Grid (T): logits, top-k and weights (tg_router_topk_dev).
+__global__ __launch_bounds__(RO_THREADS) void k_topk(const float *__restrict__ raw, const float *__restrict__ x, int E,
+                                                     int H, int k, float eps, float *__restrict__ logits,
+                                                     int32_t *__restrict__ idx, float *__restrict__ w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    RouteLds L = route_lds(smem, H);
+    const int t = blockIdx.x;
+    float xv[RO_MAXPASS][8];
+    route_token(x + (size_t)t * H, raw + (size_t)t * E, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx,
+                L.sred);
+    for (int e = threadIdx.x; e < E; e += blockDim.x) logits[(size_t)t * E + e] = L.slog[e];
+    if (threadIdx.x == 0) {
+        topk_softmax(L.slog, L.sidx, k, L.sw, L.sex);
+        for (int i = 0; i < k; i++) {
+            if (idx) idx[(size_t)t * k + i] = L.sidx[i];
+            if (w) w[(size_t)t * k + i] = L.sw[i];
+        }
+    }
+}
+
+// ================================================================ Q8_0
+// Q8_0 of 8 values held by this thread; 4 consecutive threads form one block
+// of 32.  Writes the LDS activation form (qs, float(half d), block sum).
+TG_DEV void q8_group8(const float *v, bool on, int i0, int8_t *qs, float *dsc, int *sum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) a = fabsf(v[c]) > a ? fabsf(v[c]) : a;
+    float o = __shfl_xor(a, 1, WAVE);
+    a = o > a ? o : a;
+    o = __shfl_xor(a, 2, WAVE);
+    a = o > a ? o : a;
+    float d = a / 127.0f;
+    float inv = a > 0.0f ? 127.0f / a : 0.0f;
+    int q[8], qsum = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        q[c] = (int)__builtin_rintf(v[c] * inv);
+        qsum += q[c];
+    }
+    qsum += __shfl_xor(qsum, 1, WAVE);
+    qsum += __shfl_xor(qsum, 2, WAVE);
+    if (on) {
+        uint32_t lo = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+                      ((uint32_t)(q[3] & 255) << 24);
+        uint32_t hi = (uint32_t)(q[4] & 255) | ((uint32_t)(q[5] & 255) << 8) | ((uint32_t)(q[6] & 255) << 16) |
+                      ((uint32_t)(q[7] & 255) << 24);
+        *reinterpret_cast<uint2 *>(qs + i0) = make_uint2(lo, hi);
+        if ((i0 & 31) == 0) {
+            dsc[i0 >> 5] = h2f(f2h(d));
+            sum[i0 >> 5] = qsum;
+        }
+    }
+}
+
+// Sequential row accumulation acc = fma(U_b, dx_b, acc), operands read from
+// LDS four at a time (U and dx 16-byte aligned).
+TG_DEV float chain4(const float *U, const float *dx, int nb) {
+    float acc = 0.0f;
+    const float4 *u4 = reinterpret_cast<const float4 *>(U);
+    const float4 *d4 = reinterpret_cast<const float4 *>(dx);
+    int q = 0;
+#pragma unroll 4
+    for (; q < nb / 4; q++) {
+        float4 u = u4[q], d = d4[q];
+        acc = __builtin_fmaf(u.x, d.x, acc);
+        acc = __builtin_fmaf(u.y, d.y, acc);
+        acc = __builtin_fmaf(u.z, d.z, acc);
+        acc = __builtin_fmaf(u.w, d.w, acc);
+    }
+    for (int b = 4 * q; b < nb; b++) acc = __builtin_fmaf(U[b], dx[b], acc);
+    return acc;
+}
+
+__host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
+
+// ============================================================ gate / up
+// Block (rt, j, t): the token's routing (every block derives it identically),
+// then rows [rt*RT, rt*RT+RT) of gate and up of the j-th selected expert,
+// h = SiLU(gate) * up.  The nibble loads are issued as soon as the expert is
+// known; Q8_0(x * s) is formed while they are in flight.
+constexpr int GU_RT = 8;
+
+__host__ __device__ inline size_t gateup_lds_bytes(int H, int nbH) {
+    // route | xq[H] | xd[r4] | xs[r4] | U[2RT * (r4 + 4)] | accs[2RT]
+    return route_lds_bytes(H) + (size_t)H + 8 * (size_t)round4(nbH) + 4 * (size_t)2 * GU_RT * (round4(nbH) + 4) +
+           4 * 2 * GU_RT;
+}
+
+template <int UNR>
+__global__ __launch_bounds__(RO_THREADS) void k_gateup(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                       const float *__restrict__ x, const float *__restrict__ raw,
+                                                       float eps, float *__restrict__ h,
+                                                       int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RT = GU_RT;
+    const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, I = s.I, tid = threadIdx.x;
+    RouteLds L = route_lds(smem, H);
+    int8_t *xq = reinterpret_cast<int8_t *>(smem + route_lds_bytes(H));
+    float *xd = reinterpret_cast<float *>(xq + H);
+    int *xs = reinterpret_cast<int *>(xd + round4(nb));
+    float *U = reinterpret_cast<float *>(xs + round4(nb));
+    float *accs = U + 2 * RT * ust;
+
+    const int t = blockIdx.z, j = blockIdx.y, r0 = blockIdx.x * RT;
+    float xv[RO_MAXPASS][8];
+    route_token(x + (size_t)t * H, raw + (size_t)t * s.E, s.E, H, s.k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx,
+                L.sred);
+
+    // nibble groups and scales of this block's 2*RT row-dots
+    const uint8_t *ex = layer_pl + (size_t)L.sidx[j] * s.EB;
+    const size_t ntb = (size_t)I * nb;
+    const int items = 2 * RT * nb;
+    uint4 wv[UNR];
+    uint16_t dv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        int p = u * RO_THREADS + tid;
+        wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        dv[u] = 0;
+        if (p < items) {
+            int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            int mat = rd >= RT ? 1 : 0;
+            int row = r0 + rd - mat * RT;
+            if (row < I) {
+                const uint8_t *tb = ex + (size_t)mat * s.GB;
+                size_t o = (size_t)row * nb + b;
+                wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+                dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
+            }
+        }
+    }
+    // Q8_0(x * s) while the loads are in flight
+    const float sc = L.sred[0];
+#pragma unroll
+    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+        int i0 = ps * RO_THREADS * 8 + tid * 8;
+        if (ps * RO_THREADS * 8 < H) {
+            float v[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) v[c] = xv[ps][c] * sc;
+            q8_group8(v, i0 < H, i0, xq, xd, xs);
+        }
+    }
+    if (blockIdx.x == 0 && j == 0 && tid == 0) {
+        topk_softmax(L.slog, L.sidx, s.k, L.sw, L.sex);
+        for (int i = 0; i < s.k; i++) {
+            if (idx_out) idx_out[(size_t)t * s.k + i] = L.sidx[i];
+            if (w_out) w_out[(size_t)t * s.k + i] = L.sw[i];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        int p = u * RO_THREADS + tid;
+        if (p < items) {
+            int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(xq + b * QK)) - 8 * xs[b];
+            U[rd * ust + b] = (float)S * h2f(dv[u]);
+        }
+    }
+    __syncthreads();
+    if (tid < 2 * RT) accs[tid] = chain4(U + tid * ust, xd, nb);
+    __syncthreads();
+    if (tid < RT && r0 + tid < I) h[((size_t)t * s.k + j) * I + r0 + tid] = silu_mul(accs[tid], accs[RT + tid]);
+}
+
+// ============================================================ down
+// Block (g, t): rows [g*RD, g*RD+RD) of down for the k experts of token t,
+// combined: out = sum_j w_j down_j in ascending logit order (j = k-1 .. 0)
+// plus resid when given.  The nibble loads are issued before the block
+// quantizes h, so their latency overlaps the quantization.
+constexpr int DN_RD = 8;
+constexpr int DN_THREADS = 256;
+constexpr int DN_MAXPASS = 8;  // k * I <= 8 * 8 * 256
+
+__host__ __device__ inline size_t down_lds_bytes(int k, int I, int nbI) {
+    // hq[k*I] | hd[k*r4] | hs[k*r4] | U[k*RD*(r4+4)] | D[k*RD] | sw[MAX_K] | sidx[MAX_K]
+    return (size_t)k * I + 8 * (size_t)k * round4(nbI) + 4 * (size_t)k * DN_RD * (round4(nbI) + 4) +
+           4 * (size_t)k * DN_RD + 8 * MAX_K;
+}
+
+template <int UNR>
+__global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                     const float *__restrict__ h, const int32_t *__restrict__ idx,
+                                                     const float *__restrict__ w, const float *resid, float *out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RD = DN_RD;
+    const int k = s.k, nb = s.nbI, nbp = round4(nb), I = s.I, H = s.H, ust = round4(nb) + 4;
+    const int tid = threadIdx.x;
+    int8_t *hq = reinterpret_cast<int8_t *>(smem);
+    float *hd = reinterpret_cast<float *>(smem + (size_t)k * I);
+    int *hs = reinterpret_cast<int *>(hd + k * nbp);
+    float *U = reinterpret_cast<float *>(hs + k * nbp);
+    float *D = U + k * RD * ust;
+    float *sw = D + k * RD;
+    int *sidx = reinterpret_cast<int *>(sw + MAX_K);
+
+    const int t = blockIdx.y, r0 = blockIdx.x * RD;
+    if (tid < k) {
+        int e = idx[(size_t)t * k + tid];
+        sidx[tid] = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);  // never address outside the layer
+        sw[tid] = w[(size_t)t * k + tid];
+    }
+    const float *ht = h + (size_t)t * k * I;
+    const int nh = k * I;
+    const int npass = (nh + DN_THREADS * 8 - 1) / (DN_THREADS * 8);
+    float hv[DN_MAXPASS][8];
+#pragma unroll
+    for (int ps = 0; ps < DN_MAXPASS; ps++) {
+        int i0 = ps * DN_THREADS * 8 + tid * 8;
+        if (ps < npass && i0 < nh) {
+            float4 a = *reinterpret_cast<const float4 *>(ht + i0);
+            float4 b = *reinterpret_cast<const float4 *>(ht + i0 + 4);
+            hv[ps][0] = a.x; hv[ps][1] = a.y; hv[ps][2] = a.z; hv[ps][3] = a.w;
+            hv[ps][4] = b.x; hv[ps][5] = b.y; hv[ps][6] = b.z; hv[ps][7] = b.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c++) hv[ps][c] = 0.0f;
+        }
+    }
+    float rv = 0.0f;
+    if (resid && tid < RD && r0 + tid < H) rv = resid[(size_t)t * H + r0 + tid];
+    __syncthreads();
+
+    const size_t ntb = (size_t)H * nb;
+    const int items = k * RD * nb;
+    uint4 wv[UNR];
+    uint16_t dv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        int p = u * DN_THREADS + tid;
+        wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        dv[u] = 0;
+        if (p < items) {
+            int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            int jj = rd / RD, row = r0 + (rd - jj * RD);
+            if (row < H) {
+                const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
+                size_t o = (size_t)row * nb + b;
+                wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+                dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
+            }
+        }
+    }
+    // Q8_0 of each expert's h while the nibble loads are in flight; expert jj's
+    // blocks go to hq + jj*I, hd/hs + jj*nbp
+#pragma unroll
+    for (int ps = 0; ps < DN_MAXPASS; ps++) {
+        if (ps < npass) {
+            int i0 = ps * DN_THREADS * 8 + tid * 8;
+            bool on = i0 < nh;
+            int jj = on ? i0 / I : 0, il = on ? i0 - jj * I : 0;
+            q8_group8(hv[ps], on, il, hq + (size_t)jj * I, hd + jj * nbp, hs + jj * nbp);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        int p = u * DN_THREADS + tid;
+        if (p < items) {
+            int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            int jj = rd / RD;
+            int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
+                    8 * hs[jj * nbp + b];
+            U[rd * ust + b] = (float)S * h2f(dv[u]);
+        }
+    }
+    __syncthreads();
+    for (int rd = tid; rd < k * RD; rd += DN_THREADS) D[rd] = chain4(U + rd * ust, hd + (rd / RD) * nbp, nb);
+    __syncthreads();
+    if (tid < RD && r0 + tid < H) {
+        float acc = 0.0f;
+        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        out[(size_t)t * H + r0 + tid] = resid ? rv + acc : acc;
+    }
+}
+
+// ================================================================ launchers
+static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+// Kernels whose LDS exceeds the 64 KiB default opt in to more (gfx950 has
+// 160 KiB per CU).
+static hipError_t allow_lds(const void *fn, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+bool decode_shape_ok(const Shape &s) {
+    return s.H <= RO_MAXPASS * RO_THREADS * 8 && s.H / RG <= RT_THREADS && s.k * s.I <= DN_MAXPASS * DN_THREADS * 8 &&
+           2 * GU_RT * s.nbH <= 16 * RO_THREADS && s.k * DN_RD * s.nbI <= 16 * DN_THREADS && s.E < RO_THREADS &&
+           s.E % 4 == 0 && s.k <= MAX_K;
+}
+
+hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
+    hipLaunchKernelGGL(k_route, dim3(E, T), dim3(RT_THREADS), 0, st, Wr, x, E, H, raw);
+    return hipGetLastError();
+}
+
+hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, int k, float eps, float *logits,
+                       int32_t *idx, float *w, hipStream_t st) {
+    size_t lds = route_lds_bytes(H);
+    hipError_t e = allow_lds((const void *)k_topk, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_topk, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, logits, idx, w);
+    return hipGetLastError();
+}
+
+template <int UNR>
+static hipError_t gateup_go(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T,
+                            float eps, float *h, int32_t *idx, float *w, hipStream_t st) {
+    size_t lds = gateup_lds_bytes(s.H, s.nbH);
+    hipError_t e = allow_lds((const void *)k_gateup<UNR>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_gateup<UNR>, dim3(cdiv((size_t)s.I, GU_RT), s.k, T), dim3(RO_THREADS), lds, st, layer_pl, s,
+                       x, raw, eps, h, idx, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T, float eps,
+                         float *h, int32_t *idx, float *w, hipStream_t st) {
+    if (!decode_shape_ok(s)) return hipErrorInvalidValue;
+    int per = (int)cdiv((size_t)2 * GU_RT * s.nbH, RO_THREADS);
+    if (per <= 4) return gateup_go<4>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
+    if (per <= 8) return gateup_go<8>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
+    return gateup_go<16>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
+}
+
+template <int UNR>
+static hipError_t down_go(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx,
+                          const float *w, int T, const float *resid, float *out, hipStream_t st) {
+    size_t lds = down_lds_bytes(s.k, s.I, s.nbI);
+    hipError_t e = allow_lds((const void *)k_down<UNR>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_down<UNR>, dim3(cdiv((size_t)s.H, DN_RD), T), dim3(DN_THREADS), lds, st, layer_pl, s, h,
+                       idx, w, resid, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
+                       int T, const float *resid, float *out, hipStream_t st) {
+    if (!decode_shape_ok(s)) return hipErrorInvalidValue;
+    int per = (int)cdiv((size_t)s.k * DN_RD * s.nbI, DN_THREADS);
+    if (per <= 2) return down_go<2>(layer_pl, s, h, idx, w, T, resid, out, st);
+    if (per <= 6) return down_go<6>(layer_pl, s, h, idx, w, T, resid, out, st);
+    if (per <= 12) return down_go<12>(layer_pl, s, h, idx, w, T, resid, out, st);
+    return down_go<16>(layer_pl, s, h, idx, w, T, resid, out, st);
+}
+
+}  // namespace tg
