@@ -45,6 +45,7 @@ def lib():
         L = ctypes.CDLL(str(LIB_PATH))
         sigs = {
             "tgo_f16_to_f32": (_F, [ctypes.c_uint16]),
+            "tgo_f16_to_f32_n": (None, [_P, _SZ, _P]),
             "tgo_f32_to_f16": (ctypes.c_uint16, [_F]),
             "tgo_expf": (_F, [_F]),
             "tgo_ln_unit": (_F, [_F]),
@@ -111,6 +112,13 @@ Q8K_DTYPE = np.dtype([("scale", "<f4"), ("sum", "<i4"), ("qs", "i1", (256,))])
 
 def f16_to_f32(h: int) -> float:
     return lib().tgo_f16_to_f32(int(h))
+
+
+def f16_to_f32_n(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.size, np.float32)
+    lib().tgo_f16_to_f32_n(_p(h), h.size, _p(out))
+    return out
 
 
 def f32_to_f16(f: float) -> int:

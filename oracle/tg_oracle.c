@@ -67,6 +67,12 @@ float tgo_f16_to_f32(uint16_t h) {
     return u2f(sign | ((exp + 112) << 23) | (man << 13));
 }
 
+/* Array form (keeps signalling-NaN payloads, which a float return value
+ * passed through a host ABI may quiet). */
+void tgo_f16_to_f32_n(const uint16_t *h, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = tgo_f16_to_f32(h[i]);
+}
+
 /* binary32 -> binary16, round to nearest even, overflow to inf, NaN quieted.
  * This is the rounding of ggml's fp16 store (D1/D2 scale storage) and of the
  * GPU's v_cvt_f16_f32.  Pinned by

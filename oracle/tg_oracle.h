@@ -36,6 +36,7 @@ extern "C" {
 
 /* ---- scalar conversions and math ---- */
 float    tgo_f16_to_f32(uint16_t h);
+void     tgo_f16_to_f32_n(const uint16_t *h, size_t n, float *out);
 uint16_t tgo_f32_to_f16(float f);
 float    tgo_expf(float x);
 float    tgo_ln_unit(float u);
