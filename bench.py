@@ -96,6 +96,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--path", choices=["auto", "persistent", "per-layer"], default="auto",
+                    help="decode path of one-token stack calls")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -117,6 +119,7 @@ def main() -> int:
     arena = HBMExpertArena(L, E, H, I, K_TOP)
     for l in range(L):
         arena.synth_layer(l, args.seed)
+    arena.set_decode_path({"auto": 0, "persistent": 1, "per-layer": 2}[args.path])
     stream = torch.cuda.current_stream().cuda_stream
     X = torch.empty((W + K, H), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, O.stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
@@ -138,6 +141,7 @@ def main() -> int:
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    arena.status()
     ms_step = wall * 1e3 / K
     tok_s = K / wall
     bytes_per_tok = L * K_TOP * EXPERT_Q4_BYTES
@@ -152,17 +156,26 @@ def main() -> int:
         blk.step(X[i:i + 1])
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
+    arena.status()
+    import ctypes
     kern = {}
-    for name in ("route", "gateup", "down"):
-        import ctypes
+    for name in ("persist", "route", "gateup", "down"):
         n = ctypes.c_int()
         ms = ctypes.c_double()
         call("tg_prof_read", name.encode(), ctypes.byref(n), ctypes.byref(ms))
-        kern[name] = (n.value, ms.value)
-    n_gu, ms_gu = kern["gateup"]
-    avg_gu = ms_gu / max(n_gu, 1) * 1e-3
-    achieved = K_TOP * GATEUP_BYTES_PER_EXPERT / avg_gu
+        if n.value:
+            kern[name] = (n.value, ms.value)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    if "persist" in kern:
+        # one launch = one token through all L layers
+        n_p, ms_p = kern["persist"]
+        avg = ms_p / n_p * 1e-3
+        roof_kernel, roof_bytes = "k_persist", L * K_TOP * EXPERT_Q4_BYTES
+    else:
+        n_gu, ms_gu = kern["gateup"]
+        avg = ms_gu / max(n_gu, 1) * 1e-3
+        roof_kernel, roof_bytes = "k_gateup", K_TOP * GATEUP_BYTES_PER_EXPERT
+    achieved = roof_bytes / avg
 
     cpu = None
     if not args.no_cpu:
@@ -193,7 +206,9 @@ def main() -> int:
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "event_ms_per_step": round(ev0.elapsed_time(ev1) / K, 4),
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": "k_gateup", "achieved": round(achieved / 1e9, 1),
+        "decode_path": "persistent" if "persist" in kern else "per-layer",
+        "roofline": {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
+                     "achieved": round(achieved / 1e9, 1),
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": None},
         "cpu_baseline": cpu,

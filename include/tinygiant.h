@@ -180,11 +180,40 @@ int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x,
 int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out,
                      int n_tokens, int32_t *topk_idx, float *topk_w,
                      float eps);
-/* x <- x + MoE_l(x) for l = layer0 .. layer0+n_layers-1, in place. */
+/* x <- x + MoE_l(x) for l = layer0 .. layer0+n_layers-1, in place.  The
+ * decode path of one-token calls is chosen by tg_arena_set_decode_path. */
 int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int layer0,
                          int n_layers, float eps, void *stream);
 int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
                      int n_layers, float eps);
+/* One token through layers layer0.. with the routing of every layer
+ * recorded: topk_idx / topk_w are device arrays [n_layers x k]. */
+int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
+                               int n_layers, float eps, int32_t *topk_idx,
+                               float *topk_w, void *stream);
+/* Decode path of one-token stack calls: PERSISTENT (one cooperative launch
+ * over every layer; error when the shape / device does not allow it),
+ * PER_LAYER (three kernels per layer, replayed as a HIP graph), AUTO (the
+ * faster of the two; currently PER_LAYER). */
+#define TG_DECODE_AUTO 0
+#define TG_DECODE_PERSISTENT 1
+#define TG_DECODE_PER_LAYER 2
+int tg_arena_set_decode_path(tg_arena *a, int path);
+/* Timeline of the persistent decode kernel (tracing): while set, every
+ * persistent launch writes wall-clock stamps [n_layers][blocks][8] into
+ * dev_words (device memory, at least the size tg_timeline_info gives):
+ * per block and layer, slot 0 layer start, 1 routing known / expert ids
+ * received, 2 Q8_0 x published / received, 3 h block published, 4 down
+ * loads issued, 5 h received, 6 next layer's partials published (unset
+ * slots keep their contents).  n_words = 0 switches it off.  The clock
+ * runs at clock_khz kHz. */
+int tg_arena_set_timeline(tg_arena *a, uint64_t *dev_words, size_t n_words);
+int tg_timeline_info(const tg_arena *a, int n_layers, size_t *n_words,
+                     int *blocks, int *clock_khz);
+/* Waits for the device and reports a device-side failure of an earlier
+ * asynchronous call on this arena (a persistent-kernel wait that ran out of
+ * tries). */
+int tg_arena_status(tg_arena *a);
 
 /* ------------------------------------------------------------------ */
 /* building blocks (device pointers; used by the parity tests)          */

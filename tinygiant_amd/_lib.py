@@ -70,6 +70,11 @@ NEW_SYMBOLS = [
     ("tg_moe_layer_q40", CI, [VP, CI, VP, VP, CI, VP, VP, CF]),
     ("tg_moe_stack_q40_dev", CI, [VP, VP, CI, CI, CI, CF, VP]),
     ("tg_moe_stack_q40", CI, [VP, VP, CI, CI, CI, CF]),
+    ("tg_moe_stack_q40_trace_dev", CI, [VP, VP, CI, CI, CF, VP, VP, VP]),
+    ("tg_arena_set_decode_path", CI, [VP, CI]),
+    ("tg_arena_status", CI, [VP]),
+    ("tg_arena_set_timeline", CI, [VP, VP, SZ]),
+    ("tg_timeline_info", CI, [VP, CI, VP, VP, VP]),
     ("tg_q40_quantize_q8_0_dev", CI, [VP, VP, CI, VP]),
     ("tg_q40_to_planar_dev", CI, [VP, VP, CI, CI, VP]),
     ("tg_q40_from_planar_dev", CI, [VP, VP, CI, CI, VP]),

@@ -65,6 +65,20 @@ class HBMExpertArena:
         except Exception:
             pass
 
+    # ------------------------------------------------------------ decode path
+    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER = 0, 1, 2
+
+    def set_decode_path(self, path: int) -> None:
+        """AUTO: one-token stack calls run as one persistent launch when the
+        shape allows; PERSISTENT: always (error otherwise); PER_LAYER: three
+        kernels per layer replayed as a HIP graph."""
+        call("tg_arena_set_decode_path", self.handle, int(path))
+
+    def status(self) -> None:
+        """Wait for the device; raise if an earlier asynchronous call failed
+        on the device (a persistent-kernel wait that ran out of tries)."""
+        call("tg_arena_status", self.handle)
+
     # ------------------------------------------------------------ contents
     def load_layer(self, layer: int, data) -> None:
         """Upload one relayout layer file's bytes (bytes or uint8 array)."""

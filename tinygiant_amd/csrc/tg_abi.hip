@@ -187,6 +187,15 @@ struct tg_arena {
     };
     std::vector<Graph> graphs;
     hipStream_t capture = nullptr;
+    // one-launch decode (T = 1): exchange buffers and sync words
+    int decode_path = TG_DECODE_AUTO;
+    int n_cu = 0;
+    bool coop = false;
+    uint8_t *ps_scratch = nullptr;
+    uint32_t *ps_sync = nullptr;
+    uint32_t ps_gen = 0;          // launch generation of the tagged exchange words
+    uint64_t *tl = nullptr;       // optional persistent-kernel timeline (caller's device buffer)
+    size_t tl_words = 0;
 };
 
 static void drop_graphs(tg_arena *a) {
@@ -227,6 +236,8 @@ static void arena_free(tg_arena *a) {
     dfree(a->w);
     dfree(a->xbuf);
     dfree(a->obuf);
+    dfree(a->ps_scratch);
+    dfree(a->ps_sync);
     delete a;
 }
 
@@ -243,6 +254,13 @@ extern "C" tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim,
     tg_arena *a = new tg_arena();
     a->s = shape;
     a->L = n_layers;
+    {
+        int dev = 0, v = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) a->n_cu = v;
+        v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess) a->coop = v != 0;
+    }
     size_t eb = a->s.LB * (size_t)n_layers;
     size_t rb = sizeof(float) * (size_t)n_experts * embed_dim * n_layers;
     if (hipMalloc(&a->experts, eb) != hipSuccess || hipMalloc(&a->routers, rb) != hipSuccess) {
@@ -394,10 +412,51 @@ static bool graphs_enabled() {
     return on == 1 && !g_prof_on;
 }
 
-// Replays the stack as a HIP graph captured on first use for this
-// (x, T, layer range, eps); falls back to direct launches while kernel
-// timing is on.
+// The persistent path runs when asked for; AUTO keeps the per-layer graph,
+// which is the faster of the two on MI355X today (profiles/).
+static bool persist_usable(tg_arena *a, int T) {
+    return T == 1 && a->decode_path == TG_DECODE_PERSISTENT && a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s);
+}
+
+static int persist_buffers(tg_arena *a) {
+    if (!a->ps_scratch) {
+        size_t n = tg::persist_scratch_bytes(a->s);
+        if (hipMalloc(&a->ps_scratch, n) != hipSuccess) {
+            (void)hipGetLastError();
+            return set_err(TG_E_NOMEM, "persistent decode exchange buffers");
+        }
+        HIP_TRY(hipMemset(a->ps_scratch, 0, n));  // tag 0 never matches a launch
+    }
+    if (!a->ps_sync) {
+        if (hipMalloc(&a->ps_sync, 64) != hipSuccess) {
+            (void)hipGetLastError();
+            return set_err(TG_E_NOMEM, "persistent decode sync words");
+        }
+        HIP_TRY(hipMemset(a->ps_sync, 0, 64));
+    }
+    return TG_OK;
+}
+
+// One cooperative launch for the whole layer range (one token).
+static int persist_run(tg_arena *a, float *x, int l0, int n, float eps, int32_t *idx_out, float *w_out,
+                       hipStream_t st) {
+    int rc = persist_buffers(a);
+    if (rc) return rc;
+    a->ps_gen = a->ps_gen + 1 >= (1u << 24) ? 1u : a->ps_gen + 1;
+    PROFILED("persist", st,
+             tg::launch_persist(a->experts, a->routers, a->s, l0, n, eps, x, a->ps_scratch, a->ps_sync, a->ps_gen,
+                                idx_out, w_out, a->tl, a->tl_words, a->n_cu, st));
+    return TG_OK;
+}
+
+// Decode of one token (T = 1) runs as one persistent launch when the shape
+// and device allow it.  Otherwise the stack is replayed as a HIP graph
+// captured on first use for this (x, T, layer range, eps), or launched
+// layer by layer while kernel timing is on.
 static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
+    if (persist_usable(a, T)) return persist_run(a, x, l0, n, eps, nullptr, nullptr, st);
+    if (T == 1 && a->decode_path == TG_DECODE_PERSISTENT)
+        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     if (!graphs_enabled()) return stack_launch(a, x, T, l0, n, eps, st);
     for (auto &g : a->graphs)
         if (g.x == x && g.T == T && g.layer0 == l0 && g.n == n && g.eps == eps) {
@@ -477,6 +536,69 @@ extern "C" int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int lay
     return stack_run(a, x, n_tokens, layer0, n_layers, eps, as_stream(stream));
 }
 
+extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int n_layers, float eps,
+                                          int32_t *topk_idx, float *topk_w, void *stream) {
+    int rc = stack_check(a, layer0, n_layers, 1, x);
+    if (rc) return rc;
+    if (!topk_idx || !topk_w) return set_err(TG_E_INVALID, "topk_idx / topk_w is NULL");
+    hipStream_t st = as_stream(stream);
+    if (persist_usable(a, 1)) return persist_run(a, x, layer0, n_layers, eps, topk_idx, topk_w, st);
+    if (a->decode_path == TG_DECODE_PERSISTENT)
+        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
+    const size_t k = (size_t)a->s.k;
+    for (int l = 0; l < n_layers; l++) {
+        if ((rc = layer_kernels(a, layer0 + l, x, x, x, 1, eps, st))) return rc;
+        HIP_TRY(hipMemcpyAsync(topk_idx + l * k, a->idx, sizeof(int32_t) * k, hipMemcpyDeviceToDevice, st));
+        HIP_TRY(hipMemcpyAsync(topk_w + l * k, a->w, sizeof(float) * k, hipMemcpyDeviceToDevice, st));
+    }
+    return TG_OK;
+}
+
+extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER)
+        return set_err(TG_E_INVALID, "unknown decode path %d", path);
+    if (path == TG_DECODE_PERSISTENT && !(a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s)))
+        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
+    a->decode_path = path;
+    return TG_OK;
+}
+
+extern "C" int tg_arena_set_timeline(tg_arena *a, uint64_t *dev_words, size_t n_words) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    a->tl = n_words ? dev_words : nullptr;
+    a->tl_words = dev_words ? n_words : 0;
+    return TG_OK;
+}
+
+extern "C" int tg_timeline_info(const tg_arena *a, int n_layers, size_t *n_words, int *blocks, int *clock_khz) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (n_words) *n_words = tg::persist_timeline_words(n_layers, a->n_cu);
+    if (blocks) *blocks = a->n_cu;
+    if (clock_khz) {
+        int dev = 0, v = 0;
+        HIP_TRY(hipGetDevice(&dev));
+        HIP_TRY(hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, dev));
+        *clock_khz = v;
+    }
+    return TG_OK;
+}
+
+extern "C" int tg_arena_status(tg_arena *a) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    int rc = ensure_device();
+    if (rc) return rc;
+    HIP_TRY(hipDeviceSynchronize());
+    if (a->ps_sync) {
+        uint32_t w[4] = {0, 0, 0, 0};
+        HIP_TRY(hipMemcpy(w, a->ps_sync, sizeof w, hipMemcpyDeviceToHost));
+        if (w[1] != 0u) return set_err(TG_E_HIP, "persistent decode: a device-side poll ran out of tries");
+    }
+    return TG_OK;
+}
+
 extern "C" int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0, int n_layers, float eps) {
     int rc = stack_check(a, layer0, n_layers, n_tokens, x);
     if (rc) return rc;
@@ -484,7 +606,7 @@ extern "C" int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
     HIP_TRY(hipMemcpy(a->xbuf, x, nx * sizeof(float), hipMemcpyHostToDevice));
     if ((rc = stack_run(a, a->xbuf, n_tokens, layer0, n_layers, eps, nullptr))) return rc;
     HIP_TRY(hipMemcpy(x, a->xbuf, nx * sizeof(float), hipMemcpyDeviceToHost));
-    return TG_OK;
+    return tg_arena_status(a);
 }
 
 // ================================================================ building blocks

@@ -85,4 +85,16 @@ hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x
 hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
                        int T, const float *resid, float *out, hipStream_t st);
 
+// one-token decode of a layer range in one cooperative launch
+bool persist_shape_ok(const Shape &s);
+size_t persist_scratch_bytes(const Shape &s);
+// gen: launch generation in 1 .. 2^24 - 1, different from the previous
+// launch on the same scratch
+// timeline: optional [nl][blocks][8] wall-clock stamps (used when
+// timeline_words covers nl * blocks * 8)
+hipError_t launch_persist(const uint8_t *experts, const float *routers, const Shape &s, int layer0, int nl, float eps,
+                          float *x, void *scratch, uint32_t *sync, uint32_t gen, int32_t *idx_out, float *w_out,
+                          uint64_t *timeline, size_t timeline_words, int n_cu, hipStream_t st);
+size_t persist_timeline_words(int nl, int n_cu);
+
 }  // namespace tg

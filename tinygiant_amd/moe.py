@@ -72,6 +72,21 @@ class MoEBlock:
         call("tg_moe_stack_q40_dev", a.handle, x.data_ptr(), T, layer0, n, self.eps, _stream_ptr(x))
         return x
 
+    def step_trace(self, x, layer0: int = 0, n_layers: int | None = None):
+        """One token: x <- x + MoE_l(x) over the layers, in place, with the
+        routing of every layer: returns (idx [n, k] int32, w [n, k] float32)."""
+        torch = _torch()
+        _check_dev(x, torch.float32, "x")
+        a = self.arena
+        if x.numel() != a.embed_dim:
+            raise ValueError("step_trace takes one token")
+        n = a.n_layers - layer0 if n_layers is None else n_layers
+        idx = torch.empty((n, a.top_k), dtype=torch.int32, device=x.device)
+        w = torch.empty((n, a.top_k), dtype=torch.float32, device=x.device)
+        call("tg_moe_stack_q40_trace_dev", a.handle, x.data_ptr(), layer0, n, self.eps, idx.data_ptr(),
+             w.data_ptr(), _stream_ptr(x))
+        return idx, w
+
     # ---------------------------------------------------------- host
     def forward_host(self, layer: int, x: np.ndarray):
         """Synchronous host-pointer form (the reference's calling convention)."""
