@@ -199,6 +199,18 @@ int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
 #define TG_DECODE_PERSISTENT 1
 #define TG_DECODE_PER_LAYER 2
 int tg_arena_set_decode_path(tg_arena *a, int path);
+/* Path of calls over n_tokens > 1 tokens (batched decode, prefill):
+ * GROUPED (the (token, slot) pairs grouped by expert, each selected
+ * expert's weights read once per layer; int8 MFMA tiles), GROUPED_DOT (the
+ * same grouping on packed int8 dot instructions), PER_TOKEN (every token
+ * reads its own k experts), AUTO (GROUPED for n_tokens >= 2).  GROUPED and
+ * GROUPED_DOT also serve a single token when asked for explicitly.  Every
+ * path gives the same bytes. */
+#define TG_BATCH_AUTO 0
+#define TG_BATCH_GROUPED 1
+#define TG_BATCH_PER_TOKEN 2
+#define TG_BATCH_GROUPED_DOT 3
+int tg_arena_set_batch_path(tg_arena *a, int path);
 /* Timeline of the persistent decode kernel (tracing): while set, every
  * persistent launch writes wall-clock stamps [n_layers][blocks][8] into
  * dev_words (device memory, at least the size tg_timeline_info gives):
@@ -238,6 +250,11 @@ int tg_q40_matvec_dev(const void *w_planar, int rows, int cols,
 int tg_router_topk_dev(const float *Wr, const float *x, int n_experts,
                        int embed_dim, int top_k, float eps, int n_tokens,
                        float *logits, int32_t *topk_idx, float *topk_w,
+                       void *stream);
+/* Measurement: one launch that reads nbytes (multiple of 16) of device
+ * memory with plain 128-bit loads over `grid` 256-thread blocks; sink is one
+ * device word.  The HBM read ceiling the expert kernels are compared with. */
+int tg_stream_read_dev(const void *p, size_t nbytes, int grid, uint32_t *sink,
                        void *stream);
 /* Synthetic generators (bit-identical to the host definition). */
 int tg_synth_normal_dev(uint64_t seed, uint64_t stream_id, float sigma,

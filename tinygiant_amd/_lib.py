@@ -72,6 +72,7 @@ NEW_SYMBOLS = [
     ("tg_moe_stack_q40", CI, [VP, VP, CI, CI, CI, CF]),
     ("tg_moe_stack_q40_trace_dev", CI, [VP, VP, CI, CI, CF, VP, VP, VP]),
     ("tg_arena_set_decode_path", CI, [VP, CI]),
+    ("tg_arena_set_batch_path", CI, [VP, CI]),
     ("tg_arena_status", CI, [VP]),
     ("tg_arena_set_timeline", CI, [VP, VP, SZ]),
     ("tg_timeline_info", CI, [VP, CI, VP, VP, VP]),
@@ -81,6 +82,7 @@ NEW_SYMBOLS = [
     ("tg_q40_block_sums_dev", CI, [VP, CI, CI, VP, VP, VP]),
     ("tg_q40_matvec_dev", CI, [VP, CI, CI, VP, VP, VP]),
     ("tg_router_topk_dev", CI, [VP, VP, CI, CI, CI, CF, CI, VP, VP, VP, VP]),
+    ("tg_stream_read_dev", CI, [VP, SZ, CI, VP, VP]),
     ("tg_synth_normal_dev", CI, [U64, U64, CF, SZ, VP, VP]),
     ("tg_synth_q40_dev", CI, [U64, U64, CF, CI, CI, VP, VP]),
 ]

@@ -74,6 +74,15 @@ class HBMExpertArena:
         kernels per layer replayed as a HIP graph."""
         call("tg_arena_set_decode_path", self.handle, int(path))
 
+    BATCH_AUTO, BATCH_GROUPED, BATCH_PER_TOKEN, BATCH_GROUPED_DOT = 0, 1, 2, 3
+
+    def set_batch_path(self, path: int) -> None:
+        """GROUPED: tokens grouped by expert, each selected expert read once
+        per layer, on int8 MFMA tiles; GROUPED_DOT: the same grouping on
+        packed int8 dot instructions; PER_TOKEN: every token reads its own
+        experts; AUTO: GROUPED for two or more tokens."""
+        call("tg_arena_set_batch_path", self.handle, int(path))
+
     def status(self) -> None:
         """Wait for the device; raise if an earlier asynchronous call failed
         on the device (a persistent-kernel wait that ran out of tries)."""

@@ -177,6 +177,21 @@ struct tg_arena {
     float *w = nullptr;           // T * k
     float *xbuf = nullptr;        // T * H (host-pointer entry points)
     float *obuf = nullptr;        // T * H
+    // grouped (batched) path, carved from one allocation
+    uint8_t *grp = nullptr;
+    int8_t *xq = nullptr;         // T * H      Q8_0 x * s per token
+    float *xd = nullptr;          // T * nbH
+    int *xs = nullptr;            // T * nbH
+    int32_t *counts = nullptr;    // E
+    int32_t *offsets = nullptr;   // E + 1
+    int32_t *entries = nullptr;   // T * k
+    int32_t *work = nullptr;      // 2 lists x 3 * group_work_max
+    int32_t *work_n = nullptr;    // 2
+    int8_t *hq = nullptr;         // T * k * I  Q8_0 h per (token, slot)
+    float *hd = nullptr;          // T * k * nbI
+    int *hs = nullptr;            // T * k * nbI
+    float *D = nullptr;           // T * k * H  down rows per (token, slot)
+    int batch_path = TG_BATCH_AUTO;
     // captured stacks, replayed as HIP graphs
     struct Graph {
         const float *x;
@@ -236,6 +251,7 @@ static void arena_free(tg_arena *a) {
     dfree(a->w);
     dfree(a->xbuf);
     dfree(a->obuf);
+    dfree(a->grp);
     dfree(a->ps_scratch);
     dfree(a->ps_sync);
     delete a;
@@ -348,9 +364,9 @@ extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float
 static int arena_scratch(tg_arena *a, int T) {
     if (T <= a->cap_T) return TG_OK;
     drop_graphs(a);  // captured graphs point at the old buffers
-    dfree(a->raw); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf);
+    dfree(a->raw); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf); dfree(a->grp);
     a->raw = nullptr; a->h = nullptr; a->idx = nullptr; a->w = nullptr;
-    a->xbuf = nullptr; a->obuf = nullptr;
+    a->xbuf = nullptr; a->obuf = nullptr; a->grp = nullptr;
     a->cap_T = 0;
     const Shape &s = a->s;
     bool ok = hipMalloc(&a->raw, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
@@ -359,6 +375,36 @@ static int arena_scratch(tg_arena *a, int T) {
               hipMalloc(&a->w, sizeof(float) * (size_t)T * s.k) == hipSuccess &&
               hipMalloc(&a->xbuf, sizeof(float) * (size_t)T * s.H) == hipSuccess &&
               hipMalloc(&a->obuf, sizeof(float) * (size_t)T * s.H) == hipSuccess;
+    if (ok) {
+        // grouped path: every piece 256-byte aligned
+        const size_t n = (size_t)T * s.k;
+        const size_t wmax = (size_t)tg::group_work_max(s, (int)n);
+        size_t sizes[] = {(size_t)T * s.H,     4 * (size_t)T * s.nbH,  4 * (size_t)T * s.nbH,
+                          4 * (size_t)s.E,     4 * ((size_t)s.E + 1), 4 * n,
+                          n * s.I,             4 * n * s.nbI,          4 * n * s.nbI,
+                          4 * n * s.H,         4 * 2 * 3 * wmax,       4 * 2};
+        size_t off[12], tot = 0;
+        for (int i = 0; i < 12; i++) {
+            off[i] = tot;
+            tot += (sizes[i] + 255) & ~(size_t)255;
+        }
+        ok = hipMalloc(&a->grp, tot) == hipSuccess;
+        if (ok) {
+            uint8_t *b = a->grp;
+            a->xq = reinterpret_cast<int8_t *>(b + off[0]);
+            a->xd = reinterpret_cast<float *>(b + off[1]);
+            a->xs = reinterpret_cast<int *>(b + off[2]);
+            a->counts = reinterpret_cast<int32_t *>(b + off[3]);
+            a->offsets = reinterpret_cast<int32_t *>(b + off[4]);
+            a->entries = reinterpret_cast<int32_t *>(b + off[5]);
+            a->hq = reinterpret_cast<int8_t *>(b + off[6]);
+            a->hd = reinterpret_cast<float *>(b + off[7]);
+            a->hs = reinterpret_cast<int *>(b + off[8]);
+            a->D = reinterpret_cast<float *>(b + off[9]);
+            a->work = reinterpret_cast<int32_t *>(b + off[10]);
+            a->work_n = reinterpret_cast<int32_t *>(b + off[11]);
+        }
+    }
     if (!ok) {
         (void)hipGetLastError();
         return set_err(TG_E_NOMEM, "scratch for %d tokens", T);
@@ -374,8 +420,57 @@ static const float *router_of(tg_arena *a, int layer) {
 
 // One MoE block: raw router dots, gate/up (norm, routing and Q8_0 fused),
 // down + combine.  out = moe_out (resid NULL) or resid + moe_out.
+static bool grouped_usable(tg_arena *a, int T) {
+    if (a->batch_path == TG_BATCH_PER_TOKEN) return false;
+    if (a->batch_path == TG_BATCH_GROUPED || a->batch_path == TG_BATCH_GROUPED_DOT) return tg::grouped_shape_ok(a->s);
+    return T >= 2 && tg::grouped_shape_ok(a->s);
+}
+
+// The MFMA kernels address activation rows with 32-bit offsets.
+static bool mfma_usable(tg_arena *a, int T) {
+    const Shape &s = a->s;
+    const size_t span = (size_t)T * s.k * (size_t)(s.H > s.I ? s.H : s.I);
+    return a->batch_path != TG_BATCH_GROUPED_DOT && tg::mfma_shape_ok(s) && span < (size_t)INT32_MAX;
+}
+
+// One MoE block over T tokens grouped by expert: every selected expert's
+// weights stream once for all its tokens.
+static int layer_kernels_grouped(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T,
+                                 float eps, hipStream_t st) {
+    const Shape &s = a->s;
+    const uint8_t *lp = a->experts + (size_t)layer * s.LB;
+    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
+    PROFILED("route_q8", st,
+             tg::launch_route_q8(a->raw, x, T, s.E, s.H, s.k, eps, a->idx, a->w, a->xq, a->xd, a->xs, st));
+    const int n = T * s.k;
+    if (mfma_usable(a, T)) {
+        const int mt = tg::mfma_tiles(s, T), ch = 32 * mt, wmax = tg::group_work_max(s, n, ch);
+        PROFILED("group", st,
+                 tg::launch_group_chunked(s, a->idx, n, ch, a->counts, a->offsets, a->entries, a->work, a->work_n,
+                                          st));
+        PROFILED("gateup_mfma", st,
+                 tg::launch_gateup_mfma(lp, s, mt, wmax, a->work, a->work_n, a->entries, a->xq, a->xd, a->xs, a->hq,
+                                        a->hd, a->hs, st));
+        PROFILED("down_mfma", st,
+                 tg::launch_down_mfma(lp, s, mt, wmax, a->work, a->work_n, a->entries, a->hq, a->hd, a->hs, a->D,
+                                      st));
+        PROFILED("combine", st, tg::launch_combine(a->D, a->w, T, s.H, s.k, resid, out, st));
+        return TG_OK;
+    }
+    PROFILED("group", st,
+             tg::launch_group(s, a->idx, n, a->counts, a->offsets, a->entries, a->work, a->work_n, st));
+    PROFILED("gateup_grouped", st,
+             tg::launch_gateup_grouped(lp, s, n, a->work, a->work_n, a->entries, a->xq, a->xd, a->xs, a->hq, a->hd,
+                                       a->hs, st));
+    PROFILED("down_grouped", st,
+             tg::launch_down_grouped(lp, s, n, a->work, a->work_n, a->entries, a->hq, a->hd, a->hs, a->D, st));
+    PROFILED("combine", st, tg::launch_combine(a->D, a->w, T, s.H, s.k, resid, out, st));
+    return TG_OK;
+}
+
 static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T, float eps,
                          hipStream_t st) {
+    if (grouped_usable(a, T)) return layer_kernels_grouped(a, layer, x, out, resid, T, eps, st);
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
     PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
@@ -554,12 +649,25 @@ extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int
     return TG_OK;
 }
 
+extern "C" int tg_arena_set_batch_path(tg_arena *a, int path) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (path != TG_BATCH_AUTO && path != TG_BATCH_GROUPED && path != TG_BATCH_PER_TOKEN &&
+        path != TG_BATCH_GROUPED_DOT)
+        return set_err(TG_E_INVALID, "unknown batch path %d", path);
+    if ((path == TG_BATCH_GROUPED || path == TG_BATCH_GROUPED_DOT) && !tg::grouped_shape_ok(a->s))
+        return set_err(TG_E_UNSUPPORTED, "the grouped path is not available for this shape");
+    drop_graphs(a);  // captured graphs hold the previous path's kernels
+    a->batch_path = path;
+    return TG_OK;
+}
+
 extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
     if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER)
         return set_err(TG_E_INVALID, "unknown decode path %d", path);
     if (path == TG_DECODE_PERSISTENT && !(a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s)))
         return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
+    drop_graphs(a);
     a->decode_path = path;
     return TG_OK;
 }
@@ -680,6 +788,14 @@ extern "C" int tg_router_topk_dev(const float *Wr, const float *x, int n_experts
     dfree(raw);
     HIP_TRY(e2);
     HIP_TRY(e3);
+    return TG_OK;
+}
+
+extern "C" int tg_stream_read_dev(const void *p, size_t nbytes, int grid, uint32_t *sink, void *stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!p || !sink || grid <= 0 || nbytes % 16) return set_err(TG_E_INVALID, "bad stream-read arguments");
+    HIP_TRY(tg::launch_stream_read(p, nbytes, grid, sink, as_stream(stream)));
     return TG_OK;
 }
 

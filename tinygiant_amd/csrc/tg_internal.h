@@ -85,6 +85,37 @@ hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x
 hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
                        int T, const float *resid, float *out, hipStream_t st);
 
+hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *sink, hipStream_t st);
+
+// grouped (batched decode / prefill) MoE layer pieces
+bool grouped_shape_ok(const Shape &s);
+hipError_t launch_route_q8(const float *raw, const float *x, int T, int E, int H, int k, float eps, int32_t *idx,
+                           float *w, int8_t *xq, float *xd, int *xs, hipStream_t st);
+// work list: at most group_work_max(s, n) items per list, two lists
+int group_work_max(const Shape &s, int n);
+int group_work_max(const Shape &s, int n, int ch);
+hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
+                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st);
+// int8-MFMA grouped gate/up and down (mt = M-tiles of 32 entries per item)
+bool mfma_shape_ok(const Shape &s);
+int mfma_tiles(const Shape &s, int T);
+hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
+                              const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                              const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);
+hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
+                            const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
+                            const int *hs, float *D, hipStream_t st);
+hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
+                        int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st);
+hipError_t launch_gateup_grouped(const uint8_t *layer_pl, const Shape &s, int n, const int32_t *work,
+                                 const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                                 const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);
+hipError_t launch_down_grouped(const uint8_t *layer_pl, const Shape &s, int n, const int32_t *work,
+                               const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
+                               const int *hs, float *D, hipStream_t st);
+hipError_t launch_combine(const float *D, const float *w, int T, int H, int k, const float *resid, float *out,
+                          hipStream_t st);
+
 // one-token decode of a layer range in one cooperative launch
 bool persist_shape_ok(const Shape &s);
 size_t persist_scratch_bytes(const Shape &s);

@@ -1,0 +1,360 @@
+// tg_mfma.hip -- grouped-expert GEMM on int8 MFMA (batched decode, prefill).
+//
+// Work item = (expert e, up to MT*32 entries of its group).  A block of four
+// waves shares the item's activations, staged through LDS in chunks of
+// MF_KC Q4_0 blocks (double-buffered, loaded by all 256 threads); each wave
+// owns one tile of 32 weight rows and walks its Q4_0 blocks b.  Per block and
+// tile of 32 entries, one v_mfma_i32_32x32x32_i8 computes the block's 32 x 32
+// integer dot products exactly; K = 32 is one Q4_0 / Q8_0 block.
+//
+// Operands (lane l, half h = l / 32; A lane h*32+m byte j pairs with B lane
+// h*32+n byte j, measured on gfx950):
+//   A  q - 8 of weight row m = l % 32, block b, elements 16h .. 16h+15 (the
+//      low (h = 0) or high (h = 1) nibbles of the row's 16 bytes) as int8,
+//      from byte-wise (q | 0x80) - 8 ^ 0x80, which never borrows across bytes
+//   B  Q8_0 values of entry n = l % 32 of the tile, block b, elements
+//      16h .. 16h+15 (one 128-bit LDS read)
+//   C  0x4B400000 for every element
+// so D = 0x4B400000 + S with S = sum (q_w - 8) q_x, |S| <= 32512: D's bits
+// are the float 1.5 * 2^23 + S exactly.  Output layout: lane l, register r
+// holds (weight row m, entry n) = (8 (r/4) + 4h + r%4, l % 32).
+//
+// Epilogue per block (the row-dot definition, bit for bit):
+//   u   = fma(float_bits(D), dw_m, -1.5 * 2^23 * dw_m)   = round(S * dw_m)
+//         (the constant is exact: dw is a half)
+//   acc = fma(u, dx_n, acc)
+// dx_n is one value per lane; the 16 row scales dw_m a lane needs are read
+// from a per-wave LDS table kept in register order, shared by the M-tiles.
+// Gate/up then applies SwiGLU and Q8_0 per (entry, 32 rows): the 32 values
+// of one entry sit in lanes n and n + 32, 16 registers each.  Down writes
+// fp32 rows per entry for the combine.
+#include "tg_device.h"
+#include "tg_internal.h"
+
+namespace tg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int MF_THREADS = 256;        // four waves, one weight tile each
+constexpr int MF_PF = 4;               // Q4_0 blocks of A prefetched ahead (per wave)
+constexpr int MF_KC = 8;               // Q4_0 blocks per staged activation chunk
+constexpr int MF_TS = MF_KC * 32 + 16;  // LDS bytes per staged activation row (16 pad)
+constexpr uint32_t MAGIC_I = 0x4B400000u;
+constexpr float MAGIC_F = 12582912.0f;  // 1.5 * 2^23
+
+// nibble bytes (0..15 each) -> q - 8 as int8 per byte
+TG_DEV int nib_s8(uint32_t nb4) { return (int)(((nb4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u); }
+
+TG_DEV v4i nib_lo(uint4 w) {
+    v4i r;
+    r.x = nib_s8(w.x & 0x0F0F0F0Fu); r.y = nib_s8(w.y & 0x0F0F0F0Fu);
+    r.z = nib_s8(w.z & 0x0F0F0F0Fu); r.w = nib_s8(w.w & 0x0F0F0F0Fu);
+    return r;
+}
+
+TG_DEV v4i nib_hi(uint4 w) {
+    v4i r;
+    r.x = nib_s8((w.x >> 4) & 0x0F0F0F0Fu); r.y = nib_s8((w.y >> 4) & 0x0F0F0F0Fu);
+    r.z = nib_s8((w.z >> 4) & 0x0F0F0F0Fu); r.w = nib_s8((w.w >> 4) & 0x0F0F0F0Fu);
+    return r;
+}
+
+// LDS: two chunk buffers of [M rows][MF_TS bytes] activations and
+// [MF_KC][M] activation scales, then per wave two [MF_KC][2][16] tables of
+// weight scales.  Gate/up's hand-off of the up sums (2 tiles x MT x 16
+// registers x 64 lanes) reuses the activation buffers after the block loop.
+__host__ __device__ inline size_t mf_lds_bytes(int mt) {
+    const size_t m = 32 * (size_t)mt;
+    return 2 * m * MF_TS + 2 * MF_KC * m * 4 + 4 * 2 * MF_KC * 32 * 4;
+}
+
+// PAIR: gate/up.  Waves 0/1 of a block take gate/up of tile 2x, waves 2/3
+// gate/up of tile 2x+1; after the block loop the up waves hand their sums
+// to the gate waves through LDS, which apply SwiGLU and Q8_0 and write h.
+// Otherwise down: four tiles of down rows per block, fp32 rows out.
+// Activations are indexed by token (entry / k) for gate/up and by entry for
+// down.
+template <int MT, bool PAIR>
+__global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                             const int32_t *__restrict__ work,
+                                                             const int32_t *__restrict__ work_n,
+                                                             const int32_t *__restrict__ entries,
+                                                             const int8_t *__restrict__ aq,
+                                                             const float *__restrict__ ad, int8_t *__restrict__ oq,
+                                                             float *__restrict__ od, int *__restrict__ os,
+                                                             float *__restrict__ D) {
+    constexpr int M = MT * 32;
+    constexpr int TP = 2 * MF_KC;                    // 16-byte pieces per row and chunk
+    constexpr int NTP = M * TP / MF_THREADS;         // pieces staged per thread
+    constexpr int NDX = M * MF_KC / MF_THREADS;      // activation scales staged per thread
+    static_assert(MF_THREADS % TP == 0 && MF_THREADS % MF_KC == 0 && MF_KC % MF_PF == 0, "staging map");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wi = blockIdx.y;
+    if (wi >= work_n[0]) return;  // uniform over the block
+    const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+    const int K = PAIR ? s.H : s.I, nb = K / QK, rows = PAIR ? s.I : s.H, k = s.k;
+    const int nch = (nb + MF_KC - 1) / MF_KC;
+
+    uint8_t *tokl = smem;                                                     // [2][M][MF_TS]
+    float *dxl = reinterpret_cast<float *>(smem + 2 * M * MF_TS);             // [2][MF_KC][M]
+    float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 32);               // [2][MF_KC][2][16]
+
+    // staging map: piece p of row t = tid / TP + u * (256 / TP); scale of
+    // block tid % MF_KC of row tid / MF_KC + u * (256 / MF_KC)
+    const int sp = tid % TP, sb = tid % MF_KC;
+    int toff[NTP], doff[NDX];
+#pragma unroll
+    for (int u = 0; u < NTP; u++) {
+        const int t = tid / TP + u * (MF_THREADS / TP);
+        toff[u] = -1;
+        if (t < c) {
+            const int ent = entries[o + t];
+            toff[u] = (PAIR ? ent / k : ent) * K;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NDX; u++) {
+        const int t = tid / MF_KC + u * (MF_THREADS / MF_KC);
+        doff[u] = -1;
+        if (t < c) {
+            const int ent = entries[o + t];
+            doff[u] = (PAIR ? ent / k : ent) * nb;
+        }
+    }
+
+    // this wave's weight tile; an out-of-range tile computes on row n and
+    // stores nothing
+    const int mat = PAIR ? (wave & 1) : 0;  // 0 gate / down, 1 up
+    const int nt = PAIR ? blockIdx.x * 2 + (wave >> 1) : blockIdx.x * 4 + wave;
+    const bool valid = nt * 32 < rows;
+    const int R = valid ? nt * 32 + n : n;
+    const uint8_t *ex = layer_pl + (size_t)e * s.EB;
+    const uint8_t *tb = PAIR ? ex + (size_t)mat * s.GB : ex + 2 * s.GB;
+    const size_t ntb = (size_t)rows * nb;
+    const uint4 *q0 = reinterpret_cast<const uint4 *>(tb) + (size_t)R * nb;
+    const uint16_t *s0 = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + (size_t)R * nb;
+    // slot of row n in the register-ordered scale table
+    const int wslot = ((n >> 2) & 1) * 16 + 4 * (n >> 3) + (n & 3);
+
+    uint4 sv[NTP];
+    float sd[NDX];
+    uint16_t ws[MF_KC];
+    auto stage = [&](int ch) {
+#pragma unroll
+        for (int u = 0; u < NTP; u++) {
+            const int kb = ch * MF_KC * 32 + sp * 16;
+            sv[u] = make_uint4(0u, 0u, 0u, 0u);
+            if (toff[u] >= 0 && kb < K) sv[u] = *reinterpret_cast<const uint4 *>(aq + toff[u] + kb);
+        }
+#pragma unroll
+        for (int u = 0; u < NDX; u++) {
+            const int b = ch * MF_KC + sb;
+            sd[u] = (doff[u] >= 0 && b < nb) ? ad[doff[u] + b] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < MF_KC; j++) {
+            const int b = ch * MF_KC + j;
+            ws[j] = (h == 0 && b < nb) ? s0[b] : (uint16_t)0;
+        }
+    };
+    auto commit = [&](int q) {
+#pragma unroll
+        for (int u = 0; u < NTP; u++) {
+            const int t = tid / TP + u * (MF_THREADS / TP);
+            *reinterpret_cast<uint4 *>(tokl + ((size_t)q * M + t) * MF_TS + sp * 16) = sv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < NDX; u++) {
+            const int t = tid / MF_KC + u * (MF_THREADS / MF_KC);
+            dxl[(q * MF_KC + sb) * M + t] = sd[u];
+        }
+        if (h == 0) {
+#pragma unroll
+            for (int j = 0; j < MF_KC; j++) dwl[(q * MF_KC + j) * 32 + wslot] = h2f(ws[j]);
+        }
+    };
+
+    float acc[MT][16];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
+
+    stage(0);
+    commit(0);
+    // A prefetch ring: block b sits in slot b % MF_PF
+    uint4 w0[MF_PF];
+#pragma unroll
+    for (int p = 0; p < MF_PF; p++)
+        if (p < nb) w0[p] = q0[p];
+    v16i cmag;
+#pragma unroll
+    for (int r = 0; r < 16; r++) cmag[r] = (int)MAGIC_I;
+    __syncthreads();
+
+    for (int ch = 0; ch < nch; ch++) {
+        const int q = ch & 1;
+        if (ch + 1 < nch) stage(ch + 1);
+        const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
+        const float *xq = dxl + q * MF_KC * M + n;
+        const float *wq = dwl + q * MF_KC * 32 + 16 * h;
+#pragma unroll
+        for (int bl = 0; bl < MF_KC; bl++) {
+            const int b = ch * MF_KC + bl;
+            if (b < nb) {
+                const v4i wa = h ? nib_hi(w0[bl % MF_PF]) : nib_lo(w0[bl % MF_PF]);
+                if (b + MF_PF < nb) w0[bl % MF_PF] = q0[b + MF_PF];
+                v4i tbv[MT];
+                float dx[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    tbv[mt] = *reinterpret_cast<const v4i *>(tq + (size_t)mt * 32 * MF_TS + bl * 32);
+                    dx[mt] = xq[bl * M + mt * 32];
+                }
+                v16i r0[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    r0[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[mt], cmag, 0, 0, 0);
+                float dw[16], cw[16];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 v = *reinterpret_cast<const float4 *>(wq + bl * 32 + 4 * g);
+                    dw[4 * g] = v.x; dw[4 * g + 1] = v.y; dw[4 * g + 2] = v.z; dw[4 * g + 3] = v.w;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) cw[r] = -MAGIC_F * dw[r];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float u = __builtin_fmaf(__int_as_float(r0[mt][r]), dw[r], cw[r]);
+                        acc[mt][r] = __builtin_fmaf(u, dx[mt], acc[mt][r]);
+                    }
+            }
+        }
+        if (ch + 1 < nch) commit(q ^ 1);
+        __syncthreads();
+    }
+
+    if (PAIR) {
+        // up sums -> LDS (over the activation buffers), gate waves combine
+        float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * MT * 16 * 64;
+        if (mat == 1) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) x[(mt * 16 + r) * 64 + lane] = acc[mt][r];
+        }
+        __syncthreads();
+        if (mat == 1) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int t = mt * 32 + n;
+            const bool on = valid && t < c;
+            // SwiGLU, then Q8_0 over the entry's 32 rows (16 here, 16 in lane ^ 32)
+            float hv[16], a = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                hv[r] = on ? silu_mul(acc[mt][r], x[(mt * 16 + r) * 64 + lane]) : 0.0f;
+                const float v = fabsf(hv[r]);
+                a = v > a ? v : a;
+            }
+            const float ao = __shfl_xor(a, 32, WAVE);
+            a = ao > a ? ao : a;
+            const float d = a / 127.0f;
+            const float inv = a > 0.0f ? 127.0f / a : 0.0f;
+            int qv[16], sum = 0;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                qv[r] = (int)__builtin_rintf(hv[r] * inv);
+                sum += qv[r];
+            }
+            sum += __shfl_xor(sum, 32, WAVE);
+            if (on) {
+                const int ent = entries[o + t];
+                int8_t *dst = oq + (size_t)ent * s.I + nt * 32 + 4 * h;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t w = (uint32_t)(qv[4 * j] & 0xFF) | ((uint32_t)(qv[4 * j + 1] & 0xFF) << 8) |
+                                       ((uint32_t)(qv[4 * j + 2] & 0xFF) << 16) |
+                                       ((uint32_t)(qv[4 * j + 3] & 0xFF) << 24);
+                    *reinterpret_cast<uint32_t *>(dst + 8 * j) = w;
+                }
+                if (h == 0) {
+                    od[(size_t)ent * s.nbI + nt] = h2f(f2h(d));
+                    os[(size_t)ent * s.nbI + nt] = sum;
+                }
+            }
+        }
+    } else if (valid) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int t = mt * 32 + n;
+            if (t < c) {
+                float *dst = D + (size_t)entries[o + t] * s.H + nt * 32 + 4 * h;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    *reinterpret_cast<float4 *>(dst + 8 * j) =
+                        make_float4(acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]);
+            }
+        }
+    }
+}
+
+// ================================================================ launchers
+static inline unsigned mf_cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+int mfma_tiles(const Shape &s, int T) {
+    // entries per expert in a work item: up to 4 M-tiles of 32; fewer when
+    // the batch is small or the LDS staging would not fit
+    const int avg = (T * s.k + s.E - 1) / s.E;
+    return avg > 64 ? 4 : (avg > 16 ? 2 : 1);
+}
+
+bool mfma_shape_ok(const Shape &s) {
+    return s.I % 32 == 0 && s.H % 32 == 0 && s.k <= MAX_K;
+}
+
+template <int MT, bool PAIR>
+static hipError_t mf_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work, const int32_t *work_n,
+                        const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
+                        float *D, hipStream_t st) {
+    const int rows = PAIR ? s.I : s.H;
+    const size_t lds = mf_lds_bytes(MT);
+    const void *fn = reinterpret_cast<const void *>(&k_mfma_grouped<MT, PAIR>);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    // gate/up: two N-tiles (each as a gate wave and an up wave) per block
+    const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 64) : mf_cdiv((size_t)rows, 128);
+    hipLaunchKernelGGL((k_mfma_grouped<MT, PAIR>), dim3(gx, wmax), dim3(MF_THREADS), lds, st, layer_pl, s, work,
+                       work_n, entries, aq, ad, oq, od, os, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
+                              const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                              const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
+    if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
+    (void)xs;
+    if (mt == 1) return mf_go<1, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+    if (mt == 2) return mf_go<2, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+    return mf_go<4, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+}
+
+hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
+                            const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
+                            const int *hs, float *D, hipStream_t st) {
+    if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
+    (void)hs;
+    if (mt == 1) return mf_go<1, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
+                                        D, st);
+    if (mt == 2) return mf_go<2, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
+                                        D, st);
+    return mf_go<4, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
+}
+
+}  // namespace tg

@@ -61,6 +61,80 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(const float *__restrict__ 
     }
 }
 
+// Many tokens: block = 32 tokens x 32 experts, 256 threads, each thread 2
+// tokens x 2 experts.  Four groups (128 consecutive elements) of x and of the
+// router rows are staged in LDS per step, the next step's loads in flight
+// while the current one is used; every (t, e) pair runs each group's fma
+// chain and adds it to its total in ascending group order, exactly as
+// k_route does.
+constexpr int RTT = 32;
+constexpr int RT_CH = 4;               // groups per staging step
+constexpr int RT_W = RT_CH * RG + 4;   // LDS row stride (floats)
+
+__global__ __launch_bounds__(256) void k_route_tiled(const float *__restrict__ Wr, const float *__restrict__ x,
+                                                     int T, int E, int H, float *__restrict__ raw) {
+    __shared__ __align__(16) float xs[RTT][RT_W];
+    __shared__ __align__(16) float ws[RTT][RT_W];
+    const int tid = threadIdx.x, t0 = blockIdx.x * RTT, e0 = blockIdx.y * RTT;
+    const int tt = (tid >> 4) * 2, ee = (tid & 15) * 2;  // this thread's 2 tokens, 2 experts
+    // staging: thread loads rows r = tid / 32 + 8 v (v < 4), float4 column c4
+    const int sr = tid >> 5, sc = (tid & 31) * 4;
+    float tot[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    const int G = H / RG, nst = G / RT_CH;
+    float4 xv[4], wv[4];
+    auto fetch = [&](int st) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int r = sr + 8 * v, t = t0 + r, e = e0 + r;
+            const size_t col = (size_t)st * RT_CH * RG + sc;
+            xv[v] = t < T ? *reinterpret_cast<const float4 *>(x + (size_t)t * H + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[v] = e < E ? *reinterpret_cast<const float4 *>(Wr + (size_t)e * H + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    fetch(0);
+    for (int st = 0; st < nst; st++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            *reinterpret_cast<float4 *>(&xs[sr + 8 * v][sc]) = xv[v];
+            *reinterpret_cast<float4 *>(&ws[sr + 8 * v][sc]) = wv[v];
+        }
+        __syncthreads();
+        if (st + 1 < nst) fetch(st + 1);
+#pragma unroll
+        for (int gg = 0; gg < RT_CH; gg++) {
+            float a[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+#pragma unroll
+            for (int q = 0; q < RG / 4; q++) {
+                const int c = gg * RG + 4 * q;
+                const float4 x0 = *reinterpret_cast<const float4 *>(&xs[tt][c]);
+                const float4 x1 = *reinterpret_cast<const float4 *>(&xs[tt + 1][c]);
+                const float4 w0 = *reinterpret_cast<const float4 *>(&ws[ee][c]);
+                const float4 w1 = *reinterpret_cast<const float4 *>(&ws[ee + 1][c]);
+                const float xa[2][4] = {{x0.x, x0.y, x0.z, x0.w}, {x1.x, x1.y, x1.z, x1.w}};
+                const float wa[2][4] = {{w0.x, w0.y, w0.z, w0.w}, {w1.x, w1.y, w1.z, w1.w}};
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+#pragma unroll
+                        for (int j = 0; j < 2; j++) a[i][j] = __builtin_fmaf(wa[j][cc], xa[i][cc], a[i][j]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) tot[i][j] = tot[i][j] + a[i][j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int t = t0 + tt + i, e = e0 + ee + j;
+            if (t < T && e < E) raw[(size_t)t * E + e] = tot[i][j];
+        }
+}
+
 // NaN logits rank below every number (as -inf) and -0 equals +0, so the
 // 64-bit key orders experts by (logit descending, index ascending) and the
 // ranks always form a permutation.
@@ -459,6 +533,323 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
     }
 }
 
+// ================================================================ grouped
+// Batched decode / prefill: the (token, slot) pairs of a layer are grouped
+// by expert, so each selected expert's weights stream once for all of its
+// tokens.  Per layer:
+//
+//   k_route          raw router dots (as above)
+//   k_route_q8       grid (T): routing of token t (route_token), its top-k
+//                    ids and weights, and Q8_0(x_t * s_t) to global
+//   k_group          one block: per-expert counts, offsets, and the entry
+//                    list (entry i = t * k + j) of every expert
+//   k_gateup_grouped grid (I/32, E): rows [32m, 32m+32) of gate and up of
+//                    expert e for every entry of its group, SwiGLU, Q8_0
+//                    block m of h for that entry
+//   k_down_grouped   grid (H/32, E): rows [32g, 32g+32) of down of expert e
+//                    for every entry of its group -> D[entry][row]
+//   k_combine        grid (H/256, T): out = resid + sum_j w_j D[t*k+j] in
+//                    ascending logit order
+//
+// The position of an entry inside its group comes from LDS atomics and is
+// not deterministic, but every (token, expert) product is computed by the
+// same steps wherever it sits, and the combine visits the experts of a
+// token in its own slot order, so every output is deterministic and equal
+// to the per-token path bit for bit.
+
+__global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ x,
+                                                         int E, int H, int k, float eps, int32_t *__restrict__ idx,
+                                                         float *__restrict__ w, int8_t *__restrict__ xq,
+                                                         float *__restrict__ xd, int *__restrict__ xs) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    RouteLds L = route_lds(smem, H);
+    const int t = blockIdx.x, tid = threadIdx.x, nbH = H / QK;
+    float xv[RO_MAXPASS][8];
+    route_token(x + (size_t)t * H, raw + (size_t)t * E, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx,
+                L.sred);
+    if (tid == 0) {
+        topk_softmax(L.slog, L.sidx, k, L.sw, L.sex);
+        for (int i = 0; i < k; i++) {
+            idx[(size_t)t * k + i] = L.sidx[i];
+            w[(size_t)t * k + i] = L.sw[i];
+        }
+    }
+    const float sc = L.sred[0];
+#pragma unroll
+    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+        const int i0 = ps * RO_THREADS * 8 + tid * 8;
+        if (ps * RO_THREADS * 8 < H) {
+            float v[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) v[c] = xv[ps][c] * sc;
+            q8_group8(v, i0 < H, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
+        }
+    }
+}
+
+constexpr int GR_THREADS = 1024;
+
+// Work list: the entries of each expert cut into chunks of at most `ch`
+// (gate/up) and `chd` (down) entries; item w = (expert, first entry, count)
+// in work[3 * w ..], the number of items in work_n[0] (gate/up) and
+// work_n[1] (down; its items start at work + 3 * wmax).
+__global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict__ idx, int n, int E, int ch, int chd,
+                                                      int wmax, int32_t *__restrict__ counts,
+                                                      int32_t *__restrict__ offsets, int32_t *__restrict__ entries,
+                                                      int32_t *__restrict__ work, int32_t *__restrict__ work_n) {
+    __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += GR_THREADS) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += GR_THREADS) {
+        int e = idx[i];
+        e = e < 0 ? 0 : (e >= E ? E - 1 : e);  // never index outside the table
+        atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; e++) {
+            off[e] = acc;
+            acc += cnt[e];
+        }
+        off[E] = acc;
+    }
+    __syncthreads();
+    if (tid < 2) {
+        // two lists, one per thread; sizes bounded by E + n / ch <= wmax
+        const int c = tid == 0 ? ch : chd;
+        int32_t *wl = work + (size_t)tid * 3 * wmax;
+        int w = 0;
+        for (int e = 0; e < E; e++)
+            for (int c0 = 0; c0 < cnt[e] && w < wmax; c0 += c) {
+                wl[3 * w] = e;
+                wl[3 * w + 1] = off[e] + c0;
+                wl[3 * w + 2] = cnt[e] - c0 < c ? cnt[e] - c0 : c;
+                w++;
+            }
+        work_n[tid] = w;
+    }
+    for (int e = tid; e <= E; e += GR_THREADS) {
+        offsets[e] = off[e];
+        if (e < E) counts[e] = cnt[e];
+    }
+    for (int i = tid; i < n; i += GR_THREADS) {
+        int e = idx[i];
+        e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+        const int pos = atomicAdd(&fill[e], 1);
+        entries[off[e] + pos] = i;
+    }
+}
+
+// Tokens (entries) per chunk of the grouped kernels, from an LDS budget.
+constexpr size_t GRP_LDS_BUDGET = 72 * 1024;
+
+__host__ __device__ inline int gu_chunk(int nbH) {
+    size_t per = (size_t)64 * (round4(nbH) + 4) * 4 + (size_t)nbH * QK + 8 * (size_t)round4(nbH);
+    int tc = (int)(GRP_LDS_BUDGET / per);
+    return tc < 1 ? 1 : (tc > 8 ? 8 : tc);
+}
+
+__host__ __device__ inline size_t gu_grouped_lds(int nbH) {
+    const int tc = gu_chunk(nbH);
+    return (size_t)tc * ((size_t)64 * (round4(nbH) + 4) * 4 + (size_t)nbH * QK + 8 * (size_t)round4(nbH)) +
+           4 * (size_t)tc * 64 + 4 * 8;
+}
+
+template <int NT, int UNR>
+__global__ __launch_bounds__(NT) void k_gateup_grouped(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                               const int32_t *__restrict__ work,
+                                                               const int32_t *__restrict__ work_n,
+                                                               const int32_t *__restrict__ entries,
+                                                               const int8_t *__restrict__ xq,
+                                                               const float *__restrict__ xd,
+                                                               const int *__restrict__ xs, int8_t *__restrict__ hq,
+                                                               float *__restrict__ hd, int *__restrict__ hs) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wi = blockIdx.y, m = blockIdx.x, tid = threadIdx.x;
+    if (wi >= work_n[0]) return;
+    const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
+    const int nb = s.nbH, nbp = round4(nb), ust = nbp + 4, H = s.H, k = s.k, tc = gu_chunk(nb);
+    float *U = reinterpret_cast<float *>(smem);                         // [tc][64][ust]
+    int8_t *lq = reinterpret_cast<int8_t *>(U + (size_t)tc * 64 * ust); // [tc][H]
+    float *ld = reinterpret_cast<float *>(lq + (size_t)tc * H);         // [tc][nbp]
+    int *ls = reinterpret_cast<int *>(ld + (size_t)tc * nbp);           // [tc][nbp]
+    float *D = reinterpret_cast<float *>(ls + (size_t)tc * nbp);        // [tc][64]
+    int *ent = reinterpret_cast<int *>(D + (size_t)tc * 64);            // [8]
+
+    // gate and up rows [32m, 32m+32) of expert e, all issued first
+    const uint8_t *ex = layer_pl + (size_t)e * s.EB;
+    const size_t ntb = (size_t)s.I * nb;
+    const int items = 64 * nb;
+    uint4 wv[UNR];
+    uint16_t dv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const int p = u * NT + tid;
+        wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        dv[u] = 0;
+        if (p < items) {
+            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            const uint8_t *tb = ex + (size_t)(rd >> 5) * s.GB;
+            const size_t ob = (size_t)(m * 32 + (rd & 31)) * nb + b;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
+        }
+    }
+    for (int c0 = 0; c0 < c; c0 += tc) {
+        const int nt = c - c0 < tc ? c - c0 : tc;
+        if (tid < nt) ent[tid] = entries[o + c0 + tid];
+        __syncthreads();
+        // Q8_0 x of the chunk's tokens -> LDS
+        for (int q = 0; q < nt; q++) {
+            const int t = ent[q] / k;
+            const int *src = reinterpret_cast<const int *>(xq + (size_t)t * H);
+            int *dst = reinterpret_cast<int *>(lq + (size_t)q * H);
+            for (int i = tid; i < H / 4; i += NT) dst[i] = src[i];
+            for (int b = tid; b < nb; b += NT) {
+                ld[q * nbp + b] = xd[(size_t)t * nb + b];
+                ls[q * nbp + b] = xs[(size_t)t * nb + b];
+            }
+        }
+        __syncthreads();
+        for (int q = 0; q < nt; q++) {
+            const int8_t *xqq = lq + (size_t)q * H;
+            const int *lsq = ls + q * nbp;
+            float *Uq = U + (size_t)q * 64 * ust;
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int p = u * NT + tid;
+                if (p < items) {
+                    const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+                    const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(xqq + b * QK)) - 8 * lsq[b];
+                    Uq[rd * ust + b] = (float)S * h2f(dv[u]);
+                }
+            }
+        }
+        __syncthreads();
+        for (int r = tid; r < nt * 64; r += NT) {
+            const int q = r >> 6;
+            D[r] = chain4(U + (size_t)r * ust, ld + q * nbp, nb);
+        }
+        __syncthreads();
+        // h rows -> Q8_0 block m of each entry (32 lanes per entry)
+        {
+            const int q = tid >> 5, rr = tid & 31;
+            const bool on = q < nt;
+            const float hv = on ? silu_mul(D[q * 64 + rr], D[q * 64 + 32 + rr]) : 0.0f;
+            float dq; int qsum; uint16_t dh;
+            const int qv = q8_lane(hv, dq, qsum, dh);
+            if (on) {
+                const int i = ent[q];
+                hq[(size_t)i * s.I + m * 32 + rr] = (int8_t)qv;
+                if (rr == 0) {
+                    hd[(size_t)i * s.nbI + m] = dq;
+                    hs[(size_t)i * s.nbI + m] = qsum;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__host__ __device__ inline int dn_chunk(int nbI, int I) {
+    size_t per = (size_t)32 * (round4(nbI) + 4) * 4 + (size_t)I + 8 * (size_t)round4(nbI);
+    int tc = (int)(GRP_LDS_BUDGET / per);
+    return tc < 1 ? 1 : (tc > 16 ? 16 : tc);
+}
+
+__host__ __device__ inline size_t dn_grouped_lds(int nbI, int I) {
+    const int tc = dn_chunk(nbI, I);
+    return (size_t)tc * ((size_t)32 * (round4(nbI) + 4) * 4 + (size_t)I + 8 * (size_t)round4(nbI)) + 4 * 16;
+}
+
+template <int UNR>
+__global__ __launch_bounds__(RO_THREADS) void k_down_grouped(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                             const int32_t *__restrict__ work,
+                                                             const int32_t *__restrict__ work_n,
+                                                             const int32_t *__restrict__ entries,
+                                                             const int8_t *__restrict__ hq,
+                                                             const float *__restrict__ hd,
+                                                             const int *__restrict__ hs, float *__restrict__ D) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wi = blockIdx.y, g = blockIdx.x, tid = threadIdx.x;
+    if (wi >= work_n[1]) return;
+    const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
+    const int nb = s.nbI, nbp = round4(nb), ust = nbp + 4, I = s.I, tc = dn_chunk(nb, I);
+    float *U = reinterpret_cast<float *>(smem);                          // [tc][32][ust]
+    int8_t *lq = reinterpret_cast<int8_t *>(U + (size_t)tc * 32 * ust);  // [tc][I]
+    float *ld = reinterpret_cast<float *>(lq + (size_t)tc * I);          // [tc][nbp]
+    int *ls = reinterpret_cast<int *>(ld + (size_t)tc * nbp);            // [tc][nbp]
+    int *ent = reinterpret_cast<int *>(ls + (size_t)tc * nbp);           // [16]
+
+    const uint8_t *tb = layer_pl + (size_t)e * s.EB + 2 * s.GB;
+    const size_t ntb = (size_t)s.H * nb;
+    const int items = 32 * nb;
+    uint4 wv[UNR];
+    uint16_t dv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const int p = u * RO_THREADS + tid;
+        wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        dv[u] = 0;
+        if (p < items) {
+            const size_t ob = (size_t)g * 32 * nb + p;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
+        }
+    }
+    for (int c0 = 0; c0 < c; c0 += tc) {
+        const int nt = c - c0 < tc ? c - c0 : tc;
+        if (tid < nt) ent[tid] = entries[o + c0 + tid];
+        __syncthreads();
+        for (int q = 0; q < nt; q++) {
+            const int i = ent[q];
+            const int *src = reinterpret_cast<const int *>(hq + (size_t)i * I);
+            int *dst = reinterpret_cast<int *>(lq + (size_t)q * I);
+            for (int a = tid; a < I / 4; a += RO_THREADS) dst[a] = src[a];
+            for (int b = tid; b < nb; b += RO_THREADS) {
+                ld[q * nbp + b] = hd[(size_t)i * nb + b];
+                ls[q * nbp + b] = hs[(size_t)i * nb + b];
+            }
+        }
+        __syncthreads();
+        for (int q = 0; q < nt; q++) {
+            const int8_t *hqq = lq + (size_t)q * I;
+            const int *lsq = ls + q * nbp;
+            float *Uq = U + (size_t)q * 32 * ust;
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int p = u * RO_THREADS + tid;
+                if (p < items) {
+                    const int row = (int)fdiv((uint32_t)p, s.divI), b = p - row * nb;
+                    const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hqq + b * QK)) - 8 * lsq[b];
+                    Uq[row * ust + b] = (float)S * h2f(dv[u]);
+                }
+            }
+        }
+        __syncthreads();
+        for (int r = tid; r < nt * 32; r += RO_THREADS) {
+            const int q = r >> 5;
+            D[(size_t)ent[q] * s.H + g * 32 + (r & 31)] = chain4(U + (size_t)r * ust, ld + q * nbp, nb);
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ D, const float *__restrict__ w, int H,
+                                                 int k, const float *resid, float *out) {
+    const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= H) return;
+    float acc = 0.0f;
+    for (int jj = k - 1; jj >= 0; jj--)
+        acc = __builtin_fmaf(w[(size_t)t * k + jj], D[((size_t)t * k + jj) * H + r], acc);
+    out[(size_t)t * H + r] = resid ? resid[(size_t)t * H + r] + acc : acc;
+}
+
 // ================================================================ launchers
 static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
@@ -476,7 +867,12 @@ bool decode_shape_ok(const Shape &s) {
 }
 
 hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
-    hipLaunchKernelGGL(k_route, dim3(E, T), dim3(RT_THREADS), 0, st, Wr, x, E, H, raw);
+    if (T >= 128 && (H / RG) % RT_CH == 0) {
+        hipLaunchKernelGGL(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
+                           T, E, H, raw);
+    } else {
+        hipLaunchKernelGGL(k_route, dim3(E, T), dim3(RT_THREADS), 0, st, Wr, x, E, H, raw);
+    }
     return hipGetLastError();
 }
 
@@ -528,6 +924,98 @@ hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, 
     if (per <= 6) return down_go<6>(layer_pl, s, h, idx, w, T, resid, out, st);
     if (per <= 12) return down_go<12>(layer_pl, s, h, idx, w, T, resid, out, st);
     return down_go<16>(layer_pl, s, h, idx, w, T, resid, out, st);
+}
+
+bool grouped_shape_ok(const Shape &s) {
+    return decode_shape_ok(s) && 64 * s.nbH <= 16 * 512 && 32 * s.nbI <= 16 * RO_THREADS &&
+           gu_grouped_lds(s.nbH) <= 160 * 1024 && dn_grouped_lds(s.nbI, s.I) <= 160 * 1024;
+}
+
+hipError_t launch_route_q8(const float *raw, const float *x, int T, int E, int H, int k, float eps, int32_t *idx,
+                           float *w, int8_t *xq, float *xd, int *xs, hipStream_t st) {
+    size_t lds = route_lds_bytes(H);
+    hipError_t e = allow_lds((const void *)k_route_q8, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, idx, w, xq, xd, xs);
+    return hipGetLastError();
+}
+
+int group_chunk_gateup(const Shape &s) { return gu_chunk(s.nbH); }
+int group_chunk_down(const Shape &s) { return dn_chunk(s.nbI, s.I); }
+
+int group_work_max(const Shape &s, int n, int ch) { return s.E + (n + ch - 1) / ch; }
+
+int group_work_max(const Shape &s, int n) {
+    const int ch = gu_chunk(s.nbH) < dn_chunk(s.nbI, s.I) ? gu_chunk(s.nbH) : dn_chunk(s.nbI, s.I);
+    return group_work_max(s, n, ch);
+}
+
+hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
+                        int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
+                       dn_chunk(s.nbI, s.I), group_work_max(s, n), counts, offsets, entries, work, work_n);
+    return hipGetLastError();
+}
+
+hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
+                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch, group_work_max(s, n, ch),
+                       counts, offsets, entries, work, work_n);
+    return hipGetLastError();
+}
+
+template <int NT, int UNR>
+static hipError_t gug_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                         const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                         const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
+    size_t lds = gu_grouped_lds(s.nbH);
+    hipError_t e = allow_lds((const void *)k_gateup_grouped<NT, UNR>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_gateup_grouped<NT, UNR>), dim3(s.nbI, wmax), dim3(NT), lds, st, layer_pl, s, work,
+                       work_n, entries, xq, xd, xs, hq, hd, hs);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup_grouped(const uint8_t *layer_pl, const Shape &s, int n, const int32_t *work,
+                                 const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                                 const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
+    if (!grouped_shape_ok(s)) return hipErrorInvalidValue;
+    const int wmax = group_work_max(s, n);
+    const int per = (int)cdiv((size_t)64 * s.nbH, 256);
+    if (per <= 4) return gug_go<256, 4>(layer_pl, s, wmax, work, work_n, entries, xq, xd, xs, hq, hd, hs, st);
+    if (per <= 8) return gug_go<256, 8>(layer_pl, s, wmax, work, work_n, entries, xq, xd, xs, hq, hd, hs, st);
+    if (per <= 16) return gug_go<256, 16>(layer_pl, s, wmax, work, work_n, entries, xq, xd, xs, hq, hd, hs, st);
+    return gug_go<512, 16>(layer_pl, s, wmax, work, work_n, entries, xq, xd, xs, hq, hd, hs, st);
+}
+
+template <int UNR>
+static hipError_t dng_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                         const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
+                         const int *hs, float *D, hipStream_t st) {
+    size_t lds = dn_grouped_lds(s.nbI, s.I);
+    hipError_t e = allow_lds((const void *)k_down_grouped<UNR>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_down_grouped<UNR>, dim3(s.H / 32, wmax), dim3(RO_THREADS), lds, st, layer_pl, s,
+                       work + 3 * (size_t)wmax, work_n, entries, hq, hd, hs, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_grouped(const uint8_t *layer_pl, const Shape &s, int n, const int32_t *work,
+                               const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
+                               const int *hs, float *D, hipStream_t st) {
+    if (!grouped_shape_ok(s)) return hipErrorInvalidValue;
+    const int wmax = group_work_max(s, n);
+    const int per = (int)cdiv((size_t)32 * s.nbI, RO_THREADS);
+    if (per <= 2) return dng_go<2>(layer_pl, s, wmax, work, work_n, entries, hq, hd, hs, D, st);
+    if (per <= 4) return dng_go<4>(layer_pl, s, wmax, work, work_n, entries, hq, hd, hs, D, st);
+    if (per <= 8) return dng_go<8>(layer_pl, s, wmax, work, work_n, entries, hq, hd, hs, D, st);
+    return dng_go<16>(layer_pl, s, wmax, work, work_n, entries, hq, hd, hs, D, st);
+}
+
+hipError_t launch_combine(const float *D, const float *w, int T, int H, int k, const float *resid, float *out,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_combine, dim3(cdiv((size_t)H, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
+    return hipGetLastError();
 }
 
 }  // namespace tg
