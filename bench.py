@@ -159,7 +159,7 @@ def run_decode_stack(args, torch, call):
     arena = HBMExpertArena(L, E, H, I, K_TOP)
     for l in range(L):
         arena.synth_layer(l, args.seed)
-    arena.set_decode_path({"auto": 0, "persistent": 1, "per-layer": 2}[args.path])
+    arena.set_decode_path({"auto": 0, "persistent": 1, "per-layer": 2, "fused": 3}[args.path])
     stream = torch.cuda.current_stream().cuda_stream
     X = torch.empty((W + K, H), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
@@ -197,14 +197,22 @@ def run_decode_stack(args, torch, call):
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     arena.status()
-    kern = kernel_times(call, ("persist", "route", "gateup", "down"))
+    kern = kernel_times(call, ("persist", "route", "experts", "gateup", "down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     if "persist" in kern:
         # one launch = one token through all L layers
         n_p, ms_p = kern["persist"]
         avg = ms_p / n_p * 1e-3
         roof_kernel, roof_bytes = "k_persist", L * K_TOP * EXPERT_Q4_BYTES
+        path = "persistent"
+    elif "experts" in kern:
+        # one launch = gate/up and down of the token's k experts in one layer
+        n_x, ms_x = kern["experts"]
+        avg = ms_x / max(n_x, 1) * 1e-3
+        roof_kernel, roof_bytes = "k_experts", K_TOP * EXPERT_Q4_BYTES
+        path = "fused"
     else:
+        path = "per-layer"
         n_gu, ms_gu = kern["gateup"]
         avg = ms_gu / max(n_gu, 1) * 1e-3
         roof_kernel, roof_bytes = "k_gateup", K_TOP * GATEUP_BYTES_PER_EXPERT
@@ -240,7 +248,7 @@ def run_decode_stack(args, torch, call):
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "event_ms_per_step": round(ev0.elapsed_time(ev1) / K, 4),
         "kernel_avg_us": kern_us,
-        "decode_path": "persistent" if "persist" in kern else "per-layer",
+        "decode_path": path,
         "roofline": {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
@@ -503,7 +511,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", choices=["auto", "persistent", "per-layer"], default="auto",
+    ap.add_argument("--path", choices=["auto", "persistent", "per-layer", "fused"], default="auto",
                     help="decode path of one-token stack calls")
     args = ap.parse_args()
 

@@ -191,13 +191,16 @@ int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
 int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
                                int n_layers, float eps, int32_t *topk_idx,
                                float *topk_w, void *stream);
-/* Decode path of one-token stack calls: PERSISTENT (one cooperative launch
- * over every layer; error when the shape / device does not allow it),
- * PER_LAYER (three kernels per layer, replayed as a HIP graph), AUTO (the
- * faster of the two; currently PER_LAYER). */
+/* Decode path of one-token calls: FUSED (per layer a routing kernel and
+ * one launch for gate/up and down, stack calls replayed as a HIP graph),
+ * PER_LAYER (routing, gate/up and down as three kernels per layer),
+ * PERSISTENT (one cooperative launch over every layer of a stack call;
+ * error when the shape / device does not allow it), AUTO (FUSED where the
+ * shape allows it, else PER_LAYER). */
 #define TG_DECODE_AUTO 0
 #define TG_DECODE_PERSISTENT 1
 #define TG_DECODE_PER_LAYER 2
+#define TG_DECODE_FUSED 3
 int tg_arena_set_decode_path(tg_arena *a, int path);
 /* Path of calls over n_tokens > 1 tokens (batched decode, prefill):
  * GROUPED (the (token, slot) pairs grouped by expert, each selected

@@ -66,12 +66,14 @@ class HBMExpertArena:
             pass
 
     # ------------------------------------------------------------ decode path
-    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER = 0, 1, 2
+    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER, DECODE_FUSED = 0, 1, 2, 3
 
     def set_decode_path(self, path: int) -> None:
-        """AUTO: one-token stack calls run as one persistent launch when the
-        shape allows; PERSISTENT: always (error otherwise); PER_LAYER: three
-        kernels per layer replayed as a HIP graph."""
+        """One-token calls.  FUSED: per layer a routing kernel and one
+        launch for gate/up and down; PER_LAYER: routing, gate/up and down
+        as three kernels; PERSISTENT: one cooperative launch over every
+        layer of a stack call (error where the shape / device does not
+        allow it); AUTO: FUSED where the shape allows, else PER_LAYER."""
         call("tg_arena_set_decode_path", self.handle, int(path))
 
     BATCH_AUTO, BATCH_GROUPED, BATCH_PER_TOKEN, BATCH_GROUPED_DOT = 0, 1, 2, 3

@@ -172,7 +172,13 @@ struct tg_arena {
     // per-call scratch, grown on demand
     int cap_T = 0;
     float *raw = nullptr;         // T * E raw router dots
-    float *h = nullptr;           // T * k * I
+    // decode exchange words: tagged logits [T][E] u64 | tagged h blocks of
+    // the fused expert launch | counter, generation [T][2] u32 | error word
+    uint8_t *dec = nullptr;
+    uint64_t *dec_lw = nullptr;
+    uint64_t *dec_hw = nullptr;
+    uint32_t *dec_ctl = nullptr;
+    uint32_t *dec_err = nullptr;
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
     float *xbuf = nullptr;        // T * H (host-pointer entry points)
@@ -246,7 +252,7 @@ static void arena_free(tg_arena *a) {
     dfree(a->routers);
     dfree(a->staging);
     dfree(a->raw);
-    dfree(a->h);
+    dfree(a->dec);
     dfree(a->idx);
     dfree(a->w);
     dfree(a->xbuf);
@@ -361,20 +367,33 @@ extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float
     return TG_OK;
 }
 
+static size_t dec_bytes(const Shape &s, int T) {
+    return 8 * ((size_t)T * s.E + tg::experts_fused_words(s)) + 8 * (size_t)T + 16;
+}
+
 static int arena_scratch(tg_arena *a, int T) {
     if (T <= a->cap_T) return TG_OK;
     drop_graphs(a);  // captured graphs point at the old buffers
-    dfree(a->raw); dfree(a->h); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf); dfree(a->grp);
-    a->raw = nullptr; a->h = nullptr; a->idx = nullptr; a->w = nullptr;
+    dfree(a->raw); dfree(a->dec); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf); dfree(a->grp);
+    a->raw = nullptr; a->dec = nullptr; a->idx = nullptr; a->w = nullptr;
+    a->dec_lw = nullptr; a->dec_hw = nullptr; a->dec_ctl = nullptr; a->dec_err = nullptr;
     a->xbuf = nullptr; a->obuf = nullptr; a->grp = nullptr;
     a->cap_T = 0;
     const Shape &s = a->s;
     bool ok = hipMalloc(&a->raw, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
-              hipMalloc(&a->h, sizeof(float) * (size_t)T * s.k * s.I) == hipSuccess &&
+              hipMalloc(&a->dec, dec_bytes(s, T)) == hipSuccess &&
               hipMalloc(&a->idx, sizeof(int32_t) * (size_t)T * s.k) == hipSuccess &&
               hipMalloc(&a->w, sizeof(float) * (size_t)T * s.k) == hipSuccess &&
               hipMalloc(&a->xbuf, sizeof(float) * (size_t)T * s.H) == hipSuccess &&
               hipMalloc(&a->obuf, sizeof(float) * (size_t)T * s.H) == hipSuccess;
+    if (ok) {
+        // counters, generations and tags start at zero (tag 0 never matches)
+        ok = hipMemset(a->dec, 0, dec_bytes(s, T)) == hipSuccess;
+        a->dec_lw = reinterpret_cast<uint64_t *>(a->dec);
+        a->dec_hw = a->dec_lw + (size_t)T * s.E;
+        a->dec_ctl = reinterpret_cast<uint32_t *>(a->dec_hw + tg::experts_fused_words(s));
+        a->dec_err = a->dec_ctl + 2 * (size_t)T;
+    }
     if (ok) {
         // grouped path: every piece 256-byte aligned
         const size_t n = (size_t)T * s.k;
@@ -468,14 +487,28 @@ static int layer_kernels_grouped(tg_arena *a, int layer, const float *x, float *
     return TG_OK;
 }
 
+// One token, gate/up and down in one launch (the default one-token path).
+static bool fused_usable(tg_arena *a, int T) {
+    return T == 1 && (a->decode_path == TG_DECODE_AUTO || a->decode_path == TG_DECODE_FUSED) &&
+           tg::experts_fused_ok(a->s, a->n_cu);
+}
+
 static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T, float eps,
                          hipStream_t st) {
     if (grouped_usable(a, T)) return layer_kernels_grouped(a, layer, x, out, resid, T, eps, st);
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
-    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
-    PROFILED("gateup", st, tg::launch_gateup(lp, s, x, a->raw, T, eps, a->h, a->idx, a->w, st));
-    PROFILED("down", st, tg::launch_down(lp, s, a->h, a->idx, a->w, T, resid, out, st));
+    PROFILED("route", st,
+             tg::launch_route_dec(router_of(a, layer), x, T, s, eps, a->dec_lw, a->dec_ctl, a->dec_err, a->idx, a->w,
+                                  a->xq, a->xd, a->xs, st));
+    if (fused_usable(a, T)) {
+        PROFILED("experts", st,
+                 tg::launch_experts_fused(lp, s, a->n_cu, a->idx, a->w, a->xq, a->xd, a->xs, a->dec_hw, a->dec_ctl,
+                                          a->dec_err, resid, out, st));
+        return TG_OK;
+    }
+    PROFILED("gateup", st, tg::launch_gateup(lp, s, T, a->idx, a->xq, a->xd, a->xs, a->hq, a->hd, a->hs, st));
+    PROFILED("down", st, tg::launch_down(lp, s, T, a->idx, a->w, a->hq, a->hd, a->hs, resid, out, st));
     return TG_OK;
 }
 
@@ -663,10 +696,13 @@ extern "C" int tg_arena_set_batch_path(tg_arena *a, int path) {
 
 extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
-    if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER)
+    if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER &&
+        path != TG_DECODE_FUSED)
         return set_err(TG_E_INVALID, "unknown decode path %d", path);
     if (path == TG_DECODE_PERSISTENT && !(a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s)))
         return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
+    if (path == TG_DECODE_FUSED && !tg::experts_fused_ok(a->s, a->n_cu))
+        return set_err(TG_E_UNSUPPORTED, "the fused expert launch is not available for this shape");
     drop_graphs(a);
     a->decode_path = path;
     return TG_OK;
@@ -703,6 +739,11 @@ extern "C" int tg_arena_status(tg_arena *a) {
         uint32_t w[4] = {0, 0, 0, 0};
         HIP_TRY(hipMemcpy(w, a->ps_sync, sizeof w, hipMemcpyDeviceToHost));
         if (w[1] != 0u) return set_err(TG_E_HIP, "persistent decode: a device-side poll ran out of tries");
+    }
+    if (a->dec_err) {
+        uint32_t v = 0;
+        HIP_TRY(hipMemcpy(&v, a->dec_err, sizeof v, hipMemcpyDeviceToHost));
+        if (v != 0u) return set_err(TG_E_HIP, "decode routing: a device-side poll ran out of tries");
     }
     return TG_OK;
 }

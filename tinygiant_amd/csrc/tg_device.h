@@ -148,6 +148,17 @@ TG_DEV float block_sumsq(const float *__restrict__ x, int n, float *red) {
     return tot;
 }
 
+// Tagged words: a 32-bit payload and a 32-bit tag in one 64-bit word,
+// stored and loaded with relaxed agent-scope atomics, so a reader that sees
+// the tag it expects also sees the payload stored with it.
+TG_DEV void ll_put(uint64_t *p, uint32_t v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+TG_DEV uint64_t ll_get(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 TG_DEV float rms_scale(float ss, int n, float eps) {
     return 1.0f / __builtin_sqrtf(ss / (float)n + eps);
 }

@@ -80,10 +80,28 @@ hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, in
                        int32_t *idx, float *w, hipStream_t st);
 // decode MoE layer pieces
 bool decode_shape_ok(const Shape &s);
-hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T, float eps,
-                         float *h, int32_t *idx, float *w, hipStream_t st);
-hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
-                       int T, const float *resid, float *out, hipStream_t st);
+// routing of T tokens in one launch: lw [T][E] tagged logits, ctl [T][2]
+// arrival counter and generation (zero before first use), err set to
+// nonzero when a poll ran out of tries; writes idx, w [T][k] and the Q8_0
+// activations xq [T][H], xd / xs [T][H/32]
+hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape &s, float eps, uint64_t *lw,
+                            uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
+                            hipStream_t st);
+// gate/up + SwiGLU -> Q8_0 h [T][k][I] (hd / hs [T][k][I/32])
+hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const int8_t *xq,
+                         const float *xd, const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);
+// one token: gate/up and down in one launch (h handed over as hw tagged
+// words, experts_fused_words of them, zero before first use; tags from the
+// routing generation ctl[1])
+bool experts_fused_ok(const Shape &s, int n_cu);
+size_t experts_fused_words(const Shape &s);
+hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_cu, const int32_t *idx, const float *w,
+                                const int8_t *xq, const float *xd, const int *xs, uint64_t *hw, const uint32_t *ctl,
+                                uint32_t *err, const float *resid, float *out, hipStream_t st);
+// down + combine (+ resid) -> out [T][H]
+hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const float *w,
+                       const int8_t *hq, const float *hd, const int *hs, const float *resid, float *out,
+                       hipStream_t st);
 
 hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *sink, hipStream_t st);
 

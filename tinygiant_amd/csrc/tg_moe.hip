@@ -4,15 +4,21 @@
 // Per layer three kernels, separated by kernel boundaries (replayed as a HIP
 // graph, where a boundary costs little):
 //
-//   k_route   grid (E, T)       raw router dot of one expert for one token
-//   k_gateup  grid (I/RT, k, T) norm scale, logits, top-k, then RT rows of
-//                               gate and up of one selected expert and
-//                               h = SiLU(gate) * up
-//   k_down    grid (H/RD, T)    RD rows of down for all k experts, combine,
-//                               residual
+//   k_route_dec grid (E, T)        raw router dot of one expert for one token
+//                                  and the token's RMS scale; the token's
+//                                  last block ranks the logits (top-k,
+//                                  softmax) and writes Q8_0(x * s)
+//   k_gateup    grid (I/32, k, T)  32 rows of gate and up of one selected
+//                                  expert, h = SiLU(gate) * up, Q8_0 block
+//                                  of h
+//   k_down      grid (H/RD, T)     RD rows of down for all k experts,
+//                                  combine, residual
 //
-// One CU streams only a few tens of GB/s from HBM, so every weight-streaming
-// kernel spreads its bytes over at least one block per CU (256 CUs).
+// Routing, the activation Q8_0 and the h Q8_0 happen once per token, so the
+// weight-streaming kernels start their loads after one dependent read of
+// the expert ids.  One CU streams only a few tens of GB/s from HBM, so every
+// weight-streaming kernel spreads its bytes over at least one block per CU
+// (256 CUs).
 //
 // Numerics: see tg_kernels.hip (row dots) and the routing definition below;
 // every result is bit-identical to the host definition.
@@ -331,105 +337,259 @@ TG_DEV float chain4(const float *U, const float *dx, int nb) {
 
 __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 
+// ============================================================ decode routing
+// Block (e, t): the raw router dot of expert e for token t (grouped sums as
+// k_route) and, from the same x, the token's RMS scale s (grouped sums of
+// squares as route_token), so logit = raw * s as in route_token.  Thread 0
+// publishes the logit as a tagged word (see tg_persist.hip) and counts the
+// block in the token's arrival counter; both are relaxed agent-scope
+// atomics.  The block that arrives last reads the E logits (bounded polls
+// on the tags), ranks them, forms the softmax weights and Q8_0(x * s), and
+// writes idx / w / xq / xd / xs for the expert kernels.
+//
+// ctl[2t] is the token's arrival counter, ctl[2t+1] the generation of its
+// last routing.  A launch publishes with the next generation, so words left
+// by earlier launches never match; its last block resets the counter and
+// stores the new generation, which the next launch reads (after the kernel
+// boundary).  A poll that runs out of tries sets *err and routes the token
+// to experts 0..k-1 with weight 0, so the expert kernels stay in bounds.
+constexpr uint32_t RD_SPIN_LIMIT = 1u << 20;
+
+TG_DEV uint32_t next_gen(uint32_t g) { return g >= 0x7FFFFFFFu ? 1u : g + 1u; }
+
+__global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restrict__ Wr, const float *__restrict__ x,
+                                                          int E, int H, int k, float eps, uint64_t *__restrict__ lw,
+                                                          uint32_t *__restrict__ ctl, uint32_t *__restrict__ err,
+                                                          int32_t *__restrict__ idx, float *__restrict__ w,
+                                                          int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                          int *__restrict__ xs) {
+    __shared__ __align__(16) float gp[RO_THREADS];
+    __shared__ __align__(16) float gq[RO_THREADS];
+    __shared__ __align__(16) uint64_t keys[MAX_E];
+    __shared__ float slog[MAX_E];
+    __shared__ float sw[MAX_K], sex[MAX_K];
+    __shared__ int sidx[MAX_K];
+    __shared__ float ssc;
+    __shared__ int last, bad;
+    const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, G = H / RG, nbH = H / QK;
+    const float *xt = x + (size_t)t * H;
+    const uint32_t tag = next_gen(__hip_atomic_load(ctl + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float aw = 0.0f, aq = 0.0f;
+    if (tid < G) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + tid * RG);
+        const float4 *x4 = reinterpret_cast<const float4 *>(xt + tid * RG);
+        float4 wv[RG / 4], xv[RG / 4];
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            wv[q] = w4[q];
+            xv[q] = x4[q];
+        }
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            aq = __builtin_fmaf(xv[q].x, xv[q].x, aq);
+            aq = __builtin_fmaf(xv[q].y, xv[q].y, aq);
+            aq = __builtin_fmaf(xv[q].z, xv[q].z, aq);
+            aq = __builtin_fmaf(xv[q].w, xv[q].w, aq);
+        }
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            aw = __builtin_fmaf(wv[q].x, xv[q].x, aw);
+            aw = __builtin_fmaf(wv[q].y, xv[q].y, aw);
+            aw = __builtin_fmaf(wv[q].z, xv[q].z, aw);
+            aw = __builtin_fmaf(wv[q].w, xv[q].w, aw);
+        }
+    }
+    gp[tid] = aw;
+    gq[tid] = aq;
+    if (tid == 0) bad = 0;
+    __syncthreads();
+    if (tid == 0) {
+        // both totals in ascending group order (G is a multiple of 8)
+        const float4 *p4 = reinterpret_cast<const float4 *>(gp);
+        const float4 *q4 = reinterpret_cast<const float4 *>(gq);
+        float tr = 0.0f, ts = 0.0f;
+#pragma unroll 4
+        for (int g = 0; g < G / 4; g++) {
+            const float4 a = p4[g], b = q4[g];
+            tr = tr + a.x; tr = tr + a.y; tr = tr + a.z; tr = tr + a.w;
+            ts = ts + b.x; ts = ts + b.y; ts = ts + b.z; ts = ts + b.w;
+        }
+        const float sc = rms_scale(ts, H, eps);
+        ll_put(lw + (size_t)t * E + e, __float_as_uint(tr * sc), tag);
+        const uint32_t old = __hip_atomic_fetch_add(ctl + 2 * t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ssc = sc;
+        last = old == (uint32_t)(E - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!last) return;
+
+    // ---- last block of token t
+    const float sc = ssc;
+#pragma unroll
+    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+        if (ps * RO_THREADS * 8 < H) {
+            const int i0 = ps * RO_THREADS * 8 + tid * 8;
+            float v[8];
+            if (i0 < H) {
+                const float4 a4 = *reinterpret_cast<const float4 *>(xt + i0);
+                const float4 b4 = *reinterpret_cast<const float4 *>(xt + i0 + 4);
+                v[0] = a4.x * sc; v[1] = a4.y * sc; v[2] = a4.z * sc; v[3] = a4.w * sc;
+                v[4] = b4.x * sc; v[5] = b4.y * sc; v[6] = b4.z * sc; v[7] = b4.w * sc;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; c++) v[c] = 0.0f;
+            }
+            q8_group8(v, i0 < H, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
+        }
+    }
+    if (tid < k) sidx[tid] = 0;
+    if (tid < E) {
+        const uint64_t *src = lw + (size_t)t * E + tid;
+        uint64_t v = ll_get(src);
+        uint32_t tries = 0;
+        while ((uint32_t)(v >> 32) != tag) {
+            if (++tries >= RD_SPIN_LIMIT) {
+                bad = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            v = ll_get(src);
+        }
+        const float l = __uint_as_float((uint32_t)v);
+        slog[tid] = l;
+        keys[tid] = rank_key(l, tid);
+    }
+    __syncthreads();
+    // rank = number of larger keys; two threads per expert when E <= 128
+    const int tpe = 2 * E <= RO_THREADS ? 2 : 1;
+    const int ee = tpe == 2 ? tid >> 1 : tid;
+    if (ee < E) {
+        const uint64_t my = keys[ee];
+        const int half = tpe == 2 ? (tid & 1) : 0;
+        const int n = E / tpe, b0 = half * n;
+        int cnt = 0;
+#pragma unroll 8
+        for (int i = 0; i < n; i += 2) {
+            const ulonglong2 o = *reinterpret_cast<const ulonglong2 *>(keys + b0 + i);
+            cnt += o.x > my ? 1 : 0;
+            cnt += o.y > my ? 1 : 0;
+        }
+        if (tpe == 2) cnt += __shfl_xor(cnt, 1, WAVE);
+        if (half == 0 && cnt < k) sidx[cnt] = ee;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (bad) {
+            __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < k; i++) {
+                idx[(size_t)t * k + i] = i;
+                w[(size_t)t * k + i] = 0.0f;
+            }
+        } else {
+            topk_softmax(slog, sidx, k, sw, sex);
+            for (int i = 0; i < k; i++) {
+                idx[(size_t)t * k + i] = sidx[i];
+                w[(size_t)t * k + i] = sw[i];
+            }
+        }
+        __hip_atomic_store(ctl + 2 * t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ctl + 2 * t + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ============================================================ gate / up
-// Block (rt, j, t): the token's routing (every block derives it identically),
-// then rows [rt*RT, rt*RT+RT) of gate and up of the j-th selected expert,
-// h = SiLU(gate) * up.  The nibble loads are issued as soon as the expert is
-// known; Q8_0(x * s) is formed while they are in flight.
-constexpr int GU_RT = 8;
+// Block (m, j, t): rows [32m, 32m+32) of gate and of up of token t's j-th
+// selected expert against Q8_0(x_t * s_t), h = SiLU(gate) * up, and the
+// Q8_0 block m of h.  The nibble loads are issued right after the expert id
+// is read; thread p of the block owns the row-block items p + u * 1024.
+constexpr int GU_THREADS = 1024;
+constexpr int GU_ROWS = 32;  // one Q8_0 block of h
 
 __host__ __device__ inline size_t gateup_lds_bytes(int H, int nbH) {
-    // route | xq[H] | xd[r4] | xs[r4] | U[2RT * (r4 + 4)] | accs[2RT]
-    return route_lds_bytes(H) + (size_t)H + 8 * (size_t)round4(nbH) + 4 * (size_t)2 * GU_RT * (round4(nbH) + 4) +
-           4 * 2 * GU_RT;
+    // xq[H] | xd[r4] | xs[r4] | U[2 * 32 * (r4 + 4)] | accs[64]
+    return (size_t)H + 8 * (size_t)round4(nbH) + 4 * (size_t)2 * GU_ROWS * (round4(nbH) + 4) + 4 * 2 * GU_ROWS;
 }
 
 template <int UNR>
-__global__ __launch_bounds__(RO_THREADS) void k_gateup(const uint8_t *__restrict__ layer_pl, Shape s,
-                                                       const float *__restrict__ x, const float *__restrict__ raw,
-                                                       float eps, float *__restrict__ h,
-                                                       int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+__global__ __launch_bounds__(GU_THREADS) void k_gateup(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                       const int32_t *__restrict__ idx,
+                                                       const int8_t *__restrict__ xq_g,
+                                                       const float *__restrict__ xd_g, const int *__restrict__ xs_g,
+                                                       int8_t *__restrict__ hq, float *__restrict__ hd,
+                                                       int *__restrict__ hs) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RT = GU_RT;
+    constexpr int RT = GU_ROWS;
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, I = s.I, tid = threadIdx.x;
-    RouteLds L = route_lds(smem, H);
-    int8_t *xq = reinterpret_cast<int8_t *>(smem + route_lds_bytes(H));
+    int8_t *xq = reinterpret_cast<int8_t *>(smem);
     float *xd = reinterpret_cast<float *>(xq + H);
     int *xs = reinterpret_cast<int *>(xd + round4(nb));
     float *U = reinterpret_cast<float *>(xs + round4(nb));
     float *accs = U + 2 * RT * ust;
-
-    const int t = blockIdx.z, j = blockIdx.y, r0 = blockIdx.x * RT;
-    float xv[RO_MAXPASS][8];
-    route_token(x + (size_t)t * H, raw + (size_t)t * s.E, s.E, H, s.k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx,
-                L.sred);
-
-    // nibble groups and scales of this block's 2*RT row-dots
-    const uint8_t *ex = layer_pl + (size_t)L.sidx[j] * s.EB;
+    const int m = blockIdx.x, j = blockIdx.y, t = blockIdx.z, r0 = m * RT;
+    const size_t slot = (size_t)t * s.k + j;
+    int e = idx[slot];
+    e = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);  // never address outside the layer
+    const uint8_t *ex = layer_pl + (size_t)e * s.EB;
     const size_t ntb = (size_t)I * nb;
     const int items = 2 * RT * nb;
     uint4 wv[UNR];
     uint16_t dv[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        int p = u * RO_THREADS + tid;
+        const int p = u * GU_THREADS + tid;
         wv[u] = make_uint4(0u, 0u, 0u, 0u);
         dv[u] = 0;
         if (p < items) {
-            int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
-            int mat = rd >= RT ? 1 : 0;
-            int row = r0 + rd - mat * RT;
-            if (row < I) {
-                const uint8_t *tb = ex + (size_t)mat * s.GB;
-                size_t o = (size_t)row * nb + b;
-                wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-                dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-            }
+            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            const int mat = rd >= RT ? 1 : 0;
+            const uint8_t *tb = ex + (size_t)mat * s.GB;
+            const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
         }
     }
-    // Q8_0(x * s) while the loads are in flight
-    const float sc = L.sred[0];
-#pragma unroll
-    for (int ps = 0; ps < RO_MAXPASS; ps++) {
-        int i0 = ps * RO_THREADS * 8 + tid * 8;
-        if (ps * RO_THREADS * 8 < H) {
-            float v[8];
-#pragma unroll
-            for (int c = 0; c < 8; c++) v[c] = xv[ps][c] * sc;
-            q8_group8(v, i0 < H, i0, xq, xd, xs);
-        }
-    }
-    if (blockIdx.x == 0 && j == 0 && tid == 0) {
-        topk_softmax(L.slog, L.sidx, s.k, L.sw, L.sex);
-        for (int i = 0; i < s.k; i++) {
-            if (idx_out) idx_out[(size_t)t * s.k + i] = L.sidx[i];
-            if (w_out) w_out[(size_t)t * s.k + i] = L.sw[i];
-        }
+    if (tid < H / 8) reinterpret_cast<uint2 *>(xq)[tid] = reinterpret_cast<const uint2 *>(xq_g + (size_t)t * H)[tid];
+    if (tid < nb) {
+        xd[tid] = xd_g[(size_t)t * nb + tid];
+        xs[tid] = xs_g[(size_t)t * nb + tid];
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        int p = u * RO_THREADS + tid;
+        const int p = u * GU_THREADS + tid;
         if (p < items) {
-            int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
-            int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(xq + b * QK)) - 8 * xs[b];
+            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(xq + b * QK)) - 8 * xs[b];
             U[rd * ust + b] = (float)S * h2f(dv[u]);
         }
     }
     __syncthreads();
     if (tid < 2 * RT) accs[tid] = chain4(U + tid * ust, xd, nb);
     __syncthreads();
-    if (tid < RT && r0 + tid < I) h[((size_t)t * s.k + j) * I + r0 + tid] = silu_mul(accs[tid], accs[RT + tid]);
+    if (tid < 64) {  // wave 0; both halves compute, the first writes
+        const int i = tid & 31;
+        const float hv = silu_mul(accs[i], accs[RT + i]);
+        float dq;
+        int qsum;
+        uint16_t dh;
+        const int q = q8_lane(hv, dq, qsum, dh);
+        if (tid < 32) {
+            hq[slot * I + r0 + i] = (int8_t)q;
+            if (i == 0) {
+                hd[slot * s.nbI + m] = dq;
+                hs[slot * s.nbI + m] = qsum;
+            }
+        }
+    }
 }
 
 // ============================================================ down
-// Block (g, t): rows [g*RD, g*RD+RD) of down for the k experts of token t,
-// combined: out = sum_j w_j down_j in ascending logit order (j = k-1 .. 0)
-// plus resid when given.  The nibble loads are issued before the block
-// quantizes h, so their latency overlaps the quantization.
+// Block (g, t): rows [g*RD, g*RD+RD) of down for the k experts of token t
+// against their Q8_0 h, combined: out = sum_j w_j down_j in ascending logit
+// order (j = k-1 .. 0) plus resid when given.  The nibble loads are issued
+// before h is staged in LDS.
 constexpr int DN_RD = 8;
 constexpr int DN_THREADS = 256;
-constexpr int DN_MAXPASS = 8;  // k * I <= 8 * 8 * 256
 
 __host__ __device__ inline size_t down_lds_bytes(int k, int I, int nbI) {
     // hq[k*I] | hd[k*r4] | hs[k*r4] | U[k*RD*(r4+4)] | D[k*RD] | sw[MAX_K] | sidx[MAX_K]
@@ -439,8 +599,9 @@ __host__ __device__ inline size_t down_lds_bytes(int k, int I, int nbI) {
 
 template <int UNR>
 __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__ layer_pl, Shape s,
-                                                     const float *__restrict__ h, const int32_t *__restrict__ idx,
-                                                     const float *__restrict__ w, const float *resid, float *out) {
+                                                     const int32_t *__restrict__ idx, const float *__restrict__ w,
+                                                     const int8_t *__restrict__ hq_g, const float *__restrict__ hd_g,
+                                                     const int *__restrict__ hs_g, const float *resid, float *out) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int RD = DN_RD;
     const int k = s.k, nb = s.nbI, nbp = round4(nb), I = s.I, H = s.H, ust = round4(nb) + 4;
@@ -455,29 +616,12 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
 
     const int t = blockIdx.y, r0 = blockIdx.x * RD;
     if (tid < k) {
-        int e = idx[(size_t)t * k + tid];
+        const int e = idx[(size_t)t * k + tid];
         sidx[tid] = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);  // never address outside the layer
         sw[tid] = w[(size_t)t * k + tid];
     }
-    const float *ht = h + (size_t)t * k * I;
-    const int nh = k * I;
-    const int npass = (nh + DN_THREADS * 8 - 1) / (DN_THREADS * 8);
-    float hv[DN_MAXPASS][8];
-#pragma unroll
-    for (int ps = 0; ps < DN_MAXPASS; ps++) {
-        int i0 = ps * DN_THREADS * 8 + tid * 8;
-        if (ps < npass && i0 < nh) {
-            float4 a = *reinterpret_cast<const float4 *>(ht + i0);
-            float4 b = *reinterpret_cast<const float4 *>(ht + i0 + 4);
-            hv[ps][0] = a.x; hv[ps][1] = a.y; hv[ps][2] = a.z; hv[ps][3] = a.w;
-            hv[ps][4] = b.x; hv[ps][5] = b.y; hv[ps][6] = b.z; hv[ps][7] = b.w;
-        } else {
-#pragma unroll
-            for (int c = 0; c < 8; c++) hv[ps][c] = 0.0f;
-        }
-    }
     float rv = 0.0f;
-    if (resid && tid < RD && r0 + tid < H) rv = resid[(size_t)t * H + r0 + tid];
+    if (resid && tid < RD) rv = resid[(size_t)t * H + r0 + tid];
     __syncthreads();
 
     const size_t ntb = (size_t)H * nb;
@@ -486,51 +630,315 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
     uint16_t dv[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        int p = u * DN_THREADS + tid;
+        const int p = u * DN_THREADS + tid;
         wv[u] = make_uint4(0u, 0u, 0u, 0u);
         dv[u] = 0;
         if (p < items) {
-            int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            int jj = rd / RD, row = r0 + (rd - jj * RD);
-            if (row < H) {
-                const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
-                size_t o = (size_t)row * nb + b;
-                wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-                dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-            }
+            const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            const int jj = rd / RD, row = r0 + (rd - jj * RD);
+            const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
+            const size_t o = (size_t)row * nb + b;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
         }
     }
-    // Q8_0 of each expert's h while the nibble loads are in flight; expert jj's
-    // blocks go to hq + jj*I, hd/hs + jj*nbp
-#pragma unroll
-    for (int ps = 0; ps < DN_MAXPASS; ps++) {
-        if (ps < npass) {
-            int i0 = ps * DN_THREADS * 8 + tid * 8;
-            bool on = i0 < nh;
-            int jj = on ? i0 / I : 0, il = on ? i0 - jj * I : 0;
-            q8_group8(hv[ps], on, il, hq + (size_t)jj * I, hd + jj * nbp, hs + jj * nbp);
-        }
+    // the token's Q8_0 h: k * I bytes, k * nbI scales and sums
+    const size_t hbase = (size_t)t * k;
+    const uint4 *hq4 = reinterpret_cast<const uint4 *>(hq_g + hbase * I);
+    for (int i = tid; i < k * I / 16; i += DN_THREADS) reinterpret_cast<uint4 *>(hq)[i] = hq4[i];
+    for (int i = tid; i < k * nb; i += DN_THREADS) {
+        const int jj = i / nb, b = i - jj * nb;
+        hd[jj * nbp + b] = hd_g[hbase * nb + i];
+        hs[jj * nbp + b] = hs_g[hbase * nb + i];
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        int p = u * DN_THREADS + tid;
+        const int p = u * DN_THREADS + tid;
         if (p < items) {
-            int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            int jj = rd / RD;
-            int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
-                    8 * hs[jj * nbp + b];
+            const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            const int jj = rd / RD;
+            const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
+                          8 * hs[jj * nbp + b];
             U[rd * ust + b] = (float)S * h2f(dv[u]);
         }
     }
     __syncthreads();
     for (int rd = tid; rd < k * RD; rd += DN_THREADS) D[rd] = chain4(U + rd * ust, hd + (rd / RD) * nbp, nb);
     __syncthreads();
-    if (tid < RD && r0 + tid < H) {
+    if (tid < RD) {
         float acc = 0.0f;
         for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
         out[(size_t)t * H + r0 + tid] = resid ? rv + acc : acc;
     }
+}
+
+// ============================================================ fused experts (one token)
+// One launch per layer for gate/up and down of a single token, so the down
+// weights stream while gate/up runs instead of after it.  The grid has one
+// block of 1024 threads per down unit (H / RD units of RD output rows, at
+// most one block per CU, so every block is resident at once).  Block b:
+//   1. runs the gate/up units u = b, b + grid, ... (unit (m, j): rows
+//      [32m, 32m+32) of gate and up of the j-th expert, as k_gateup),
+//      issuing its down loads (RD rows of down for all k experts) once the
+//      first unit's weights have arrived, and publishes each Q8_0 block of h
+//      as FX_QW tagged words;
+//   2. polls the last word of every unit (thread u polls unit u; the words
+//      are stored word-major, hw[w * units + u], so a wave's polls touch a
+//      few cache lines), reads all words of every unit (plain loads, so the
+//      blocks of an XCD share its L2; a word with an old tag is polled
+//      again), and computes dots, chains, combine and residual for its RD
+//      rows.
+// Tags: the routing generation of the layer (ctl[1], stored by k_route_dec
+// of the same layer), so words of earlier layers never match.  A block finishes its own gate/up units
+// before it waits, so no wait depends on a block that is not running.
+// Polls are bounded; when one runs out the block sets *err and writes NaN
+// rows.
+constexpr int FX_THREADS = 1024;
+constexpr int FX_QW = 10;
+
+struct FxArgs {
+    const uint8_t *layer_pl;
+    const int32_t *idx;
+    const float *w;
+    const int8_t *xq;
+    const float *xd;
+    const int *xs;
+    uint64_t *hw;         // [FX_QW][k * I/32] tagged h blocks, word-major
+    const uint32_t *ctl;  // routing counter / generation of token 0
+    uint32_t *err;
+    const float *resid;
+    float *out;
+    int rd;               // down rows per block (grid = H / rd)
+};
+
+__host__ __device__ inline size_t fx_down_lds_bytes(int k, int I, int nbI, int rd) {
+    // hq[k*I] | hd[k*r4] | hs[k*r4] | U[k*rd*(r4+4)] | D[k*rd]
+    return (size_t)k * I + 8 * (size_t)k * round4(nbI) + 4 * (size_t)k * rd * (round4(nbI) + 4) +
+           4 * (size_t)k * rd;
+}
+
+__host__ __device__ inline size_t fx_lds_bytes(const Shape &s, int rd) {
+    const size_t a = gateup_lds_bytes(s.H, s.nbH), b = fx_down_lds_bytes(s.k, s.I, s.nbI, rd);
+    return a > b ? a : b;
+}
+
+// Gate/up unit (m, j) in three steps, so a block can issue its down loads
+// between the dots and the rest: the nibble and scale loads of rows
+// [32m, 32m+32) of gate and up of the j-th expert ...
+template <int UG>
+struct FxGu {
+    uint4 wv[UG];
+    uint16_t dv[UG];
+};
+
+template <int UG>
+TG_DEV void fx_gu_load(const FxArgs &A, const Shape &s, int unit, FxGu<UG> &g) {
+    constexpr int RT = GU_ROWS;
+    const int nb = s.nbH, I = s.I, tid = threadIdx.x;
+    const int mI = I / RT, m = unit % mI, j = unit / mI, r0 = m * RT;
+    int e = A.idx[j];
+    e = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);
+    const uint8_t *ex = A.layer_pl + (size_t)e * s.EB;
+    const size_t ntb = (size_t)I * nb;
+    const int items = 2 * RT * nb;
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        const int p = u * FX_THREADS + tid;
+        g.wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        g.dv[u] = 0;
+        if (p < items) {
+            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            const int mat = rd >= RT ? 1 : 0;
+            const uint8_t *tb = ex + (size_t)mat * s.GB;
+            const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
+            g.wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+            g.dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
+        }
+    }
+}
+
+// ... the block dots against Q8_0(x * s) into U (LDS) ...
+template <int UG>
+TG_DEV void fx_gu_dots(const FxArgs &A, const Shape &s, const FxGu<UG> &g, uint8_t *smem) {
+    constexpr int RT = GU_ROWS;
+    const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
+    int8_t *xq = reinterpret_cast<int8_t *>(smem);
+    float *xd = reinterpret_cast<float *>(xq + H);
+    int *xs = reinterpret_cast<int *>(xd + round4(nb));
+    float *U = reinterpret_cast<float *>(xs + round4(nb));
+    const int items = 2 * RT * nb;
+    if (tid < H / 8) reinterpret_cast<uint2 *>(xq)[tid] = reinterpret_cast<const uint2 *>(A.xq)[tid];
+    if (tid < nb) {
+        xd[tid] = A.xd[tid];
+        xs[tid] = A.xs[tid];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        const int p = u * FX_THREADS + tid;
+        if (p < items) {
+            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+            const int S = dot_q4_q8(g.wv[u], reinterpret_cast<const int *>(xq + b * QK)) - 8 * xs[b];
+            U[rd * ust + b] = (float)S * h2f(g.dv[u]);
+        }
+    }
+    __syncthreads();
+}
+
+// ... and the chains, SwiGLU and Q8_0 of the 32 h rows, published as FX_QW
+// tagged words.  Wave 0 alone does this part (lane r chains row r: gate
+// rows in lanes 0..31, up rows in 32..63) and needs no block barrier, so it
+// never waits for the down loads the block has in flight.
+TG_DEV void fx_gu_publish(const FxArgs &A, const Shape &s, int unit, uint32_t tag, const uint8_t *smem) {
+    constexpr int RT = GU_ROWS;
+    static_assert(2 * RT == 64, "one wave holds the gate and up rows of a unit");
+    const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
+    const float *xd = reinterpret_cast<const float *>(smem + H);
+    const float *U = xd + 2 * round4(nb);
+    if (tid < 64) {  // both halves compute the block, lanes 0..9 publish it
+        const float a = chain4(U + tid * ust, xd, nb);
+        const int i = tid & 31;
+        const float hv = silu_mul(__shfl(a, i, WAVE), __shfl(a, i + RT, WAVE));
+        float dq;
+        int qsum;
+        uint16_t dh;
+        const int q = q8_lane(hv, dq, qsum, dh);
+        const int l4 = 4 * (tid & 7);
+        const uint32_t word = (uint32_t)(__shfl(q, l4, WAVE) & 255) | ((uint32_t)(__shfl(q, l4 + 1, WAVE) & 255) << 8) |
+                              ((uint32_t)(__shfl(q, l4 + 2, WAVE) & 255) << 16) |
+                              ((uint32_t)(__shfl(q, l4 + 3, WAVE) & 255) << 24);
+        const size_t ng = (size_t)(s.I / GU_ROWS) * s.k;
+        uint64_t *dst = A.hw + unit;
+        if (tid < 8) ll_put(dst + tid * ng, word, tag);
+        if (tid == 8) ll_put(dst + 8 * ng, __float_as_uint(dq), tag);
+        if (tid == 9) ll_put(dst + 9 * ng, (uint32_t)qsum, tag);
+    }
+}
+
+// Bounded poll of one tagged word; false when it ran out of tries.
+TG_DEV bool fx_wait(const uint64_t *p, uint32_t tag, uint32_t &pay) {
+    uint64_t v = ll_get(p);
+    uint32_t tries = 0;
+    while ((uint32_t)(v >> 32) != tag) {
+        if (++tries >= RD_SPIN_LIMIT) return false;
+        __builtin_amdgcn_s_sleep(2);
+        v = ll_get(p);
+    }
+    pay = (uint32_t)v;
+    return true;
+}
+
+template <int UG, int UD>
+__global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int bad;
+    __shared__ int sidx[MAX_K];
+    __shared__ float sw[MAX_K];
+    const int tid = threadIdx.x, RD = A.rd, k = s.k, nb = s.nbI, nbp = round4(nb), I = s.I, H = s.H;
+    const int ust = round4(nb) + 4;
+    const uint32_t tag = __hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int r0 = blockIdx.x * RD, ng = (I / GU_ROWS) * k;
+    if (tid < k) {
+        const int e = A.idx[tid];
+        sidx[tid] = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);
+        sw[tid] = A.w[tid];
+    }
+    if (tid == 0) bad = 0;
+    float rv = 0.0f;
+    if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+
+    // 1. first gate/up unit: loads, dots and (wave 0) publication; then this
+    //    block's down loads.  They are needed last, so they are issued after
+    //    the unit's weights are in and after wave 0 has issued the h stores
+    //    (loads queued ahead of them would hold the stores back behind the
+    //    HBM stream).
+    FxGu<UG> g;
+    const int u0 = blockIdx.x;
+    if (u0 < ng) fx_gu_load<UG>(A, s, u0, g);
+    __syncthreads();  // sidx
+    if (u0 < ng) {
+        fx_gu_dots<UG>(A, s, g, smem);
+        fx_gu_publish(A, s, u0, tag, smem);
+        __builtin_amdgcn_s_barrier();  // issue order only, no memory fence
+    }
+    const size_t ntb = (size_t)H * nb;
+    const int items = k * RD * nb;
+    uint4 wv[UD];
+    uint16_t dv[UD];
+#pragma unroll
+    for (int u = 0; u < UD; u++) {
+        const int p = u * FX_THREADS + tid;
+        wv[u] = make_uint4(0u, 0u, 0u, 0u);
+        dv[u] = 0;
+        if (p < items) {
+            const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            const int jj = rd / RD, row = r0 + (rd - jj * RD);
+            const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
+            const size_t o = (size_t)row * nb + b;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
+        }
+    }
+    // keep these loads here, in flight during the rest of the gate/up work
+    // (the compiler would otherwise sink them next to their use)
+    __asm__ volatile("" ::: "memory");
+    for (int unit = u0 + gridDim.x; unit < ng; unit += gridDim.x) {
+        fx_gu_load<UG>(A, s, unit, g);
+        __syncthreads();  // wave 0 has read the previous unit's LDS
+        fx_gu_dots<UG>(A, s, g, smem);
+        fx_gu_publish(A, s, unit, tag, smem);
+    }
+
+    // 2. wait for every unit's last word, read h into LDS, then this block's
+    //    down rows
+    for (int unit = tid; unit < ng; unit += FX_THREADS) {
+        uint32_t pay;
+        if (!fx_wait(A.hw + (size_t)9 * ng + unit, tag, pay)) bad = 1;
+    }
+    __syncthreads();
+    int8_t *hq = reinterpret_cast<int8_t *>(smem);
+    float *hd = reinterpret_cast<float *>(smem + (size_t)k * I);
+    int *hs = reinterpret_cast<int *>(hd + k * nbp);
+    float *U = reinterpret_cast<float *>(hs + k * nbp);
+    float *D = U + k * RD * ust;
+    const int nw = ng * FX_QW;
+    for (int p = tid; p < nw; p += FX_THREADS) {
+        const uint64_t v = A.hw[p];  // plain load: shared through the L2
+        uint32_t pay = (uint32_t)v;
+        if ((uint32_t)(v >> 32) != tag && !fx_wait(A.hw + p, tag, pay)) bad = 1;
+        const int wd = p / ng, unit = p - wd * ng;
+        const int jj = unit / nb, b = unit - jj * nb;
+        if (wd < 8)
+            *reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK + 4 * wd) = pay;
+        else if (wd == 8)
+            hd[jj * nbp + b] = __uint_as_float(pay);
+        else
+            hs[jj * nbp + b] = (int)pay;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < UD; u++) {
+        const int p = u * FX_THREADS + tid;
+        if (p < items) {
+            const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+            const int jj = rd / RD;
+            const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
+                          8 * hs[jj * nbp + b];
+            U[rd * ust + b] = (float)S * h2f(dv[u]);
+        }
+    }
+    __syncthreads();
+    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid / RD) * nbp, nb);
+    __syncthreads();
+    if (tid < RD) {
+        float acc = 0.0f;
+        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        float o = A.resid ? rv + acc : acc;
+        if (bad) o = __builtin_nanf("");
+        A.out[r0 + tid] = o;
+    }
+    if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ================================================================ grouped
@@ -861,9 +1269,10 @@ static hipError_t allow_lds(const void *fn, size_t bytes) {
 }
 
 bool decode_shape_ok(const Shape &s) {
-    return s.H <= RO_MAXPASS * RO_THREADS * 8 && s.H / RG <= RT_THREADS && s.k * s.I <= DN_MAXPASS * DN_THREADS * 8 &&
-           2 * GU_RT * s.nbH <= 16 * RO_THREADS && s.k * DN_RD * s.nbI <= 16 * DN_THREADS && s.E < RO_THREADS &&
-           s.E % 4 == 0 && s.k <= MAX_K;
+    return s.H <= RO_MAXPASS * RO_THREADS * 8 && s.H / RG <= RT_THREADS && s.H / 8 <= GU_THREADS &&
+           s.nbH <= GU_THREADS && 2 * GU_ROWS * s.nbH <= 16 * GU_THREADS && gateup_lds_bytes(s.H, s.nbH) <= 160 * 1024 &&
+           s.k * DN_RD * s.nbI <= 16 * DN_THREADS && down_lds_bytes(s.k, s.I, s.nbI) <= 160 * 1024 &&
+           s.E < RO_THREADS && s.E <= MAX_E && s.E % 4 == 0 && s.k <= MAX_K;
 }
 
 hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
@@ -885,45 +1294,106 @@ hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, in
     return hipGetLastError();
 }
 
+hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape &s, float eps, uint64_t *lw,
+                            uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
+                            hipStream_t st) {
+    if (!decode_shape_ok(s)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_dec, dim3(s.E, T), dim3(RO_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
+                       w, xq, xd, xs);
+    return hipGetLastError();
+}
+
 template <int UNR>
-static hipError_t gateup_go(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T,
-                            float eps, float *h, int32_t *idx, float *w, hipStream_t st) {
-    size_t lds = gateup_lds_bytes(s.H, s.nbH);
+static hipError_t gateup_go(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const int8_t *xq,
+                            const float *xd, const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
+    const size_t lds = gateup_lds_bytes(s.H, s.nbH);
     hipError_t e = allow_lds((const void *)k_gateup<UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_gateup<UNR>, dim3(cdiv((size_t)s.I, GU_RT), s.k, T), dim3(RO_THREADS), lds, st, layer_pl, s,
-                       x, raw, eps, h, idx, w);
+    hipLaunchKernelGGL(k_gateup<UNR>, dim3(s.I / GU_ROWS, s.k, T), dim3(GU_THREADS), lds, st, layer_pl, s, idx, xq,
+                       xd, xs, hq, hd, hs);
     return hipGetLastError();
 }
 
-hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, const float *x, const float *raw, int T, float eps,
-                         float *h, int32_t *idx, float *w, hipStream_t st) {
+hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const int8_t *xq,
+                         const float *xd, const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
     if (!decode_shape_ok(s)) return hipErrorInvalidValue;
-    int per = (int)cdiv((size_t)2 * GU_RT * s.nbH, RO_THREADS);
-    if (per <= 4) return gateup_go<4>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
-    if (per <= 8) return gateup_go<8>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
-    return gateup_go<16>(layer_pl, s, x, raw, T, eps, h, idx, w, st);
+    const int per = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, GU_THREADS);
+    if (per <= 1) return gateup_go<1>(layer_pl, s, T, idx, xq, xd, xs, hq, hd, hs, st);
+    if (per <= 2) return gateup_go<2>(layer_pl, s, T, idx, xq, xd, xs, hq, hd, hs, st);
+    if (per <= 4) return gateup_go<4>(layer_pl, s, T, idx, xq, xd, xs, hq, hd, hs, st);
+    if (per <= 8) return gateup_go<8>(layer_pl, s, T, idx, xq, xd, xs, hq, hd, hs, st);
+    return gateup_go<16>(layer_pl, s, T, idx, xq, xd, xs, hq, hd, hs, st);
 }
 
 template <int UNR>
-static hipError_t down_go(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx,
-                          const float *w, int T, const float *resid, float *out, hipStream_t st) {
-    size_t lds = down_lds_bytes(s.k, s.I, s.nbI);
+static hipError_t down_go(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const float *w,
+                          const int8_t *hq, const float *hd, const int *hs, const float *resid, float *out,
+                          hipStream_t st) {
+    const size_t lds = down_lds_bytes(s.k, s.I, s.nbI);
     hipError_t e = allow_lds((const void *)k_down<UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_down<UNR>, dim3(cdiv((size_t)s.H, DN_RD), T), dim3(DN_THREADS), lds, st, layer_pl, s, h,
-                       idx, w, resid, out);
+    hipLaunchKernelGGL(k_down<UNR>, dim3(s.H / DN_RD, T), dim3(DN_THREADS), lds, st, layer_pl, s, idx, w, hq, hd, hs,
+                       resid, out);
     return hipGetLastError();
 }
 
-hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, const float *h, const int32_t *idx, const float *w,
-                       int T, const float *resid, float *out, hipStream_t st) {
+hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const float *w,
+                       const int8_t *hq, const float *hd, const int *hs, const float *resid, float *out,
+                       hipStream_t st) {
     if (!decode_shape_ok(s)) return hipErrorInvalidValue;
-    int per = (int)cdiv((size_t)s.k * DN_RD * s.nbI, DN_THREADS);
-    if (per <= 2) return down_go<2>(layer_pl, s, h, idx, w, T, resid, out, st);
-    if (per <= 6) return down_go<6>(layer_pl, s, h, idx, w, T, resid, out, st);
-    if (per <= 12) return down_go<12>(layer_pl, s, h, idx, w, T, resid, out, st);
-    return down_go<16>(layer_pl, s, h, idx, w, T, resid, out, st);
+    const int per = (int)cdiv((size_t)s.k * DN_RD * s.nbI, DN_THREADS);
+    if (per <= 2) return down_go<2>(layer_pl, s, T, idx, w, hq, hd, hs, resid, out, st);
+    if (per <= 6) return down_go<6>(layer_pl, s, T, idx, w, hq, hd, hs, resid, out, st);
+    if (per <= 12) return down_go<12>(layer_pl, s, T, idx, w, hq, hd, hs, resid, out, st);
+    return down_go<16>(layer_pl, s, T, idx, w, hq, hd, hs, resid, out, st);
+}
+
+// Down rows per block: the smallest power of two that keeps the grid within
+// the CU count (one resident block per CU).
+static int fx_rows(const Shape &s, int n_cu) {
+    int rd = 1;
+    while (s.H / rd > n_cu || s.H % rd) rd *= 2;
+    return rd;
+}
+
+bool experts_fused_ok(const Shape &s, int n_cu) {
+    if (!decode_shape_ok(s) || n_cu <= 0) return false;
+    const int rd = fx_rows(s, n_cu);
+    // unroll variants that stay within 128 VGPRs without spills
+    const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
+    const int ud = (int)cdiv((size_t)s.k * rd * s.nbI, FX_THREADS);
+    const bool regs = ud <= 6 && ug <= 4 && !(ug > 2 && ud > 2);
+    return regs && s.H % rd == 0 && s.k * rd <= FX_THREADS && fx_lds_bytes(s, rd) <= 160 * 1024 && s.k <= MAX_K;
+}
+
+size_t experts_fused_words(const Shape &s) { return (size_t)s.k * s.nbI * FX_QW; }
+
+template <int UG, int UD>
+static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
+    const size_t lds = fx_lds_bytes(s, A.rd);
+    hipError_t e = allow_lds((const void *)k_experts<UG, UD>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_experts<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    return hipGetLastError();
+}
+
+template <int UG, int UDMAX>
+static hipError_t experts_ud(const FxArgs &A, const Shape &s, hipStream_t st) {
+    const int ud = (int)cdiv((size_t)s.k * A.rd * s.nbI, FX_THREADS);
+    if (ud <= 1) return experts_go<UG, 1>(A, s, st);
+    if (ud <= 2 || UDMAX <= 2) return experts_go<UG, 2>(A, s, st);
+    return experts_go<UG, UDMAX>(A, s, st);
+}
+
+hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_cu, const int32_t *idx, const float *w,
+                                const int8_t *xq, const float *xd, const int *xs, uint64_t *hw, const uint32_t *ctl,
+                                uint32_t *err, const float *resid, float *out, hipStream_t st) {
+    if (!experts_fused_ok(s, n_cu)) return hipErrorInvalidValue;
+    const FxArgs A{layer_pl, idx, w, xq, xd, xs, hw, ctl, err, resid, out, fx_rows(s, n_cu)};
+    const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
+    if (ug <= 1) return experts_ud<1, 6>(A, s, st);
+    if (ug <= 2) return experts_ud<2, 6>(A, s, st);
+    return experts_ud<4, 2>(A, s, st);
 }
 
 bool grouped_shape_ok(const Shape &s) {

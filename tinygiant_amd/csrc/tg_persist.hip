@@ -92,13 +92,6 @@ TG_DEV void ps_stamp(const PersistArgs &A, int l, int slot) {
 }
 
 // ------------------------------------------------------------ tagged words
-TG_DEV void ll_put(uint64_t *p, uint32_t v, uint32_t tag) {
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-TG_DEV uint64_t ll_get(const uint64_t *p) {
-    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Reads n tagged words into dst (LDS payloads).  Each thread owns the words
 // i = tid + u * NT; per round it loads every word of a batch that is still
