@@ -354,27 +354,26 @@ __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 // boundary).  A poll that runs out of tries sets *err and routes the token
 // to experts 0..k-1 with weight 0, so the expert kernels stay in bounds.
 constexpr uint32_t RD_SPIN_LIMIT = 1u << 20;
+constexpr int RD_THREADS = 1024;  // several threads per expert in the ranking
 
 TG_DEV uint32_t next_gen(uint32_t g) { return g >= 0x7FFFFFFFu ? 1u : g + 1u; }
 
-__global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restrict__ Wr, const float *__restrict__ x,
+__global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restrict__ Wr, const float *__restrict__ x,
                                                           int E, int H, int k, float eps, uint64_t *__restrict__ lw,
                                                           uint32_t *__restrict__ ctl, uint32_t *__restrict__ err,
                                                           int32_t *__restrict__ idx, float *__restrict__ w,
                                                           int8_t *__restrict__ xq, float *__restrict__ xd,
                                                           int *__restrict__ xs) {
-    __shared__ __align__(16) float gp[RO_THREADS];
-    __shared__ __align__(16) float gq[RO_THREADS];
+    __shared__ __align__(16) float gp[RT_THREADS];
+    __shared__ __align__(16) float gq[RT_THREADS];
     __shared__ __align__(16) uint64_t keys[MAX_E];
     __shared__ float slog[MAX_E];
-    __shared__ float sw[MAX_K], sex[MAX_K];
     __shared__ int sidx[MAX_K];
     __shared__ float ssc;
     __shared__ int last, bad;
     const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, G = H / RG, nbH = H / QK;
     const float *xt = x + (size_t)t * H;
     const uint32_t tag = next_gen(__hip_atomic_load(ctl + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float aw = 0.0f, aq = 0.0f;
     if (tid < G) {
         const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + tid * RG);
         const float4 *x4 = reinterpret_cast<const float4 *>(xt + tid * RG);
@@ -384,6 +383,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restric
             wv[q] = w4[q];
             xv[q] = x4[q];
         }
+        float aw = 0.0f, aq = 0.0f;
 #pragma unroll
         for (int q = 0; q < RG / 4; q++) {
             aq = __builtin_fmaf(xv[q].x, xv[q].x, aq);
@@ -398,9 +398,9 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restric
             aw = __builtin_fmaf(wv[q].z, xv[q].z, aw);
             aw = __builtin_fmaf(wv[q].w, xv[q].w, aw);
         }
+        gp[tid] = aw;
+        gq[tid] = aq;
     }
-    gp[tid] = aw;
-    gq[tid] = aq;
     if (tid == 0) bad = 0;
     __syncthreads();
     if (tid == 0) {
@@ -423,23 +423,16 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restric
     __syncthreads();
     if (!last) return;
 
-    // ---- last block of token t
+    // ---- last block of token t: Q8_0(x * s), then the E logits
     const float sc = ssc;
-#pragma unroll
-    for (int ps = 0; ps < RO_MAXPASS; ps++) {
-        if (ps * RO_THREADS * 8 < H) {
-            const int i0 = ps * RO_THREADS * 8 + tid * 8;
-            float v[8];
-            if (i0 < H) {
-                const float4 a4 = *reinterpret_cast<const float4 *>(xt + i0);
-                const float4 b4 = *reinterpret_cast<const float4 *>(xt + i0 + 4);
-                v[0] = a4.x * sc; v[1] = a4.y * sc; v[2] = a4.z * sc; v[3] = a4.w * sc;
-                v[4] = b4.x * sc; v[5] = b4.y * sc; v[6] = b4.z * sc; v[7] = b4.w * sc;
-            } else {
-#pragma unroll
-                for (int c = 0; c < 8; c++) v[c] = 0.0f;
-            }
-            q8_group8(v, i0 < H, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
+    {
+        const int i0 = tid * 8;
+        if (i0 < H) {  // H / 8 is a multiple of 32: whole 4-lane groups
+            const float4 a4 = *reinterpret_cast<const float4 *>(xt + i0);
+            const float4 b4 = *reinterpret_cast<const float4 *>(xt + i0 + 4);
+            const float v[8] = {a4.x * sc, a4.y * sc, a4.z * sc, a4.w * sc,
+                                b4.x * sc, b4.y * sc, b4.z * sc, b4.w * sc};
+            q8_group8(v, true, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
         }
     }
     if (tid < k) sidx[tid] = 0;
@@ -460,38 +453,38 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_dec(const float *__restric
         keys[tid] = rank_key(l, tid);
     }
     __syncthreads();
-    // rank = number of larger keys; two threads per expert when E <= 128
-    const int tpe = 2 * E <= RO_THREADS ? 2 : 1;
-    const int ee = tpe == 2 ? tid >> 1 : tid;
+    // rank = number of larger keys, tpe consecutive threads per expert
+    // (each counts a slice of the keys, then a shuffle sum)
+    const int tpe = E <= RD_THREADS / 8 ? 8 : 4;
+    const int ee = tid / tpe, part = tid % tpe;
     if (ee < E) {
         const uint64_t my = keys[ee];
-        const int half = tpe == 2 ? (tid & 1) : 0;
-        const int n = E / tpe, b0 = half * n;
+        const int b0 = part * E / tpe, b1 = (part + 1) * E / tpe;
         int cnt = 0;
-#pragma unroll 8
-        for (int i = 0; i < n; i += 2) {
-            const ulonglong2 o = *reinterpret_cast<const ulonglong2 *>(keys + b0 + i);
-            cnt += o.x > my ? 1 : 0;
-            cnt += o.y > my ? 1 : 0;
-        }
-        if (tpe == 2) cnt += __shfl_xor(cnt, 1, WAVE);
-        if (half == 0 && cnt < k) sidx[cnt] = ee;
+        for (int i = b0; i < b1; i++) cnt += keys[i] > my ? 1 : 0;
+        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, WAVE);
+        if (part == 0 && cnt < k) sidx[cnt] = ee;
     }
     __syncthreads();
-    if (tid == 0) {
-        if (bad) {
-            __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int i = 0; i < k; i++) {
-                idx[(size_t)t * k + i] = i;
-                w[(size_t)t * k + i] = 0.0f;
-            }
-        } else {
-            topk_softmax(slog, sidx, k, sw, sex);
-            for (int i = 0; i < k; i++) {
-                idx[(size_t)t * k + i] = sidx[i];
-                w[(size_t)t * k + i] = sw[i];
-            }
+    // renormalised softmax over the selected logits (engine.py:233-236), one
+    // lane per selected expert: e_i = exp(l - lmax) in ascending order,
+    // numpy's pairwise sum, w = e / sum
+    if (tid < WAVE) {
+        const float lmax = slog[sidx[0]];
+        const bool on = tid < k;
+        const float ex = on ? expf_tg(slog[sidx[on ? k - 1 - tid : 0]] - lmax) : 0.0f;
+        float sex[MAX_K];
+#pragma unroll
+        for (int i = 0; i < MAX_K; i++) sex[i] = __shfl(ex, i, WAVE);
+        const float sum = np_pairwise_sum(sex, k);
+        if (on) {
+            const int j = k - 1 - tid;
+            idx[(size_t)t * k + j] = bad ? j : sidx[j];
+            w[(size_t)t * k + j] = bad ? 0.0f : ex / sum;
         }
+    }
+    if (tid == 0) {
+        if (bad) __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ctl + 2 * t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ctl + 2 * t + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -678,23 +671,26 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
 // weights stream while gate/up runs instead of after it.  The grid has one
 // block of 1024 threads per down unit (H / RD units of RD output rows, at
 // most one block per CU, so every block is resident at once).  Block b:
-//   1. runs the gate/up units u = b, b + grid, ... (unit (m, j): rows
-//      [32m, 32m+32) of gate and up of the j-th expert, as k_gateup),
-//      issuing its down loads (RD rows of down for all k experts) once the
-//      first unit's weights have arrived, and publishes each Q8_0 block of h
-//      as FX_QW tagged words;
-//   2. polls the last word of every unit (thread u polls unit u; the words
-//      are stored word-major, hw[w * units + u], so a wave's polls touch a
-//      few cache lines), reads all words of every unit (plain loads, so the
-//      blocks of an XCD share its L2; a word with an old tag is polled
-//      again), and computes dots, chains, combine and residual for its RD
-//      rows.
+//   1. runs its first gate/up unit (unit (m, j): rows [32m, 32m+32) of gate
+//      and up of the j-th expert, as k_gateup), wave 0 publishing the Q8_0
+//      block of h as FX_QW tagged words;
+//   2. issues, from waves 3.., the loads of its down unit (RD rows of down
+//      for all k experts), then runs any further gate/up units;
+//   3. waves 0..2 read the FX_QW words of every unit (thread u: unit u; the
+//      last word polled with coherent loads, the rest read through the L2;
+//      stored word-major, hw[w * units + u], so a wave's loads touch a few
+//      cache lines), then waves 3.. dot the down rows and the block chains,
+//      combines and adds the residual for its RD rows.  The reading waves
+//      hold no down load, so their waits (vmcnt retires in order) never
+//      stand behind the down stream.
 // Tags: the routing generation of the layer (ctl[1], stored by k_route_dec
 // of the same layer), so words of earlier layers never match.  A block finishes its own gate/up units
 // before it waits, so no wait depends on a block that is not running.
 // Polls are bounded; when one runs out the block sets *err and writes NaN
 // rows.
 constexpr int FX_THREADS = 1024;
+constexpr int FX_PT = 3 * WAVE;              // threads that poll the h words (waves 0..2)
+constexpr int FX_DT = FX_THREADS - FX_PT;    // threads that load and dot the down rows
 constexpr int FX_QW = 10;
 
 struct FxArgs {
@@ -704,7 +700,7 @@ struct FxArgs {
     const int8_t *xq;
     const float *xd;
     const int *xs;
-    uint64_t *hw;         // [FX_QW][k * I/32] tagged h blocks, word-major
+    uint64_t *hw;         // [2][FX_QW][k * I/32] tagged h blocks, word-major, by tag parity
     const uint32_t *ctl;  // routing counter / generation of token 0
     uint32_t *err;
     const float *resid;
@@ -790,7 +786,7 @@ TG_DEV void fx_gu_dots(const FxArgs &A, const Shape &s, const FxGu<UG> &g, uint8
 // tagged words.  Wave 0 alone does this part (lane r chains row r: gate
 // rows in lanes 0..31, up rows in 32..63) and needs no block barrier, so it
 // never waits for the down loads the block has in flight.
-TG_DEV void fx_gu_publish(const FxArgs &A, const Shape &s, int unit, uint32_t tag, const uint8_t *smem) {
+TG_DEV void fx_gu_publish(const FxArgs &A, const Shape &s, int unit, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
     constexpr int RT = GU_ROWS;
     static_assert(2 * RT == 64, "one wave holds the gate and up rows of a unit");
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
@@ -809,23 +805,56 @@ TG_DEV void fx_gu_publish(const FxArgs &A, const Shape &s, int unit, uint32_t ta
                               ((uint32_t)(__shfl(q, l4 + 2, WAVE) & 255) << 16) |
                               ((uint32_t)(__shfl(q, l4 + 3, WAVE) & 255) << 24);
         const size_t ng = (size_t)(s.I / GU_ROWS) * s.k;
-        uint64_t *dst = A.hw + unit;
+        uint64_t *dst = hw + unit;
         if (tid < 8) ll_put(dst + tid * ng, word, tag);
         if (tid == 8) ll_put(dst + 8 * ng, __float_as_uint(dq), tag);
         if (tid == 9) ll_put(dst + 9 * ng, (uint32_t)qsum, tag);
     }
 }
 
-// Bounded poll of one tagged word; false when it ran out of tries.
-TG_DEV bool fx_wait(const uint64_t *p, uint32_t tag, uint32_t &pay) {
-    uint64_t v = ll_get(p);
+// Reads the FX_QW tagged words of one unit (stride `ng` words apart):
+// polls the last word with coherent loads until it carries `tag`, then
+// reads the other words with plain loads (shared through the L2 by the
+// blocks of an XCD) and polls again only a word that still carries an old
+// tag.  Bounded; false when a poll ran out of tries.
+TG_DEV bool fx_read_unit(const uint64_t *src, int ng, uint32_t tag, uint32_t (&pay)[FX_QW]) {
+    constexpr int LAST = FX_QW - 1;
     uint32_t tries = 0;
+#pragma unroll
+    for (int i = 0; i < FX_QW; i++) pay[i] = 0u;
+    uint64_t v = ll_get(src + (size_t)LAST * ng);
     while ((uint32_t)(v >> 32) != tag) {
         if (++tries >= RD_SPIN_LIMIT) return false;
         __builtin_amdgcn_s_sleep(2);
-        v = ll_get(p);
+        v = ll_get(src + (size_t)LAST * ng);
     }
-    pay = (uint32_t)v;
+    pay[LAST] = (uint32_t)v;
+    __asm__ volatile("" ::: "memory");  // the plain loads stay after the poll
+    uint32_t pend = 0;
+    uint64_t w[LAST];
+#pragma unroll
+    for (int i = 0; i < LAST; i++) w[i] = src[(size_t)i * ng];
+#pragma unroll
+    for (int i = 0; i < LAST; i++) {
+        if ((uint32_t)(w[i] >> 32) == tag)
+            pay[i] = (uint32_t)w[i];
+        else
+            pend |= 1u << i;
+    }
+    while (pend) {
+#pragma unroll
+        for (int i = 0; i < LAST; i++)
+            if (pend >> i & 1u) w[i] = ll_get(src + (size_t)i * ng);
+#pragma unroll
+        for (int i = 0; i < LAST; i++)
+            if ((pend >> i & 1u) && (uint32_t)(w[i] >> 32) == tag) {
+                pay[i] = (uint32_t)w[i];
+                pend &= ~(1u << i);
+            }
+        if (!pend) break;
+        if (++tries >= RD_SPIN_LIMIT) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
     return true;
 }
 
@@ -847,31 +876,33 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     if (tid == 0) bad = 0;
     float rv = 0.0f;
     if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+    __syncthreads();  // sidx
 
-    // 1. first gate/up unit: loads, dots and (wave 0) publication; then this
-    //    block's down loads.  They are needed last, so they are issued after
-    //    the unit's weights are in and after wave 0 has issued the h stores
-    //    (loads queued ahead of them would hold the stores back behind the
-    //    HBM stream).
+    // h words of this layer: one of two buffers by tag parity, so a copy of
+    // a line that an L2 still holds is at least two layers old
+    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QW;
+
+    // 1. the first gate/up unit: loads, dots (every wave), publication
+    //    (wave 0)
     FxGu<UG> g;
     const int u0 = blockIdx.x;
-    if (u0 < ng) fx_gu_load<UG>(A, s, u0, g);
-    __syncthreads();  // sidx
     if (u0 < ng) {
+        fx_gu_load<UG>(A, s, u0, g);
         fx_gu_dots<UG>(A, s, g, smem);
-        fx_gu_publish(A, s, u0, tag, smem);
-        __builtin_amdgcn_s_barrier();  // issue order only, no memory fence
+        fx_gu_publish(A, s, u0, tag, hw, smem);
     }
+    // 2. this block's down weights (waves 3.., item p on down thread
+    //    p % FX_DT), then further gate/up units
     const size_t ntb = (size_t)H * nb;
-    const int items = k * RD * nb;
+    const int items = k * RD * nb, dt = tid - FX_PT;
     uint4 wv[UD];
     uint16_t dv[UD];
 #pragma unroll
     for (int u = 0; u < UD; u++) {
-        const int p = u * FX_THREADS + tid;
+        const int p = u * FX_DT + dt;
         wv[u] = make_uint4(0u, 0u, 0u, 0u);
         dv[u] = 0;
-        if (p < items) {
+        if (dt >= 0 && p < items) {
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
             const int jj = rd / RD, row = r0 + (rd - jj * RD);
             const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
@@ -880,47 +911,40 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
             dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
         }
     }
-    // keep these loads here, in flight during the rest of the gate/up work
-    // (the compiler would otherwise sink them next to their use)
+    // keep these loads here, in flight during the rest (the compiler would
+    // otherwise sink them next to their use)
     __asm__ volatile("" ::: "memory");
     for (int unit = u0 + gridDim.x; unit < ng; unit += gridDim.x) {
         fx_gu_load<UG>(A, s, unit, g);
         __syncthreads();  // wave 0 has read the previous unit's LDS
         fx_gu_dots<UG>(A, s, g, smem);
-        fx_gu_publish(A, s, unit, tag, smem);
+        fx_gu_publish(A, s, unit, tag, hw, smem);
     }
 
-    // 2. wait for every unit's last word, read h into LDS, then this block's
-    //    down rows
-    for (int unit = tid; unit < ng; unit += FX_THREADS) {
-        uint32_t pay;
-        if (!fx_wait(A.hw + (size_t)9 * ng + unit, tag, pay)) bad = 1;
-    }
-    __syncthreads();
+    // 3. waves 0..2 read h of every unit into LDS; then the down rows
     int8_t *hq = reinterpret_cast<int8_t *>(smem);
     float *hd = reinterpret_cast<float *>(smem + (size_t)k * I);
     int *hs = reinterpret_cast<int *>(hd + k * nbp);
     float *U = reinterpret_cast<float *>(hs + k * nbp);
     float *D = U + k * RD * ust;
-    const int nw = ng * FX_QW;
-    for (int p = tid; p < nw; p += FX_THREADS) {
-        const uint64_t v = A.hw[p];  // plain load: shared through the L2
-        uint32_t pay = (uint32_t)v;
-        if ((uint32_t)(v >> 32) != tag && !fx_wait(A.hw + p, tag, pay)) bad = 1;
-        const int wd = p / ng, unit = p - wd * ng;
-        const int jj = unit / nb, b = unit - jj * nb;
-        if (wd < 8)
-            *reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK + 4 * wd) = pay;
-        else if (wd == 8)
-            hd[jj * nbp + b] = __uint_as_float(pay);
-        else
-            hs[jj * nbp + b] = (int)pay;
+    if (tid < FX_PT) {
+        for (int unit = tid; unit < ng; unit += FX_PT) {
+            uint32_t pay[FX_QW];
+            const bool ok = fx_read_unit(hw + unit, ng, tag, pay);
+            const int jj = unit / nb, b = unit - jj * nb;
+            uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
+#pragma unroll
+            for (int wd = 0; wd < 8; wd++) dq[wd] = pay[wd];
+            hd[jj * nbp + b] = __uint_as_float(pay[8]);
+            hs[jj * nbp + b] = (int)pay[9];
+            if (!ok) bad = 1;
+        }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < UD; u++) {
-        const int p = u * FX_THREADS + tid;
-        if (p < items) {
+        const int p = u * FX_DT + dt;
+        if (dt >= 0 && p < items) {
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
             const int jj = rd / RD;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
@@ -1298,7 +1322,7 @@ hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape 
                             uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
                             hipStream_t st) {
     if (!decode_shape_ok(s)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route_dec, dim3(s.E, T), dim3(RO_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
+    hipLaunchKernelGGL(k_route_dec, dim3(s.E, T), dim3(RD_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
                        w, xq, xd, xs);
     return hipGetLastError();
 }
@@ -1361,12 +1385,12 @@ bool experts_fused_ok(const Shape &s, int n_cu) {
     const int rd = fx_rows(s, n_cu);
     // unroll variants that stay within 128 VGPRs without spills
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
-    const int ud = (int)cdiv((size_t)s.k * rd * s.nbI, FX_THREADS);
+    const int ud = (int)cdiv((size_t)s.k * rd * s.nbI, FX_DT);
     const bool regs = ud <= 6 && ug <= 4 && !(ug > 2 && ud > 2);
     return regs && s.H % rd == 0 && s.k * rd <= FX_THREADS && fx_lds_bytes(s, rd) <= 160 * 1024 && s.k <= MAX_K;
 }
 
-size_t experts_fused_words(const Shape &s) { return (size_t)s.k * s.nbI * FX_QW; }
+size_t experts_fused_words(const Shape &s) { return 2 * (size_t)s.k * s.nbI * FX_QW; }
 
 template <int UG, int UD>
 static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
@@ -1379,7 +1403,7 @@ static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
 
 template <int UG, int UDMAX>
 static hipError_t experts_ud(const FxArgs &A, const Shape &s, hipStream_t st) {
-    const int ud = (int)cdiv((size_t)s.k * A.rd * s.nbI, FX_THREADS);
+    const int ud = (int)cdiv((size_t)s.k * A.rd * s.nbI, FX_DT);
     if (ud <= 1) return experts_go<UG, 1>(A, s, st);
     if (ud <= 2 || UDMAX <= 2) return experts_go<UG, 2>(A, s, st);
     return experts_go<UG, UDMAX>(A, s, st);
