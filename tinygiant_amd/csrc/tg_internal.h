@@ -81,9 +81,9 @@ hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, in
 // decode MoE layer pieces
 bool decode_shape_ok(const Shape &s);
 // routing of T tokens in one launch: lw [T][E] tagged logits, ctl [T][2]
-// arrival counter and generation (zero before first use), err set to
-// nonzero when a poll ran out of tries; writes idx, w [T][k] and the Q8_0
-// activations xq [T][H], xd / xs [T][H/32]
+// (word 1: generation of the token's last routing; zero before first use),
+// err set to nonzero when a poll ran out of tries; writes idx, w [T][k]
+// and the Q8_0 activations xq [T][H], xd / xs [T][H/32]
 hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape &s, float eps, uint64_t *lw,
                             uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
                             hipStream_t st);

@@ -341,18 +341,18 @@ __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 // Block (e, t): the raw router dot of expert e for token t (grouped sums as
 // k_route) and, from the same x, the token's RMS scale s (grouped sums of
 // squares as route_token), so logit = raw * s as in route_token.  Thread 0
-// publishes the logit as a tagged word (see tg_persist.hip) and counts the
-// block in the token's arrival counter; both are relaxed agent-scope
-// atomics.  The block that arrives last reads the E logits (bounded polls
-// on the tags), ranks them, forms the softmax weights and Q8_0(x * s), and
-// writes idx / w / xq / xd / xs for the expert kernels.
+// publishes the logit as a tagged word (see tg_persist.hip; relaxed
+// agent-scope atomics).  Block (0, t) also ranks the token: it forms
+// Q8_0(x * s), reads the E logits (bounded polls on the tags), ranks them,
+// forms the softmax weights, and writes idx / w / xq / xd / xs for the
+// expert kernels.
 //
-// ctl[2t] is the token's arrival counter, ctl[2t+1] the generation of its
-// last routing.  A launch publishes with the next generation, so words left
-// by earlier launches never match; its last block resets the counter and
-// stores the new generation, which the next launch reads (after the kernel
-// boundary).  A poll that runs out of tries sets *err and routes the token
-// to experts 0..k-1 with weight 0, so the expert kernels stay in bounds.
+// ctl[2t+1] is the generation of the token's last routing (ctl[2t] is
+// unused).  A launch publishes with the next generation, so words left by
+// earlier launches never match; block (0, t) stores the new generation,
+// which the next launch reads (after the kernel boundary).  A poll that
+// runs out of tries sets *err and routes the token to experts 0..k-1 with
+// weight 0, so the expert kernels stay in bounds.
 constexpr uint32_t RD_SPIN_LIMIT = 1u << 20;
 constexpr int RD_THREADS = 1024;  // several threads per expert in the ranking
 
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
     __shared__ float slog[MAX_E];
     __shared__ int sidx[MAX_K];
     __shared__ float ssc;
-    __shared__ int last, bad;
+    __shared__ int bad;
     const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, G = H / RG, nbH = H / QK;
     const float *xt = x + (size_t)t * H;
     const uint32_t tag = next_gen(__hip_atomic_load(ctl + 2 * t + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -416,14 +416,12 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
         }
         const float sc = rms_scale(ts, H, eps);
         ll_put(lw + (size_t)t * E + e, __float_as_uint(tr * sc), tag);
-        const uint32_t old = __hip_atomic_fetch_add(ctl + 2 * t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ssc = sc;
-        last = old == (uint32_t)(E - 1) ? 1 : 0;
     }
+    if (e != 0) return;
     __syncthreads();
-    if (!last) return;
 
-    // ---- last block of token t: Q8_0(x * s), then the E logits
+    // ---- block (0, t): Q8_0(x * s), then the E logits
     const float sc = ssc;
     {
         const int i0 = tid * 8;
@@ -485,7 +483,6 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
     }
     if (tid == 0) {
         if (bad) __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(ctl + 2 * t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(ctl + 2 * t + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
