@@ -57,6 +57,24 @@ def cpu_model() -> str:
     return platform.processor()
 
 
+def profiled_traffic(kernel):
+    """HBM bytes per launch (read + write) of `kernel` as measured by the
+    FETCH_SIZE / WRITE_SIZE counter runs summarised under profiles/ (line
+    `traffic_bytes_per_launch <kernel> <bytes>`), or None."""
+    root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+    if not os.path.isdir(root):
+        return None
+    for name in sorted(os.listdir(root)):
+        if not name.endswith(".md"):
+            continue
+        with open(os.path.join(root, name)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                    return int(parts[2])
+    return None
+
+
 def kernel_times(call, names):
     """(launches, total ms) per kernel name from the library's event timing."""
     out = {}
@@ -251,7 +269,7 @@ def run_decode_stack(args, torch, call):
         "decode_path": path,
         "roofline": {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(roof_kernel)},
         "cpu_baseline": cpu,
     }
     arena.close()
