@@ -15,6 +15,9 @@ Other workloads (--workload):
                layers (5.4 GB) so no step finds its experts in the 256 MB MALL.
   prefill      2048 tokens through the 48-layer stack on the grouped int8
                MFMA path; int8 TOPS against the MFMA peak.
+  decode-235b  the Qwen3-235B-A22B-shaped stack (H=4096, I=1536, 94 layers,
+               127.7 GB resident), one token per step.
+  batched-235b the same stack, 32 tokens per step with Zipf(1.1) routing.
   hbm-ceiling  what one launch of plain 128-bit loads reads from HBM.
 
 Prints one JSON line: tok/s (value), expert-weight HBM GB/s, the roofline
@@ -89,11 +92,12 @@ def kernel_times(call, names):
 
 # ----------------------------------------------------------------- CPU legs
 
-def cpu_baseline_stack(arena, seed, n_layers_total, seconds, gpu_check):
+def cpu_baseline_stack(arena, seed, n_layers_total, seconds, gpu_check, shape=(H, I, E, K_TOP), n_sample=4):
     """The C oracle on this host: one token at a time through a sample of
     layers read back from the arena; extrapolated to the full stack."""
     from oracle import oracle as O
-    n_s = min(4, n_layers_total)
+    H, I, E, K_TOP = shape
+    n_s = min(n_sample, n_layers_total)
     layers = [arena.read_layer(l) for l in range(n_s)]
     routers = [O.synth_normal(seed, O.stream_id(l, 0, 3), 0.02, E * H).reshape(E, H) for l in range(n_s)]
     x_ref, x_gpu = gpu_check
@@ -129,10 +133,11 @@ def cpu_baseline_stack(arena, seed, n_layers_total, seconds, gpu_check):
     }
 
 
-def cpu_baseline_layer(layer_bytes, router, X, seconds, gpu_check):
+def cpu_baseline_layer(layer_bytes, router, X, seconds, gpu_check, shape=(H, I, E, K_TOP)):
     """The C oracle on this host over the batched workload: steps of T tokens
     through one layer, as many as fit in the time budget."""
     from oracle import oracle as O
+    H, I, E, K_TOP = shape
     x0, out_gpu = gpu_check
     ref, _, _, _ = O.moe_layer(layer_bytes, router, H, I, E, K_TOP, x0)
     parity = "bit-exact" if np.array_equal(ref.view(np.uint32), out_gpu.view(np.uint32)) else "MISMATCH"
@@ -387,6 +392,167 @@ def run_batched(args, torch, call):
     return res
 
 
+# Qwen3-235B-A22B MoE shape (config 5)
+H5, I5, E5, K5, L5 = 4096, 1536, 128, 8, 94
+EXPERT5_BYTES = 3 * I5 * (H5 // 32) * 18          # 10,616,832
+GATEUP5_BYTES = 2 * I5 * (H5 // 32) * 18          # 7,077,888
+
+
+def skewed_stack_routers(arena, blk, x0, u, c, shape, rng, torch):
+    """Routers of a stack whose expert popularity follows Zipf(1.1) at every
+    depth: a per-expert component along the direction u that tokens share.
+    Layer l's component is scaled by rms(x_l) / (u . x_l) measured on the
+    hidden states that reach it (x0 pushed through the layers before it), so
+    the logit bias stays the same although the residual stream grows."""
+    from tinygiant_amd.synth import zipf_router_bias
+    Hs, _, Es, _ = shape
+    rms0 = np.sqrt(1.0 + c * c / Hs)
+    noise_std = 0.02 * np.sqrt(Hs) / rms0
+    bias = zipf_router_bias(Es, 0.54 * noise_std / 0.905)
+    ut = torch.from_numpy(u.astype(np.float32)).cuda()
+    x = x0.clone()
+    routers = []
+    for l in range(arena.n_layers):
+        rms_l = float(torch.sqrt((x * x).mean(dim=1)).mean())
+        proj_l = float((x @ ut).mean())
+        Wr = (rng.standard_normal((Es, Hs)) * 0.02).astype(np.float32)
+        Wr += (bias[:, None] * (rms_l / proj_l) * u[None, :]).astype(np.float32)
+        arena.load_router(l, Wr)
+        routers.append(Wr)
+        x += blk.forward(l, x)
+    torch.cuda.synchronize()
+    return routers
+
+
+def run_235b(args, torch, call, T):
+    """Config 5: the Qwen3-235B-A22B-shaped MoE stack (H=4096, I=1536, 128
+    experts, top-8, 94 layers, 127.7 GB of Q4_0 resident in HBM); one step =
+    T tokens through all 94 layers.  T = 1: synthetic N(0, 0.02) routers,
+    one-token decode path.  T = 32: Zipf(1.1)-skewed routers, grouped path."""
+    from tinygiant_amd.arena import HBMExpertArena
+    from tinygiant_amd.moe import MoEBlock
+    from tinygiant_amd.synth import fit_zipf_exponent, stream_id
+
+    shape = (H5, I5, E5, K5)
+    L = args.layers if args.layers != 48 else L5
+    K = args.steps or (64 if T == 1 else 16)
+    W = (8 if T == 1 else 2) if args.warmup is None else args.warmup
+    log(f"arena: {L} layers x {E5} experts ({L * E5 * EXPERT5_BYTES / 1e9:.1f} GB Q4_0)")
+    arena = HBMExpertArena(L, E5, H5, I5, K5)
+    for l in range(L):
+        arena.synth_layer(l, args.seed)
+    rng = np.random.default_rng(args.seed)
+    stream = torch.cuda.current_stream().cuda_stream
+    X = torch.empty((W + K, T, H5), dtype=torch.float32, device="cuda")
+    call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
+    blk = MoEBlock(arena)
+    routers = None
+    if T > 1:
+        u = rng.standard_normal(H5)
+        u /= np.linalg.norm(u)
+        c = 0.5 * np.sqrt(H5)
+        X += torch.from_numpy((c * u).astype(np.float32)).cuda()
+        log("router calibration through the stack")
+        routers = skewed_stack_routers(arena, blk, X[0], u, c, shape, rng, torch)
+    X0 = X.clone()
+    torch.cuda.synchronize()
+
+    log(f"warmup {W} steps")
+    for i in range(W):
+        blk.step(X[i])
+    torch.cuda.synchronize()
+    log(f"timing {K} steps of {T} token(s) x {L} layers")
+    t0 = time.perf_counter()
+    for i in range(W, W + K):
+        blk.step(X[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    arena.status()
+    ms_step = wall * 1e3 / K
+    tok_s = T * K / wall
+
+    # distinct experts per layer-step and the skew (untimed, layer by layer)
+    n_uniq, zipf_s = float(K5), None
+    if T > 1:
+        uniq, all_idx = [], []
+        for i in range(W, min(W + K, W + 4)):
+            x = X0[i].clone()
+            for l in range(L):
+                out, idx, _ = blk.forward(l, x, return_routing=True)
+                ih = idx.cpu().numpy()
+                uniq.append(len(np.unique(ih)))
+                all_idx.append(ih)
+                x += out
+        n_uniq = float(np.mean(uniq))
+        zipf_s = fit_zipf_exponent(np.concatenate(all_idx), E5)
+    bytes_step = L * n_uniq * EXPERT5_BYTES
+    gbps = bytes_step / (ms_step * 1e-3) / 1e9
+
+    log("kernel timing pass")
+    X.copy_(X0)
+    torch.cuda.synchronize()
+    call("tg_prof_enable", 1)
+    for i in range(W, W + min(K, 8)):
+        blk.step(X[i])
+    torch.cuda.synchronize()
+    call("tg_prof_enable", 0)
+    names = ("route", "experts", "gateup", "down", "route_q8", "group", "gateup_mfma", "down_mfma", "combine")
+    kern = kernel_times(call, names)
+    kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    if "experts" in kern:
+        rk, rb = "experts", K5 * EXPERT5_BYTES
+        roof = "k_experts"
+    elif "gateup" in kern:
+        rk, rb = "gateup", K5 * GATEUP5_BYTES
+        roof = "k_gateup"
+    else:
+        rk, rb = "gateup_mfma", round(n_uniq * GATEUP5_BYTES)
+        roof = "k_mfma_grouped (gate/up)"
+    n_r, ms_r = kern[rk]
+    achieved = rb / (ms_r / n_r * 1e-3)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        if T == 1:
+            xt = X0[W, :1].cpu().numpy()
+            xg = X0[W, :1].clone()
+            blk.step(xg, 0, 2)
+            torch.cuda.synchronize()
+            cpu = cpu_baseline_stack(arena, args.seed, L, args.cpu_seconds, (xt, xg.cpu().numpy()), shape, 2)
+        else:
+            lb = arena.read_layer(0)
+            out = blk.forward(0, X0[W])
+            cpu = cpu_baseline_layer(lb, routers[0], [X0[W].cpu().numpy()], args.cpu_seconds,
+                                     (X0[W].cpu().numpy(), out.cpu().numpy()), shape)
+            cpu["sample"] += f"; the stack rate is this over {L} layers"
+            cpu["value"] = round(cpu["value"] / L, 3)
+            cpu["single_thread"]["value"] = round(cpu["single_thread"]["value"] / L, 3)
+
+    cfg = {"workload": f"qwen3-235b-a22b-moe-stack-{'decode' if T == 1 else 'batched-decode'}", "layers": L,
+           "hidden": H5, "experts": E5, "moe_intermediate": I5, "top_k": K5, "tokens_per_step": T}
+    if zipf_s is not None:
+        cfg.update({"zipf_fit": round(zipf_s, 3), "unique_experts_per_layer_step": round(n_uniq, 2)})
+    res = {
+        "metric": f"MoE stack decode tok/s (94-layer 235B-shaped Q4_0 stack, {T} token(s)/step)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_0 x q8_0 (int8 dot / int8 MFMA, fp32 accumulate)",
+        "data": "synthetic (N(0,0.02) Q4_0 experts, fp32 routers" + (", Zipf-skewed" if T > 1 else "") +
+                ", N(0,1) tokens)",
+        "config": cfg,
+        "hbm_gbps_expert_weights": round(gbps, 1),
+        "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
+        "kernel_avg_us": kern_us,
+        "roofline": {"bound": "hbm", "kernel": roof, "bytes_per_launch": rb, "achieved": round(achieved / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": profiled_traffic(roof)},
+        "cpu_baseline": cpu,
+    }
+    arena.close()
+    return res
+
+
 MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA, ops/s
 
 
@@ -516,6 +682,8 @@ def run_hbm_ceiling(args, torch, call):
 
 
 WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill": run_prefill,
+             "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
+             "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
              "hbm-ceiling": run_hbm_ceiling}
 
 
