@@ -36,34 +36,50 @@ namespace tg {
 constexpr int RG = 32;
 constexpr int RT_THREADS = 256;  // groups per k_route block (H <= 8192)
 
-__global__ __launch_bounds__(RT_THREADS) void k_route(const float *__restrict__ Wr, const float *__restrict__ x, int E,
-                                                      int H, float *__restrict__ raw) {
-    __shared__ __align__(16) float gp[RT_THREADS];
-    const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, G = H / RG;
-    float acc = 0.0f;
-    if (tid < G) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + tid * RG);
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * H + tid * RG);
-        float4 wv[RG / 4], xv[RG / 4];
+// Block (e, tb): expert e for tokens [8 tb, 8 tb + 8).  Thread (g, ts) runs
+// the fma chain of group g for tokens ts, ts + TS, ... (TS = 256 / G token
+// slots per pass), keeping the router group in registers; then one thread
+// per token adds the G group sums in ascending order.
+constexpr int RT_TOK = 8;
+
+__global__ __launch_bounds__(RT_THREADS) void k_route(const float *__restrict__ Wr, const float *__restrict__ x, int T,
+                                                      int E, int H, float *__restrict__ raw) {
+    __shared__ __align__(16) float gp[RT_TOK][RT_THREADS];
+    const int e = blockIdx.x, t0 = blockIdx.y * RT_TOK, tid = threadIdx.x, G = H / RG;
+    const int TS = RT_THREADS / G, g = tid % G, ts = tid / G;
+    if (ts < TS) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + g * RG);
+        float4 wv[RG / 4];
 #pragma unroll
-        for (int q = 0; q < RG / 4; q++) {
-            wv[q] = w4[q];
-            xv[q] = x4[q];
-        }
+        for (int q = 0; q < RG / 4; q++) wv[q] = w4[q];
+        for (int tt = ts; tt < RT_TOK; tt += TS) {
+            const int t = t0 + tt;
+            if (t >= T) break;
+            const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * H + g * RG);
+            float4 xv[RG / 4];
 #pragma unroll
-        for (int q = 0; q < RG / 4; q++) {
-            acc = __builtin_fmaf(wv[q].x, xv[q].x, acc);
-            acc = __builtin_fmaf(wv[q].y, xv[q].y, acc);
-            acc = __builtin_fmaf(wv[q].z, xv[q].z, acc);
-            acc = __builtin_fmaf(wv[q].w, xv[q].w, acc);
+            for (int q = 0; q < RG / 4; q++) xv[q] = x4[q];
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < RG / 4; q++) {
+                acc = __builtin_fmaf(wv[q].x, xv[q].x, acc);
+                acc = __builtin_fmaf(wv[q].y, xv[q].y, acc);
+                acc = __builtin_fmaf(wv[q].z, xv[q].z, acc);
+                acc = __builtin_fmaf(wv[q].w, xv[q].w, acc);
+            }
+            gp[tt][g] = acc;
         }
     }
-    gp[tid] = acc;
     __syncthreads();
-    if (tid == 0) {
+    if (tid < RT_TOK && t0 + tid < T) {
+        const float4 *p4 = reinterpret_cast<const float4 *>(gp[tid]);
         float tot = 0.0f;
-        for (int g = 0; g < G; g++) tot = tot + gp[g];
-        raw[(size_t)t * E + e] = tot;
+#pragma unroll 4
+        for (int q = 0; q < G / 4; q++) {
+            const float4 v = p4[q];
+            tot = tot + v.x; tot = tot + v.y; tot = tot + v.z; tot = tot + v.w;
+        }
+        raw[(size_t)(t0 + tid) * E + e] = tot;
     }
 }
 
@@ -1018,15 +1034,34 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
 
 constexpr int GR_THREADS = 1024;
 
+// Exclusive prefix sum of one int per thread over threads 0..255 (values of
+// threads >= n count as 0), through one shuffle scan per wave and the wave
+// totals in LDS (tmp[4]).  Every thread of the block must call it.
+TG_DEV int scan_256(int v, int n, int *tmp) {
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
+    int x = tid < n ? v : 0;
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int y = __shfl_up(x, o, WAVE);
+        if (lane >= o) x += y;
+    }
+    if (tid < 4 * WAVE && lane == WAVE - 1) tmp[wv] = x;
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < wv && i < 4; i++) base += tmp[i];
+    __syncthreads();
+    return x - (tid < n ? v : 0) + base;
+}
+
 // Work list: the entries of each expert cut into chunks of at most `ch`
 // (gate/up) and `chd` (down) entries; item w = (expert, first entry, count)
 // in work[3 * w ..], the number of items in work_n[0] (gate/up) and
-// work_n[1] (down; its items start at work + 3 * wmax).
+// work_n[1] (down; its items start at work + 3 * wmax).  Thread e handles
+// expert e: its count, offset and work items come from block scans.
 __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict__ idx, int n, int E, int ch, int chd,
                                                       int wmax, int32_t *__restrict__ counts,
                                                       int32_t *__restrict__ offsets, int32_t *__restrict__ entries,
                                                       int32_t *__restrict__ work, int32_t *__restrict__ work_n) {
-    __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E];
+    __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E], tmp[4];
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += GR_THREADS) {
         cnt[e] = 0;
@@ -1039,33 +1074,34 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = acc;
-            acc += cnt[e];
+    const int c = tid < E ? cnt[tid] : 0;
+    const int ng = (c + ch - 1) / ch, nd = (c + chd - 1) / chd;
+    const int o = scan_256(c, E, tmp);
+    const int bg = scan_256(ng, E, tmp);
+    const int bd = scan_256(nd, E, tmp);
+    if (tid < E) {
+        off[tid] = o;
+        offsets[tid] = o;
+        counts[tid] = c;
+        for (int i = 0; i < ng && bg + i < wmax; i++) {
+            int32_t *it = work + 3 * (size_t)(bg + i);
+            it[0] = tid;
+            it[1] = o + i * ch;
+            it[2] = c - i * ch < ch ? c - i * ch : ch;
         }
-        off[E] = acc;
+        for (int i = 0; i < nd && bd + i < wmax; i++) {
+            int32_t *it = work + 3 * ((size_t)wmax + bd + i);
+            it[0] = tid;
+            it[1] = o + i * chd;
+            it[2] = c - i * chd < chd ? c - i * chd : chd;
+        }
+        if (tid == E - 1) {
+            offsets[E] = o + c;
+            work_n[0] = bg + ng < wmax ? bg + ng : wmax;
+            work_n[1] = bd + nd < wmax ? bd + nd : wmax;
+        }
     }
     __syncthreads();
-    if (tid < 2) {
-        // two lists, one per thread; sizes bounded by E + n / ch <= wmax
-        const int c = tid == 0 ? ch : chd;
-        int32_t *wl = work + (size_t)tid * 3 * wmax;
-        int w = 0;
-        for (int e = 0; e < E; e++)
-            for (int c0 = 0; c0 < cnt[e] && w < wmax; c0 += c) {
-                wl[3 * w] = e;
-                wl[3 * w + 1] = off[e] + c0;
-                wl[3 * w + 2] = cnt[e] - c0 < c ? cnt[e] - c0 : c;
-                w++;
-            }
-        work_n[tid] = w;
-    }
-    for (int e = tid; e <= E; e += GR_THREADS) {
-        offsets[e] = off[e];
-        if (e < E) counts[e] = cnt[e];
-    }
     for (int i = tid; i < n; i += GR_THREADS) {
         int e = idx[i];
         e = e < 0 ? 0 : (e >= E ? E - 1 : e);
@@ -1301,7 +1337,7 @@ hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, fl
         hipLaunchKernelGGL(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
                            T, E, H, raw);
     } else {
-        hipLaunchKernelGGL(k_route, dim3(E, T), dim3(RT_THREADS), 0, st, Wr, x, E, H, raw);
+        hipLaunchKernelGGL(k_route, dim3(E, cdiv((size_t)T, RT_TOK)), dim3(RT_THREADS), 0, st, Wr, x, T, E, H, raw);
     }
     return hipGetLastError();
 }
