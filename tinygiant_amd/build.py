@@ -50,13 +50,18 @@ def _run(cmd, verbose):
         print(out)
 
 
+# Per-source extra flags.  tg_mfma.hip: MFMA results in ordinary VGPRs, so the
+# fp32 epilogue reads them without a v_accvgpr_read per element.
+EXTRA_FLAGS = {"tg_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source for gfx950 and link libtinygiant.so."""
     BUILD.mkdir(exist_ok=True)
     objs = []
     for src in SOURCES:
         obj = BUILD / (Path(src).stem + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", CSRC / src, "-o", obj], verbose)
+        _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", CSRC / src, "-o", obj], verbose)
         objs.append(obj)
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)

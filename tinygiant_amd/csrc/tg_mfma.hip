@@ -213,10 +213,6 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
                     tbv[mt] = *reinterpret_cast<const v4i *>(tq + (size_t)mt * 32 * MF_TS + bl * 32);
                     dx[mt] = xq[bl * M + mt * 32];
                 }
-                v16i r0[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    r0[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[mt], cmag, 0, 0, 0);
                 float dw[16], cw[16];
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
@@ -225,13 +221,20 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
                 }
 #pragma unroll
                 for (int r = 0; r < 16; r++) cw[r] = -MAGIC_F * dw[r];
+                // tile mt + 1's MFMA is issued before tile mt's epilogue: two
+                // result sets live at a time, which keeps them in VGPRs
+                v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[0], cmag, 0, 0, 0);
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++)
+                for (int mt = 0; mt < MT; mt++) {
+                    v16i rn;
+                    if (mt + 1 < MT) rn = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[mt + 1], cmag, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
-                        const float u = __builtin_fmaf(__int_as_float(r0[mt][r]), dw[r], cw[r]);
+                        const float u = __builtin_fmaf(__int_as_float(rc[r]), dw[r], cw[r]);
                         acc[mt][r] = __builtin_fmaf(u, dx[mt], acc[mt][r]);
                     }
+                    if (mt + 1 < MT) rc = rn;
+                }
             }
         }
         if (ch + 1 < nch) commit(q ^ 1);
