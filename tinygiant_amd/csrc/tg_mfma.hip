@@ -36,7 +36,6 @@ namespace tg {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int MF_THREADS = 256;        // four waves, one weight tile each
 constexpr int MF_PF = 4;               // Q4_0 blocks of A prefetched ahead (per wave)
 constexpr int MF_KC = 8;               // Q4_0 blocks per staged activation chunk
 constexpr int MF_TS = MF_KC * 32 + 16;  // LDS bytes per staged activation row (16 pad)
@@ -64,19 +63,23 @@ TG_DEV v4i nib_hi(uint4 w) {
 // [MF_KC][M] activation scales, then per wave two [MF_KC][2][16] tables of
 // weight scales.  Gate/up's hand-off of the up sums (2 tiles x MT x 16
 // registers x 64 lanes) reuses the activation buffers after the block loop.
-__host__ __device__ inline size_t mf_lds_bytes(int mt) {
+__host__ __device__ inline size_t mf_lds_bytes(int mt, int nw) {
     const size_t m = 32 * (size_t)mt;
-    return 2 * m * MF_TS + 2 * MF_KC * m * 4 + 4 * 2 * MF_KC * 32 * 4;
+    return 2 * m * MF_TS + 2 * MF_KC * m * 4 + (size_t)nw * 2 * MF_KC * 32 * 4;
 }
 
-// PAIR: gate/up.  Waves 0/1 of a block take gate/up of tile 2x, waves 2/3
-// gate/up of tile 2x+1; after the block loop the up waves hand their sums
-// to the gate waves through LDS, which apply SwiGLU and Q8_0 and write h.
-// Otherwise down: four tiles of down rows per block, fp32 rows out.
+// waves per block: 8 at four M-tiles (two waves per SIMD share one staged
+// activation tile), else 4
+__host__ __device__ constexpr int mf_waves(int mt) { return mt >= 4 ? 8 : 4; }
+
+// PAIR: gate/up.  Waves 2i / 2i+1 of a block take gate / up of tile
+// (NW/2) x + i; after the block loop the up waves hand their sums to the
+// gate waves through LDS, which apply SwiGLU and Q8_0 and write h.
+// Otherwise down: NW tiles of down rows per block, fp32 rows out.
 // Activations are indexed by token (entry / k) for gate/up and by entry for
 // down.
-template <int MT, bool PAIR>
-__global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__restrict__ layer_pl, Shape s,
+template <int MT, bool PAIR, int NW = mf_waves(MT)>
+__global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restrict__ layer_pl, Shape s,
                                                              const int32_t *__restrict__ work,
                                                              const int32_t *__restrict__ work_n,
                                                              const int32_t *__restrict__ entries,
@@ -85,10 +88,12 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
                                                              float *__restrict__ od, int *__restrict__ os,
                                                              float *__restrict__ D) {
     constexpr int M = MT * 32;
+    constexpr int NT = NW * 64;                      // threads per block
     constexpr int TP = 2 * MF_KC;                    // 16-byte pieces per row and chunk
-    constexpr int NTP = M * TP / MF_THREADS;         // pieces staged per thread
-    constexpr int NDX = M * MF_KC / MF_THREADS;      // activation scales staged per thread
-    static_assert(MF_THREADS % TP == 0 && MF_THREADS % MF_KC == 0 && MF_KC % MF_PF == 0, "staging map");
+    constexpr int NTP = M * TP / NT;                 // pieces staged per thread
+    constexpr int NDX = M * MF_KC / NT;              // activation scales staged per thread
+    static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC % MF_PF == 0, "staging map");
+    static_assert(NTP >= 1 && NDX >= 1 && (M * TP) % NT == 0 && (M * MF_KC) % NT == 0, "staging map");
     extern __shared__ __align__(16) uint8_t smem[];
     const int wi = blockIdx.y;
     if (wi >= work_n[0]) return;  // uniform over the block
@@ -101,13 +106,13 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
     float *dxl = reinterpret_cast<float *>(smem + 2 * M * MF_TS);             // [2][MF_KC][M]
     float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 32);               // [2][MF_KC][2][16]
 
-    // staging map: piece p of row t = tid / TP + u * (256 / TP); scale of
-    // block tid % MF_KC of row tid / MF_KC + u * (256 / MF_KC)
+    // staging map: piece p of row t = tid / TP + u * (NT / TP); scale of
+    // block tid % MF_KC of row tid / MF_KC + u * (NT / MF_KC)
     const int sp = tid % TP, sb = tid % MF_KC;
     int toff[NTP], doff[NDX];
 #pragma unroll
     for (int u = 0; u < NTP; u++) {
-        const int t = tid / TP + u * (MF_THREADS / TP);
+        const int t = tid / TP + u * (NT / TP);
         toff[u] = -1;
         if (t < c) {
             const int ent = entries[o + t];
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
     }
 #pragma unroll
     for (int u = 0; u < NDX; u++) {
-        const int t = tid / MF_KC + u * (MF_THREADS / MF_KC);
+        const int t = tid / MF_KC + u * (NT / MF_KC);
         doff[u] = -1;
         if (t < c) {
             const int ent = entries[o + t];
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
     // this wave's weight tile; an out-of-range tile computes on row n and
     // stores nothing
     const int mat = PAIR ? (wave & 1) : 0;  // 0 gate / down, 1 up
-    const int nt = PAIR ? blockIdx.x * 2 + (wave >> 1) : blockIdx.x * 4 + wave;
+    const int nt = PAIR ? blockIdx.x * (NW / 2) + (wave >> 1) : blockIdx.x * NW + wave;
     const bool valid = nt * 32 < rows;
     const int R = valid ? nt * 32 + n : n;
     const uint8_t *ex = layer_pl + (size_t)e * s.EB;
@@ -162,12 +167,12 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_grouped(const uint8_t *__re
     auto commit = [&](int q) {
 #pragma unroll
         for (int u = 0; u < NTP; u++) {
-            const int t = tid / TP + u * (MF_THREADS / TP);
+            const int t = tid / TP + u * (NT / TP);
             *reinterpret_cast<uint4 *>(tokl + ((size_t)q * M + t) * MF_TS + sp * 16) = sv[u];
         }
 #pragma unroll
         for (int u = 0; u < NDX; u++) {
-            const int t = tid / MF_KC + u * (MF_THREADS / MF_KC);
+            const int t = tid / MF_KC + u * (NT / MF_KC);
             dxl[(q * MF_KC + sb) * M + t] = sd[u];
         }
         if (h == 0) {
@@ -320,20 +325,20 @@ bool mfma_shape_ok(const Shape &s) {
     return s.I % 32 == 0 && s.H % 32 == 0 && s.k <= MAX_K;
 }
 
-template <int MT, bool PAIR>
+template <int MT, bool PAIR, int NW = mf_waves(MT)>
 static hipError_t mf_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work, const int32_t *work_n,
                         const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
                         float *D, hipStream_t st) {
     const int rows = PAIR ? s.I : s.H;
-    const size_t lds = mf_lds_bytes(MT);
-    const void *fn = reinterpret_cast<const void *>(&k_mfma_grouped<MT, PAIR>);
+    const size_t lds = mf_lds_bytes(MT, NW);
+    const void *fn = reinterpret_cast<const void *>(&k_mfma_grouped<MT, PAIR, NW>);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    // gate/up: two N-tiles (each as a gate wave and an up wave) per block
-    const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 64) : mf_cdiv((size_t)rows, 128);
-    hipLaunchKernelGGL((k_mfma_grouped<MT, PAIR>), dim3(gx, wmax), dim3(MF_THREADS), lds, st, layer_pl, s, work,
+    // gate/up: NW/2 tiles (each as a gate wave and an up wave) per block
+    const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (NW / 2)) : mf_cdiv((size_t)rows, 32 * NW);
+    hipLaunchKernelGGL((k_mfma_grouped<MT, PAIR, NW>), dim3(gx, wmax), dim3(NW * 64), lds, st, layer_pl, s, work,
                        work_n, entries, aq, ad, oq, od, os, D);
     return hipGetLastError();
 }
