@@ -43,6 +43,8 @@ sys.path.insert(0, str(ROOT))
 H, I, E, K_TOP = 2048, 768, 128, 8
 HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
 EXPERT_Q4_BYTES = 3 * I * (H // 32) * 18          # 2,654,208
+ROUTER_BYTES = E * H * 4                           # 1,048,576 (fp32 router of one layer)
+DECODE_PATHS = {"auto": 0, "persistent": 1, "per-layer": 2, "fused": 3, "routed": 4}
 GATEUP_BYTES_PER_EXPERT = 2 * I * (H // 32) * 18  # 1,769,472
 
 
@@ -182,7 +184,7 @@ def run_decode_stack(args, torch, call):
     arena = HBMExpertArena(L, E, H, I, K_TOP)
     for l in range(L):
         arena.synth_layer(l, args.seed)
-    arena.set_decode_path({"auto": 0, "persistent": 1, "per-layer": 2, "fused": 3}[args.path])
+    arena.set_decode_path(DECODE_PATHS[args.path])
     stream = torch.cuda.current_stream().cuda_stream
     X = torch.empty((W + K, H), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
@@ -220,9 +222,16 @@ def run_decode_stack(args, torch, call):
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     arena.status()
-    kern = kernel_times(call, ("persist", "route", "experts", "gateup", "down"))
+    kern = kernel_times(call, ("persist", "dec_part", "layer", "route", "experts", "gateup", "down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    if "persist" in kern:
+    if "layer" in kern:
+        # one launch = routing, gate/up and down of one layer (expert weights
+        # plus the next layer's router columns)
+        n_x, ms_x = kern["layer"]
+        avg = ms_x / max(n_x, 1) * 1e-3
+        roof_kernel, roof_bytes = "k_layer_dec", K_TOP * EXPERT_Q4_BYTES + ROUTER_BYTES
+        path = "routed"
+    elif "persist" in kern:
         # one launch = one token through all L layers
         n_p, ms_p = kern["persist"]
         avg = ms_p / n_p * 1e-3
@@ -697,7 +706,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--path", choices=["auto", "persistent", "per-layer", "fused"], default="auto",
+    ap.add_argument("--path", choices=list(DECODE_PATHS), default="auto",
                     help="decode path of one-token stack calls")
     args = ap.parse_args()
 

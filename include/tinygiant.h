@@ -191,16 +191,19 @@ int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
 int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
                                int n_layers, float eps, int32_t *topk_idx,
                                float *topk_w, void *stream);
-/* Decode path of one-token calls: FUSED (per layer a routing kernel and
- * one launch for gate/up and down, stack calls replayed as a HIP graph),
+/* Decode path of one-token calls: ROUTED (one launch per layer that also
+ * routes, from router partial sums the layer before it leaves; stack
+ * calls add one small prologue launch and replay as a HIP graph), FUSED
+ * (per layer a routing kernel and one launch for gate/up and down),
  * PER_LAYER (routing, gate/up and down as three kernels per layer),
  * PERSISTENT (one cooperative launch over every layer of a stack call;
- * error when the shape / device does not allow it), AUTO (FUSED where the
- * shape allows it, else PER_LAYER). */
+ * error when the shape / device does not allow it), AUTO (ROUTED where
+ * the shape allows it, else FUSED, else PER_LAYER). */
 #define TG_DECODE_AUTO 0
 #define TG_DECODE_PERSISTENT 1
 #define TG_DECODE_PER_LAYER 2
 #define TG_DECODE_FUSED 3
+#define TG_DECODE_ROUTED 4
 int tg_arena_set_decode_path(tg_arena *a, int path);
 /* Path of calls over n_tokens > 1 tokens (batched decode, prefill):
  * GROUPED (the (token, slot) pairs grouped by expert, each selected

@@ -1,9 +1,11 @@
-"""GPU parity of the one-token decode paths: FUSED (routing kernel, then one
-launch for gate/up and down with h handed over as tagged words) and
-PER_LAYER (routing, gate/up and down as three kernels).  Both must equal the
-oracle bit for bit, layer by layer and through a stack, and must agree with
-each other when calls alternate on one arena (the tag generations of the
-exchange words carry over between paths)."""
+"""GPU parity of the one-token decode paths: ROUTED (one launch per layer
+that also routes, from router partials the layer before it leaves), FUSED
+(routing kernel, then one launch for gate/up and down with h handed over as
+tagged words) and PER_LAYER (routing, gate/up and down as three kernels).
+All must equal the oracle bit for bit, layer by layer and through a stack
+(with the routing of every layer), and must agree with each other when
+calls alternate on one arena (the tag generations of the exchange words
+carry over between paths)."""
 import numpy as np
 import pytest
 
@@ -40,10 +42,10 @@ def make_arena(O, n_layers, H, I, E, k, seed):
     return a, layers, routers
 
 
-PATHS = {"fused": 3, "per_layer": 2}
+PATHS = {"routed": 4, "fused": 3, "per_layer": 2}
 
 
-@pytest.mark.parametrize("path", ["fused", "per_layer"])
+@pytest.mark.parametrize("path", ["routed", "fused", "per_layer"])
 @pytest.mark.parametrize("H,I,E,k", [(256, 64, 16, 4), (512, 96, 32, 8), (1024, 256, 64, 8), (2048, 768, 128, 8)])
 def test_one_token_layer_matches_oracle(O, tglib, path, H, I, E, k):
     gpu_note(f"one-token layer path={path} H={H} I={I} E={E} k={k}")
@@ -65,7 +67,7 @@ def test_one_token_layer_matches_oracle(O, tglib, path, H, I, E, k):
         a.close()
 
 
-@pytest.mark.parametrize("path", ["fused", "per_layer"])
+@pytest.mark.parametrize("path", ["routed", "fused", "per_layer"])
 @pytest.mark.parametrize("H,I,E,k,L", [(256, 64, 16, 4, 5), (2048, 768, 128, 8, 4)])
 def test_one_token_stack_matches_oracle(O, tglib, path, H, I, E, k, L):
     gpu_note(f"one-token stack path={path} H={H} L={L}")
@@ -86,16 +88,17 @@ def test_one_token_stack_matches_oracle(O, tglib, path, H, I, E, k, L):
 
 
 def test_paths_alternate_on_one_arena(O, tglib):
-    """Fused and per-layer calls interleaved on the same arena: each call's
-    words carry a fresh generation, so no call can read another's."""
+    """Routed, fused and per-layer calls interleaved on the same arena: each
+    call's words carry a fresh generation, so no call can read another's."""
     gpu_note("one-token paths alternating")
     from tinygiant_amd.moe import MoEBlock
     H, I, E, k = 512, 96, 32, 8
     a, layers, routers = make_arena(O, 2, H, I, E, k, seed=93)
+    order = ["routed", "fused", "routed", "per_layer", "fused", "routed", "routed", "per_layer", "fused"]
     try:
         blk = MoEBlock(a)
-        for rep in range(6):
-            a.set_decode_path(PATHS["fused"] if rep % 2 == 0 else PATHS["per_layer"])
+        for rep, path in enumerate(order):
+            a.set_decode_path(PATHS[path])
             layer = rep % 2
             x = O.synth_normal(93, O.stream_id(layer, rep, 4), 1.0, H).reshape(1, H)
             ref, ridx, _, _ = O.moe_layer(layers[layer], routers[layer], H, I, E, k, x)
@@ -122,6 +125,49 @@ def test_235b_shape_layer(O, tglib):
         assert np.array_equal(host(idx), ridx)
         assert np.array_equal(bits(host(w)), bits(rw))
         assert np.array_equal(bits(host(out)), bits(ref))
+        a.status()
+    finally:
+        a.close()
+
+
+@pytest.mark.parametrize("path", ["routed", "per_layer"])
+def test_stack_trace_matches_oracle(O, tglib, path):
+    """The routing of every layer of a stack call (trace entry point) and the
+    final x, against the oracle's stack trace."""
+    gpu_note(f"one-token stack trace path={path}")
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k, L = 1024, 256, 64, 8, 6
+    a, layers, routers = make_arena(O, L, H, I, E, k, seed=95)
+    try:
+        a.set_decode_path(PATHS[path])
+        x0 = O.synth_normal(95, O.stream_id(0, 2, 4), 1.0, H).reshape(1, H)
+        ref, trace = O.moe_stack(layers, routers, H, I, E, k, x0)
+        xd = dev(x0)
+        idx, w = MoEBlock(a).step_trace(xd)
+        assert np.array_equal(host(idx), trace[:, 0, :])
+        assert np.array_equal(bits(host(xd)), bits(ref))
+        a.status()
+    finally:
+        a.close()
+
+
+def test_routed_stack_sub_ranges(O, tglib):
+    """Routed stack calls over layer sub-ranges (the prologue forms the
+    partials of the first layer of each call) give the oracle's stack."""
+    gpu_note("routed stack sub-ranges")
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k, L = 512, 96, 32, 8, 5
+    a, layers, routers = make_arena(O, L, H, I, E, k, seed=96)
+    try:
+        a.set_decode_path(PATHS["routed"])
+        x0 = O.synth_normal(96, O.stream_id(0, 3, 4), 1.0, H).reshape(1, H)
+        ref, _ = O.moe_stack(layers, routers, H, I, E, k, x0)
+        xd = dev(x0)
+        blk = MoEBlock(a)
+        blk.step(xd, 0, 2)
+        blk.step(xd, 2, 1)
+        blk.step(xd, 3, 2)
+        assert np.array_equal(bits(host(xd)), bits(ref))
         a.status()
     finally:
         a.close()

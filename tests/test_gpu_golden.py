@@ -17,7 +17,7 @@ torch = pytest.importorskip("torch")
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "moe_q40_golden.npz")
 # decode paths (tg_arena_set_decode_path) and batch paths (tg_arena_set_batch_path)
-PATHS = {"fused": (3, 0), "per_layer": (2, 0), "grouped_mfma": (0, 1), "grouped_dot": (0, 3)}
+PATHS = {"routed": (4, 0), "fused": (3, 0), "per_layer": (2, 0), "grouped_mfma": (0, 1), "grouped_dot": (0, 3)}
 
 
 @pytest.fixture(scope="module")
@@ -67,7 +67,7 @@ def test_small_layer_golden_gpu(tglib, G, seed, path):
     assert np.array_equal(out, G[f"s{seed}_out"])
 
 
-@pytest.mark.parametrize("path", ["fused", "per_layer", "grouped_mfma"])
+@pytest.mark.parametrize("path", ["routed", "fused", "per_layer", "grouped_mfma"])
 def test_full_30b_layer_golden_gpu(tglib, G, path):
     gpu_note(f"golden 30B layer path={path}")
     out, idx, w = run_layer(2048, 768, 128, 8, 7, path)

@@ -66,14 +66,17 @@ class HBMExpertArena:
             pass
 
     # ------------------------------------------------------------ decode path
-    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER, DECODE_FUSED = 0, 1, 2, 3
+    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER, DECODE_FUSED, DECODE_ROUTED = 0, 1, 2, 3, 4
 
     def set_decode_path(self, path: int) -> None:
-        """One-token calls.  FUSED: per layer a routing kernel and one
-        launch for gate/up and down; PER_LAYER: routing, gate/up and down
-        as three kernels; PERSISTENT: one cooperative launch over every
-        layer of a stack call (error where the shape / device does not
-        allow it); AUTO: FUSED where the shape allows, else PER_LAYER."""
+        """One-token calls.  ROUTED: one launch per layer that also routes
+        (from router partial sums the layer before it leaves, plus one
+        prologue launch per call); FUSED: per layer a routing kernel and
+        one launch for gate/up and down; PER_LAYER: routing, gate/up and
+        down as three kernels; PERSISTENT: one cooperative launch over
+        every layer of a stack call (error where the shape / device does
+        not allow it); AUTO: ROUTED, else FUSED, else PER_LAYER, as the
+        shape allows."""
         call("tg_arena_set_decode_path", self.handle, int(path))
 
     BATCH_AUTO, BATCH_GROUPED, BATCH_PER_TOKEN, BATCH_GROUPED_DOT = 0, 1, 2, 3

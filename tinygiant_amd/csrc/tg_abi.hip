@@ -179,6 +179,8 @@ struct tg_arena {
     uint64_t *dec_hw = nullptr;
     uint32_t *dec_ctl = nullptr;
     uint32_t *dec_err = nullptr;
+    float *dec_part = nullptr;    // two router-partial buffers of the routed one-token path
+    uint64_t *dec_ow = nullptr;   // its group hand-off words
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
     float *xbuf = nullptr;        // T * H (host-pointer entry points)
@@ -367,16 +369,25 @@ extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float
     return TG_OK;
 }
 
-static size_t dec_bytes(const Shape &s, int T) {
+static size_t dec_words_bytes(const Shape &s, int T) {
     return 8 * ((size_t)T * s.E + tg::experts_fused_words(s)) + 8 * (size_t)T + 16;
 }
+
+static size_t dec_part_off(const Shape &s, int T) { return (dec_words_bytes(s, T) + 255) & ~(size_t)255; }
+
+static size_t dec_ow_off(const Shape &s, int T) {
+    return (dec_part_off(s, T) + 4 * tg::dec_part_floats(s) + 255) & ~(size_t)255;
+}
+
+static size_t dec_bytes(const Shape &s, int T) { return dec_ow_off(s, T) + 8 * tg::dec_ow_words(s); }
 
 static int arena_scratch(tg_arena *a, int T) {
     if (T <= a->cap_T) return TG_OK;
     drop_graphs(a);  // captured graphs point at the old buffers
     dfree(a->raw); dfree(a->dec); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf); dfree(a->grp);
     a->raw = nullptr; a->dec = nullptr; a->idx = nullptr; a->w = nullptr;
-    a->dec_lw = nullptr; a->dec_hw = nullptr; a->dec_ctl = nullptr; a->dec_err = nullptr;
+    a->dec_lw = nullptr; a->dec_hw = nullptr; a->dec_ctl = nullptr; a->dec_err = nullptr; a->dec_part = nullptr;
+    a->dec_ow = nullptr;
     a->xbuf = nullptr; a->obuf = nullptr; a->grp = nullptr;
     a->cap_T = 0;
     const Shape &s = a->s;
@@ -393,6 +404,8 @@ static int arena_scratch(tg_arena *a, int T) {
         a->dec_hw = a->dec_lw + (size_t)T * s.E;
         a->dec_ctl = reinterpret_cast<uint32_t *>(a->dec_hw + tg::experts_fused_words(s));
         a->dec_err = a->dec_ctl + 2 * (size_t)T;
+        a->dec_part = reinterpret_cast<float *>(a->dec + dec_part_off(s, T));
+        a->dec_ow = reinterpret_cast<uint64_t *>(a->dec + dec_ow_off(s, T));
     }
     if (ok) {
         // grouped path: every piece 256-byte aligned
@@ -487,15 +500,46 @@ static int layer_kernels_grouped(tg_arena *a, int layer, const float *x, float *
     return TG_OK;
 }
 
-// One token, gate/up and down in one launch (the default one-token path).
+// One token, one launch per layer that also routes (the default one-token
+// path where the shape allows it).
+static bool routed_usable(tg_arena *a, int T) {
+    return T == 1 && (a->decode_path == TG_DECODE_AUTO || a->decode_path == TG_DECODE_ROUTED) &&
+           tg::layer_dec_ok(a->s, a->n_cu);
+}
+
+// One token, gate/up and down in one launch after a routing kernel.
 static bool fused_usable(tg_arena *a, int T) {
     return T == 1 && (a->decode_path == TG_DECODE_AUTO || a->decode_path == TG_DECODE_FUSED) &&
            tg::experts_fused_ok(a->s, a->n_cu);
 }
 
+// Layers [l0, l0 + n) of one token on the routed path: the prologue forms the
+// first layer's router partials and reserves one generation per layer; layer
+// j reads the partials buffer j % 2 and leaves the next layer's in the
+// other.  Layer j's top-k ids / weights go to idx + j * k_step (k_step 0:
+// every layer overwrites the same k entries).
+static int routed_layers(tg_arena *a, int l0, int n, const float *x, float *out, const float *resid, float eps,
+                         int32_t *idx, float *w, int k_step, hipStream_t st) {
+    const Shape &s = a->s;
+    const size_t half = tg::dec_part_floats(s) / 2;
+    PROFILED("dec_part", st, tg::launch_dec_part(router_of(a, l0), x, s, a->dec_part, a->dec_ctl, n, st));
+    for (int j = 0; j < n; j++) {
+        const int l = l0 + j;
+        const float *wr_next = j + 1 < n ? router_of(a, l + 1) : nullptr;
+        PROFILED("layer", st,
+                 tg::launch_layer_dec(a->experts + (size_t)l * s.LB, s, a->n_cu, j == 0 ? x : out,
+                                      a->dec_part + (size_t)(j & 1) * half, wr_next,
+                                      a->dec_part + (size_t)((j + 1) & 1) * half, a->dec_hw, a->dec_ow, a->dec_ctl,
+                                      (uint32_t)(n - 1 - j), a->dec_err, j == 0 ? resid : out, out,
+                                      idx + (size_t)j * k_step, w + (size_t)j * k_step, eps, st));
+    }
+    return TG_OK;
+}
+
 static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T, float eps,
                          hipStream_t st) {
     if (grouped_usable(a, T)) return layer_kernels_grouped(a, layer, x, out, resid, T, eps, st);
+    if (routed_usable(a, T)) return routed_layers(a, layer, 1, x, out, resid, eps, a->idx, a->w, 0, st);
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
     PROFILED("route", st,
@@ -524,6 +568,7 @@ static int moe_layer_launch(tg_arena *a, int layer, const float *x, float *out, 
 
 // x <- x + MoE_l(x) for layers [l0, l0+n), in place.
 static int stack_launch(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
+    if (routed_usable(a, T)) return routed_layers(a, l0, n, x, x, x, eps, a->idx, a->w, 0, st);
     for (int l = l0; l < l0 + n; l++) {
         int rc = layer_kernels(a, l, x, x, x, T, eps, st);
         if (rc) return rc;
@@ -674,6 +719,7 @@ extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int
     if (a->decode_path == TG_DECODE_PERSISTENT)
         return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     const size_t k = (size_t)a->s.k;
+    if (routed_usable(a, 1)) return routed_layers(a, layer0, n_layers, x, x, x, eps, topk_idx, topk_w, (int)k, st);
     for (int l = 0; l < n_layers; l++) {
         if ((rc = layer_kernels(a, layer0 + l, x, x, x, 1, eps, st))) return rc;
         HIP_TRY(hipMemcpyAsync(topk_idx + l * k, a->idx, sizeof(int32_t) * k, hipMemcpyDeviceToDevice, st));
@@ -697,12 +743,14 @@ extern "C" int tg_arena_set_batch_path(tg_arena *a, int path) {
 extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
     if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER &&
-        path != TG_DECODE_FUSED)
+        path != TG_DECODE_FUSED && path != TG_DECODE_ROUTED)
         return set_err(TG_E_INVALID, "unknown decode path %d", path);
     if (path == TG_DECODE_PERSISTENT && !(a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s)))
         return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     if (path == TG_DECODE_FUSED && !tg::experts_fused_ok(a->s, a->n_cu))
         return set_err(TG_E_UNSUPPORTED, "the fused expert launch is not available for this shape");
+    if (path == TG_DECODE_ROUTED && !tg::layer_dec_ok(a->s, a->n_cu))
+        return set_err(TG_E_UNSUPPORTED, "the routed one-token launch is not available for this shape");
     drop_graphs(a);
     a->decode_path = path;
     return TG_OK;

@@ -95,6 +95,20 @@ hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, int T, const i
 // routing generation ctl[1])
 bool experts_fused_ok(const Shape &s, int n_cu);
 size_t experts_fused_words(const Shape &s);
+
+// One-token layer with routing inside (k_layer_dec) and the prologue that
+// forms the first layer's router partials (k_dec_part).  part buffers hold
+// [E+1][H/32] floats, dec_part_floats() the size of two; the group hand-off
+// takes dec_ow_words() tagged words.
+bool layer_dec_ok(const Shape &s, int n_cu);
+size_t dec_part_floats(const Shape &s);
+size_t dec_ow_words(const Shape &s);
+hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, float *part, uint32_t *ctl, int n_layers,
+                           hipStream_t st);
+hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *part_in,
+                            const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow, const uint32_t *ctl,
+                            uint32_t back, uint32_t *err, const float *resid, float *out, int32_t *idx, float *w,
+                            float eps, hipStream_t st);
 hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_cu, const int32_t *idx, const float *w,
                                 const int8_t *xq, const float *xd, const int *xs, uint64_t *hw, const uint32_t *ctl,
                                 uint32_t *err, const float *resid, float *out, hipStream_t st);

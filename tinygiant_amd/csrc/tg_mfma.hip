@@ -23,8 +23,10 @@
 //   u   = fma(float_bits(D), dw_m, -1.5 * 2^23 * dw_m)   = round(S * dw_m)
 //         (the constant is exact: dw is a half)
 //   acc = fma(u, dx_n, acc)
-// dx_n is one value per lane; the 16 row scales dw_m a lane needs are read
-// from a per-wave LDS table kept in register order, shared by the M-tiles.
+// dx_n is one value per lane; the 16 row scales dw_m a lane needs, and
+// their -1.5 * 2^23 multiples, are read from a per-wave LDS table kept in
+// register order, shared by the M-tiles.  M-tiles past the item's last
+// entry are skipped (the loop is compiled once per active-tile count).
 // Gate/up then applies SwiGLU and Q8_0 per (entry, 32 rows): the 32 values
 // of one entry sit in lanes n and n + 32, 16 registers each.  Down writes
 // fp32 rows per entry for the combine.
@@ -35,6 +37,8 @@ namespace tg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+
+template <int N> struct Tiles { static constexpr int value = N; };
 
 constexpr int MF_PF = 4;               // Q4_0 blocks of A prefetched ahead (per wave)
 constexpr int MF_KC = 8;               // Q4_0 blocks per staged activation chunk
@@ -60,12 +64,13 @@ TG_DEV v4i nib_hi(uint4 w) {
 }
 
 // LDS: two chunk buffers of [M rows][MF_TS bytes] activations and
-// [MF_KC][M] activation scales, then per wave two [MF_KC][2][16] tables of
-// weight scales.  Gate/up's hand-off of the up sums (2 tiles x MT x 16
-// registers x 64 lanes) reuses the activation buffers after the block loop.
+// [MF_KC][M] activation scales, then per wave two [MF_KC][2][2][16] tables
+// of weight scales (per half: 16 dw, then their -1.5 * 2^23 multiples).
+// Gate/up's hand-off of the up sums (NW/2 tiles x MT x 16 registers x 64
+// lanes) reuses the activation buffers after the block loop.
 __host__ __device__ inline size_t mf_lds_bytes(int mt, int nw) {
     const size_t m = 32 * (size_t)mt;
-    return 2 * m * MF_TS + 2 * MF_KC * m * 4 + (size_t)nw * 2 * MF_KC * 32 * 4;
+    return 2 * m * MF_TS + 2 * MF_KC * m * 4 + (size_t)nw * 2 * MF_KC * 64 * 4;
 }
 
 // waves per block: 8 at four M-tiles (two waves per SIMD share one staged
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
 
     uint8_t *tokl = smem;                                                     // [2][M][MF_TS]
     float *dxl = reinterpret_cast<float *>(smem + 2 * M * MF_TS);             // [2][MF_KC][M]
-    float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 32);               // [2][MF_KC][2][16]
+    float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 64);               // [2][MF_KC][2][2][16]
 
     // staging map: piece p of row t = tid / TP + u * (NT / TP); scale of
     // block tid % MF_KC of row tid / MF_KC + u * (NT / MF_KC)
@@ -140,8 +145,9 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
     const size_t ntb = (size_t)rows * nb;
     const uint4 *q0 = reinterpret_cast<const uint4 *>(tb) + (size_t)R * nb;
     const uint16_t *s0 = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + (size_t)R * nb;
-    // slot of row n in the register-ordered scale table
-    const int wslot = ((n >> 2) & 1) * 16 + 4 * (n >> 3) + (n & 3);
+    // slot of row n in the register-ordered scale table: half (n / 4) % 2,
+    // register 4 (n / 8) + n % 4; its -1.5 * 2^23 multiple 16 slots on
+    const int wslot = ((n >> 2) & 1) * 32 + 4 * (n >> 3) + (n & 3);
 
     uint4 sv[NTP];
     float sd[NDX];
@@ -177,7 +183,11 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
         }
         if (h == 0) {
 #pragma unroll
-            for (int j = 0; j < MF_KC; j++) dwl[(q * MF_KC + j) * 32 + wslot] = h2f(ws[j]);
+            for (int j = 0; j < MF_KC; j++) {
+                const float d = h2f(ws[j]);
+                dwl[(q * MF_KC + j) * 64 + wslot] = d;
+                dwl[(q * MF_KC + j) * 64 + wslot + 16] = -MAGIC_F * d;
+            }
         }
     };
 
@@ -199,51 +209,68 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
     for (int r = 0; r < 16; r++) cmag[r] = (int)MAGIC_I;
     __syncthreads();
 
-    for (int ch = 0; ch < nch; ch++) {
-        const int q = ch & 1;
-        if (ch + 1 < nch) stage(ch + 1);
-        const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
-        const float *xq = dxl + q * MF_KC * M + n;
-        const float *wq = dwl + q * MF_KC * 32 + 16 * h;
+    // The block loop runs the item's active M-tiles only (tiles at or past
+    // c hold no entries); `na` is their count as a compile-time constant.
+    auto run = [&](auto na) {
+        constexpr int NA = decltype(na)::value;
+        for (int ch = 0; ch < nch; ch++) {
+            const int q = ch & 1;
+            if (ch + 1 < nch) stage(ch + 1);
+            const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
+            const float *xq = dxl + q * MF_KC * M + n;
+            const float *wq = dwl + q * MF_KC * 64 + 32 * h;
 #pragma unroll
-        for (int bl = 0; bl < MF_KC; bl++) {
-            const int b = ch * MF_KC + bl;
-            if (b < nb) {
-                const v4i wa = h ? nib_hi(w0[bl % MF_PF]) : nib_lo(w0[bl % MF_PF]);
-                if (b + MF_PF < nb) w0[bl % MF_PF] = q0[b + MF_PF];
-                v4i tbv[MT];
-                float dx[MT];
+            for (int bl = 0; bl < MF_KC; bl++) {
+                const int b = ch * MF_KC + bl;
+                if (b < nb) {
+                    const v4i wa = h ? nib_hi(w0[bl % MF_PF]) : nib_lo(w0[bl % MF_PF]);
+                    if (b + MF_PF < nb) w0[bl % MF_PF] = q0[b + MF_PF];
+                    v4i tbv[NA];
+                    float dx[NA];
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    tbv[mt] = *reinterpret_cast<const v4i *>(tq + (size_t)mt * 32 * MF_TS + bl * 32);
-                    dx[mt] = xq[bl * M + mt * 32];
-                }
-                float dw[16], cw[16];
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 v = *reinterpret_cast<const float4 *>(wq + bl * 32 + 4 * g);
-                    dw[4 * g] = v.x; dw[4 * g + 1] = v.y; dw[4 * g + 2] = v.z; dw[4 * g + 3] = v.w;
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r++) cw[r] = -MAGIC_F * dw[r];
-                // tile mt + 1's MFMA is issued before tile mt's epilogue: two
-                // result sets live at a time, which keeps them in VGPRs
-                v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[0], cmag, 0, 0, 0);
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    v16i rn;
-                    if (mt + 1 < MT) rn = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[mt + 1], cmag, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float u = __builtin_fmaf(__int_as_float(rc[r]), dw[r], cw[r]);
-                        acc[mt][r] = __builtin_fmaf(u, dx[mt], acc[mt][r]);
+                    for (int mt = 0; mt < NA; mt++) {
+                        tbv[mt] = *reinterpret_cast<const v4i *>(tq + (size_t)mt * 32 * MF_TS + bl * 32);
+                        dx[mt] = xq[bl * M + mt * 32];
                     }
-                    if (mt + 1 < MT) rc = rn;
+                    float dw[16], cw[16];
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const float4 v = *reinterpret_cast<const float4 *>(wq + bl * 64 + 4 * g);
+                        dw[4 * g] = v.x; dw[4 * g + 1] = v.y; dw[4 * g + 2] = v.z; dw[4 * g + 3] = v.w;
+                        const float4 u = *reinterpret_cast<const float4 *>(wq + bl * 64 + 16 + 4 * g);
+                        cw[4 * g] = u.x; cw[4 * g + 1] = u.y; cw[4 * g + 2] = u.z; cw[4 * g + 3] = u.w;
+                    }
+                    // tile mt + 1's MFMA is issued before tile mt's epilogue:
+                    // two result sets live at a time, which keeps them in VGPRs
+                    v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[0], cmag, 0, 0, 0);
+#pragma unroll
+                    for (int mt = 0; mt < NA; mt++) {
+                        v16i rn;
+                        if (mt + 1 < NA) rn = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, tbv[mt + 1], cmag, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const float u = __builtin_fmaf(__int_as_float(rc[r]), dw[r], cw[r]);
+                            acc[mt][r] = __builtin_fmaf(u, dx[mt], acc[mt][r]);
+                        }
+                        if (mt + 1 < NA) rc = rn;
+                    }
                 }
             }
+            if (ch + 1 < nch) commit(q ^ 1);
+            __syncthreads();
         }
-        if (ch + 1 < nch) commit(q ^ 1);
-        __syncthreads();
+    };
+    // (a three-tile variant spills registers: three active tiles run as four)
+    const int na = (c + 31) >> 5;
+    if constexpr (MT >= 4) {
+        if (na >= 3) run(Tiles<4>{});
+        else if (na == 2) run(Tiles<2>{});
+        else run(Tiles<1>{});
+    } else if constexpr (MT == 2) {
+        if (na >= 2) run(Tiles<2>{});
+        else run(Tiles<1>{});
+    } else {
+        run(Tiles<1>{});
     }
 
     if (PAIR) {

@@ -374,6 +374,41 @@ constexpr int RD_THREADS = 1024;  // several threads per expert in the ranking
 
 TG_DEV uint32_t next_gen(uint32_t g) { return g >= 0x7FFFFFFFu ? 1u : g + 1u; }
 
+// Top-k of E ranked keys (LDS) by a block of RD_THREADS threads: rank =
+// number of larger keys, tpe consecutive threads per expert (each counts a
+// slice of the keys, then a shuffle sum); sidx[rank] = expert for rank < k.
+// Ends with a barrier.
+TG_DEV void rank_topk(const uint64_t *keys, int E, int k, int *sidx) {
+    const int tid = threadIdx.x;
+    const int tpe = E <= RD_THREADS / 8 ? 8 : 4;
+    const int ee = tid / tpe, part = tid % tpe;
+    if (ee < E) {
+        const uint64_t my = keys[ee];
+        const int b0 = part * E / tpe, b1 = (part + 1) * E / tpe;
+        int cnt = 0;
+        for (int i = b0; i < b1; i++) cnt += keys[i] > my ? 1 : 0;
+        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, WAVE);
+        if (part == 0 && cnt < k) sidx[cnt] = ee;
+    }
+    __syncthreads();
+}
+
+// Renormalised softmax over the selected logits (engine.py:233-236) by one
+// wave, lane i < k holding slot j = k-1-i: e_i = exp(l - lmax) in
+// ascending order, numpy's pairwise sum, returns w_j = e / sum (lanes >= k
+// return 0).
+TG_DEV float topk_softmax_lane(const float *slog, const int *sidx, int k) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const float lmax = slog[sidx[0]];
+    const bool on = lane < k;
+    const float ex = on ? expf_tg(slog[sidx[on ? k - 1 - lane : 0]] - lmax) : 0.0f;
+    float sex[MAX_K];
+#pragma unroll
+    for (int i = 0; i < MAX_K; i++) sex[i] = __shfl(ex, i, WAVE);
+    const float sum = np_pairwise_sum(sex, k);
+    return on ? ex / sum : 0.0f;
+}
+
 __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restrict__ Wr, const float *__restrict__ x,
                                                           int E, int H, int k, float eps, uint64_t *__restrict__ lw,
                                                           uint32_t *__restrict__ ctl, uint32_t *__restrict__ err,
@@ -467,34 +502,13 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
         keys[tid] = rank_key(l, tid);
     }
     __syncthreads();
-    // rank = number of larger keys, tpe consecutive threads per expert
-    // (each counts a slice of the keys, then a shuffle sum)
-    const int tpe = E <= RD_THREADS / 8 ? 8 : 4;
-    const int ee = tid / tpe, part = tid % tpe;
-    if (ee < E) {
-        const uint64_t my = keys[ee];
-        const int b0 = part * E / tpe, b1 = (part + 1) * E / tpe;
-        int cnt = 0;
-        for (int i = b0; i < b1; i++) cnt += keys[i] > my ? 1 : 0;
-        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, WAVE);
-        if (part == 0 && cnt < k) sidx[cnt] = ee;
-    }
-    __syncthreads();
-    // renormalised softmax over the selected logits (engine.py:233-236), one
-    // lane per selected expert: e_i = exp(l - lmax) in ascending order,
-    // numpy's pairwise sum, w = e / sum
+    rank_topk(keys, E, k, sidx);
     if (tid < WAVE) {
-        const float lmax = slog[sidx[0]];
-        const bool on = tid < k;
-        const float ex = on ? expf_tg(slog[sidx[on ? k - 1 - tid : 0]] - lmax) : 0.0f;
-        float sex[MAX_K];
-#pragma unroll
-        for (int i = 0; i < MAX_K; i++) sex[i] = __shfl(ex, i, WAVE);
-        const float sum = np_pairwise_sum(sex, k);
-        if (on) {
+        const float wj = topk_softmax_lane(slog, sidx, k);
+        if (tid < k) {
             const int j = k - 1 - tid;
             idx[(size_t)t * k + j] = bad ? j : sidx[j];
-            w[(size_t)t * k + j] = bad ? 0.0f : ex / sum;
+            w[(size_t)t * k + j] = bad ? 0.0f : wj;
         }
     }
     if (tid == 0) {
@@ -538,21 +552,19 @@ __global__ __launch_bounds__(GU_THREADS) void k_gateup(const uint8_t *__restrict
     const uint8_t *ex = layer_pl + (size_t)e * s.EB;
     const size_t ntb = (size_t)I * nb;
     const int items = 2 * RT * nb;
+    // every thread loads (items past the end clamped to the last, unused):
+    // no branch between the loads, so all are in flight before the first wait
     uint4 wv[UNR];
-    uint16_t dv[UNR];
+    uint32_t dv[UNR];
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        const int p = u * GU_THREADS + tid;
-        wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        dv[u] = 0;
-        if (p < items) {
-            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
-            const int mat = rd >= RT ? 1 : 0;
-            const uint8_t *tb = ex + (size_t)mat * s.GB;
-            const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
-            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-        }
+        const int p = min(u * GU_THREADS + tid, items - 1);
+        const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+        const int mat = rd >= RT ? 1 : 0;
+        const uint8_t *tb = ex + (size_t)mat * s.GB;
+        const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
+        wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+        dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
     }
     if (tid < H / 8) reinterpret_cast<uint2 *>(xq)[tid] = reinterpret_cast<const uint2 *>(xq_g + (size_t)t * H)[tid];
     if (tid < nb) {
@@ -633,20 +645,16 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
     const size_t ntb = (size_t)H * nb;
     const int items = k * RD * nb;
     uint4 wv[UNR];
-    uint16_t dv[UNR];
+    uint32_t dv[UNR];
 #pragma unroll
-    for (int u = 0; u < UNR; u++) {
-        const int p = u * DN_THREADS + tid;
-        wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        dv[u] = 0;
-        if (p < items) {
-            const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            const int jj = rd / RD, row = r0 + (rd - jj * RD);
-            const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
-            const size_t o = (size_t)row * nb + b;
-            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-        }
+    for (int u = 0; u < UNR; u++) {  // clamped, unbranched loads (as k_gateup)
+        const int p = min(u * DN_THREADS + tid, items - 1);
+        const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
+        const int jj = rd / RD, row = r0 + (rd - jj * RD);
+        const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
+        const size_t o = (size_t)row * nb + b;
+        wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+        dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
     }
     // the token's Q8_0 h: k * I bytes, k * nbI scales and sums
     const size_t hbase = (size_t)t * k;
@@ -727,9 +735,12 @@ __host__ __device__ inline size_t fx_down_lds_bytes(int k, int I, int nbI, int r
            4 * (size_t)k * rd;
 }
 
+// The down part sits after the gate/up part: the reading waves fill it while
+// wave 0 may still be publishing the block's last unit from the gate/up part.
+__host__ __device__ inline size_t fx_down_off(const Shape &s) { return (gateup_lds_bytes(s.H, s.nbH) + 15) & ~(size_t)15; }
+
 __host__ __device__ inline size_t fx_lds_bytes(const Shape &s, int rd) {
-    const size_t a = gateup_lds_bytes(s.H, s.nbH), b = fx_down_lds_bytes(s.k, s.I, s.nbI, rd);
-    return a > b ? a : b;
+    return fx_down_off(s) + fx_down_lds_bytes(s.k, s.I, s.nbI, rd);
 }
 
 // Gate/up unit (m, j) in three steps, so a block can issue its down loads
@@ -738,38 +749,35 @@ __host__ __device__ inline size_t fx_lds_bytes(const Shape &s, int rd) {
 template <int UG>
 struct FxGu {
     uint4 wv[UG];
-    uint16_t dv[UG];
+    uint32_t dv[UG];
 };
 
+// (eid: the block's clamped expert ids by slot, in LDS)
 template <int UG>
-TG_DEV void fx_gu_load(const FxArgs &A, const Shape &s, int unit, FxGu<UG> &g) {
+TG_DEV void fx_gu_load(const uint8_t *layer_pl, const Shape &s, int unit, const int *eid, FxGu<UG> &g) {
     constexpr int RT = GU_ROWS;
     const int nb = s.nbH, I = s.I, tid = threadIdx.x;
     const int mI = I / RT, m = unit % mI, j = unit / mI, r0 = m * RT;
-    int e = A.idx[j];
-    e = e < 0 ? 0 : (e >= s.E ? s.E - 1 : e);
-    const uint8_t *ex = A.layer_pl + (size_t)e * s.EB;
+    const uint8_t *ex = layer_pl + (size_t)eid[j] * s.EB;
     const size_t ntb = (size_t)I * nb;
     const int items = 2 * RT * nb;
 #pragma unroll
-    for (int u = 0; u < UG; u++) {
-        const int p = u * FX_THREADS + tid;
-        g.wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        g.dv[u] = 0;
-        if (p < items) {
-            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
-            const int mat = rd >= RT ? 1 : 0;
-            const uint8_t *tb = ex + (size_t)mat * s.GB;
-            const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
-            g.wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-            g.dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-        }
+    for (int u = 0; u < UG; u++) {  // clamped, unbranched loads (as k_gateup)
+        const int p = min(u * FX_THREADS + tid, items - 1);
+        const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+        const int mat = rd >= RT ? 1 : 0;
+        const uint8_t *tb = ex + (size_t)mat * s.GB;
+        const size_t o = (size_t)(r0 + rd - mat * RT) * nb + b;
+        g.wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+        g.dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
     }
 }
 
-// ... the block dots against Q8_0(x * s) into U (LDS) ...
+// ... the block dots against Q8_0(x * s) into U (LDS; Q8_0 x copied in
+// from gxq / gxd / gxs first unless gxq is null, when it is already there) ...
 template <int UG>
-TG_DEV void fx_gu_dots(const FxArgs &A, const Shape &s, const FxGu<UG> &g, uint8_t *smem) {
+TG_DEV void fx_gu_dots(const int8_t *gxq, const float *gxd, const int *gxs, const Shape &s, const FxGu<UG> &g,
+                       uint8_t *smem) {
     constexpr int RT = GU_ROWS;
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
     int8_t *xq = reinterpret_cast<int8_t *>(smem);
@@ -777,10 +785,12 @@ TG_DEV void fx_gu_dots(const FxArgs &A, const Shape &s, const FxGu<UG> &g, uint8
     int *xs = reinterpret_cast<int *>(xd + round4(nb));
     float *U = reinterpret_cast<float *>(xs + round4(nb));
     const int items = 2 * RT * nb;
-    if (tid < H / 8) reinterpret_cast<uint2 *>(xq)[tid] = reinterpret_cast<const uint2 *>(A.xq)[tid];
-    if (tid < nb) {
-        xd[tid] = A.xd[tid];
-        xs[tid] = A.xs[tid];
+    if (gxq) {
+        if (tid < H / 8) reinterpret_cast<uint2 *>(xq)[tid] = reinterpret_cast<const uint2 *>(gxq)[tid];
+        if (tid < nb) {
+            xd[tid] = gxd[tid];
+            xs[tid] = gxs[tid];
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -799,7 +809,7 @@ TG_DEV void fx_gu_dots(const FxArgs &A, const Shape &s, const FxGu<UG> &g, uint8
 // tagged words.  Wave 0 alone does this part (lane r chains row r: gate
 // rows in lanes 0..31, up rows in 32..63) and needs no block barrier, so it
 // never waits for the down loads the block has in flight.
-TG_DEV void fx_gu_publish(const FxArgs &A, const Shape &s, int unit, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
+TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
     constexpr int RT = GU_ROWS;
     static_assert(2 * RT == 64, "one wave holds the gate and up rows of a unit");
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
@@ -900,22 +910,20 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     FxGu<UG> g;
     const int u0 = blockIdx.x;
     if (u0 < ng) {
-        fx_gu_load<UG>(A, s, u0, g);
-        fx_gu_dots<UG>(A, s, g, smem);
-        fx_gu_publish(A, s, u0, tag, hw, smem);
+        fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
+        fx_gu_dots<UG>(A.xq, A.xd, A.xs, s, g, smem);
+        fx_gu_publish(s, u0, tag, hw, smem);
     }
     // 2. this block's down weights (waves 3.., item p on down thread
     //    p % FX_DT), then further gate/up units
     const size_t ntb = (size_t)H * nb;
     const int items = k * RD * nb, dt = tid - FX_PT;
     uint4 wv[UD];
-    uint16_t dv[UD];
+    uint32_t dv[UD];
+    if (dt >= 0) {  // whole waves; clamped, unbranched loads inside (as k_gateup)
 #pragma unroll
-    for (int u = 0; u < UD; u++) {
-        const int p = u * FX_DT + dt;
-        wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        dv[u] = 0;
-        if (dt >= 0 && p < items) {
+        for (int u = 0; u < UD; u++) {
+            const int p = min(u * FX_DT + dt, items - 1);
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
             const int jj = rd / RD, row = r0 + (rd - jj * RD);
             const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
@@ -928,15 +936,15 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     // otherwise sink them next to their use)
     __asm__ volatile("" ::: "memory");
     for (int unit = u0 + gridDim.x; unit < ng; unit += gridDim.x) {
-        fx_gu_load<UG>(A, s, unit, g);
+        fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
         __syncthreads();  // wave 0 has read the previous unit's LDS
-        fx_gu_dots<UG>(A, s, g, smem);
-        fx_gu_publish(A, s, unit, tag, hw, smem);
+        fx_gu_dots<UG>(A.xq, A.xd, A.xs, s, g, smem);
+        fx_gu_publish(s, unit, tag, hw, smem);
     }
 
     // 3. waves 0..2 read h of every unit into LDS; then the down rows
-    int8_t *hq = reinterpret_cast<int8_t *>(smem);
-    float *hd = reinterpret_cast<float *>(smem + (size_t)k * I);
+    int8_t *hq = reinterpret_cast<int8_t *>(smem + fx_down_off(s));
+    float *hd = reinterpret_cast<float *>(hq + (size_t)k * I);
     int *hs = reinterpret_cast<int *>(hd + k * nbp);
     float *U = reinterpret_cast<float *>(hs + k * nbp);
     float *D = U + k * RD * ust;
@@ -978,6 +986,356 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ============================================================ one-token layer, routing inside
+// One launch per layer that also routes: the layer before it (or the
+// prologue k_dec_part, for the first layer of a call) leaves, per group g of
+// RG output rows, the router's partial sums of that group for this layer's
+// router, part[e][g] = fma chain over the group of W[e][i] * x[i] and
+// part[E][g] = fma chain of x[i]^2 (the chains k_route_dec forms).  The grid
+// has one block per chunk of `rd` output rows (rd = 8, 16 or 32; GQ = 32 / rd
+// chunks per group, the blocks of a group on one XCD).  Every block
+//   1. adds the G partials of each expert, and of the squares, in ascending
+//      group order (the order of k_route_dec), scales by the RMS factor,
+//      ranks, and forms the renormalised top-k weights: the same values in
+//      every block, from the same inputs by the same steps;
+//   2. forms Q8_0(x * s) in its LDS and runs its gate/up units as k_experts
+//      (units go to the blocks that do not own a group first), publishing h
+//      as tagged words;
+//   3. loads its down rows for the k experts (issued before it waits), reads
+//      every h word, dots, chains, combines and adds the residual (as
+//      k_experts);
+// and then, per group, the blocks other than the group's owner (its last
+// chunk) publish their combined rows as tagged words, and the owner, with
+// all RG rows, forms the next layer's partials of the group.  Waits: h (all
+// blocks) and the group's rows (owners); every block publishes what it owes
+// before it waits, so no wait depends on a block that is not running.
+// Tags: the prologue advances the generation word past every layer of the
+// call; a layer `back` launches before the call's last takes the
+// generation `back` steps before it.  Polls are bounded; when one runs out
+// the block sets *err and writes NaN rows (and NaN partials).
+constexpr int LD_PC = 16;  // float4 of partials per load round of one thread
+
+struct LdArgs {
+    const uint8_t *layer_pl;
+    const float *x;         // this layer's input row (H)
+    const float *part_in;   // [E + 1][G] partials of x for this layer's router
+    const float *wr_next;   // next layer's router [E][H], or null (no partials out)
+    float *part_out;        // [E + 1][G] partials of out for the next layer
+    uint64_t *hw;           // [2][FX_QW][k * I/32] tagged h blocks, word-major, by tag parity
+    uint64_t *ow;           // [2][H] tagged combined rows of the group hand-off, by tag parity
+    const uint32_t *ctl;    // ctl[1]: generation of the call's last layer
+    uint32_t back;          // launches of this call after this one
+    uint32_t *err;
+    const float *resid;
+    float *out;
+    int32_t *idx;           // this layer's top-k ids and weights (block 0 writes them)
+    float *w;
+    float eps;
+    int rd;                 // output rows per block (grid = H / rd)
+};
+
+// generation `back` steps before g in next_gen's cycle 1 .. 2^31 - 1
+TG_DEV uint32_t gen_back(uint32_t g, uint32_t back) {
+    const int64_t M = 0x7FFFFFFF;
+    int64_t v = ((int64_t)(g == 0u ? 1u : g) - 1 - (int64_t)back) % M;
+    if (v < 0) v += M;
+    return (uint32_t)(v + 1);
+}
+
+// Block b's chunk and role.  With NB % (8 GQ) == 0 the GQ chunks of group g
+// go to blocks that share b % 8 (one XCD when blocks are dealt round robin
+// over 8 XCDs); `rank` orders blocks for the gate/up units, non-owners
+// first.
+struct LdRole {
+    int chunk, group, q, rank;
+    bool owner;
+};
+
+TG_DEV LdRole ld_role(int b, int NB, int GQ) {
+    LdRole r;
+    if (NB % (8 * GQ) == 0) {
+        const int x = b % 8, q = (b / 8) % GQ, t = b / (8 * GQ);
+        r.group = t * 8 + x;
+        r.q = q;
+    } else {
+        r.group = b / GQ;
+        r.q = b % GQ;
+    }
+    r.chunk = r.group * GQ + r.q;
+    r.owner = r.q == GQ - 1;
+    const int n_groups = NB / GQ;
+    r.rank = r.owner ? n_groups * (GQ - 1) + r.group : r.group * (GQ - 1) + r.q;
+    return r;
+}
+
+// LDS: the gate/up part, then the down part (k_experts' layout for rd rows),
+// the group's RG combined rows and the next router's columns [E][RG + 1].
+__host__ __device__ inline size_t ld_lds_bytes(const Shape &s, int rd) {
+    return fx_down_off(s) + fx_down_lds_bytes(s.k, s.I, s.nbI, rd) + 4 * (size_t)RG + 4 * (size_t)s.E * (RG + 1);
+}
+
+template <int UG, int UD>
+__global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ __align__(16) uint64_t keys[MAX_E];
+    __shared__ float slog[MAX_E];
+    __shared__ int sidx[MAX_K];
+    __shared__ float sw[MAX_K];
+    __shared__ float ssc;
+    __shared__ int bad;
+    const int tid = threadIdx.x, k = s.k, E = s.E, H = s.H, I = s.I, G = H / RG, RD = A.rd, GQ = RG / RD;
+    const int nb = s.nbI, nbp = round4(nb), ust = round4(nb) + 4;
+    const int ng = (I / GU_ROWS) * k, NB = gridDim.x;
+    const LdRole role = ld_role(blockIdx.x, NB, GQ);
+    const int r0 = role.chunk * RD;
+    const uint32_t tag =
+        gen_back(__hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 A.back);
+    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QW;
+    uint64_t *ow = A.ow + (size_t)(tag & 1u) * H;
+    const bool nx = role.owner && A.wr_next;
+
+    // 0. loads that depend on nothing: x (blocks with gate/up units), the
+    //    residual rows, (owners) the next router's columns of the group, then
+    //    the partials
+    // x is read by the threads that quantize it (waves 1.., H / 8 of them)
+    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa;
+    const int u0 = role.rank;  // first gate/up unit
+    const int qt = tid - WAVE;
+    const bool qon = u0 < ng && qt >= 0 && qt < H / 8;
+    if (qon) {
+        xa = reinterpret_cast<const float4 *>(A.x)[2 * qt];
+        xb = reinterpret_cast<const float4 *>(A.x)[2 * qt + 1];
+    }
+    float rv = 0.0f;
+    if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+    float4 wn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (nx && tid < E * (RG / 4))
+        wn = reinterpret_cast<const float4 *>(A.wr_next + (size_t)(tid >> 3) * H + (size_t)role.group * RG)[tid & 7];
+    if (tid == 0) bad = 0;
+
+    // 1. routing: thread e <= E adds row e of the partials in ascending group
+    //    order (LD_PC float4 loaded per round, all before the adds), then
+    //    scale, rank, softmax
+    if (tid <= E) {
+        const float4 *row = reinterpret_cast<const float4 *>(A.part_in + (size_t)tid * G);
+        float tot = 0.0f;
+        for (int c = 0; c < G / 4; c += LD_PC) {
+            float4 pv[LD_PC];
+#pragma unroll
+            for (int q = 0; q < LD_PC; q++) pv[q] = row[min(c + q, G / 4 - 1)];
+#pragma unroll
+            for (int q = 0; q < LD_PC; q++)
+                if (c + q < G / 4) {
+                    tot = tot + pv[q].x; tot = tot + pv[q].y; tot = tot + pv[q].z; tot = tot + pv[q].w;
+                }
+        }
+        if (tid < E)
+            slog[tid] = tot;
+        else
+            ssc = rms_scale(tot, H, A.eps);
+    }
+    if (tid < k) sidx[tid] = 0;
+    __syncthreads();
+    const float sc = ssc;
+    if (tid < E) {
+        const float l = slog[tid] * sc;
+        slog[tid] = l;
+        keys[tid] = rank_key(l, tid);
+    }
+    __syncthreads();
+    rank_topk(keys, E, k, sidx);
+    // softmax on wave 0, Q8_0(x * s) into the gate/up LDS layout on waves 1..4
+    if (tid < WAVE) {
+        const float wj = topk_softmax_lane(slog, sidx, k);
+        if (tid < k) {
+            const int j = k - 1 - tid;
+            sw[j] = wj;
+            if (blockIdx.x == 0) {
+                A.idx[j] = sidx[j];
+                A.w[j] = wj;
+            }
+        }
+    }
+    int8_t *xq = reinterpret_cast<int8_t *>(smem);
+    float *xd = reinterpret_cast<float *>(xq + H);
+    int *xs = reinterpret_cast<int *>(xd + round4(s.nbH));
+    if (qon) {
+        const float v[8] = {xa.x * sc, xa.y * sc, xa.z * sc, xa.w * sc, xb.x * sc, xb.y * sc, xb.z * sc, xb.w * sc};
+        q8_group8(v, true, qt * 8, xq, xd, xs);
+    }
+    __syncthreads();  // sw, sidx, Q8_0 x
+
+    FxGu<UG> g;
+    if (u0 < ng) {
+        fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
+        fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
+        fx_gu_publish(s, u0, tag, hw, smem);
+    }
+    // 2. this block's down weights (waves 3.., item p on down thread
+    //    p % FX_DT), then further gate/up units
+    const size_t ntb = (size_t)H * nb;
+    const int items = k * RD * nb, dt = tid - FX_PT;
+    uint4 wv[UD];
+    uint32_t dv[UD];
+    if (dt >= 0) {  // whole waves; clamped, unbranched loads inside (as k_gateup)
+#pragma unroll
+        for (int u = 0; u < UD; u++) {
+            const int p = min(u * FX_DT + dt, items - 1);
+            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
+            const int jj = rdi / RD, row = r0 + (rdi - jj * RD);
+            const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
+            const size_t o = (size_t)row * nb + b;
+            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
+            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
+        }
+    }
+    __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
+    for (int unit = u0 + NB; unit < ng; unit += NB) {
+        fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
+        __syncthreads();  // wave 0 has read the previous unit's LDS
+        fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
+        fx_gu_publish(s, unit, tag, hw, smem);
+    }
+
+    // 3. waves 0..2 read h of every unit into LDS (after the gate/up part,
+    //    which wave 0 may still be reading); then the down rows
+    int8_t *hq = reinterpret_cast<int8_t *>(smem + fx_down_off(s));
+    float *hd = reinterpret_cast<float *>(hq + (size_t)k * I);
+    int *hs = reinterpret_cast<int *>(hd + k * nbp);
+    float *U = reinterpret_cast<float *>(hs + k * nbp);
+    float *D = U + k * RD * ust;
+    float *xo = D + k * RD;
+    float *wl = xo + RG;  // [E][RG + 1]
+    if (tid < FX_PT) {
+        for (int unit = tid; unit < ng; unit += FX_PT) {
+            uint32_t pay[FX_QW];
+            const bool ok = fx_read_unit(hw + unit, ng, tag, pay);
+            const int jj = unit / nb, b = unit - jj * nb;
+            uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
+#pragma unroll
+            for (int wd = 0; wd < 8; wd++) dq[wd] = pay[wd];
+            hd[jj * nbp + b] = __uint_as_float(pay[8]);
+            hs[jj * nbp + b] = (int)pay[9];
+            if (!ok) bad = 1;
+        }
+    }
+    if (nx && tid < E * (RG / 4)) {
+        const int e = tid >> 3, c = 4 * (tid & 7);
+        wl[e * (RG + 1) + c] = wn.x;
+        wl[e * (RG + 1) + c + 1] = wn.y;
+        wl[e * (RG + 1) + c + 2] = wn.z;
+        wl[e * (RG + 1) + c + 3] = wn.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < UD; u++) {
+        const int p = u * FX_DT + dt;
+        if (dt >= 0 && p < items) {
+            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
+            const int jj = rdi / RD;
+            const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
+                          8 * hs[jj * nbp + b];
+            U[rdi * ust + b] = (float)S * h2f(dv[u]);
+        }
+    }
+    __syncthreads();
+    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid / RD) * nbp, nb);
+    __syncthreads();
+    // combine; a non-owner publishes its rows to the group's owner
+    if (tid < RD) {
+        float acc = 0.0f;
+        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        float o = A.resid ? rv + acc : acc;
+        if (bad) o = __builtin_nanf("");
+        A.out[r0 + tid] = o;
+        if (A.wr_next) {
+            if (role.owner)
+                xo[role.q * RD + tid] = o;
+            else
+                ll_put(ow + r0 + tid, __float_as_uint(o), tag);
+        }
+    }
+    if (!nx) {  // uniform
+        if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // 4. (owners) the group's other rows, then the next layer's partials of
+    //    the group from its RG rows
+    const int gr0 = role.group * RG;
+    if (tid < RG - RD) {
+        const uint64_t *src = ow + gr0 + tid;
+        uint64_t v = ll_get(src);
+        uint32_t tries = 0;
+        while ((uint32_t)(v >> 32) != tag) {
+            if (++tries >= RD_SPIN_LIMIT) {
+                bad = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            v = ll_get(src);
+        }
+        xo[tid] = __uint_as_float((uint32_t)v);
+    }
+    __syncthreads();
+    const int gi = role.group;
+    if (tid < E) {
+        float aw = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RG; r++) aw = __builtin_fmaf(wl[tid * (RG + 1) + r], xo[r], aw);
+        A.part_out[(size_t)tid * G + gi] = bad ? __builtin_nanf("") : aw;
+    } else if (tid == E) {
+        float aq = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RG; r++) aq = __builtin_fmaf(xo[r], xo[r], aq);
+        A.part_out[(size_t)E * G + gi] = bad ? __builtin_nanf("") : aq;
+    }
+    if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Prologue of a one-token call: the partials of x for the router of the
+// call's first layer (block g: group g; thread e < E the chain of expert e,
+// thread E the chain of squares), and block 0 advances the generation word
+// by n_layers (one generation per layer launch of the call).
+__global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, const float *__restrict__ x, int E,
+                                                  int H, float *__restrict__ part, uint32_t *ctl, int n_layers) {
+    const int g = blockIdx.x, tid = threadIdx.x, G = H / RG;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)g * RG);
+    float4 xv[RG / 4];
+#pragma unroll
+    for (int q = 0; q < RG / 4; q++) xv[q] = x4[q];
+    if (tid < E) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)tid * H + (size_t)g * RG);
+        float4 wv[RG / 4];
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) wv[q] = w4[q];
+        float aw = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            aw = __builtin_fmaf(wv[q].x, xv[q].x, aw);
+            aw = __builtin_fmaf(wv[q].y, xv[q].y, aw);
+            aw = __builtin_fmaf(wv[q].z, xv[q].z, aw);
+            aw = __builtin_fmaf(wv[q].w, xv[q].w, aw);
+        }
+        part[(size_t)tid * G + g] = aw;
+    } else if (tid == E) {
+        float aq = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RG / 4; q++) {
+            aq = __builtin_fmaf(xv[q].x, xv[q].x, aq);
+            aq = __builtin_fmaf(xv[q].y, xv[q].y, aq);
+            aq = __builtin_fmaf(xv[q].z, xv[q].z, aq);
+            aq = __builtin_fmaf(xv[q].w, xv[q].w, aq);
+        }
+        part[(size_t)E * G + g] = aq;
+    }
+    if (g == 0 && tid == 0) {
+        uint32_t v = __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = 0; i < n_layers; i++) v = next_gen(v);
+        __hip_atomic_store(ctl + 1, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ================================================================ grouped
 // Batched decode / prefill: the (token, slot) pairs of a layer are grouped
 // by expert, so each selected expert's weights stream once for all of its
@@ -993,7 +1351,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
 //                    block m of h for that entry
 //   k_down_grouped   grid (H/32, E): rows [32g, 32g+32) of down of expert e
 //                    for every entry of its group -> D[entry][row]
-//   k_combine        grid (H/256, T): out = resid + sum_j w_j D[t*k+j] in
+//   k_combine        grid (H/1024, T): out = resid + sum_j w_j D[t*k+j] in
 //                    ascending logit order
 //
 // The position of an entry inside its group comes from LDS atomics and is
@@ -1033,6 +1391,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
 }
 
 constexpr int GR_THREADS = 1024;
+constexpr int GR_PER = 16;  // entries per thread per pass of k_group
 
 // Exclusive prefix sum of one int per thread over threads 0..255 (values of
 // threads >= n count as 0), through one shuffle scan per wave and the wave
@@ -1068,10 +1427,22 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         fill[e] = 0;
     }
     __syncthreads();
-    for (int i = tid; i < n; i += GR_THREADS) {
-        int e = idx[i];
-        e = e < 0 ? 0 : (e >= E ? E - 1 : e);  // never index outside the table
-        atomicAdd(&cnt[e], 1);
+    // GR_PER entries per thread per pass, loaded together before the atomics
+    // (one load latency per pass rather than one per entry)
+    for (int base = 0; base < n; base += GR_THREADS * GR_PER) {
+        int ev[GR_PER];
+#pragma unroll
+        for (int u = 0; u < GR_PER; u++) {
+            const int i = base + u * GR_THREADS + tid;
+            ev[u] = i < n ? idx[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < GR_PER; u++) {
+            if (base + u * GR_THREADS + tid < n) {
+                const int e = ev[u] < 0 ? 0 : (ev[u] >= E ? E - 1 : ev[u]);  // never index outside the table
+                atomicAdd(&cnt[e], 1);
+            }
+        }
     }
     __syncthreads();
     const int c = tid < E ? cnt[tid] : 0;
@@ -1102,11 +1473,22 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         }
     }
     __syncthreads();
-    for (int i = tid; i < n; i += GR_THREADS) {
-        int e = idx[i];
-        e = e < 0 ? 0 : (e >= E ? E - 1 : e);
-        const int pos = atomicAdd(&fill[e], 1);
-        entries[off[e] + pos] = i;
+    for (int base = 0; base < n; base += GR_THREADS * GR_PER) {
+        int ev[GR_PER];
+#pragma unroll
+        for (int u = 0; u < GR_PER; u++) {
+            const int i = base + u * GR_THREADS + tid;
+            ev[u] = i < n ? idx[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < GR_PER; u++) {
+            const int i = base + u * GR_THREADS + tid;
+            if (i < n) {
+                const int e = ev[u] < 0 ? 0 : (ev[u] >= E ? E - 1 : ev[u]);
+                const int pos = atomicAdd(&fill[e], 1);
+                entries[off[e] + pos] = i;
+            }
+        }
     }
 }
 
@@ -1151,19 +1533,15 @@ __global__ __launch_bounds__(NT) void k_gateup_grouped(const uint8_t *__restrict
     const size_t ntb = (size_t)s.I * nb;
     const int items = 64 * nb;
     uint4 wv[UNR];
-    uint16_t dv[UNR];
+    uint32_t dv[UNR];
 #pragma unroll
-    for (int u = 0; u < UNR; u++) {
-        const int p = u * NT + tid;
-        wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        dv[u] = 0;
-        if (p < items) {
-            const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
-            const uint8_t *tb = ex + (size_t)(rd >> 5) * s.GB;
-            const size_t ob = (size_t)(m * 32 + (rd & 31)) * nb + b;
-            wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
-            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
-        }
+    for (int u = 0; u < UNR; u++) {  // clamped, unbranched loads (as k_gateup)
+        const int p = min(u * NT + tid, items - 1);
+        const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
+        const uint8_t *tb = ex + (size_t)(rd >> 5) * s.GB;
+        const size_t ob = (size_t)(m * 32 + (rd & 31)) * nb + b;
+        wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
+        dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
     }
     for (int c0 = 0; c0 < c; c0 += tc) {
         const int nt = c - c0 < tc ? c - c0 : tc;
@@ -1255,17 +1633,12 @@ __global__ __launch_bounds__(RO_THREADS) void k_down_grouped(const uint8_t *__re
     const size_t ntb = (size_t)s.H * nb;
     const int items = 32 * nb;
     uint4 wv[UNR];
-    uint16_t dv[UNR];
+    uint32_t dv[UNR];
 #pragma unroll
-    for (int u = 0; u < UNR; u++) {
-        const int p = u * RO_THREADS + tid;
-        wv[u] = make_uint4(0u, 0u, 0u, 0u);
-        dv[u] = 0;
-        if (p < items) {
-            const size_t ob = (size_t)g * 32 * nb + p;
-            wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
-            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
-        }
+    for (int u = 0; u < UNR; u++) {  // clamped, unbranched loads (as k_gateup)
+        const size_t ob = (size_t)g * 32 * nb + min(u * RO_THREADS + tid, items - 1);
+        wv[u] = reinterpret_cast<const uint4 *>(tb)[ob];
+        dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[ob];
     }
     for (int c0 = 0; c0 < c; c0 += tc) {
         const int nt = c - c0 < tc ? c - c0 : tc;
@@ -1305,14 +1678,45 @@ __global__ __launch_bounds__(RO_THREADS) void k_down_grouped(const uint8_t *__re
     }
 }
 
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ D, const float *__restrict__ w, int H,
-                                                 int k, const float *resid, float *out) {
+// One column per thread: for out / resid pointers that are not 16-byte
+// aligned.
+__global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ D, const float *__restrict__ w, int H,
+                                                  int k, const float *resid, float *out) {
     const int t = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
     if (r >= H) return;
     float acc = 0.0f;
     for (int jj = k - 1; jj >= 0; jj--)
         acc = __builtin_fmaf(w[(size_t)t * k + jj], D[((size_t)t * k + jj) * H + r], acc);
     out[(size_t)t * H + r] = resid ? resid[(size_t)t * H + r] + acc : acc;
+}
+
+// Four columns per thread (H % 4 == 0): the k rows' float4 loads are issued
+// together, then folded in slot order k-1 .. 0 per column, as k_combine1.
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ D, const float *__restrict__ w, int H,
+                                                 int k, const float *resid, float *out) {
+    const int t = blockIdx.y, c4 = blockIdx.x * 256 + threadIdx.x, H4 = H >> 2;
+    if (c4 >= H4) return;
+    const float4 *D4 = reinterpret_cast<const float4 *>(D + (size_t)t * k * H) + c4;
+    float4 v[MAX_K];
+#pragma unroll
+    for (int jj = 0; jj < MAX_K; jj++)
+        if (jj < k) v[jj] = D4[(size_t)jj * H4];
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int jj = MAX_K - 1; jj >= 0; jj--) {
+        if (jj < k) {
+            const float wj = w[(size_t)t * k + jj];
+            acc.x = __builtin_fmaf(wj, v[jj].x, acc.x);
+            acc.y = __builtin_fmaf(wj, v[jj].y, acc.y);
+            acc.z = __builtin_fmaf(wj, v[jj].z, acc.z);
+            acc.w = __builtin_fmaf(wj, v[jj].w, acc.w);
+        }
+    }
+    if (resid) {
+        const float4 r = reinterpret_cast<const float4 *>(resid + (size_t)t * H)[c4];
+        acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
+    reinterpret_cast<float4 *>(out + (size_t)t * H)[c4] = acc;
 }
 
 // ================================================================ launchers
@@ -1453,6 +1857,54 @@ hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_c
     return experts_ud<4, 2>(A, s, st);
 }
 
+// One-token layer with routing inside: rd output rows per block, the
+// smallest of 8, 16, 32 that keeps the grid (H / rd blocks, one per CU at
+// most, all resident at once) within the CUs.
+static int ld_rows(const Shape &s, int n_cu) {
+    for (int rd = 8; rd <= RG; rd *= 2)
+        if (s.H % rd == 0 && s.H / rd <= n_cu) return rd;
+    return 0;
+}
+
+static int ld_ud(const Shape &s, int rd) { return (int)cdiv((size_t)s.k * rd * s.nbI, FX_DT); }
+
+bool layer_dec_ok(const Shape &s, int n_cu) {
+    const int rd = n_cu > 0 ? ld_rows(s, n_cu) : 0;
+    if (!rd) return false;
+    const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
+    return decode_shape_ok(s) && s.H % RG == 0 && (s.H / RG) % 4 == 0 && s.E * (RG / 4) <= FX_THREADS &&
+           s.E < 256 && s.k * rd <= FX_THREADS && s.H / 8 + WAVE <= FX_THREADS && ug <= 4 && ld_ud(s, rd) <= 6 &&
+           RG - rd <= FX_THREADS && ld_lds_bytes(s, rd) <= 160 * 1024;
+}
+
+hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, float *part, uint32_t *ctl, int n_layers,
+                           hipStream_t st) {
+    hipLaunchKernelGGL(k_dec_part, dim3(s.H / RG), dim3(256), 0, st, Wr, x, s.E, s.H, part, ctl, n_layers);
+    return hipGetLastError();
+}
+
+template <int UD>
+static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
+    const size_t lds = ld_lds_bytes(s, A.rd);
+    hipError_t e = allow_lds((const void *)k_layer_dec<4, UD>, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_layer_dec<4, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *part_in,
+                            const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow, const uint32_t *ctl,
+                            uint32_t back, uint32_t *err, const float *resid, float *out, int32_t *idx, float *w,
+                            float eps, hipStream_t st) {
+    if (!layer_dec_ok(s, n_cu)) return hipErrorInvalidValue;
+    const int rd = ld_rows(s, n_cu);
+    const LdArgs A{layer_pl, x, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
+    return ld_ud(s, rd) <= 2 ? ld_go<2>(A, s, st) : ld_go<6>(A, s, st);
+}
+
+size_t dec_part_floats(const Shape &s) { return 2 * (size_t)(s.H / RG) * (s.E + 1); }
+size_t dec_ow_words(const Shape &s) { return 2 * (size_t)s.H; }
+
 bool grouped_shape_ok(const Shape &s) {
     return decode_shape_ok(s) && 64 * s.nbH <= 16 * 512 && 32 * s.nbI <= 16 * RO_THREADS &&
            gu_grouped_lds(s.nbH) <= 160 * 1024 && dn_grouped_lds(s.nbI, s.I) <= 160 * 1024;
@@ -1541,7 +1993,12 @@ hipError_t launch_down_grouped(const uint8_t *layer_pl, const Shape &s, int n, c
 
 hipError_t launch_combine(const float *D, const float *w, int T, int H, int k, const float *resid, float *out,
                           hipStream_t st) {
-    hipLaunchKernelGGL(k_combine, dim3(cdiv((size_t)H, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
+    const bool vec = H % 4 == 0 && k <= MAX_K && ((uintptr_t)out & 15) == 0 && ((uintptr_t)resid & 15) == 0 &&
+                     ((uintptr_t)D & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_combine, dim3(cdiv((size_t)H / 4, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
+    else
+        hipLaunchKernelGGL(k_combine1, dim3(cdiv((size_t)H, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
     return hipGetLastError();
 }
 
