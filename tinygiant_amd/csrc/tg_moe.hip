@@ -332,6 +332,26 @@ TG_DEV void q8_group8(const float *v, bool on, int i0, int8_t *qs, float *dsc, i
     }
 }
 
+// Weighted combine of one output row over the k slots, acc = fma(w_j, D_j,
+// acc) for j = k-1 .. 0 (ascending logit order): D_j = D[j * stride + r],
+// both operands read from LDS eight slots per round before the fmas.
+TG_DEV float combine_slots(const float *sw, const float *D, int stride, int k, int r) {
+    float acc = 0.0f;
+    for (int c = k - 1; c >= 0; c -= 8) {
+        float dd[8], ww[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = c - q < 0 ? 0 : c - q;
+            dd[q] = D[j * stride + r];
+            ww[q] = sw[j];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (c - q >= 0) acc = __builtin_fmaf(ww[q], dd[q], acc);
+    }
+    return acc;
+}
+
 // Sequential row accumulation acc = fma(U_b, dx_b, acc), operands read from
 // LDS four at a time (U and dx 16-byte aligned).
 TG_DEV float chain4(const float *U, const float *dx, int nb) {
@@ -375,21 +395,32 @@ constexpr int RD_THREADS = 1024;  // several threads per expert in the ranking
 TG_DEV uint32_t next_gen(uint32_t g) { return g >= 0x7FFFFFFFu ? 1u : g + 1u; }
 
 // Top-k of E ranked keys (LDS) by a block of RD_THREADS threads: rank =
-// number of larger keys, tpe consecutive threads per expert (each counts a
-// slice of the keys, then a shuffle sum); sidx[rank] = expert for rank < k.
-// Ends with a barrier.
-TG_DEV void rank_topk(const uint64_t *keys, int E, int k, int *sidx) {
+// number of larger keys; sidx[rank] = expert for rank < k.  Thread t takes
+// expert t % EW (EW = E rounded up to a whole number of waves) against
+// slice t / EW of the keys, so all lanes of a wave read the same keys
+// (LDS broadcast); the slice counts meet in rcnt[] (LDS, zero on entry) by
+// LDS atomics.  Ends with a barrier.
+TG_DEV void rank_topk(const uint64_t *keys, int E, int k, int *sidx, int *rcnt) {
     const int tid = threadIdx.x;
-    const int tpe = E <= RD_THREADS / 8 ? 8 : 4;
-    const int ee = tid / tpe, part = tid % tpe;
-    if (ee < E) {
-        const uint64_t my = keys[ee];
-        const int b0 = part * E / tpe, b1 = (part + 1) * E / tpe;
+    // per-wave (scalar) slice arithmetic: a wave lies in one slice
+    const int ewv = (E + WAVE - 1) / WAVE, parts = (RD_THREADS / WAVE) / ewv;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int part = wv / ewv, e = tid - part * ewv * WAVE;
+    if (e < E && part < parts) {
+        const uint64_t my = keys[e];
+        const int b0 = part * E / parts, b1 = (part + 1) * E / parts;
         int cnt = 0;
-        for (int i = b0; i < b1; i++) cnt += keys[i] > my ? 1 : 0;
-        for (int o = 1; o < tpe; o <<= 1) cnt += __shfl_xor(cnt, o, WAVE);
-        if (part == 0 && cnt < k) sidx[cnt] = ee;
+        for (int c = b0; c < b1; c += 8) {  // 8 keys loaded per round, then compared
+            uint64_t kk[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) kk[q] = keys[min(c + q, b1 - 1)];
+#pragma unroll
+            for (int q = 0; q < 8; q++) cnt += (c + q < b1 && kk[q] > my) ? 1 : 0;
+        }
+        if (cnt) atomicAdd(rcnt + e, cnt);
     }
+    __syncthreads();
+    if (tid < E && rcnt[tid] < k) sidx[rcnt[tid]] = tid;
     __syncthreads();
 }
 
@@ -418,6 +449,7 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
     __shared__ __align__(16) float gp[RT_THREADS];
     __shared__ __align__(16) float gq[RT_THREADS];
     __shared__ __align__(16) uint64_t keys[MAX_E];
+    __shared__ int rcnt[MAX_E];
     __shared__ float slog[MAX_E];
     __shared__ int sidx[MAX_K];
     __shared__ float ssc;
@@ -500,9 +532,10 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
         const float l = __uint_as_float((uint32_t)v);
         slog[tid] = l;
         keys[tid] = rank_key(l, tid);
+        rcnt[tid] = 0;
     }
     __syncthreads();
-    rank_topk(keys, E, k, sidx);
+    rank_topk(keys, E, k, sidx, rcnt);
     if (tid < WAVE) {
         const float wj = topk_softmax_lane(slog, sidx, k);
         if (tid < k) {
@@ -621,7 +654,8 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
                                                      const int8_t *__restrict__ hq_g, const float *__restrict__ hd_g,
                                                      const int *__restrict__ hs_g, const float *resid, float *out) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RD = DN_RD;
+    constexpr int RD = DN_RD, lrd = 3;  // RD = 2^lrd
+    static_assert(RD == 1 << lrd, "down rows per block");
     const int k = s.k, nb = s.nbI, nbp = round4(nb), I = s.I, H = s.H, ust = round4(nb) + 4;
     const int tid = threadIdx.x;
     int8_t *hq = reinterpret_cast<int8_t *>(smem);
@@ -650,7 +684,7 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
     for (int u = 0; u < UNR; u++) {  // clamped, unbranched loads (as k_gateup)
         const int p = min(u * DN_THREADS + tid, items - 1);
         const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-        const int jj = rd / RD, row = r0 + (rd - jj * RD);
+        const int jj = rd >> lrd, row = r0 + (rd - (jj << lrd));
         const uint8_t *tb = layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
         const size_t o = (size_t)row * nb + b;
         wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
@@ -671,7 +705,7 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
         const int p = u * DN_THREADS + tid;
         if (p < items) {
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            const int jj = rd / RD;
+            const int jj = rd >> lrd;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
                           8 * hs[jj * nbp + b];
             U[rd * ust + b] = (float)S * h2f(dv[u]);
@@ -681,8 +715,7 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
     for (int rd = tid; rd < k * RD; rd += DN_THREADS) D[rd] = chain4(U + rd * ust, hd + (rd / RD) * nbp, nb);
     __syncthreads();
     if (tid < RD) {
-        float acc = 0.0f;
-        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        const float acc = combine_slots(sw, D, RD, k, tid);
         out[(size_t)t * H + r0 + tid] = resid ? rv + acc : acc;
     }
 }
@@ -697,10 +730,10 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
 //      block of h as FX_QW tagged words;
 //   2. issues, from waves 3.., the loads of its down unit (RD rows of down
 //      for all k experts), then runs any further gate/up units;
-//   3. waves 0..2 read the FX_QW words of every unit (thread u: unit u; the
-//      last word polled with coherent loads, the rest read through the L2;
-//      stored word-major, hw[w * units + u], so a wave's loads touch a few
-//      cache lines), then waves 3.. dot the down rows and the block chains,
+//   3. waves 0..2 read the FX_QW words of every unit (thread u: unit u; a
+//      unit's words fill one 128-byte line of their own, written by one
+//      store; the last word polled with coherent loads, the rest read
+//      through the L2), then waves 3.. dot the down rows and the block chains,
 //      combines and adds the residual for its RD rows.  The reading waves
 //      hold no down load, so their waits (vmcnt retires in order) never
 //      stand behind the down stream.
@@ -712,7 +745,8 @@ __global__ __launch_bounds__(DN_THREADS) void k_down(const uint8_t *__restrict__
 constexpr int FX_THREADS = 1024;
 constexpr int FX_PT = 3 * WAVE;              // threads that poll the h words (waves 0..2)
 constexpr int FX_DT = FX_THREADS - FX_PT;    // threads that load and dot the down rows
-constexpr int FX_QW = 10;
+constexpr int FX_QW = 10;                    // tagged words per unit of h
+constexpr int FX_QS = 16;                    // word stride of the units (one 128-byte line each)
 
 struct FxArgs {
     const uint8_t *layer_pl;
@@ -721,7 +755,7 @@ struct FxArgs {
     const int8_t *xq;
     const float *xd;
     const int *xs;
-    uint64_t *hw;         // [2][FX_QW][k * I/32] tagged h blocks, word-major, by tag parity
+    uint64_t *hw;         // [2][k * I/32][FX_QS] tagged h blocks, by tag parity
     const uint32_t *ctl;  // routing counter / generation of token 0
     uint32_t *err;
     const float *resid;
@@ -827,36 +861,35 @@ TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, 
         const uint32_t word = (uint32_t)(__shfl(q, l4, WAVE) & 255) | ((uint32_t)(__shfl(q, l4 + 1, WAVE) & 255) << 8) |
                               ((uint32_t)(__shfl(q, l4 + 2, WAVE) & 255) << 16) |
                               ((uint32_t)(__shfl(q, l4 + 3, WAVE) & 255) << 24);
-        const size_t ng = (size_t)(s.I / GU_ROWS) * s.k;
-        uint64_t *dst = hw + unit;
-        if (tid < 8) ll_put(dst + tid * ng, word, tag);
-        if (tid == 8) ll_put(dst + 8 * ng, __float_as_uint(dq), tag);
-        if (tid == 9) ll_put(dst + 9 * ng, (uint32_t)qsum, tag);
+        // lanes 0..7 the packed bytes, 8 the scale, 9 the sum: one store
+        const uint32_t pay = tid < 8 ? word : (tid == 8 ? __float_as_uint(dq) : (uint32_t)qsum);
+        if (tid < FX_QW) ll_put(hw + (size_t)unit * FX_QS + tid, pay, tag);
     }
 }
 
-// Reads the FX_QW tagged words of one unit (stride `ng` words apart):
-// polls the last word with coherent loads until it carries `tag`, then
-// reads the other words with plain loads (shared through the L2 by the
-// blocks of an XCD) and polls again only a word that still carries an old
-// tag.  Bounded; false when a poll ran out of tries.
-TG_DEV bool fx_read_unit(const uint64_t *src, int ng, uint32_t tag, uint32_t (&pay)[FX_QW]) {
+// Reads the FX_QW tagged words of one unit (its line at src): polls the
+// last word with coherent loads until it carries `tag`, then reads the
+// others with plain loads (the line holds this unit's words only, written
+// by one store, and is shared through the L2 by the blocks of an XCD), and
+// polls again only a word that still carries an old tag.  Bounded; false
+// when a poll ran out of tries.
+TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW]) {
     constexpr int LAST = FX_QW - 1;
     uint32_t tries = 0;
 #pragma unroll
     for (int i = 0; i < FX_QW; i++) pay[i] = 0u;
-    uint64_t v = ll_get(src + (size_t)LAST * ng);
+    uint64_t v = ll_get(src + LAST);
     while ((uint32_t)(v >> 32) != tag) {
         if (++tries >= RD_SPIN_LIMIT) return false;
         __builtin_amdgcn_s_sleep(2);
-        v = ll_get(src + (size_t)LAST * ng);
+        v = ll_get(src + LAST);
     }
     pay[LAST] = (uint32_t)v;
     __asm__ volatile("" ::: "memory");  // the plain loads stay after the poll
     uint32_t pend = 0;
     uint64_t w[LAST];
 #pragma unroll
-    for (int i = 0; i < LAST; i++) w[i] = src[(size_t)i * ng];
+    for (int i = 0; i < LAST; i++) w[i] = src[i];
 #pragma unroll
     for (int i = 0; i < LAST; i++) {
         if ((uint32_t)(w[i] >> 32) == tag)
@@ -867,7 +900,7 @@ TG_DEV bool fx_read_unit(const uint64_t *src, int ng, uint32_t tag, uint32_t (&p
     while (pend) {
 #pragma unroll
         for (int i = 0; i < LAST; i++)
-            if (pend >> i & 1u) w[i] = ll_get(src + (size_t)i * ng);
+            if (pend >> i & 1u) w[i] = ll_get(src + i);
 #pragma unroll
         for (int i = 0; i < LAST; i++)
             if ((pend >> i & 1u) && (uint32_t)(w[i] >> 32) == tag) {
@@ -888,6 +921,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     __shared__ int sidx[MAX_K];
     __shared__ float sw[MAX_K];
     const int tid = threadIdx.x, RD = A.rd, k = s.k, nb = s.nbI, nbp = round4(nb), I = s.I, H = s.H;
+    const int lrd = __builtin_ctz(RD);  // RD is a power of two
     const int ust = round4(nb) + 4;
     const uint32_t tag = __hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int r0 = blockIdx.x * RD, ng = (I / GU_ROWS) * k;
@@ -903,7 +937,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
 
     // h words of this layer: one of two buffers by tag parity, so a copy of
     // a line that an L2 still holds is at least two layers old
-    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QW;
+    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QS;
 
     // 1. the first gate/up unit: loads, dots (every wave), publication
     //    (wave 0)
@@ -925,7 +959,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
         for (int u = 0; u < UD; u++) {
             const int p = min(u * FX_DT + dt, items - 1);
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            const int jj = rd / RD, row = r0 + (rd - jj * RD);
+            const int jj = rd >> lrd, row = r0 + (rd - (jj << lrd));
             const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
             const size_t o = (size_t)row * nb + b;
             wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
@@ -951,7 +985,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     if (tid < FX_PT) {
         for (int unit = tid; unit < ng; unit += FX_PT) {
             uint32_t pay[FX_QW];
-            const bool ok = fx_read_unit(hw + unit, ng, tag, pay);
+            const bool ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
             const int jj = unit / nb, b = unit - jj * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
 #pragma unroll
@@ -967,18 +1001,17 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
         const int p = u * FX_DT + dt;
         if (dt >= 0 && p < items) {
             const int rd = (int)fdiv((uint32_t)p, s.divI), b = p - rd * nb;
-            const int jj = rd / RD;
+            const int jj = rd >> lrd;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
                           8 * hs[jj * nbp + b];
             U[rd * ust + b] = (float)S * h2f(dv[u]);
         }
     }
     __syncthreads();
-    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid / RD) * nbp, nb);
+    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid >> lrd) * nbp, nb);
     __syncthreads();
     if (tid < RD) {
-        float acc = 0.0f;
-        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        const float acc = combine_slots(sw, D, RD, k, tid);
         float o = A.resid ? rv + acc : acc;
         if (bad) o = __builtin_nanf("");
         A.out[r0 + tid] = o;
@@ -1021,7 +1054,7 @@ struct LdArgs {
     const float *part_in;   // [E + 1][G] partials of x for this layer's router
     const float *wr_next;   // next layer's router [E][H], or null (no partials out)
     float *part_out;        // [E + 1][G] partials of out for the next layer
-    uint64_t *hw;           // [2][FX_QW][k * I/32] tagged h blocks, word-major, by tag parity
+    uint64_t *hw;           // [2][k * I/32][FX_QS] tagged h blocks, by tag parity
     uint64_t *ow;           // [2][H] tagged combined rows of the group hand-off, by tag parity
     const uint32_t *ctl;    // ctl[1]: generation of the call's last layer
     uint32_t back;          // launches of this call after this one
@@ -1078,12 +1111,14 @@ template <int UG, int UD>
 __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ __align__(16) uint64_t keys[MAX_E];
+    __shared__ int rcnt[MAX_E];
     __shared__ float slog[MAX_E];
     __shared__ int sidx[MAX_K];
     __shared__ float sw[MAX_K];
     __shared__ float ssc;
     __shared__ int bad;
     const int tid = threadIdx.x, k = s.k, E = s.E, H = s.H, I = s.I, G = H / RG, RD = A.rd, GQ = RG / RD;
+    const int lrd = __builtin_ctz(RD);  // RD is a power of two
     const int nb = s.nbI, nbp = round4(nb), ust = round4(nb) + 4;
     const int ng = (I / GU_ROWS) * k, NB = gridDim.x;
     const LdRole role = ld_role(blockIdx.x, NB, GQ);
@@ -1091,7 +1126,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     const uint32_t tag =
         gen_back(__hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                  A.back);
-    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QW;
+    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QS;
     uint64_t *ow = A.ow + (size_t)(tag & 1u) * H;
     const bool nx = role.owner && A.wr_next;
 
@@ -1142,9 +1177,10 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         const float l = slog[tid] * sc;
         slog[tid] = l;
         keys[tid] = rank_key(l, tid);
+        rcnt[tid] = 0;
     }
     __syncthreads();
-    rank_topk(keys, E, k, sidx);
+    rank_topk(keys, E, k, sidx, rcnt);
     // softmax on wave 0, Q8_0(x * s) into the gate/up LDS layout on waves 1..4
     if (tid < WAVE) {
         const float wj = topk_softmax_lane(slog, sidx, k);
@@ -1183,7 +1219,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         for (int u = 0; u < UD; u++) {
             const int p = min(u * FX_DT + dt, items - 1);
             const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int jj = rdi / RD, row = r0 + (rdi - jj * RD);
+            const int jj = rdi >> lrd, row = r0 + (rdi - (jj << lrd));
             const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
             const size_t o = (size_t)row * nb + b;
             wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
@@ -1210,7 +1246,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     if (tid < FX_PT) {
         for (int unit = tid; unit < ng; unit += FX_PT) {
             uint32_t pay[FX_QW];
-            const bool ok = fx_read_unit(hw + unit, ng, tag, pay);
+            const bool ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
             const int jj = unit / nb, b = unit - jj * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
 #pragma unroll
@@ -1233,19 +1269,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         const int p = u * FX_DT + dt;
         if (dt >= 0 && p < items) {
             const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int jj = rdi / RD;
+            const int jj = rdi >> lrd;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
                           8 * hs[jj * nbp + b];
             U[rdi * ust + b] = (float)S * h2f(dv[u]);
         }
     }
     __syncthreads();
-    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid / RD) * nbp, nb);
+    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid >> lrd) * nbp, nb);
     __syncthreads();
     // combine; a non-owner publishes its rows to the group's owner
     if (tid < RD) {
-        float acc = 0.0f;
-        for (int jj = k - 1; jj >= 0; jj--) acc = __builtin_fmaf(sw[jj], D[jj * RD + tid], acc);
+        const float acc = combine_slots(sw, D, RD, k, tid);
         float o = A.resid ? rv + acc : acc;
         if (bad) o = __builtin_nanf("");
         A.out[r0 + tid] = o;
@@ -1827,7 +1862,7 @@ bool experts_fused_ok(const Shape &s, int n_cu) {
     return regs && s.H % rd == 0 && s.k * rd <= FX_THREADS && fx_lds_bytes(s, rd) <= 160 * 1024 && s.k <= MAX_K;
 }
 
-size_t experts_fused_words(const Shape &s) { return 2 * (size_t)s.k * s.nbI * FX_QW; }
+size_t experts_fused_words(const Shape &s) { return 2 * (size_t)s.k * s.nbI * FX_QS; }
 
 template <int UG, int UD>
 static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
