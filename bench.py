@@ -505,10 +505,14 @@ def run_235b(args, torch, call, T):
         blk.step(X[i])
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
-    names = ("route", "experts", "gateup", "down", "route_q8", "group", "gateup_mfma", "down_mfma", "combine")
+    names = ("dec_part", "layer", "route", "experts", "gateup", "down", "route_q8", "group", "gateup_mfma", "down_mfma",
+             "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    if "experts" in kern:
+    if "layer" in kern:
+        rk, rb = "layer", K5 * EXPERT5_BYTES + E5 * H5 * 4
+        roof = "k_layer_dec"
+    elif "experts" in kern:
         rk, rb = "experts", K5 * EXPERT5_BYTES
         roof = "k_experts"
     elif "gateup" in kern:

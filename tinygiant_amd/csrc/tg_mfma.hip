@@ -40,7 +40,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 template <int N> struct Tiles { static constexpr int value = N; };
 
-constexpr int MF_PF = 4;               // Q4_0 blocks of A prefetched ahead (per wave)
+// Q4_0 blocks of A prefetched ahead per wave: deeper where a block holds
+// one M-tile (little work per weight byte, the stream is latency-bound)
+__host__ __device__ constexpr int mf_pf(int mt) { return mt == 1 ? 8 : 4; }
 constexpr int MF_KC = 8;               // Q4_0 blocks per staged activation chunk
 constexpr int MF_TS = MF_KC * 32 + 16;  // LDS bytes per staged activation row (16 pad)
 constexpr uint32_t MAGIC_I = 0x4B400000u;
@@ -97,6 +99,7 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
     constexpr int TP = 2 * MF_KC;                    // 16-byte pieces per row and chunk
     constexpr int NTP = M * TP / NT;                 // pieces staged per thread
     constexpr int NDX = M * MF_KC / NT;              // activation scales staged per thread
+    constexpr int MF_PF = mf_pf(MT);
     static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC % MF_PF == 0, "staging map");
     static_assert(NTP >= 1 && NDX >= 1 && (M * TP) % NT == 0 && (M * MF_KC) % NT == 0, "staging map");
     extern __shared__ __align__(16) uint8_t smem[];
@@ -338,6 +341,240 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
     }
 }
 
+// ================================================================ one M-tile
+// Work items of at most 32 entries (batched decode, a few entries per expert):
+// the operands swap roles, A = the item's Q8_0 activations (lane h*32+m:
+// entry m, elements 16h .. 16h+15 of the block) and B = the weight nibbles
+// (lane h*32+n: weight row n), so lane l, register r of the result holds
+// (entry 8 (r/4) + 4h + r%4, weight row l % 32).  The weight scale is then one
+// value per lane, and the epilogue runs only the register groups (8 entries
+// each) that hold entries of the item.  Per block and entry group the same
+// steps as k_mfma_grouped: u = fma(D, dw, -1.5 * 2^23 * dw) = round(S * dw),
+// acc = fma(u, dx, acc), blocks in ascending order.  Gate/up: waves 2i / 2i+1
+// take gate / up of tile 2x + i, meet in LDS, and the gate wave applies
+// SwiGLU and Q8_0 to each entry's 32 rows (one per lane of a half-wave:
+// maximum and sum by row rotations and a swap of the rows).
+constexpr int MS_NW = 4;    // waves per block
+constexpr int MS_PF = 8;    // Q4_0 blocks of B prefetched ahead per wave
+
+__host__ __device__ inline size_t ms_lds_bytes() {
+    return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4 + (size_t)MS_NW * 2 * MF_KC * 32 * 4;
+}
+
+template <int CTRL>
+TG_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+TG_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false); }
+// lane ^ 16 inside each group of 32 lanes
+TG_DEV float swz16_f(float v) { return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)); }
+TG_DEV int swz16_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+
+// maximum (NaN never taken) and sum over the 32 lanes of a half-wave, in
+// every lane of it
+TG_DEV float half_max(float a) {
+    float o;
+    o = dpp_f<0x121>(a); a = o > a ? o : a;  // row_ror:1
+    o = dpp_f<0x122>(a); a = o > a ? o : a;  // row_ror:2
+    o = dpp_f<0x124>(a); a = o > a ? o : a;  // row_ror:4
+    o = dpp_f<0x128>(a); a = o > a ? o : a;  // row_ror:8
+    o = swz16_f(a); a = o > a ? o : a;
+    return a;
+}
+TG_DEV int half_sum(int v) {
+    v += dpp_i<0x121>(v);
+    v += dpp_i<0x122>(v);
+    v += dpp_i<0x124>(v);
+    v += dpp_i<0x128>(v);
+    v += swz16_i(v);
+    return v;
+}
+
+template <bool PAIR>
+__global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                           const int32_t *__restrict__ work,
+                                                           const int32_t *__restrict__ work_n,
+                                                           const int32_t *__restrict__ entries,
+                                                           const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                           int8_t *__restrict__ oq, float *__restrict__ od,
+                                                           int *__restrict__ os, float *__restrict__ D) {
+    constexpr int M = 32, NW = MS_NW, NT = NW * 64, TP = 2 * MF_KC;
+    constexpr int NTP = M * TP / NT, NDX = M * MF_KC / NT;
+    static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC % MS_PF == 0 && NTP >= 1 && NDX >= 1, "staging map");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wi = blockIdx.y;
+    if (wi >= work_n[0]) return;  // uniform over the block
+    const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
+    const int K = PAIR ? s.H : s.I, nb = K / QK, rows = PAIR ? s.I : s.H, k = s.k;
+    const int nch = (nb + MF_KC - 1) / MF_KC;
+
+    uint8_t *tokl = smem;                                                     // [2][M][MF_TS]
+    float *dxl = reinterpret_cast<float *>(smem + 2 * M * MF_TS);             // [2][MF_KC][M]
+    float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 32);               // [2][MF_KC][32]
+
+    const int sp = tid % TP, sb = tid % MF_KC;
+    int toff[NTP], doff[NDX];
+#pragma unroll
+    for (int u = 0; u < NTP; u++) {
+        const int t = tid / TP + u * (NT / TP);
+        toff[u] = -1;
+        if (t < c) toff[u] = (PAIR ? entries[o + t] / k : entries[o + t]) * K;
+    }
+#pragma unroll
+    for (int u = 0; u < NDX; u++) {
+        const int t = tid / MF_KC + u * (NT / MF_KC);
+        doff[u] = -1;
+        if (t < c) doff[u] = (PAIR ? entries[o + t] / k : entries[o + t]) * nb;
+    }
+
+    const int mat = PAIR ? (wave & 1) : 0;  // 0 gate / down, 1 up
+    const int nt = PAIR ? blockIdx.x * (NW / 2) + (wave >> 1) : blockIdx.x * NW + wave;
+    const bool valid = nt * 32 < rows;
+    const int R = valid ? nt * 32 + n : n;
+    const uint8_t *ex = layer_pl + (size_t)e * s.EB;
+    const uint8_t *tb = PAIR ? ex + (size_t)mat * s.GB : ex + 2 * s.GB;
+    const size_t ntb = (size_t)rows * nb;
+    const uint4 *q0 = reinterpret_cast<const uint4 *>(tb) + (size_t)R * nb;
+    const uint16_t *s0 = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + (size_t)R * nb;
+
+    uint4 sv[NTP];
+    float sd[NDX];
+    uint16_t ws[MF_KC];
+    auto stage = [&](int ch) {
+#pragma unroll
+        for (int u = 0; u < NTP; u++) {
+            const int kb = ch * MF_KC * 32 + sp * 16;
+            sv[u] = make_uint4(0u, 0u, 0u, 0u);
+            if (toff[u] >= 0 && kb < K) sv[u] = *reinterpret_cast<const uint4 *>(aq + toff[u] + kb);
+        }
+#pragma unroll
+        for (int u = 0; u < NDX; u++) {
+            const int b = ch * MF_KC + sb;
+            sd[u] = (doff[u] >= 0 && b < nb) ? ad[doff[u] + b] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < MF_KC; j++) {
+            const int b = ch * MF_KC + j;
+            ws[j] = (h == 0 && b < nb) ? s0[b] : (uint16_t)0;
+        }
+    };
+    auto commit = [&](int q) {
+#pragma unroll
+        for (int u = 0; u < NTP; u++) {
+            const int t = tid / TP + u * (NT / TP);
+            *reinterpret_cast<uint4 *>(tokl + ((size_t)q * M + t) * MF_TS + sp * 16) = sv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < NDX; u++) {
+            const int t = tid / MF_KC + u * (NT / MF_KC);
+            dxl[(q * MF_KC + sb) * M + t] = sd[u];
+        }
+        if (h == 0) {
+#pragma unroll
+            for (int j = 0; j < MF_KC; j++) dwl[(q * MF_KC + j) * 32 + n] = h2f(ws[j]);
+        }
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+
+    stage(0);
+    commit(0);
+    uint4 w0[MS_PF];
+#pragma unroll
+    for (int p = 0; p < MS_PF; p++)
+        if (p < nb) w0[p] = q0[p];
+    v16i cmag;
+#pragma unroll
+    for (int r = 0; r < 16; r++) cmag[r] = (int)MAGIC_I;
+    __syncthreads();
+
+    // register groups holding entries of the item (8 entries per group)
+    auto run = [&](auto ngc) {
+        constexpr int NG = decltype(ngc)::value;
+        for (int ch = 0; ch < nch; ch++) {
+            const int q = ch & 1;
+            if (ch + 1 < nch) stage(ch + 1);
+            const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
+            const float *xq = dxl + q * MF_KC * M + 4 * h;
+            const float *wq = dwl + q * MF_KC * 32 + n;
+#pragma unroll
+            for (int bl = 0; bl < MF_KC; bl++) {
+                const int b = ch * MF_KC + bl;
+                if (b < nb) {
+                    const v4i wb = h ? nib_hi(w0[bl % MS_PF]) : nib_lo(w0[bl % MS_PF]);
+                    if (b + MS_PF < nb) w0[bl % MS_PF] = q0[b + MS_PF];
+                    const v4i ta = *reinterpret_cast<const v4i *>(tq + bl * 32);
+                    const float dw = wq[bl * 32];
+                    const float cw = -MAGIC_F * dw;
+                    float4 dx[NG];
+#pragma unroll
+                    for (int g = 0; g < NG; g++) dx[g] = *reinterpret_cast<const float4 *>(xq + bl * M + 8 * g);
+                    const v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ta, wb, cmag, 0, 0, 0);
+#pragma unroll
+                    for (int g = 0; g < NG; g++) {
+                        const float dxa[4] = {dx[g].x, dx[g].y, dx[g].z, dx[g].w};
+#pragma unroll
+                        for (int rr = 0; rr < 4; rr++) {
+                            const int r = 4 * g + rr;
+                            const float u = __builtin_fmaf(__int_as_float(rc[r]), dw, cw);
+                            acc[r] = __builtin_fmaf(u, dxa[rr], acc[r]);
+                        }
+                    }
+                }
+            }
+            if (ch + 1 < nch) commit(q ^ 1);
+            __syncthreads();
+        }
+    };
+    const int ng = (c + 7) >> 3;
+    if (ng >= 4) run(Tiles<4>{});
+    else if (ng == 3) run(Tiles<3>{});
+    else if (ng == 2) run(Tiles<2>{});
+    else run(Tiles<1>{});
+
+    if (PAIR) {
+        // up sums -> LDS (over the activation buffers), gate waves combine
+        float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * 16 * 64;
+        if (mat == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) x[r * 64 + lane] = acc[r];
+        }
+        __syncthreads();
+        if (mat == 1) return;
+        // SwiGLU, then Q8_0 over each entry's 32 rows (lanes of this half)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool on = valid && t < c;
+            const float hv = on ? silu_mul(acc[r], x[r * 64 + lane]) : 0.0f;
+            const float v = fabsf(hv);
+            const float a = half_max(v > 0.0f ? v : 0.0f);
+            const float d = a / 127.0f;
+            const float inv = a > 0.0f ? 127.0f / a : 0.0f;
+            const int qv = (int)__builtin_rintf(hv * inv);
+            const int sum = half_sum(qv);
+            if (on) {
+                const int ent = entries[o + t];
+                oq[(size_t)ent * s.I + nt * 32 + n] = (int8_t)qv;
+                if (n == 0) {
+                    od[(size_t)ent * s.nbI + nt] = h2f(f2h(d));
+                    os[(size_t)ent * s.nbI + nt] = sum;
+                }
+            }
+        }
+    } else if (valid) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+            if (t < c) D[(size_t)entries[o + t] * s.H + nt * 32 + n] = acc[r];
+        }
+    }
+}
+
 // ================================================================ launchers
 static inline unsigned mf_cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
@@ -370,12 +607,24 @@ static hipError_t mf_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
     return hipGetLastError();
 }
 
+template <bool PAIR>
+static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work, const int32_t *work_n,
+                        const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
+                        float *D, hipStream_t st) {
+    const int rows = PAIR ? s.I : s.H;
+    const size_t lds = ms_lds_bytes();
+    const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (MS_NW / 2)) : mf_cdiv((size_t)rows, 32 * MS_NW);
+    hipLaunchKernelGGL((k_mfma_small<PAIR>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work, work_n,
+                       entries, aq, ad, oq, od, os, D);
+    return hipGetLastError();
+}
+
 hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                               const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
                               const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
     if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
     (void)xs;
-    if (mt == 1) return mf_go<1, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+    if (mt == 1) return ms_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
     if (mt == 2) return mf_go<2, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
     return mf_go<4, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
 }
@@ -385,8 +634,8 @@ hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int
                             const int *hs, float *D, hipStream_t st) {
     if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
     (void)hs;
-    if (mt == 1) return mf_go<1, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
-                                        D, st);
+    if (mt == 1) return ms_go<false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
+                                     D, st);
     if (mt == 2) return mf_go<2, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
                                         D, st);
     return mf_go<4, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);

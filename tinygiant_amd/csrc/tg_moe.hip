@@ -1034,9 +1034,9 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
 //   2. forms Q8_0(x * s) in its LDS and runs its gate/up units as k_experts
 //      (units go to the blocks that do not own a group first), publishing h
 //      as tagged words;
-//   3. loads its down rows for the k experts (issued before it waits), reads
-//      every h word, dots, chains, combines and adds the residual (as
-//      k_experts);
+//   3. loads its down rows for the k experts (all threads, issued before it
+//      waits), reads every h word, dots, chains, combines and adds the
+//      residual (as k_experts);
 // and then, per group, the blocks other than the group's owner (its last
 // chunk) publish their combined rows as tagged words, and the owner, with
 // all RG rows, forms the next layer's partials of the group.  Waits: h (all
@@ -1208,16 +1208,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
         fx_gu_publish(s, u0, tag, hw, smem);
     }
-    // 2. this block's down weights (waves 3.., item p on down thread
-    //    p % FX_DT), then further gate/up units
+    // 2. this block's down weights (item p on thread p % FX_THREADS; the
+    //    polling waves' loads land long before the first h word does) and
+    //    further gate/up units.  With deep unit loads (UG > 4) the down loads
+    //    follow the units, so the two never hold registers at once.
     const size_t ntb = (size_t)H * nb;
-    const int items = k * RD * nb, dt = tid - FX_PT;
+    const int items = k * RD * nb;
     uint4 wv[UD];
     uint32_t dv[UD];
-    if (dt >= 0) {  // whole waves; clamped, unbranched loads inside (as k_gateup)
+    auto down_loads = [&]() {
 #pragma unroll
-        for (int u = 0; u < UD; u++) {
-            const int p = min(u * FX_DT + dt, items - 1);
+        for (int u = 0; u < UD; u++) {  // clamped, unbranched loads (as k_gateup)
+            const int p = min(u * FX_THREADS + tid, items - 1);
             const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
             const int jj = rdi >> lrd, row = r0 + (rdi - (jj << lrd));
             const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
@@ -1225,14 +1227,17 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
             wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
             dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
         }
-    }
-    __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
+        __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
+    };
+    constexpr bool DOWN_FIRST = UG <= 4;
+    if (DOWN_FIRST) down_loads();
     for (int unit = u0 + NB; unit < ng; unit += NB) {
         fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
         __syncthreads();  // wave 0 has read the previous unit's LDS
         fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
         fx_gu_publish(s, unit, tag, hw, smem);
     }
+    if (!DOWN_FIRST) down_loads();
 
     // 3. waves 0..2 read h of every unit into LDS (after the gate/up part,
     //    which wave 0 may still be reading); then the down rows
@@ -1266,8 +1271,8 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < UD; u++) {
-        const int p = u * FX_DT + dt;
-        if (dt >= 0 && p < items) {
+        const int p = u * FX_THREADS + tid;
+        if (p < items) {
             const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
             const int jj = rdi >> lrd;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
@@ -1901,14 +1906,14 @@ static int ld_rows(const Shape &s, int n_cu) {
     return 0;
 }
 
-static int ld_ud(const Shape &s, int rd) { return (int)cdiv((size_t)s.k * rd * s.nbI, FX_DT); }
+static int ld_ud(const Shape &s, int rd) { return (int)cdiv((size_t)s.k * rd * s.nbI, FX_THREADS); }
 
 bool layer_dec_ok(const Shape &s, int n_cu) {
     const int rd = n_cu > 0 ? ld_rows(s, n_cu) : 0;
     if (!rd) return false;
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
     return decode_shape_ok(s) && s.H % RG == 0 && (s.H / RG) % 4 == 0 && s.E * (RG / 4) <= FX_THREADS &&
-           s.E < 256 && s.k * rd <= FX_THREADS && s.H / 8 + WAVE <= FX_THREADS && ug <= 4 && ld_ud(s, rd) <= 6 &&
+           s.E < 256 && s.k * rd <= FX_THREADS && s.H / 8 + WAVE <= FX_THREADS && ug <= 8 && ld_ud(s, rd) <= 6 &&
            RG - rd <= FX_THREADS && ld_lds_bytes(s, rd) <= 160 * 1024;
 }
 
@@ -1918,12 +1923,12 @@ hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, floa
     return hipGetLastError();
 }
 
-template <int UD>
+template <int UG, int UD>
 static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
     const size_t lds = ld_lds_bytes(s, A.rd);
-    hipError_t e = allow_lds((const void *)k_layer_dec<4, UD>, lds);
+    hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_layer_dec<4, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    hipLaunchKernelGGL((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
     return hipGetLastError();
 }
 
@@ -1934,7 +1939,9 @@ hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, c
     if (!layer_dec_ok(s, n_cu)) return hipErrorInvalidValue;
     const int rd = ld_rows(s, n_cu);
     const LdArgs A{layer_pl, x, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
-    return ld_ud(s, rd) <= 2 ? ld_go<2>(A, s, st) : ld_go<6>(A, s, st);
+    const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
+    if (ug <= 4 && ld_ud(s, rd) <= 2) return ld_go<4, 2>(A, s, st);
+    return ld_go<8, 6>(A, s, st);
 }
 
 size_t dec_part_floats(const Shape &s) { return 2 * (size_t)(s.H / RG) * (s.E + 1); }
