@@ -354,11 +354,21 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
 // take gate / up of tile 2x + i, meet in LDS, and the gate wave applies
 // SwiGLU and Q8_0 to each entry's 32 rows (one per lane of a half-wave:
 // maximum and sum by row rotations and a swap of the rows).
+// Weights: per chunk of MF_KC = 8 blocks, lane (n, h) loads row n's blocks
+// 4h .. 4h+3 (64 contiguous bytes; the two lanes of a row cover its whole
+// 128-byte line) and, with nb % 8 == 0, the row's 8 scales in one 16-byte
+// load; the next chunk's loads are in flight while this one computes.  Block
+// bl's 16 bytes reach both lanes of the row through one lane-half swap.
 constexpr int MS_NW = 4;    // waves per block
-constexpr int MS_PF = 8;    // Q4_0 blocks of B prefetched ahead per wave
 
-__host__ __device__ inline size_t ms_lds_bytes() {
-    return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4 + (size_t)MS_NW * 2 * MF_KC * 32 * 4;
+__host__ __device__ inline size_t ms_lds_bytes() { return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4; }
+
+// one lane-half swap: lo takes half 0's value of v on every lane, hi half 1's
+// (lane i and lane i ^ 32 end with the same pair)
+TG_DEV void half_split(uint32_t v, uint32_t &lo, uint32_t &hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    lo = r[0];
+    hi = r[1];
 }
 
 template <int CTRL>
@@ -391,7 +401,7 @@ TG_DEV int half_sum(int v) {
     return v;
 }
 
-template <bool PAIR>
+template <bool PAIR, bool SCV>
 __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__restrict__ layer_pl, Shape s,
                                                            const int32_t *__restrict__ work,
                                                            const int32_t *__restrict__ work_n,
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                                                            int *__restrict__ os, float *__restrict__ D) {
     constexpr int M = 32, NW = MS_NW, NT = NW * 64, TP = 2 * MF_KC;
     constexpr int NTP = M * TP / NT, NDX = M * MF_KC / NT;
-    static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC % MS_PF == 0 && NTP >= 1 && NDX >= 1, "staging map");
+    static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC == 8 && NTP >= 1 && NDX >= 1, "staging map");
     extern __shared__ __align__(16) uint8_t smem[];
     const int wi = blockIdx.y;
     if (wi >= work_n[0]) return;  // uniform over the block
@@ -412,7 +422,6 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 
     uint8_t *tokl = smem;                                                     // [2][M][MF_TS]
     float *dxl = reinterpret_cast<float *>(smem + 2 * M * MF_TS);             // [2][MF_KC][M]
-    float *dwl = dxl + 2 * MF_KC * M + wave * (2 * MF_KC * 32);               // [2][MF_KC][32]
 
     const int sp = tid % TP, sb = tid % MF_KC;
     int toff[NTP], doff[NDX];
@@ -441,7 +450,6 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 
     uint4 sv[NTP];
     float sd[NDX];
-    uint16_t ws[MF_KC];
     auto stage = [&](int ch) {
 #pragma unroll
         for (int u = 0; u < NTP; u++) {
@@ -453,11 +461,6 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         for (int u = 0; u < NDX; u++) {
             const int b = ch * MF_KC + sb;
             sd[u] = (doff[u] >= 0 && b < nb) ? ad[doff[u] + b] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < MF_KC; j++) {
-            const int b = ch * MF_KC + j;
-            ws[j] = (h == 0 && b < nb) ? s0[b] : (uint16_t)0;
         }
     };
     auto commit = [&](int q) {
@@ -471,9 +474,19 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
             const int t = tid / MF_KC + u * (NT / MF_KC);
             dxl[(q * MF_KC + sb) * M + t] = sd[u];
         }
-        if (h == 0) {
+    };
+    // row R's weights of chunk ch: blocks 8ch + 4h + i (clamped; blocks past
+    // nb are never used) and the chunk's 8 scales (packed halves)
+    auto wload = [&](int ch, uint4 (&w)[4], uint4 &sc) {
 #pragma unroll
-            for (int j = 0; j < MF_KC; j++) dwl[(q * MF_KC + j) * 32 + n] = h2f(ws[j]);
+        for (int i = 0; i < 4; i++) w[i] = q0[min(ch * MF_KC + 4 * h + i, nb - 1)];
+        if (SCV) {
+            sc = *reinterpret_cast<const uint4 *>(s0 + ch * MF_KC);
+        } else {
+            uint32_t hv[MF_KC];
+#pragma unroll
+            for (int j = 0; j < MF_KC; j++) hv[j] = s0[min(ch * MF_KC + j, nb - 1)];
+            sc = make_uint4(hv[0] | hv[1] << 16, hv[2] | hv[3] << 16, hv[4] | hv[5] << 16, hv[6] | hv[7] << 16);
         }
     };
 
@@ -481,12 +494,10 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
 
+    uint4 wc[4], sc;
+    wload(0, wc, sc);
     stage(0);
     commit(0);
-    uint4 w0[MS_PF];
-#pragma unroll
-    for (int p = 0; p < MS_PF; p++)
-        if (p < nb) w0[p] = q0[p];
     v16i cmag;
 #pragma unroll
     for (int r = 0; r < 16; r++) cmag[r] = (int)MAGIC_I;
@@ -497,18 +508,33 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         constexpr int NG = decltype(ngc)::value;
         for (int ch = 0; ch < nch; ch++) {
             const int q = ch & 1;
-            if (ch + 1 < nch) stage(ch + 1);
+            uint4 wn[4], sn;
+            if (ch + 1 < nch) {
+                wload(ch + 1, wn, sn);
+                stage(ch + 1);
+            }
             const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
             const float *xq = dxl + q * MF_KC * M + 4 * h;
-            const float *wq = dwl + q * MF_KC * 32 + n;
+            const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
             for (int bl = 0; bl < MF_KC; bl++) {
                 const int b = ch * MF_KC + bl;
                 if (b < nb) {
-                    const v4i wb = h ? nib_hi(w0[bl % MS_PF]) : nib_lo(w0[bl % MS_PF]);
-                    if (b + MS_PF < nb) w0[bl % MS_PF] = q0[b + MS_PF];
+                    // block bl sits in wc[bl % 4] of the half bl / 4 lane: the swap
+                    // at bl < 4 yields block bl and keeps block bl + 4 in wc[bl]
+                    uint4 blk;
+                    if (bl < 4) {
+                        uint4 &w = wc[bl];
+                        half_split(w.x, blk.x, w.x);
+                        half_split(w.y, blk.y, w.y);
+                        half_split(w.z, blk.z, w.z);
+                        half_split(w.w, blk.w, w.w);
+                    } else {
+                        blk = wc[bl & 3];
+                    }
+                    const v4i wb = h ? nib_hi(blk) : nib_lo(blk);
                     const v4i ta = *reinterpret_cast<const v4i *>(tq + bl * 32);
-                    const float dw = wq[bl * 32];
+                    const float dw = h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1))));
                     const float cw = -MAGIC_F * dw;
                     float4 dx[NG];
 #pragma unroll
@@ -526,7 +552,12 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                     }
                 }
             }
-            if (ch + 1 < nch) commit(q ^ 1);
+            if (ch + 1 < nch) {
+                commit(q ^ 1);
+#pragma unroll
+                for (int i = 0; i < 4; i++) wc[i] = wn[i];
+                sc = sn;
+            }
             __syncthreads();
         }
     };
@@ -611,11 +642,16 @@ template <bool PAIR>
 static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work, const int32_t *work_n,
                         const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
                         float *D, hipStream_t st) {
-    const int rows = PAIR ? s.I : s.H;
+    const int rows = PAIR ? s.I : s.H, nb = (PAIR ? s.H : s.I) / QK;
     const size_t lds = ms_lds_bytes();
     const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (MS_NW / 2)) : mf_cdiv((size_t)rows, 32 * MS_NW);
-    hipLaunchKernelGGL((k_mfma_small<PAIR>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work, work_n,
-                       entries, aq, ad, oq, od, os, D);
+    // 16-byte scale loads need every row's scales 16-byte aligned (nb % 8 == 0)
+    if (nb % MF_KC == 0)
+        hipLaunchKernelGGL((k_mfma_small<PAIR, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+                           work_n, entries, aq, ad, oq, od, os, D);
+    else
+        hipLaunchKernelGGL((k_mfma_small<PAIR, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+                           work_n, entries, aq, ad, oq, od, os, D);
     return hipGetLastError();
 }
 
