@@ -135,7 +135,8 @@ def test_matvec_bitexact(O, tglib, rows, cols):
 
 # ---------------------------------------------------------------- router
 
-@pytest.mark.parametrize("E,H,k,T", [(16, 256, 4, 5), (128, 2048, 8, 4), (128, 4096, 8, 2), (20, 256, 4, 150),
+@pytest.mark.parametrize("E,H,k,T", [(16, 256, 4, 5), (128, 2048, 8, 4), (128, 4096, 8, 2), (20, 256, 4, 13),
+                                     (128, 2048, 8, 64), (128, 4096, 8, 32), (20, 256, 4, 150),
                                      (128, 2048, 8, 300)])
 def test_router_topk_exact(O, tglib, E, H, k, T):
     gpu_note(f"router E={E} H={H} k={k} T={T}")

@@ -83,6 +83,58 @@ __global__ __launch_bounds__(RT_THREADS) void k_route(const float *__restrict__ 
     }
 }
 
+// Few tokens (below 128): block = RS_T tokens x RS_E experts, 1024 threads.
+// Thread (pair p = tid % RS_PAIRS, part j = tid / RS_PAIRS) runs the fma
+// chains of pair p (token p / RS_E, expert p % RS_E) over the G / RS_PARTS
+// consecutive groups of part j, two at a time; the chain sums meet in LDS and
+// one thread per pair adds them in ascending group order, exactly as k_route
+// does.  A block reads its RS_E router rows and RS_T token rows once (through
+// the L1; every 64 lanes touch at most 2 rows of each).
+constexpr int RS_T = 4, RS_E = 8, RS_PAIRS = RS_T * RS_E, RS_PARTS = 1024 / RS_PAIRS;
+
+__host__ __device__ inline size_t route_small_lds(int H) { return 4 * (size_t)RS_PAIRS * (H / RG + 1); }
+
+__global__ __launch_bounds__(1024) void k_route_small(const float *__restrict__ Wr, const float *__restrict__ x, int T,
+                                                      int E, int H, float *__restrict__ raw) {
+    extern __shared__ __align__(16) float cs[];  // [RS_PAIRS][G + 1]
+    const int tid = threadIdx.x, p = tid % RS_PAIRS, j = tid / RS_PAIRS, G = H / RG, gp = G / RS_PARTS;
+    const int t = blockIdx.x * RS_T + p / RS_E, e = blockIdx.y * RS_E + p % RS_E;
+    if (t < T && e < E) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (size_t)e * H);
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)t * H);
+        for (int g = j * gp; g < (j + 1) * gp; g += 2) {  // gp is even
+            float4 wa[RG / 4], xa[RG / 4], wb[RG / 4], xb[RG / 4];
+#pragma unroll
+            for (int q = 0; q < RG / 4; q++) {
+                wa[q] = w4[g * (RG / 4) + q];
+                xa[q] = x4[g * (RG / 4) + q];
+                wb[q] = w4[(g + 1) * (RG / 4) + q];
+                xb[q] = x4[(g + 1) * (RG / 4) + q];
+            }
+            float a = 0.0f, b = 0.0f;
+#pragma unroll
+            for (int q = 0; q < RG / 4; q++) {
+                a = __builtin_fmaf(wa[q].x, xa[q].x, a);
+                b = __builtin_fmaf(wb[q].x, xb[q].x, b);
+                a = __builtin_fmaf(wa[q].y, xa[q].y, a);
+                b = __builtin_fmaf(wb[q].y, xb[q].y, b);
+                a = __builtin_fmaf(wa[q].z, xa[q].z, a);
+                b = __builtin_fmaf(wb[q].z, xb[q].z, b);
+                a = __builtin_fmaf(wa[q].w, xa[q].w, a);
+                b = __builtin_fmaf(wb[q].w, xb[q].w, b);
+            }
+            cs[p * (G + 1) + g] = a;
+            cs[p * (G + 1) + g + 1] = b;
+        }
+    }
+    __syncthreads();
+    if (tid < RS_PAIRS && t < T && e < E) {
+        float tot = 0.0f;
+        for (int g = 0; g < G; g++) tot = tot + cs[p * (G + 1) + g];
+        raw[(size_t)t * E + e] = tot;
+    }
+}
+
 // Many tokens: block = 32 tokens x 32 experts, 256 threads, each thread 2
 // tokens x 2 experts.  Four groups (128 consecutive elements) of x and of the
 // router rows are staged in LDS per step, the next step's loads in flight
@@ -1780,6 +1832,12 @@ hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, fl
     if (T >= 128 && (H / RG) % RT_CH == 0) {
         hipLaunchKernelGGL(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
                            T, E, H, raw);
+    } else if (T >= RS_T && (H / RG) % (2 * RS_PARTS) == 0 && route_small_lds(H) <= 64 * 1024) {
+        const size_t lds = route_small_lds(H);
+        hipError_t e = allow_lds((const void *)k_route_small, lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_route_small, dim3(cdiv((size_t)T, RS_T), cdiv((size_t)E, RS_E)), dim3(1024), lds, st,
+                           Wr, x, T, E, H, raw);
     } else {
         hipLaunchKernelGGL(k_route, dim3(E, cdiv((size_t)T, RT_TOK)), dim3(RT_THREADS), 0, st, Wr, x, T, E, H, raw);
     }
