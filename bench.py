@@ -19,6 +19,9 @@ Other workloads (--workload):
                127.7 GB resident), one token per step.
   batched-235b the same stack, 32 tokens per step with Zipf(1.1) routing.
   hbm-ceiling  what one launch of plain 128-bit loads reads from HBM.
+  legacy-moe   the reference's own legacy call, tg_moe_forward: 8 Q4_K experts
+               of the 30B shape on caller-owned host buffers (operands copied
+               in per call, as the reference's ABI hands them over).
 
 Prints one JSON line: tok/s (value), expert-weight HBM GB/s, the roofline
 of the dominant kernel (HIP events on its launch stream) and the CPU oracle
@@ -652,6 +655,88 @@ def run_prefill(args, torch, call):
     }
 
 
+def q4k_blocks(rng, n):
+    """n random Q4_K blocks (144 bytes): finite fp16 d and dmin, any 6-bit
+    scale/min field, random nibbles."""
+    b = rng.integers(0, 256, (n, 144), dtype=np.uint8)
+    b[:, 0:2] = rng.uniform(0.0005, 0.004, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    b[:, 2:4] = rng.uniform(0.0, 0.004, n).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b.reshape(-1)
+
+
+def run_legacy_moe(args, torch, call):
+    """The legacy entry point tg_moe_forward (libtinygiant.c:647-655) as the
+    reference's engine would call it: 8 Q4_K experts of the 30B shape
+    (gate | up | down, 2,654,208 bytes each) in host memory, one call per
+    layer; rotates over 16 sets of experts.  The call copies its operands to
+    the device, so the rate is bound by the host-to-device copy; the roofline
+    is the Q4_K row-dot kernel's on its device operands."""
+    from tinygiant_amd._lib import require_lib
+    lib = require_lib()
+    rng = np.random.default_rng(args.seed)
+    gb = I * (H // 256) * 144
+    eb = 2 * gb + H * (I // 256) * 144
+    NSET = 16
+    sets = [[q4k_blocks(rng, eb // 144) for _ in range(K_TOP)] for _ in range(NSET)]
+    ptrs = [(ctypes.c_void_p * K_TOP)(*[e.ctypes.data for e in st]) for st in sets]
+    w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)  # tools/nws_q8dot_bench.c:369
+    x = rng.normal(0.0, 1.0, H).astype(np.float32)
+    out = np.zeros(H, np.float32)
+    K, W = args.steps or 64, 4 if args.warmup is None else args.warmup
+
+    def step(i):
+        lib.tg_moe_forward(ptrs[i % NSET], w.ctypes.data, K_TOP, x.ctypes.data, out.ctypes.data, H, I)
+
+    log(f"warmup {W} calls")
+    for i in range(W):
+        step(i)
+    log(f"timing {K} calls")
+    t0 = time.perf_counter()
+    for i in range(K):
+        step(i)
+    wall = time.perf_counter() - t0
+    call("tg_prof_enable", 1)
+    for i in range(8):
+        step(i)
+    call("tg_prof_enable", 0)
+    kern = kernel_times(call, ("lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc"))
+    kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    n_q, ms_q = kern["lg_q4k"]
+    q_bytes = gb + (H // 256) * 264  # one gate (or up) matrix and its Q8 activations
+    achieved = q_bytes / (ms_q / n_q * 1e-3)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        from oracle import oracle as O  # the checker, timed as the CPU baseline
+        ref = O.moe_forward_q4k(sets[0], w, x, H, I)
+        step(0)
+        assert np.array_equal(ref.view(np.uint32), out.view(np.uint32)), "GPU legacy MoE differs from the oracle"
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0):
+            O.moe_forward_q4k(sets[n % NSET], w, x, H, I)
+            n += 1
+        cpu_s = (time.perf_counter() - t1) / n
+        cpu = {"value": round(1.0 / cpu_s, 2), "unit": "layer/s", "cores": 1, "kind": "port",
+               "sample": f"{n} tg_moe_forward calls (8 Q4_K experts, 2048x768) through the C oracle, one thread; "
+                         "bit-identical to the GPU call on the first set"}
+
+    return {
+        "metric": "legacy tg_moe_forward calls/s (8 Q4_K experts, 30B shape, host pointers)",
+        "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k x q8 (int dot, fp32 accumulate)",
+        "data": "synthetic (random Q4_K blocks, N(0,1) input)",
+        "config": {"workload": "legacy-q4k-moe-forward", "hidden": H, "moe_intermediate": I, "experts": K_TOP,
+                   "expert_bytes": eb, "note": "each call copies 21.2 MB of host operands to the device"},
+        "kernel_avg_us": kern_us,
+        "roofline": {"bound": "hbm", "kernel": "k_matmul_q4k (gate/up)", "bytes_per_launch": q_bytes,
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_hbm_ceiling(args, torch, call):
     """What one launch can read from HBM: plain 128-bit loads over regions of
     the sizes the MoE kernels stream, rotating over a 16 GiB buffer so no
@@ -697,7 +782,7 @@ def run_hbm_ceiling(args, torch, call):
 WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill": run_prefill,
              "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
              "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
-             "hbm-ceiling": run_hbm_ceiling}
+             "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe}
 
 
 def main() -> int:

@@ -379,6 +379,17 @@ def expert_forward_mixed(gate, up, down, down_format, x, out, weight, embed, int
     return out
 
 
+def moe_forward_q4k(experts, w, x, embed, inter):
+    """tg_moe_forward: output zeroed, then every Q4_K expert (gate | up | down
+    contiguous) accumulated with its weight, in order."""
+    n = len(experts)
+    ptrs = (ctypes.c_void_p * n)(*[np.ascontiguousarray(e).ctypes.data for e in experts])
+    out = np.empty(embed, np.float32)
+    lib().tgo_moe_forward_q4k(ctypes.cast(ptrs, ctypes.c_void_p), _p(np.ascontiguousarray(w, dtype=np.float32)), n,
+                              _p(np.ascontiguousarray(x, dtype=np.float32)), _p(out), embed, inter)
+    return out
+
+
 def matmul_q4k_scalar(W: np.ndarray, x: np.ndarray, nrows: int, ncols: int) -> np.ndarray:
     y = np.empty(nrows, np.float32)
     lib().tgo_matmul_q4k_scalar(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(y), nrows, ncols)

@@ -1,0 +1,196 @@
+"""GPU parity of the reference's legacy entry points (Q4_K / Q6_K / f16 /
+f32 products, RMS norm, expert forward) against the CPU oracle.
+
+The entry points are called exactly as the reference's ctypes surface calls
+them (tinygiant/_lib.py:39-74): host numpy buffers, synchronous.  Every
+kernel performs the reference's arithmetic in its own order with
+contraction off, so each fp32 result must equal the oracle's bit for bit;
+the reference's own threshold for the stack (max relative error 1e-5) is
+asserted as well, so a failure reports both.  Inputs are seeded: Q4_K blocks
+from a packer written from the block layout (finite fp16 d / dmin, 6-bit
+scales and mins, random nibbles), Q6_K blocks as random bytes with a finite
+fp16 d, f16 matrices from N(0, 0.02).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.conftest import gpu_note
+from tests.test_oracle_legacy import pack_scales
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+
+
+def ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def f16_bits(v):
+    return np.asarray(v, np.float32).astype(np.float16).view(np.uint16)
+
+
+def q4k_matrix(rng, nrows, bpr):
+    """nrows x bpr Q4_K blocks, row-major (144 bytes each)."""
+    n = nrows * bpr
+    blk = np.zeros((n, 144), np.uint8)
+    d = f16_bits(rng.uniform(0.0005, 0.004, n))
+    dmin = f16_bits(rng.uniform(0.0, 0.004, n))
+    blk[:, 0:2] = d.view(np.uint8).reshape(n, 2)
+    blk[:, 2:4] = dmin.view(np.uint8).reshape(n, 2)
+    for i in range(n):
+        blk[i, 4:16] = pack_scales(rng.integers(0, 64, 8), rng.integers(0, 64, 8))
+    blk[:, 16:] = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def q6k_matrix(rng, nrows, bpr):
+    n = nrows * bpr
+    blk = rng.integers(0, 256, (n, 210), dtype=np.uint8)
+    blk[:, 208:210] = f16_bits(rng.uniform(0.0002, 0.002, n)).view(np.uint8).reshape(n, 2)
+    return blk.reshape(-1)
+
+
+def f16_matrix(rng, nrows, ncols):
+    return f16_bits(rng.normal(0.0, 0.02, nrows * ncols))
+
+
+def assert_exact(got, ref, what):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    den = max(float(np.max(np.abs(ref))), 1e-30)
+    rel = float(np.max(np.abs(got.astype(np.float64) - ref))) / den
+    assert rel <= REL_TOL, f"{what}: normwise relative error {rel:.3e}"
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{what}: not bit-identical (rel {rel:.2e})"
+
+
+@pytest.fixture(scope="module")
+def L(tglib):
+    return tglib
+
+
+@pytest.mark.parametrize("nrows,ncols", [(1, 256), (64, 512), (768, 2048), (2048, 768), (37, 300), (5, 100)])
+def test_matmul_q4k(O, L, nrows, ncols):
+    gpu_note(f"tg_matmul_q4k {nrows}x{ncols}")
+    rng = np.random.default_rng(nrows * 7 + ncols)
+    bpr = ncols // 256
+    W = q4k_matrix(rng, nrows, bpr)
+    x = rng.normal(0.0, 1.0, ncols).astype(np.float32)
+    out = np.full(nrows, -1.0, np.float32)
+    L.tg_matmul_q4k(ptr(W), ptr(x), ptr(out), nrows, ncols)
+    assert_exact(out, O.matmul_q4k(W, x, nrows, ncols), f"q4k {nrows}x{ncols}")
+
+
+@pytest.mark.parametrize("nrows,ncols", [(1, 256), (2048, 768), (33, 1024)])
+def test_matmul_q4k_scalar(O, L, nrows, ncols):
+    gpu_note(f"tg_matmul_q4k_scalar {nrows}x{ncols}")
+    rng = np.random.default_rng(nrows + 3 * ncols)
+    bpr = ncols // 256
+    W = q4k_matrix(rng, nrows, bpr)
+    x = rng.normal(0.0, 1.0, ncols).astype(np.float32)
+    out = np.zeros(nrows, np.float32)
+    L.tg_matmul_q4k_scalar(ptr(W), ptr(x), ptr(out), nrows, ncols)
+    assert_exact(out, O.matmul_q4k_scalar(W, x, nrows, ncols), f"q4k scalar {nrows}x{ncols}")
+
+
+@pytest.mark.parametrize("nrows,ncols", [(1, 256), (2048, 768), (70, 1280)])
+def test_matmul_q6k(O, L, nrows, ncols):
+    gpu_note(f"tg_matmul_q6k {nrows}x{ncols}")
+    rng = np.random.default_rng(5 * nrows + ncols)
+    bpr = ncols // 256
+    W = q6k_matrix(rng, nrows, bpr)
+    x = rng.normal(0.0, 1.0, ncols).astype(np.float32)
+    out = np.zeros(nrows, np.float32)
+    L.tg_matmul_q6k(ptr(W), ptr(x), ptr(out), nrows, ncols)
+    assert_exact(out, O.matmul_q6k(W, x, nrows, ncols), f"q6k {nrows}x{ncols}")
+
+
+@pytest.mark.parametrize("half", [True, False])
+@pytest.mark.parametrize("nrows,ncols", [(2048, 768), (3, 7), (129, 777), (16, 8)])
+def test_matvec_f16_f32(O, L, half, nrows, ncols):
+    gpu_note(f"tg_{'f16' if half else 'f32'}_matvec {nrows}x{ncols}")
+    rng = np.random.default_rng(nrows + ncols + half)
+    x = rng.normal(0.0, 1.0, ncols).astype(np.float32)
+    out = np.zeros(nrows, np.float32)
+    if half:
+        A = f16_matrix(rng, nrows, ncols)
+        L.tg_f16_matvec(ptr(A), ptr(x), ptr(out), nrows, ncols)
+        ref = O.matvec_f16(A.view(np.float16).reshape(nrows, ncols), x)
+    else:
+        A = rng.normal(0.0, 0.02, nrows * ncols).astype(np.float32)
+        L.tg_f32_matvec(ptr(A), ptr(x), ptr(out), nrows, ncols)
+        ref = O.matvec_f32(A.reshape(nrows, ncols), x)
+    assert_exact(out, ref, f"matvec half={half} {nrows}x{ncols}")
+
+
+@pytest.mark.parametrize("dim", [2048, 1001, 3])
+def test_rms_norm(O, L, dim):
+    gpu_note(f"tg_rms_norm {dim}")
+    rng = np.random.default_rng(dim)
+    x = rng.normal(0.0, 1.0, dim).astype(np.float32)
+    w = rng.normal(1.0, 0.1, dim).astype(np.float32)
+    out = np.zeros(dim, np.float32)
+    L.tg_rms_norm(ptr(x), ptr(w), ptr(out), dim, ctypes.c_float(1e-6))
+    assert_exact(out, O.rms_norm(x, w, 1e-6), f"rms_norm {dim}")
+
+
+def expert_operands(rng, embed, inter, fmt):
+    gate = q4k_matrix(rng, inter, embed // 256)
+    up = q4k_matrix(rng, inter, embed // 256)
+    if fmt == 1:
+        down = f16_matrix(rng, embed, inter)
+    elif fmt == 2:
+        down = q6k_matrix(rng, embed, inter // 256)
+    else:
+        down = q4k_matrix(rng, embed, inter // 256)
+    return gate, up, down
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+@pytest.mark.parametrize("embed,inter", [(2048, 768), (512, 256)])
+def test_expert_forward_mixed(O, L, fmt, embed, inter):
+    gpu_note(f"tg_expert_forward_mixed fmt={fmt} {embed}x{inter}")
+    rng = np.random.default_rng(fmt * 1000 + embed + inter)
+    gate, up, down = expert_operands(rng, embed, inter, fmt)
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out0 = rng.normal(0.0, 0.1, embed).astype(np.float32)  # the output accumulates
+    out = out0.copy()
+    L.tg_expert_forward_mixed(ptr(gate), ptr(up), ptr(down), fmt, ptr(x), ptr(out), ctypes.c_float(0.13),
+                              embed, inter)
+    ref = O.expert_forward_mixed(gate, up, down, fmt, x, out0.copy(), 0.13, embed, inter)
+    assert_exact(out, ref, f"expert fmt={fmt}")
+
+
+def test_expert_forward_contiguous(O, L):
+    """tg_expert_forward: gate | up | down (Q4_K) in one buffer."""
+    gpu_note("tg_expert_forward 2048x768")
+    rng = np.random.default_rng(77)
+    embed, inter = 2048, 768
+    gate, up, down = expert_operands(rng, embed, inter, 0)
+    blob = np.concatenate([gate, up, down])
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out0 = rng.normal(0.0, 0.1, embed).astype(np.float32)
+    out = out0.copy()
+    L.tg_expert_forward(ptr(blob), ptr(x), ptr(out), ctypes.c_float(0.25), embed, inter)
+    ref = O.expert_forward_mixed(gate, up, down, 0, x, out0.copy(), 0.25, embed, inter)
+    assert_exact(out, ref, "expert contiguous")
+
+
+def test_moe_forward(O, L):
+    """tg_moe_forward: output zeroed, then the weighted experts in order; the
+    reference's own combine weights {.15, .14, .13, ...}
+    (tools/nws_q8dot_bench.c:369)."""
+    gpu_note("tg_moe_forward 8 experts 2048x768")
+    rng = np.random.default_rng(91)
+    embed, inter, n = 2048, 768, 8
+    experts = [np.concatenate(expert_operands(rng, embed, inter, 0)) for _ in range(n)]
+    w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out = np.full(embed, 7.0, np.float32)  # overwritten, not accumulated
+    ptrs = (ctypes.c_void_p * n)(*[e.ctypes.data for e in experts])
+    L.tg_moe_forward(ptrs, ptr(w), n, ptr(x), ptr(out), embed, inter)
+    ref = O.moe_forward_q4k(experts, w, x, embed, inter)
+    assert_exact(out, ref, "moe_forward")

@@ -929,13 +929,23 @@ extern "C" int tg_mlock(const void *addr, size_t len) {
     return mlock(aligned, alen);
 }
 
-// The Q4_K / Q6_K / f16 / attention entry points are not yet on the GPU in
-// this build.  They fail loudly: an error message (once per symbol on
-// stderr, and in tg_last_error), and NaN in every output element whose count
-// the signature gives, so a caller can never mistake the result for data.
+// ================================================================ legacy ABI
+// The reference's legacy entry points keep its conventions: synchronous
+// calls on caller-owned host pointers, no error returns.  Q4_K / Q6_K / f16
+// / f32 products, the RMS norm and the expert forward run on the GPU
+// (tg_legacy.hip): each call copies its operands into one device scratch
+// buffer (grown as needed, kept for the process), runs the kernels on one
+// stream and copies the result back.  A failure (no device, out of memory)
+// is reported loudly: tg_last_error(), one line on stderr per symbol, and
+// NaN in every output element.  Attention and the transformer layer are not
+// on the GPU in this build and fail the same way.
+static void legacy_fail(const char *name, std::atomic<bool> &warned) {
+    if (!warned.exchange(true)) fprintf(stderr, "libtinygiant (gfx950): %s: %s\n", name, g_err.c_str());
+}
+
 static void legacy_unavailable(const char *name, std::atomic<bool> &warned) {
-    set_err(TG_E_UNSUPPORTED, "%s: Q4_K/Q6_K/f16 legacy path is not available on the GPU in this build", name);
-    if (!warned.exchange(true)) fprintf(stderr, "libtinygiant (gfx950): %s\n", g_err.c_str());
+    set_err(TG_E_UNSUPPORTED, "%s: not available on the GPU in this build", name);
+    legacy_fail(name, warned);
 }
 
 static void fill_nan(float *p, long n) {
@@ -958,40 +968,323 @@ LEGACY_FLAG(transformer_layer);
 LEGACY_FLAG(moe_forward);
 LEGACY_FLAG(matmul_q4k_scalar);
 
-extern "C" void tg_expert_forward(const uint8_t *, const float *, float *output, float, int embed_dim, int) {
-    legacy_unavailable("tg_expert_forward", warned_expert_forward);
-    fill_nan(output, embed_dim);
+// One device scratch buffer and stream for the legacy calls (one call at a
+// time: the mutex serialises callers).
+static std::mutex g_lg_mu;
+static uint8_t *g_lg_buf = nullptr;
+static size_t g_lg_cap = 0;
+static int g_lg_dev = -1;
+static hipStream_t g_lg_st = nullptr;
+
+// Carves 256-byte aligned pieces of the scratch buffer; a first pass with no
+// base only counts the bytes.
+struct LgCarve {
+    uint8_t *base;
+    size_t off = 0;
+    template <class T>
+    T *take(size_t bytes) {
+        const size_t o = (off + 255) & ~(size_t)255;
+        off = o + bytes;
+        return base ? reinterpret_cast<T *>(base + o) : nullptr;
+    }
+};
+
+static int lg_reserve(size_t bytes) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (g_lg_buf && g_lg_dev != dev) {  // scratch of another device
+        HIP_TRY(hipSetDevice(g_lg_dev));
+        (void)hipFree(g_lg_buf);
+        if (g_lg_st) (void)hipStreamDestroy(g_lg_st);
+        g_lg_buf = nullptr; g_lg_cap = 0; g_lg_st = nullptr;
+        HIP_TRY(hipSetDevice(dev));
+    }
+    g_lg_dev = dev;
+    if (!g_lg_st) HIP_TRY(hipStreamCreateWithFlags(&g_lg_st, hipStreamNonBlocking));
+    if (bytes > g_lg_cap) {
+        if (g_lg_buf) HIP_TRY(hipFree(g_lg_buf));
+        g_lg_buf = nullptr;
+        g_lg_cap = 0;
+        const size_t want = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+        if (hipMalloc(&g_lg_buf, want) != hipSuccess) {
+            (void)hipGetLastError();
+            g_lg_buf = nullptr;
+            return set_err(TG_E_NOMEM, "legacy scratch of %zu bytes", want);
+        }
+        g_lg_cap = want;
+    }
+    return TG_OK;
 }
 
-extern "C" void tg_expert_forward_mixed(const uint8_t *, const uint8_t *, const void *, int, const float *,
-                                        float *output, float, int embed_dim, int) {
-    legacy_unavailable("tg_expert_forward_mixed", warned_expert_forward_mixed);
-    fill_nan(output, embed_dim);
+static int lg_h2d(void *dst, const void *src, size_t n) {
+    if (n) HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_lg_st));
+    return TG_OK;
 }
 
-extern "C" void tg_matmul_q4k(const uint8_t *, const float *, float *output, int nrows, int) {
-    legacy_unavailable("tg_matmul_q4k", warned_matmul_q4k);
-    fill_nan(output, nrows);
+static int lg_finish(void *host_dst, const void *dev_src, size_t n) {
+    if (n) HIP_TRY(hipMemcpyAsync(host_dst, dev_src, n, hipMemcpyDeviceToHost, g_lg_st));
+    HIP_TRY(hipStreamSynchronize(g_lg_st));
+    return TG_OK;
 }
 
-extern "C" void tg_matmul_q6k(const uint8_t *, const float *, float *output, int nrows, int) {
-    legacy_unavailable("tg_matmul_q6k", warned_matmul_q6k);
-    fill_nan(output, nrows);
+static size_t down_bytes(int fmt, int embed, int inter) {
+    if (fmt == 1) return (size_t)embed * inter * 2;
+    if (fmt == 2) return (size_t)embed * (inter / tg::LG_QK) * tg::LG_Q6K_BYTES;
+    return (size_t)embed * (inter / tg::LG_QK) * tg::LG_Q4K_BYTES;
 }
 
-extern "C" void tg_rms_norm(const float *, const float *, float *out, int dim, float) {
-    legacy_unavailable("tg_rms_norm", warned_rms_norm);
-    fill_nan(out, dim);
+// Device buffers of one expert forward (activations only).
+struct LgExpertBufs {
+    void *xq, *hq;
+    float *g, *u, *h, *dn;
+};
+
+static LgExpertBufs lg_expert_bufs(LgCarve &c, int embed, int inter) {
+    LgExpertBufs b;
+    b.xq = c.take<uint8_t>((size_t)(embed / tg::LG_QK) * tg::LG_Q8K_BYTES);
+    b.hq = c.take<uint8_t>((size_t)(inter / tg::LG_QK) * tg::LG_Q8K_BYTES);
+    b.g = c.take<float>(4 * (size_t)inter);
+    b.u = c.take<float>(4 * (size_t)inter);
+    b.h = c.take<float>(4 * (size_t)inter);
+    b.dn = c.take<float>(4 * (size_t)embed);
+    return b;
 }
 
-extern "C" void tg_f32_matvec(const float *, const float *, float *out, int nrows, int) {
-    legacy_unavailable("tg_f32_matvec", warned_f32_matvec);
-    fill_nan(out, nrows);
+// expert_forward_mixed on device operands (libtinygiant.c:599-643):
+// Q8(x), gate and up rows, SiLU(gate) * up, down by format (1 f16, 2 Q6_K,
+// otherwise Q4_K), out += weight * down.
+static int lg_expert(const uint8_t *gate, const uint8_t *up, const void *down, int fmt, const float *x, float *out,
+                     float weight, int embed, int inter, const LgExpertBufs &b) {
+    const int gbpr = embed / tg::LG_QK, dbpr = inter / tg::LG_QK;
+    hipStream_t st = g_lg_st;
+    PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, gbpr, st));
+    PROFILED("lg_q4k", st, tg::launch_matmul_q4k(gate, b.xq, b.g, inter, gbpr, st));
+    PROFILED("lg_q4k", st, tg::launch_matmul_q4k(up, b.xq, b.u, inter, gbpr, st));
+    PROFILED("lg_silu", st, tg::launch_silu_mul_vec(b.g, b.u, b.h, inter, st));
+    if (fmt == 1) {
+        PROFILED("lg_f16", st, tg::launch_matvec_two_acc(down, true, b.h, b.dn, embed, inter, st));
+    } else {
+        PROFILED("lg_quant", st, tg::launch_quantize_q8k(b.h, b.hq, dbpr, st));
+        if (fmt == 2)
+            PROFILED("lg_q6k", st,
+                     tg::launch_matmul_q6k(static_cast<const uint8_t *>(down), b.hq, b.dn, embed, dbpr, st));
+        else
+            PROFILED("lg_q4k_down", st,
+                     tg::launch_matmul_q4k(static_cast<const uint8_t *>(down), b.hq, b.dn, embed, dbpr, st));
+    }
+    PROFILED("lg_acc", st, tg::launch_acc_scaled(out, b.dn, weight, embed, st));
+    return TG_OK;
 }
 
-extern "C" void tg_f16_matvec(const uint16_t *, const float *, float *out, int nrows, int) {
-    legacy_unavailable("tg_f16_matvec", warned_f16_matvec);
-    fill_nan(out, nrows);
+static int lg_expert_forward_mixed(const uint8_t *gate, const uint8_t *up, const void *down, int fmt,
+                                   const float *input, float *output, float weight, int embed, int inter) {
+    const int gbpr = embed / tg::LG_QK;
+    const size_t gb = (size_t)inter * gbpr * tg::LG_Q4K_BYTES, db = down_bytes(fmt, embed, inter);
+    for (int pass = 0; pass < 2; pass++) {
+        LgCarve c{pass ? g_lg_buf : nullptr};
+        uint8_t *dg = c.take<uint8_t>(gb), *du = c.take<uint8_t>(gb), *dd = c.take<uint8_t>(db);
+        float *dx = c.take<float>(4 * (size_t)embed), *dout = c.take<float>(4 * (size_t)embed);
+        const LgExpertBufs b = lg_expert_bufs(c, embed, inter);
+        if (!pass) {
+            int rc = lg_reserve(c.off);
+            if (rc) return rc;
+            continue;
+        }
+        int rc;
+        if ((rc = lg_h2d(dg, gate, gb)) || (rc = lg_h2d(du, up, gb)) || (rc = lg_h2d(dd, down, db)) ||
+            (rc = lg_h2d(dx, input, 4 * (size_t)embed)) || (rc = lg_h2d(dout, output, 4 * (size_t)embed)) ||
+            (rc = lg_expert(dg, du, dd, fmt, dx, dout, weight, embed, inter, b)))
+            return rc;
+        return lg_finish(output, dout, 4 * (size_t)embed);
+    }
+    return TG_OK;
+}
+
+extern "C" void tg_expert_forward(const uint8_t *q4_data, const float *input, float *output, float weight,
+                                  int embed_dim, int inter_dim) {
+    if (embed_dim <= 0 || inter_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const size_t gb = (size_t)inter_dim * (embed_dim / tg::LG_QK) * tg::LG_Q4K_BYTES;
+    if (lg_expert_forward_mixed(q4_data, q4_data + gb, q4_data + 2 * gb, 0, input, output, weight, embed_dim,
+                                inter_dim)) {
+        legacy_fail("tg_expert_forward", warned_expert_forward);
+        fill_nan(output, embed_dim);
+    }
+}
+
+extern "C" void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
+                                        int down_format, const float *input, float *output, float weight,
+                                        int embed_dim, int inter_dim) {
+    if (embed_dim <= 0 || inter_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_expert_forward_mixed(gate_q4, up_q4, down_data, down_format, input, output, weight, embed_dim,
+                                inter_dim)) {
+        legacy_fail("tg_expert_forward_mixed", warned_expert_forward_mixed);
+        fill_nan(output, embed_dim);
+    }
+}
+
+extern "C" void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights, int n_experts, const float *input,
+                               float *output, int embed_dim, int inter_dim) {
+    if (embed_dim <= 0 || inter_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const size_t gb = (size_t)inter_dim * (embed_dim / tg::LG_QK) * tg::LG_Q4K_BYTES;
+    const size_t eb = 2 * gb + down_bytes(0, embed_dim, inter_dim);
+    auto run = [&]() -> int {
+        for (int pass = 0; pass < 2; pass++) {
+            LgCarve c{pass ? g_lg_buf : nullptr};
+            uint8_t *de = c.take<uint8_t>(eb);
+            float *dx = c.take<float>(4 * (size_t)embed_dim), *dout = c.take<float>(4 * (size_t)embed_dim);
+            const LgExpertBufs b = lg_expert_bufs(c, embed_dim, inter_dim);
+            if (!pass) {
+                int rc = lg_reserve(c.off);
+                if (rc) return rc;
+                continue;
+            }
+            int rc = lg_h2d(dx, input, 4 * (size_t)embed_dim);
+            if (rc) return rc;
+            HIP_TRY(hipMemsetAsync(dout, 0, 4 * (size_t)embed_dim, g_lg_st));  // the reference's memset
+            for (int e = 0; e < n_experts; e++) {
+                // one expert's bytes at a time: the copy waits for the previous expert's kernels
+                if ((rc = lg_h2d(de, expert_ptrs[e], eb)) ||
+                    (rc = lg_expert(de, de + gb, de + 2 * gb, 0, dx, dout, weights[e], embed_dim, inter_dim, b)))
+                    return rc;
+            }
+            return lg_finish(output, dout, 4 * (size_t)embed_dim);
+        }
+        return TG_OK;
+    };
+    if (run()) {
+        legacy_fail("tg_moe_forward", warned_moe_forward);
+        fill_nan(output, embed_dim);
+    }
+}
+
+// nrows x (ncols / 256) blocks of Q4_K or Q6_K times the input's Q8 blocks
+static int lg_matmul_k(bool q6, const uint8_t *W, const float *input, float *output, int nrows, int ncols,
+                       bool scalar) {
+    const int bpr = ncols / tg::LG_QK;
+    const size_t wb = (size_t)nrows * bpr * (q6 ? tg::LG_Q6K_BYTES : tg::LG_Q4K_BYTES);
+    const size_t xb = 4 * (size_t)bpr * tg::LG_QK;
+    for (int pass = 0; pass < 2; pass++) {
+        LgCarve c{pass ? g_lg_buf : nullptr};
+        uint8_t *dw = c.take<uint8_t>(wb);
+        float *dx = c.take<float>(xb);
+        void *dq = c.take<uint8_t>((size_t)bpr * tg::LG_Q8K_BYTES);
+        float *dy = c.take<float>(4 * (size_t)nrows);
+        if (!pass) {
+            int rc = lg_reserve(c.off);
+            if (rc) return rc;
+            continue;
+        }
+        int rc;
+        if ((rc = lg_h2d(dw, W, wb)) || (rc = lg_h2d(dx, input, xb))) return rc;
+        if (scalar) {
+            HIP_TRY(tg::launch_matmul_q4k_scalar(dw, dx, dy, nrows, bpr, g_lg_st));
+        } else {
+            HIP_TRY(tg::launch_quantize_q8k(dx, dq, bpr, g_lg_st));
+            if (q6)
+                HIP_TRY(tg::launch_matmul_q6k(dw, dq, dy, nrows, bpr, g_lg_st));
+            else
+                HIP_TRY(tg::launch_matmul_q4k(dw, dq, dy, nrows, bpr, g_lg_st));
+        }
+        return lg_finish(output, dy, 4 * (size_t)nrows);
+    }
+    return TG_OK;
+}
+
+extern "C" void tg_matmul_q4k(const uint8_t *q4_matrix, const float *input, float *output, int nrows, int ncols) {
+    if (nrows <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_matmul_k(false, q4_matrix, input, output, nrows, ncols, false)) {
+        legacy_fail("tg_matmul_q4k", warned_matmul_q4k);
+        fill_nan(output, nrows);
+    }
+}
+
+extern "C" void tg_matmul_q6k(const uint8_t *q6_matrix, const float *input, float *output, int nrows, int ncols) {
+    if (nrows <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_matmul_k(true, q6_matrix, input, output, nrows, ncols, false)) {
+        legacy_fail("tg_matmul_q6k", warned_matmul_q6k);
+        fill_nan(output, nrows);
+    }
+}
+
+extern "C" void tg_matmul_q4k_scalar(const uint8_t *q4_matrix, const float *input, float *output, int nrows,
+                                     int ncols) {
+    if (nrows <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_matmul_k(false, q4_matrix, input, output, nrows, ncols, true)) {
+        legacy_fail("tg_matmul_q4k_scalar", warned_matmul_q4k_scalar);
+        fill_nan(output, nrows);
+    }
+}
+
+// f16 (half) or f32 matrix nrows x ncols times x
+static int lg_matvec(bool half, const void *A, const float *x, float *out, int nrows, int ncols) {
+    const size_t ab = (size_t)nrows * ncols * (half ? 2 : 4);
+    for (int pass = 0; pass < 2; pass++) {
+        LgCarve c{pass ? g_lg_buf : nullptr};
+        uint8_t *da = c.take<uint8_t>(ab);
+        float *dx = c.take<float>(4 * (size_t)ncols), *dy = c.take<float>(4 * (size_t)nrows);
+        if (!pass) {
+            int rc = lg_reserve(c.off);
+            if (rc) return rc;
+            continue;
+        }
+        int rc;
+        if ((rc = lg_h2d(da, A, ab)) || (rc = lg_h2d(dx, x, 4 * (size_t)ncols))) return rc;
+        HIP_TRY(tg::launch_matvec_two_acc(da, half, dx, dy, nrows, ncols, g_lg_st));
+        return lg_finish(out, dy, 4 * (size_t)nrows);
+    }
+    return TG_OK;
+}
+
+extern "C" void tg_f32_matvec(const float *A, const float *x, float *out, int nrows, int ncols) {
+    if (nrows <= 0 || ncols < 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_matvec(false, A, x, out, nrows, ncols)) {
+        legacy_fail("tg_f32_matvec", warned_f32_matvec);
+        fill_nan(out, nrows);
+    }
+}
+
+extern "C" void tg_f16_matvec(const uint16_t *A, const float *x, float *out, int nrows, int ncols) {
+    if (nrows <= 0 || ncols < 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_matvec(true, A, x, out, nrows, ncols)) {
+        legacy_fail("tg_f16_matvec", warned_f16_matvec);
+        fill_nan(out, nrows);
+    }
+}
+
+extern "C" void tg_rms_norm(const float *x, const float *weight, float *out, int dim, float eps) {
+    if (dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    auto run = [&]() -> int {
+        for (int pass = 0; pass < 2; pass++) {
+            LgCarve c{pass ? g_lg_buf : nullptr};
+            float *dx = c.take<float>(4 * (size_t)dim), *dw = c.take<float>(4 * (size_t)dim);
+            float *dy = c.take<float>(4 * (size_t)dim);
+            if (!pass) {
+                int rc = lg_reserve(c.off);
+                if (rc) return rc;
+                continue;
+            }
+            int rc;
+            if ((rc = lg_h2d(dx, x, 4 * (size_t)dim)) || (rc = lg_h2d(dw, weight, 4 * (size_t)dim))) return rc;
+            HIP_TRY(tg::launch_rms_norm(dx, dw, dy, dim, eps, g_lg_st));
+            return lg_finish(out, dy, 4 * (size_t)dim);
+        }
+        return TG_OK;
+    };
+    if (run()) {
+        legacy_fail("tg_rms_norm", warned_rms_norm);
+        fill_nan(out, dim);
+    }
 }
 
 extern "C" void tg_attention_decode(const float *, const float *, const float *, const float *, const float *,
@@ -1018,13 +1311,3 @@ extern "C" void tg_transformer_layer(const float *, const float *, const float *
     fill_nan(x, embed_dim);
 }
 
-extern "C" void tg_moe_forward(const uint8_t **, const float *, int, const float *, float *output, int embed_dim,
-                               int) {
-    legacy_unavailable("tg_moe_forward", warned_moe_forward);
-    fill_nan(output, embed_dim);
-}
-
-extern "C" void tg_matmul_q4k_scalar(const uint8_t *, const float *, float *output, int nrows, int) {
-    legacy_unavailable("tg_matmul_q4k_scalar", warned_matmul_q4k_scalar);
-    fill_nan(output, nrows);
-}

@@ -96,6 +96,21 @@ hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, int T, const i
 bool experts_fused_ok(const Shape &s, int n_cu);
 size_t experts_fused_words(const Shape &s);
 
+// Legacy formats (libtinygiant.c): 256-value super-blocks; Q4_K 144 bytes,
+// Q6_K 210 bytes, the Q8 activation block (fp32 scale, int32 sum, 256 int8)
+// 264 bytes.  Launchers of tg_legacy.hip; xq buffers are 8-byte aligned,
+// Q4_K matrices 16-byte aligned.
+constexpr int LG_QK = 256, LG_Q4K_BYTES = 144, LG_Q6K_BYTES = 210, LG_Q8K_BYTES = 264;
+hipError_t launch_quantize_q8k(const float *x, void *xq, int nblocks, hipStream_t st);
+hipError_t launch_matmul_q4k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st);
+hipError_t launch_matmul_q6k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st);
+hipError_t launch_matvec_two_acc(const void *A, bool half, const float *x, float *y, int nrows, int ncols,
+                                 hipStream_t st);
+hipError_t launch_rms_norm(const float *x, const float *w, float *out, int dim, float eps, hipStream_t st);
+hipError_t launch_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y, int nrows, int bpr, hipStream_t st);
+hipError_t launch_silu_mul_vec(const float *g, const float *u, float *h, int n, hipStream_t st);
+hipError_t launch_acc_scaled(float *out, const float *v, float w, int n, hipStream_t st);
+
 // One-token layer with routing inside (k_layer_dec) and the prologue that
 // forms the first layer's router partials (k_dec_part).  part buffers hold
 // [E+1][H/32] floats, dec_part_floats() the size of two; the group hand-off
