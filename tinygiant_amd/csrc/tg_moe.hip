@@ -1485,34 +1485,50 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
 constexpr int GR_THREADS = 1024;
 constexpr int GR_PER = 16;  // entries per thread per pass of k_group
 
-// Exclusive prefix sum of one int per thread over threads 0..255 (values of
-// threads >= n count as 0), through one shuffle scan per wave and the wave
-// totals in LDS (tmp[4]).  Every thread of the block must call it.
-TG_DEV int scan_256(int v, int n, int *tmp) {
+// Exclusive prefix sums of N ints per thread over threads 0..255 (threads
+// >= n count as 0) with one pair of barriers: a shuffle scan per wave and
+// the wave totals in LDS (tmp[4 * N]).  Every thread of the block calls it.
+template <int N>
+TG_DEV void scan_256_n(int (&v)[N], int n, int *tmp) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wv = tid / WAVE;
-    int x = tid < n ? v : 0;
+    int x[N];
+#pragma unroll
+    for (int j = 0; j < N; j++) x[j] = tid < n ? v[j] : 0;
     for (int o = 1; o < WAVE; o <<= 1) {
-        const int y = __shfl_up(x, o, WAVE);
-        if (lane >= o) x += y;
+#pragma unroll
+        for (int j = 0; j < N; j++) {
+            const int y = __shfl_up(x[j], o, WAVE);
+            if (lane >= o) x[j] += y;
+        }
     }
-    if (tid < 4 * WAVE && lane == WAVE - 1) tmp[wv] = x;
+    if (tid < 4 * WAVE && lane == WAVE - 1)
+#pragma unroll
+        for (int j = 0; j < N; j++) tmp[wv * N + j] = x[j];
     __syncthreads();
-    int base = 0;
-    for (int i = 0; i < wv && i < 4; i++) base += tmp[i];
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        int base = 0;
+        for (int i = 0; i < wv && i < 4; i++) base += tmp[i * N + j];
+        v[j] = x[j] - (tid < n ? v[j] : 0) + base;
+    }
     __syncthreads();
-    return x - (tid < n ? v : 0) + base;
 }
 
 // Work list: the entries of each expert cut into chunks of at most `ch`
 // (gate/up) and `chd` (down) entries; item w = (expert, first entry, count)
 // in work[3 * w ..], the number of items in work_n[0] (gate/up) and
 // work_n[1] (down; its items start at work + 3 * wmax).  Thread e handles
-// expert e: its count, offset and work items come from block scans.
+// expert e: its count, offset and work items come from block scans.  SORT:
+// items are listed by size class, largest first (full chunks, then
+// remainders of more than half, more than a quarter, the rest), since blocks
+// are dispatched in item order and the short ones then fill the tail of the
+// grid; otherwise each expert's items follow one another in expert order.
+template <bool SORT>
 __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict__ idx, int n, int E, int ch, int chd,
                                                       int wmax, int32_t *__restrict__ counts,
                                                       int32_t *__restrict__ offsets, int32_t *__restrict__ entries,
                                                       int32_t *__restrict__ work, int32_t *__restrict__ work_n) {
-    __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E], tmp[4];
+    __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E], tmp9[4 * 9], cls_tot[8];
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += GR_THREADS) {
         cnt[e] = 0;
@@ -1538,33 +1554,87 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
     }
     __syncthreads();
     const int c = tid < E ? cnt[tid] : 0;
-    const int ng = (c + ch - 1) / ch, nd = (c + chd - 1) / chd;
-    const int o = scan_256(c, E, tmp);
-    const int bg = scan_256(ng, E, tmp);
-    const int bd = scan_256(nd, E, tmp);
+    if constexpr (!SORT) {
+        int sv[3] = {c, (c + ch - 1) / ch, (c + chd - 1) / chd};
+        scan_256_n<3>(sv, E, tmp9);
+        const int o = sv[0], bg = sv[1], bd = sv[2], ng = (c + ch - 1) / ch, nd = (c + chd - 1) / chd;
+        if (tid < E) {
+            off[tid] = o;
+            offsets[tid] = o;
+            counts[tid] = c;
+            for (int i = 0; i < ng && bg + i < wmax; i++) {
+                int32_t *it = work + 3 * (size_t)(bg + i);
+                it[0] = tid;
+                it[1] = o + i * ch;
+                it[2] = c - i * ch < ch ? c - i * ch : ch;
+            }
+            for (int i = 0; i < nd && bd + i < wmax; i++) {
+                int32_t *it = work + 3 * ((size_t)wmax + bd + i);
+                it[0] = tid;
+                it[1] = o + i * chd;
+                it[2] = c - i * chd < chd ? c - i * chd : chd;
+            }
+            if (tid == E - 1) {
+                offsets[E] = o + c;
+                work_n[0] = bg + ng < wmax ? bg + ng : wmax;
+                work_n[1] = bd + nd < wmax ? bd + nd : wmax;
+            }
+        }
+        __syncthreads();
+    } else {
+    // per list (chunk size): full chunks, then the remainder in its class;
+    // the counts and the class flags of both lists in one scan
+    int nf[2], rr[2], cl[2];
+    for (int lst = 0; lst < 2; lst++) {
+        const int chk = lst ? chd : ch;
+        nf[lst] = c / chk;
+        rr[lst] = c - nf[lst] * chk;
+        cl[lst] = rr[lst] == 0 ? -1 : (4 * rr[lst] > 2 * chk ? 0 : (4 * rr[lst] > chk ? 1 : 2));
+    }
+    int sv[9] = {c, nf[0], cl[0] == 0, cl[0] == 1, cl[0] == 2, nf[1], cl[1] == 0, cl[1] == 1, cl[1] == 2};
+    int sc[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) sc[j] = sv[j];
+    scan_256_n<9>(sc, E, tmp9);
+    const int o = sc[0];
     if (tid < E) {
         off[tid] = o;
         offsets[tid] = o;
         counts[tid] = c;
-        for (int i = 0; i < ng && bg + i < wmax; i++) {
-            int32_t *it = work + 3 * (size_t)(bg + i);
-            it[0] = tid;
-            it[1] = o + i * ch;
-            it[2] = c - i * ch < ch ? c - i * ch : ch;
-        }
-        for (int i = 0; i < nd && bd + i < wmax; i++) {
-            int32_t *it = work + 3 * ((size_t)wmax + bd + i);
-            it[0] = tid;
-            it[1] = o + i * chd;
-            it[2] = c - i * chd < chd ? c - i * chd : chd;
-        }
         if (tid == E - 1) {
             offsets[E] = o + c;
-            work_n[0] = bg + ng < wmax ? bg + ng : wmax;
-            work_n[1] = bd + nd < wmax ? bd + nd : wmax;
+            // class totals (exclusive scan + own value)
+            for (int j = 0; j < 8; j++) cls_tot[j] = sc[1 + j] + sv[1 + j];
         }
     }
     __syncthreads();
+    for (int lst = 0; lst < 2; lst++) {
+        const int chk = lst ? chd : ch, nfull = nf[lst], r = rr[lst], cls = cl[lst];
+        const int *tot4 = cls_tot + 4 * lst;
+        const int bf = sc[1 + 4 * lst], b0 = sc[2 + 4 * lst], b1 = sc[3 + 4 * lst], b2 = sc[4 + 4 * lst];
+        const int base_r = cls == 0 ? tot4[0] + b0 : cls == 1 ? tot4[0] + tot4[1] + b1 : tot4[0] + tot4[1] + tot4[2] + b2;
+        int32_t *wl = work + 3 * (size_t)(lst ? wmax : 0);
+        if (tid < E) {
+            for (int i = 0; i < nfull && bf + i < wmax; i++) {
+                int32_t *it = wl + 3 * (size_t)(bf + i);
+                it[0] = tid;
+                it[1] = o + i * chk;
+                it[2] = chk;
+            }
+            if (cls >= 0 && base_r < wmax) {
+                int32_t *it = wl + 3 * (size_t)base_r;
+                it[0] = tid;
+                it[1] = o + nfull * chk;
+                it[2] = r;
+            }
+        }
+        if (tid == 0) {
+            const int tot = tot4[0] + tot4[1] + tot4[2] + tot4[3];
+            work_n[lst] = tot < wmax ? tot : wmax;
+        }
+    }
+    __syncthreads();
+    }
     for (int base = 0; base < n; base += GR_THREADS * GR_PER) {
         int ev[GR_PER];
 #pragma unroll
@@ -2031,15 +2101,20 @@ int group_work_max(const Shape &s, int n) {
 
 hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
+    hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
                        dn_chunk(s.nbI, s.I), group_work_max(s, n), counts, offsets, entries, work, work_n);
     return hipGetLastError();
 }
 
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
                                 int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch, group_work_max(s, n, ch),
-                       counts, offsets, entries, work, work_n);
+    // items of several M-tiles: largest first (one-tile items are all alike)
+    if (ch > 32)
+        hipLaunchKernelGGL(k_group<true>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
+                           group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
+    else
+        hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
+                           group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
     return hipGetLastError();
 }
 
