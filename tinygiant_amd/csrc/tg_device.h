@@ -148,6 +148,27 @@ TG_DEV float block_sumsq(const float *__restrict__ x, int n, float *red) {
     return tot;
 }
 
+// s_waitcnt immediate (gfx9 encoding) that waits for all vector memory
+// operations of the wave and for nothing else (expcnt 7, lgkmcnt 15)
+constexpr int VMCNT0 = (7 << 4) | (15 << 8);
+
+// v through an empty asm at the point of use: a conversion of a loaded value
+// (fp16 scale to float) stays there instead of being hoisted next to its
+// load, where it would make the wave wait for the load early.
+TG_DEV uint32_t at_use(uint32_t v) {
+    __asm__ volatile("" : "+v"(v));
+    return v;
+}
+
+// Workgroup barrier that orders LDS only (waits for this wave's LDS
+// operations, not for its global loads): weight loads issued before it stay
+// in flight across it.  For barriers whose data is all in LDS.
+TG_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Tagged words: a 32-bit payload and a 32-bit tag in one 64-bit word,
 // stored and loaded with relaxed agent-scope atomics, so a reader that sees
 // the tag it expects also sees the payload stored with it.

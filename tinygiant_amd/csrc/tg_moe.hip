@@ -878,17 +878,17 @@ TG_DEV void fx_gu_dots(const int8_t *gxq, const float *gxd, const int *gxs, cons
             xs[tid] = gxs[tid];
         }
     }
-    __syncthreads();
+    lds_barrier();  // LDS only: the block's other loads stay in flight
 #pragma unroll
     for (int u = 0; u < UG; u++) {
         const int p = u * FX_THREADS + tid;
         if (p < items) {
             const int rd = (int)fdiv((uint32_t)p, s.divH), b = p - rd * nb;
             const int S = dot_q4_q8(g.wv[u], reinterpret_cast<const int *>(xq + b * QK)) - 8 * xs[b];
-            U[rd * ust + b] = (float)S * h2f(g.dv[u]);
+            U[rd * ust + b] = (float)S * h2f((uint16_t)at_use(g.dv[u]));
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // ... and the chains, SwiGLU and Q8_0 of the 32 h rows, published as FX_QW
@@ -1232,8 +1232,23 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         rcnt[tid] = 0;
     }
     __syncthreads();
-    rank_topk(keys, E, k, sidx, rcnt);
-    // softmax on wave 0, Q8_0(x * s) into the gate/up LDS layout on waves 1..4
+    rank_topk(keys, E, k, sidx, rcnt);  // ends with a barrier: sidx is set
+    // the first unit's weights are in flight while wave 0 forms the softmax
+    // and waves 1..4 Q8_0(x * s) into the gate/up LDS layout; x * s is
+    // formed (and pinned) before the unit loads are issued, so the Q8_0
+    // waits for no load
+    float xsv[8];
+    if (qon) {
+        const float v[8] = {xa.x * sc, xa.y * sc, xa.z * sc, xa.w * sc, xb.x * sc, xb.y * sc, xb.z * sc, xb.w * sc};
+#pragma unroll
+        for (int c = 0; c < 8; c++) xsv[c] = __uint_as_float(at_use(__float_as_uint(v[c])));
+    }
+    // the loads issued at launch (x, the residual rows, the router columns)
+    // landed long ago: an explicit wait for them here leaves the unit's
+    // loads as the only ones in flight, so nothing below waits for those
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    FxGu<UG> g;
+    if (u0 < ng) fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
     if (tid < WAVE) {
         const float wj = topk_softmax_lane(slog, sidx, k);
         if (tid < k) {
@@ -1248,15 +1263,10 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     int8_t *xq = reinterpret_cast<int8_t *>(smem);
     float *xd = reinterpret_cast<float *>(xq + H);
     int *xs = reinterpret_cast<int *>(xd + round4(s.nbH));
-    if (qon) {
-        const float v[8] = {xa.x * sc, xa.y * sc, xa.z * sc, xa.w * sc, xb.x * sc, xb.y * sc, xb.z * sc, xb.w * sc};
-        q8_group8(v, true, qt * 8, xq, xd, xs);
-    }
-    __syncthreads();  // sw, sidx, Q8_0 x
+    if (qon) q8_group8(xsv, true, qt * 8, xq, xd, xs);
+    lds_barrier();  // sw, Q8_0 x (the unit's loads stay in flight)
 
-    FxGu<UG> g;
     if (u0 < ng) {
-        fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
         fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
         fx_gu_publish(s, u0, tag, hw, smem);
     }
@@ -1285,7 +1295,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     if (DOWN_FIRST) down_loads();
     for (int unit = u0 + NB; unit < ng; unit += NB) {
         fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
-        __syncthreads();  // wave 0 has read the previous unit's LDS
+        lds_barrier();  // wave 0 has read the previous unit's LDS
         fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
         fx_gu_publish(s, unit, tag, hw, smem);
     }
@@ -1329,7 +1339,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
             const int jj = rdi >> lrd;
             const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
                           8 * hs[jj * nbp + b];
-            U[rdi * ust + b] = (float)S * h2f(dv[u]);
+            U[rdi * ust + b] = (float)S * h2f((uint16_t)at_use(dv[u]));
         }
     }
     __syncthreads();
