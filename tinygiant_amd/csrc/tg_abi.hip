@@ -89,6 +89,9 @@ struct ProfRec {
     std::string kernel;
     hipEvent_t start, stop;
 };
+namespace tg {
+thread_local LaunchEvents g_launch_ev = {nullptr, nullptr};
+}
 static std::mutex g_prof_mu;
 static bool g_prof_on = false;
 static std::vector<ProfRec> g_prof;
@@ -114,6 +117,9 @@ static void prof_clear() {
 }
 
 // Records the start event of one launch; returns its slot (or -1).
+// The launch inside takes the events (TG_LAUNCH), so they time the kernel's
+// own execution; a launch that does not take them is timed by the start
+// event recorded here and the stop event prof_end records.
 static int prof_begin(const char *kernel, hipStream_t st) {
     if (!g_prof_on) return -1;
     std::lock_guard<std::mutex> lk(g_prof_mu);
@@ -121,13 +127,16 @@ static int prof_begin(const char *kernel, hipStream_t st) {
     if (!r.start || !r.stop) return -1;
     (void)hipEventRecord(r.start, st);
     g_prof.push_back(r);
+    tg::g_launch_ev = {r.start, r.stop};
     return (int)g_prof.size() - 1;
 }
 
 static void prof_end(int slot, hipStream_t st) {
     if (slot < 0) return;
     std::lock_guard<std::mutex> lk(g_prof_mu);
-    (void)hipEventRecord(g_prof[(size_t)slot].stop, st);
+    const bool taken = tg::g_launch_ev.start == nullptr;  // the launch recorded both events
+    tg::g_launch_ev = {nullptr, nullptr};
+    if (!taken) (void)hipEventRecord(g_prof[(size_t)slot].stop, st);
 }
 
 extern "C" int tg_prof_enable(int on) {
@@ -155,11 +164,14 @@ extern "C" int tg_prof_read(const char *kernel, int *launches, double *total_ms)
     return TG_OK;
 }
 
-#define PROFILED(name, st, launch)             \
-    do {                                       \
-        int slot_ = prof_begin(name, st);      \
-        HIP_TRY(launch);                       \
-        prof_end(slot_, st);                   \
+#define PROFILED(name, st, launch)                                                             \
+    do {                                                                                       \
+        int slot_ = prof_begin(name, st);                                                      \
+        hipError_t pe_ = (launch);                                                             \
+        prof_end(slot_, st);                                                                   \
+        if (pe_ != hipSuccess)                                                                 \
+            return set_err(TG_E_HIP, "%s: %s (%s:%d)", #launch, hipGetErrorString(pe_), __FILE__, \
+                           __LINE__);                                                          \
     } while (0)
 
 // ================================================================ arena

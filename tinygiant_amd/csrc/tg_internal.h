@@ -1,11 +1,31 @@
 // tg_internal.h -- shapes and kernel launchers shared by the C ABI layer.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace tg {
+
+// Kernel launch.  When a profiling caller has set g_launch_ev, the launch
+// records those events at the kernel's own start and end
+// (hipExtLaunchKernelGGL, the timestamps of the dispatch itself, as a kernel
+// trace reports them) and clears them; otherwise it is hipLaunchKernelGGL.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+extern thread_local LaunchEvents g_launch_ev;
+#define TG_LAUNCH(K, grid, block, lds, st, ...)                                                             \
+    do {                                                                                                    \
+        if (::tg::g_launch_ev.start) {                                                                      \
+            const ::tg::LaunchEvents ev_ = ::tg::g_launch_ev;                                               \
+            ::tg::g_launch_ev = {nullptr, nullptr};                                                         \
+            hipExtLaunchKernelGGL(K, grid, block, (std::uint32_t)(lds), st, ev_.start, ev_.stop, 0u, __VA_ARGS__); \
+        } else {                                                                                            \
+            hipLaunchKernelGGL(K, grid, block, lds, st, __VA_ARGS__);                                       \
+        }                                                                                                   \
+    } while (0)
 
 // One layer's geometry: H = embed dim, I = expert intermediate dim, E
 // experts, top-k.  Byte sizes are those of the relayout format (18 bytes

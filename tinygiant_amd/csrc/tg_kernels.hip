@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256) void k_stream_read(const uint4 *__restrict__ p
 static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
 hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *sink, hipStream_t st) {
-    hipLaunchKernelGGL(k_stream_read, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(p), bytes / 16, sink);
+    TG_LAUNCH(k_stream_read, dim3(grid), dim3(256), 0, st, static_cast<const uint4 *>(p), bytes / 16, sink);
     return hipGetLastError();
 }
 
@@ -350,11 +350,11 @@ uint64_t host_stream_key(uint64_t seed, uint64_t stream) {
 hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, int layer, uint64_t seed,
                               float sigma, hipStream_t st) {
     size_t nblocks = (size_t)s.E * (2 * (size_t)s.I * s.nbH + (size_t)s.H * s.nbI);
-    hipLaunchKernelGGL(k_synth_layer, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, layer_pl, s, seed, layer,
+    TG_LAUNCH(k_synth_layer, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, layer_pl, s, seed, layer,
                        sigma, nblocks);
     if (router) {
         size_t n = (size_t)s.E * s.H;
-        hipLaunchKernelGGL(k_synth_normal, dim3(cdiv(n, 256)), dim3(256), 0, st, router,
+        TG_LAUNCH(k_synth_normal, dim3(cdiv(n, 256)), dim3(256), 0, st, router,
                            host_stream_key(seed, stream_id(layer, 0, 3)), sigma, n);
     }
     return hipGetLastError();
@@ -362,43 +362,43 @@ hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, 
 
 hipError_t launch_synth_q40(uint8_t *pl, uint64_t key, float sigma, int rows, int nb, hipStream_t st) {
     size_t n = (size_t)rows * nb;
-    hipLaunchKernelGGL(k_synth_q40, dim3(cdiv(n, 256)), dim3(256), 0, st, pl, key, sigma, rows, nb);
+    TG_LAUNCH(k_synth_q40, dim3(cdiv(n, 256)), dim3(256), 0, st, pl, key, sigma, rows, nb);
     return hipGetLastError();
 }
 
 hipError_t launch_synth_normal(float *out, uint64_t key, float sigma, size_t n, hipStream_t st) {
-    hipLaunchKernelGGL(k_synth_normal, dim3(cdiv(n, 256)), dim3(256), 0, st, out, key, sigma, n);
+    TG_LAUNCH(k_synth_normal, dim3(cdiv(n, 256)), dim3(256), 0, st, out, key, sigma, n);
     return hipGetLastError();
 }
 
 hipError_t launch_repack_layer(const uint8_t *src, uint8_t *dst, const Shape &s, bool to_planar, hipStream_t st) {
     size_t nblocks = (size_t)s.E * (2 * (size_t)s.I * s.nbH + (size_t)s.H * s.nbI);
-    hipLaunchKernelGGL(k_repack_layer, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, src, dst, s, nblocks,
+    TG_LAUNCH(k_repack_layer, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, src, dst, s, nblocks,
                        to_planar ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t launch_repack_tensor(const uint8_t *src, uint8_t *dst, size_t nblocks, bool to_planar, hipStream_t st) {
-    hipLaunchKernelGGL(k_repack_tensor, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, src, dst, nblocks,
+    TG_LAUNCH(k_repack_tensor, dim3(cdiv(nblocks, 256)), dim3(256), 0, st, src, dst, nblocks,
                        to_planar ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_q8_0(const float *x, uint8_t *out, int n, hipStream_t st) {
-    hipLaunchKernelGGL(k_quantize_q8_0, dim3(cdiv((size_t)n, 256)), dim3(256), 0, st, x, out, n);
+    TG_LAUNCH(k_quantize_q8_0, dim3(cdiv((size_t)n, 256)), dim3(256), 0, st, x, out, n);
     return hipGetLastError();
 }
 
 hipError_t launch_block_sums(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, int32_t *sums,
                              hipStream_t st) {
     size_t n = (size_t)rows * nb;
-    hipLaunchKernelGGL(k_block_sums, dim3(cdiv(n, 256)), dim3(256), 0, st, w_pl, rows, nb, xq8, sums);
+    TG_LAUNCH(k_block_sums, dim3(cdiv(n, 256)), dim3(256), 0, st, w_pl, rows, nb, xq8, sums);
     return hipGetLastError();
 }
 
 hipError_t launch_matvec(const uint8_t *w_pl, int rows, int nb, const uint8_t *xq8, float *out, hipStream_t st) {
     size_t lds = (size_t)nb * QK + 8 * (size_t)nb + 4 * (size_t)MV_RT * (nb + 1);
-    hipLaunchKernelGGL(k_matvec, dim3(cdiv((size_t)rows, MV_RT)), dim3(256), lds, st, w_pl, rows, nb, xq8, out);
+    TG_LAUNCH(k_matvec, dim3(cdiv((size_t)rows, MV_RT)), dim3(256), lds, st, w_pl, rows, nb, xq8, out);
     return hipGetLastError();
 }
 

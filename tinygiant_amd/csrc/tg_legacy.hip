@@ -333,20 +333,20 @@ static unsigned lg_cdiv(long n, long d) { return (unsigned)((n + d - 1) / d); }
 
 hipError_t launch_quantize_q8k(const float *x, void *xq, int nblocks, hipStream_t st) {
     if (nblocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_quantize_q8k, dim3(lg_cdiv(nblocks, 4)), dim3(256), 0, st, x, static_cast<Q8K *>(xq), nblocks);
+    TG_LAUNCH(k_quantize_q8k, dim3(lg_cdiv(nblocks, 4)), dim3(256), 0, st, x, static_cast<Q8K *>(xq), nblocks);
     return hipGetLastError();
 }
 
 hipError_t launch_matmul_q4k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_matmul_q4k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
+    TG_LAUNCH(k_matmul_q4k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
                        nrows, bpr);
     return hipGetLastError();
 }
 
 hipError_t launch_matmul_q6k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_matmul_q6k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
+    TG_LAUNCH(k_matmul_q6k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
                        nrows, bpr);
     return hipGetLastError();
 }
@@ -356,33 +356,33 @@ hipError_t launch_matvec_two_acc(const void *A, bool half, const float *x, float
     if (nrows <= 0) return hipSuccess;
     const dim3 grid(lg_cdiv(nrows, 32));
     if (half)
-        hipLaunchKernelGGL(k_matvec_two_acc<true>, grid, dim3(256), 0, st, A, x, y, nrows, ncols);
+        TG_LAUNCH(k_matvec_two_acc<true>, grid, dim3(256), 0, st, A, x, y, nrows, ncols);
     else
-        hipLaunchKernelGGL(k_matvec_two_acc<false>, grid, dim3(256), 0, st, A, x, y, nrows, ncols);
+        TG_LAUNCH(k_matvec_two_acc<false>, grid, dim3(256), 0, st, A, x, y, nrows, ncols);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int dim, float eps, hipStream_t st) {
     if (dim <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_rms_norm, dim3(1), dim3(256), 0, st, x, w, out, dim, eps);
+    TG_LAUNCH(k_rms_norm, dim3(1), dim3(256), 0, st, x, w, out, dim, eps);
     return hipGetLastError();
 }
 
 hipError_t launch_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_matmul_q4k_scalar, dim3(lg_cdiv(nrows, 256)), dim3(256), 0, st, W, x, y, nrows, bpr);
+    TG_LAUNCH(k_matmul_q4k_scalar, dim3(lg_cdiv(nrows, 256)), dim3(256), 0, st, W, x, y, nrows, bpr);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_mul_vec(const float *g, const float *u, float *h, int n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_silu_mul_vec, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, g, u, h, n);
+    TG_LAUNCH(k_silu_mul_vec, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, g, u, h, n);
     return hipGetLastError();
 }
 
 hipError_t launch_acc_scaled(float *out, const float *v, float w, int n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_acc_scaled, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, out, v, w, n);
+    TG_LAUNCH(k_acc_scaled, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, out, v, w, n);
     return hipGetLastError();
 }
 

@@ -633,7 +633,7 @@ static hipError_t mf_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
     }
     // gate/up: NW/2 tiles (each as a gate wave and an up wave) per block
     const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (NW / 2)) : mf_cdiv((size_t)rows, 32 * NW);
-    hipLaunchKernelGGL((k_mfma_grouped<MT, PAIR, NW>), dim3(gx, wmax), dim3(NW * 64), lds, st, layer_pl, s, work,
+    TG_LAUNCH((k_mfma_grouped<MT, PAIR, NW>), dim3(gx, wmax), dim3(NW * 64), lds, st, layer_pl, s, work,
                        work_n, entries, aq, ad, oq, od, os, D);
     return hipGetLastError();
 }
@@ -647,10 +647,10 @@ static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
     const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (MS_NW / 2)) : mf_cdiv((size_t)rows, 32 * MS_NW);
     // 16-byte scale loads need every row's scales 16-byte aligned (nb % 8 == 0)
     if (nb % MF_KC == 0)
-        hipLaunchKernelGGL((k_mfma_small<PAIR, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+        TG_LAUNCH((k_mfma_small<PAIR, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
                            work_n, entries, aq, ad, oq, od, os, D);
     else
-        hipLaunchKernelGGL((k_mfma_small<PAIR, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+        TG_LAUNCH((k_mfma_small<PAIR, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
                            work_n, entries, aq, ad, oq, od, os, D);
     return hipGetLastError();
 }

@@ -1910,16 +1910,16 @@ bool decode_shape_ok(const Shape &s) {
 
 hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
     if (T >= 128 && (H / RG) % RT_CH == 0) {
-        hipLaunchKernelGGL(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
+        TG_LAUNCH(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
                            T, E, H, raw);
     } else if (T >= RS_T && (H / RG) % (2 * RS_PARTS) == 0 && route_small_lds(H) <= 64 * 1024) {
         const size_t lds = route_small_lds(H);
         hipError_t e = allow_lds((const void *)k_route_small, lds);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_route_small, dim3(cdiv((size_t)T, RS_T), cdiv((size_t)E, RS_E)), dim3(1024), lds, st,
+        TG_LAUNCH(k_route_small, dim3(cdiv((size_t)T, RS_T), cdiv((size_t)E, RS_E)), dim3(1024), lds, st,
                            Wr, x, T, E, H, raw);
     } else {
-        hipLaunchKernelGGL(k_route, dim3(E, cdiv((size_t)T, RT_TOK)), dim3(RT_THREADS), 0, st, Wr, x, T, E, H, raw);
+        TG_LAUNCH(k_route, dim3(E, cdiv((size_t)T, RT_TOK)), dim3(RT_THREADS), 0, st, Wr, x, T, E, H, raw);
     }
     return hipGetLastError();
 }
@@ -1929,7 +1929,7 @@ hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, in
     size_t lds = route_lds_bytes(H);
     hipError_t e = allow_lds((const void *)k_topk, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_topk, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, logits, idx, w);
+    TG_LAUNCH(k_topk, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, logits, idx, w);
     return hipGetLastError();
 }
 
@@ -1937,7 +1937,7 @@ hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape 
                             uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
                             hipStream_t st) {
     if (!decode_shape_ok(s)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route_dec, dim3(s.E, T), dim3(RD_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
+    TG_LAUNCH(k_route_dec, dim3(s.E, T), dim3(RD_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
                        w, xq, xd, xs);
     return hipGetLastError();
 }
@@ -1948,7 +1948,7 @@ static hipError_t gateup_go(const uint8_t *layer_pl, const Shape &s, int T, cons
     const size_t lds = gateup_lds_bytes(s.H, s.nbH);
     hipError_t e = allow_lds((const void *)k_gateup<UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_gateup<UNR>, dim3(s.I / GU_ROWS, s.k, T), dim3(GU_THREADS), lds, st, layer_pl, s, idx, xq,
+    TG_LAUNCH(k_gateup<UNR>, dim3(s.I / GU_ROWS, s.k, T), dim3(GU_THREADS), lds, st, layer_pl, s, idx, xq,
                        xd, xs, hq, hd, hs);
     return hipGetLastError();
 }
@@ -1971,7 +1971,7 @@ static hipError_t down_go(const uint8_t *layer_pl, const Shape &s, int T, const 
     const size_t lds = down_lds_bytes(s.k, s.I, s.nbI);
     hipError_t e = allow_lds((const void *)k_down<UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_down<UNR>, dim3(s.H / DN_RD, T), dim3(DN_THREADS), lds, st, layer_pl, s, idx, w, hq, hd, hs,
+    TG_LAUNCH(k_down<UNR>, dim3(s.H / DN_RD, T), dim3(DN_THREADS), lds, st, layer_pl, s, idx, w, hq, hd, hs,
                        resid, out);
     return hipGetLastError();
 }
@@ -2012,7 +2012,7 @@ static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
     const size_t lds = fx_lds_bytes(s, A.rd);
     hipError_t e = allow_lds((const void *)k_experts<UG, UD>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_experts<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    TG_LAUNCH((k_experts<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
     return hipGetLastError();
 }
 
@@ -2057,7 +2057,7 @@ bool layer_dec_ok(const Shape &s, int n_cu) {
 
 hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, float *part, uint32_t *ctl, int n_layers,
                            hipStream_t st) {
-    hipLaunchKernelGGL(k_dec_part, dim3(s.H / RG), dim3(256), 0, st, Wr, x, s.E, s.H, part, ctl, n_layers);
+    TG_LAUNCH(k_dec_part, dim3(s.H / RG), dim3(256), 0, st, Wr, x, s.E, s.H, part, ctl, n_layers);
     return hipGetLastError();
 }
 
@@ -2066,7 +2066,7 @@ static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
     const size_t lds = ld_lds_bytes(s, A.rd);
     hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    TG_LAUNCH((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
     return hipGetLastError();
 }
 
@@ -2095,7 +2095,7 @@ hipError_t launch_route_q8(const float *raw, const float *x, int T, int E, int H
     size_t lds = route_lds_bytes(H);
     hipError_t e = allow_lds((const void *)k_route_q8, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, idx, w, xq, xd, xs);
+    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, idx, w, xq, xd, xs);
     return hipGetLastError();
 }
 
@@ -2111,7 +2111,7 @@ int group_work_max(const Shape &s, int n) {
 
 hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
-    hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
+    TG_LAUNCH(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
                        dn_chunk(s.nbI, s.I), group_work_max(s, n), counts, offsets, entries, work, work_n);
     return hipGetLastError();
 }
@@ -2120,10 +2120,10 @@ hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int c
                                 int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
     // items of several M-tiles: largest first (one-tile items are all alike)
     if (ch > 32)
-        hipLaunchKernelGGL(k_group<true>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
+        TG_LAUNCH(k_group<true>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
                            group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
     else
-        hipLaunchKernelGGL(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
+        TG_LAUNCH(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
                            group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
     return hipGetLastError();
 }
@@ -2135,7 +2135,7 @@ static hipError_t gug_go(const uint8_t *layer_pl, const Shape &s, int wmax, cons
     size_t lds = gu_grouped_lds(s.nbH);
     hipError_t e = allow_lds((const void *)k_gateup_grouped<NT, UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((k_gateup_grouped<NT, UNR>), dim3(s.nbI, wmax), dim3(NT), lds, st, layer_pl, s, work,
+    TG_LAUNCH((k_gateup_grouped<NT, UNR>), dim3(s.nbI, wmax), dim3(NT), lds, st, layer_pl, s, work,
                        work_n, entries, xq, xd, xs, hq, hd, hs);
     return hipGetLastError();
 }
@@ -2159,7 +2159,7 @@ static hipError_t dng_go(const uint8_t *layer_pl, const Shape &s, int wmax, cons
     size_t lds = dn_grouped_lds(s.nbI, s.I);
     hipError_t e = allow_lds((const void *)k_down_grouped<UNR>, lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_down_grouped<UNR>, dim3(s.H / 32, wmax), dim3(RO_THREADS), lds, st, layer_pl, s,
+    TG_LAUNCH(k_down_grouped<UNR>, dim3(s.H / 32, wmax), dim3(RO_THREADS), lds, st, layer_pl, s,
                        work + 3 * (size_t)wmax, work_n, entries, hq, hd, hs, D);
     return hipGetLastError();
 }
@@ -2181,9 +2181,9 @@ hipError_t launch_combine(const float *D, const float *w, int T, int H, int k, c
     const bool vec = H % 4 == 0 && k <= MAX_K && ((uintptr_t)out & 15) == 0 && ((uintptr_t)resid & 15) == 0 &&
                      ((uintptr_t)D & 15) == 0;
     if (vec)
-        hipLaunchKernelGGL(k_combine, dim3(cdiv((size_t)H / 4, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
+        TG_LAUNCH(k_combine, dim3(cdiv((size_t)H / 4, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
     else
-        hipLaunchKernelGGL(k_combine1, dim3(cdiv((size_t)H, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
+        TG_LAUNCH(k_combine1, dim3(cdiv((size_t)H, 256), T), dim3(256), 0, st, D, w, H, k, resid, out);
     return hipGetLastError();
 }
 

@@ -664,7 +664,7 @@ hipError_t launch_persist(const uint8_t *experts, const float *routers, const Sh
     // a block holds at most two gate/up units and one down unit
     if ((A.ug + G - 1) / G > 2 || A.ud > G) return hipErrorInvalidConfiguration;
     if (timeline && timeline_words >= (size_t)nl * G * PS_TL) A.tl = timeline;
-    hipLaunchKernelGGL(k_persist_reset, dim3(1), dim3(64), 0, st, sync);
+    TG_LAUNCH(k_persist_reset, dim3(1), dim3(64), 0, st, sync);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     void *args[] = {&A};
