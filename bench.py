@@ -22,6 +22,9 @@ Other workloads (--workload):
   legacy-moe   the reference's own legacy call, tg_moe_forward: 8 Q4_K experts
                of the 30B shape on caller-owned host buffers (operands copied
                in per call, as the reference's ABI hands them over).
+  legacy-layer the reference's tg_transformer_layer on the same buffers: f32
+               attention (32 heads / 4 kv heads of 128, 1024 cached positions)
+               and 8 Q4_K experts, one token.
 
 Prints one JSON line: tok/s (value), expert-weight HBM GB/s, the roofline
 of the dominant kernel (HIP events on its launch stream) and the CPU oracle
@@ -737,6 +740,97 @@ def run_legacy_moe(args, torch, call):
     }
 
 
+def run_legacy_layer(args, torch, call):
+    """The legacy entry point tg_transformer_layer (libtinygiant.c:662-702)
+    with host buffers, as the reference's engine calls it: a 30B-shaped layer
+    (embed 2048, 32 query heads and 4 kv heads of 128, f32 attention weights,
+    a cache of kv_max 2048 rows of which 1024 are filled) and 8 Q4_K experts.
+    Each call copies its operands (about 105 MB) to the device."""
+    from tinygiant_amd._lib import require_lib
+    lib = require_lib()
+    rng = np.random.default_rng(args.seed)
+    Hh, KV, hd, kv_max, kv_len = 32, 4, 128, 2048, 1024
+    qd, kvd = Hh * hd, KV * hd
+    w = [rng.normal(0, 0.02, n).astype(np.float32) for n in (qd * H, kvd * H, kvd * H, H * qd)]
+    an, fn_ = (rng.normal(1.0, 0.1, H).astype(np.float32) for _ in range(2))
+    qn, kn = (rng.normal(1.0, 0.1, hd).astype(np.float32) for _ in range(2))
+    ang = np.arange(kv_max)[:, None] * (10000.0 ** (-np.arange(hd // 2) / (hd // 2)))[None, :]
+    cos_t, sin_t = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kv_k = rng.normal(0, 1, (KV, kv_max, hd)).astype(np.float32)
+    kv_v = rng.normal(0, 1, (KV, kv_max, hd)).astype(np.float32)
+    gb = I * (H // 256) * 144
+    experts = [q4k_blocks(rng, (2 * gb + H * (I // 256) * 144) // 144) for _ in range(K_TOP)]
+    gp = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data for e in experts])
+    up = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data + gb for e in experts])
+    dp = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data + 2 * gb for e in experts])
+    dif = np.zeros(K_TOP, np.int32)
+    ew = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
+    x0 = rng.normal(0, 1, H).astype(np.float32)
+    x = x0.copy()
+    K, W = args.steps or 32, 2 if args.warmup is None else args.warmup
+
+    def step():
+        x[:] = x0
+        lib.tg_transformer_layer(*(a.ctypes.data for a in w), an.ctypes.data, qn.ctypes.data, kn.ctypes.data,
+                                 fn_.ctypes.data, kv_k.ctypes.data, kv_v.ctypes.data, kv_len, kv_max,
+                                 cos_t.ctypes.data, sin_t.ctypes.data, gp, up, dp, dif.ctypes.data, ew.ctypes.data,
+                                 K_TOP, x.ctypes.data, H, I, Hh, KV, hd, kv_len)
+
+    log(f"warmup {W} calls")
+    for _ in range(W):
+        step()
+    log(f"timing {K} calls")
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    wall = time.perf_counter() - t0
+    call("tg_prof_enable", 1)
+    for _ in range(4):
+        step()
+    call("tg_prof_enable", 0)
+    kern = kernel_times(call, ("lg_f32", "lg_rms", "lg_rope", "lg_kv", "lg_attn", "lg_add", "lg_quant", "lg_q4k",
+                               "lg_silu", "lg_q4k_down", "lg_acc"))
+    kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    n_a, ms_a = kern["lg_attn"]
+    attn_bytes = 2 * KV * (kv_len + 1) * hd * 4  # the cache rows each kv head's query heads read
+    achieved = attn_bytes / (ms_a / n_a * 1e-3)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        from oracle import oracle as O  # the checker, timed as the CPU baseline
+        rk, rv, rx = kv_k.copy(), kv_v.copy(), x0.copy()
+        O.transformer_layer(*w, an, qn, kn, fn_, rk, rv, kv_len, kv_max, cos_t, sin_t, [e for e in experts],
+                            [e[gb:] for e in experts], [e[2 * gb:] for e in experts], list(dif), ew, rx, H, I, Hh,
+                            KV, hd, kv_len)
+        step()
+        assert np.array_equal(rx.view(np.uint32), x.view(np.uint32)), "GPU legacy layer differs from the oracle"
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0):
+            O.transformer_layer(*w, an, qn, kn, fn_, kv_k.copy(), kv_v.copy(), kv_len, kv_max, cos_t, sin_t,
+                                [e for e in experts], [e[gb:] for e in experts], [e[2 * gb:] for e in experts],
+                                list(dif), ew, x0.copy(), H, I, Hh, KV, hd, kv_len)
+            n += 1
+        cpu_s = (time.perf_counter() - t1) / n
+        cpu = {"value": round(1.0 / cpu_s, 2), "unit": "layer/s", "cores": 1, "kind": "port",
+               "sample": f"{n} tg_transformer_layer calls through the C oracle, one thread; bit-identical to the "
+                         "GPU call"}
+
+    return {
+        "metric": "legacy tg_transformer_layer calls/s (30B-shaped layer, 1024 cached positions, host pointers)",
+        "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 attention, q4_k x q8 experts", "data": "synthetic",
+        "config": {"workload": "legacy-transformer-layer", "hidden": H, "heads": Hh, "kv_heads": KV, "head_dim": hd,
+                   "kv_len": kv_len, "experts": K_TOP, "moe_intermediate": I},
+        "kernel_avg_us": kern_us,
+        "roofline": {"bound": "hbm", "kernel": "k_attn_head", "bytes_per_launch": attn_bytes,
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_hbm_ceiling(args, torch, call):
     """What one launch can read from HBM: plain 128-bit loads over regions of
     the sizes the MoE kernels stream, rotating over a 16 GiB buffer so no
@@ -782,7 +876,7 @@ def run_hbm_ceiling(args, torch, call):
 WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill": run_prefill,
              "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
              "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
-             "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe}
+             "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe, "legacy-layer": run_legacy_layer}
 
 
 def main() -> int:

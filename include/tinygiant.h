@@ -8,13 +8,12 @@
  *     tinygiant/_lib.py:39-74), same names and C signatures, so that
  *     load_tinygiant_lib() binds this library unchanged.  Pointers are
  *     caller-owned host pointers and calls are synchronous, as in the
- *     reference.  The Q4_K / Q6_K / f16 / f32 products, the RMS norm, the
- *     expert forward and tg_moe_forward run on the GPU (operands copied in
- *     per call) with the reference's arithmetic order, bit-identical to its
- *     scalar definition with contraction off.  The attention entry points
- *     and tg_transformer_layer are not on the GPU in this build.  A failing
- *     call (these signatures return nothing) sets tg_last_error(), prints
- *     one line on stderr per symbol and writes NaN to every output element.
+ *     reference.  Every one of them runs on the GPU (operands copied in per
+ *     call, the new KV-cache rows copied back) with the reference's
+ *     arithmetic order, bit-identical to its scalar definition with
+ *     contraction off.  A failing call (these signatures return nothing)
+ *     sets tg_last_error(), prints one line on stderr per symbol and writes
+ *     NaN to every output element.
  *
  *  2. New entry points for the Q4_0/Q8_0 path: an all-experts-resident HBM
  *     arena (the reference's SSD/page-cache/mlock tiers collapsed into

@@ -89,6 +89,13 @@ def lib():
             "tgo_matmul_q4k_scalar": (None, [_P, _P, _P, _I, _I]),
             "tgo_dequant_q4k_block": (None, [_P, _P]),
             "tgo_dequant_q6k_block": (None, [_P, _P]),
+            "tgo_rope": (None, [_P, _I, _I, _P, _P, _I]),
+            "tgo_attention_decode": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P,
+                                             _I, _I, _I, _I, _I]),
+            "tgo_attention_decode_q4": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P,
+                                                _I, _I, _I, _I, _I]),
+            "tgo_transformer_layer": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _P,
+                                              _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I]),
             "tgo_set_threads": (_I, [_I]),
             "tgo_max_threads": (_I, []),
         }
@@ -413,3 +420,37 @@ def cpu_count() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, cos_t: np.ndarray, sin_t: np.ndarray, pos: int) -> np.ndarray:
+    """apply_rope_inplace on a copy of x (n_heads * head_dim floats)."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    lib().tgo_rope(_p(y), n_heads, head_dim, _p(np.ascontiguousarray(cos_t, dtype=np.float32)),
+                   _p(np.ascontiguousarray(sin_t, dtype=np.float32)), pos)
+    return y
+
+
+def attention_decode(q4, wq, wk, wv, wo, q_norm_w, k_norm_w, kv_k, kv_v, kv_len, kv_max, cos_t, sin_t, x, embed,
+                     n_heads, n_kv_heads, head_dim, pos):
+    """tg_attention_decode (q4 False: f32 weights) or tg_attention_decode_q4;
+    kv_k / kv_v (float32 [n_kv_heads, kv_max, head_dim]) are updated in place.
+    Returns the output (embed floats)."""
+    out = np.empty(embed, np.float32)
+    fn = lib().tgo_attention_decode_q4 if q4 else lib().tgo_attention_decode
+    fn(_p(wq), _p(wk), _p(wv), _p(wo), _p(q_norm_w), _p(k_norm_w), _p(kv_k), _p(kv_v), kv_len, kv_max, _p(cos_t),
+       _p(sin_t), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(out), embed, n_heads, n_kv_heads, head_dim, pos)
+    return out
+
+
+def transformer_layer(wq, wk, wv, wo, attn_norm_w, q_norm_w, k_norm_w, ffn_norm_w, kv_k, kv_v, kv_len, kv_max,
+                      cos_t, sin_t, gates, ups, downs, down_is_f16, expert_w, x, embed, inter, n_heads, n_kv_heads,
+                      head_dim, pos):
+    """tg_transformer_layer; x (float32, embed) and the caches are updated in place."""
+    n = len(gates)
+    arr = lambda lst: ctypes.cast((ctypes.c_void_p * n)(*[a.ctypes.data for a in lst]), ctypes.c_void_p)
+    dif = np.ascontiguousarray(down_is_f16, dtype=np.int32)
+    lib().tgo_transformer_layer(_p(wq), _p(wk), _p(wv), _p(wo), _p(attn_norm_w), _p(q_norm_w), _p(k_norm_w),
+                                _p(ffn_norm_w), _p(kv_k), _p(kv_v), kv_len, kv_max, _p(cos_t), _p(sin_t), arr(gates),
+                                arr(ups), arr(downs), _p(dif), _p(np.ascontiguousarray(expert_w, dtype=np.float32)),
+                                n, _p(x), embed, inter, n_heads, n_kv_heads, head_dim, pos)
+    return x

@@ -909,6 +909,145 @@ void tgo_dequant_q6k_block(const uint8_t *block, float *out) {
         }
 }
 
+/* apply_rope_inplace, libtinygiant.c:344-361: per head, pairs (i, i + half)
+ * rotated by the table row of `pos`: x1' = x1 c - x2 s (vmlsq_f32: product,
+ * product, difference, each rounded) and x2' = fma(x1, s, x2 c) (vfmaq_f32 on
+ * the rounded x2 c).  half is a multiple of 4 (the reference steps by 4). */
+void tgo_rope(float *x, int n_heads, int head_dim, const float *cos_t, const float *sin_t, int pos) {
+    int half = head_dim / 2;
+    const float *c = cos_t + (size_t)pos * half, *sn = sin_t + (size_t)pos * half;
+    for (int h = 0; h < n_heads; h++) {
+        float *xh = x + (size_t)h * head_dim;
+        for (int i = 0; i < half; i++) {
+            float x1 = xh[i], x2 = xh[half + i];
+            float a = x1 * c[i], b = x2 * sn[i];
+            xh[i] = a - b;
+            xh[half + i] = fmaf(x1, sn[i], x2 * c[i]);
+        }
+    }
+}
+
+/* One head's scores, softmax and weighted values (libtinygiant.c:405-446):
+ * dot = four fma lanes over steps of 4, (l0 + l1) + (l2 + l3) (vaddvq_f32),
+ * the tail one product and add at a time; score = dot * inv_sqrt; e =
+ * exp(score - max) added in order; out[d] = fma chain over t of
+ * (e_t * inv_sum) v_t[d] (vfmaq_f32; the tail d unfused). */
+static void attn_head(const float *q, const float *kc, const float *vc, int seq, int hd, float inv_sqrt,
+                      float *out, float *scores) {
+    float mx = -1e30f;
+    for (int t = 0; t < seq; t++) {
+        const float *kt = kc + (size_t)t * hd;
+        float acc[4] = {0, 0, 0, 0};
+        int d = 0;
+        for (; d + 3 < hd; d += 4)
+            for (int l = 0; l < 4; l++) acc[l] = fmaf(q[d + l], kt[d + l], acc[l]);
+        float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (; d < hd; d++) dot = dot + q[d] * kt[d];
+        scores[t] = dot * inv_sqrt;
+        if (scores[t] > mx) mx = scores[t];
+    }
+    float sum = 0.0f;
+    for (int t = 0; t < seq; t++) {
+        scores[t] = tgo_expf(scores[t] - mx);
+        sum = sum + scores[t];
+    }
+    float inv_sum = 1.0f / sum;
+    for (int d = 0; d < hd; d++) out[d] = 0.0f;
+    int hd4 = hd & ~3;
+    for (int t = 0; t < seq; t++) {
+        float w = scores[t] * inv_sum;
+        const float *vt = vc + (size_t)t * hd;
+        for (int d = 0; d < hd4; d++) out[d] = fmaf(w, vt[d], out[d]);
+        for (int d = hd4; d < hd; d++) out[d] = out[d] + w * vt[d];
+    }
+}
+
+/* tg_attention_decode (f32 weights, libtinygiant.c:365-457) and
+ * tg_attention_decode_q4 (Q4_K q / k / o, f16 v, :460-551): projections,
+ * per-head RMS norms of q and k (eps 1e-6), RoPE, the new k (after RoPE) and
+ * v appended to the caches [n_kv_heads][kv_max][head_dim] at kv_len, GQA
+ * attention over kv_len + 1 positions, output projection. */
+static void attn_decode(int q4, const void *wq, const void *wk, const void *wv, const void *wo,
+                        const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v, int kv_len,
+                        int kv_max, const float *rope_cos, const float *rope_sin, const float *input,
+                        float *output, int embed, int n_heads, int n_kv_heads, int hd, int pos) {
+    int q_dim = n_heads * hd, kv_dim = n_kv_heads * hd, ratio = n_heads / n_kv_heads;
+    float *q = (float *)malloc(sizeof(float) * (size_t)q_dim), *k = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *v = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *qn = (float *)malloc(sizeof(float) * (size_t)q_dim), *kn = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *ao = (float *)malloc(sizeof(float) * (size_t)q_dim);
+    float *sc = (float *)malloc(sizeof(float) * (size_t)(kv_len + 1));
+    if (q4) {
+        tgo_matmul_q4k((const uint8_t *)wq, input, q, q_dim, embed);
+        tgo_matmul_q4k((const uint8_t *)wk, input, k, kv_dim, embed);
+        tgo_matvec_f16((const uint16_t *)wv, input, v, kv_dim, embed);
+    } else {
+        tgo_matvec_f32((const float *)wq, input, q, q_dim, embed);
+        tgo_matvec_f32((const float *)wk, input, k, kv_dim, embed);
+        tgo_matvec_f32((const float *)wv, input, v, kv_dim, embed);
+    }
+    for (int h = 0; h < n_heads; h++) tgo_rms_norm(q + (size_t)h * hd, q_norm_w, qn + (size_t)h * hd, hd, 1e-6f);
+    for (int h = 0; h < n_kv_heads; h++) tgo_rms_norm(k + (size_t)h * hd, k_norm_w, kn + (size_t)h * hd, hd, 1e-6f);
+    tgo_rope(qn, n_heads, hd, rope_cos, rope_sin, pos);
+    tgo_rope(kn, n_kv_heads, hd, rope_cos, rope_sin, pos);
+    for (int h = 0; h < n_kv_heads; h++) {
+        memcpy(kv_k + ((size_t)h * kv_max + kv_len) * hd, kn + (size_t)h * hd, sizeof(float) * (size_t)hd);
+        memcpy(kv_v + ((size_t)h * kv_max + kv_len) * hd, v + (size_t)h * hd, sizeof(float) * (size_t)hd);
+    }
+    float inv_sqrt = 1.0f / sqrtf((float)hd);
+    for (int h = 0; h < n_heads; h++) {
+        int kh = h / ratio;
+        attn_head(qn + (size_t)h * hd, kv_k + (size_t)kh * kv_max * hd, kv_v + (size_t)kh * kv_max * hd, kv_len + 1,
+                  hd, inv_sqrt, ao + (size_t)h * hd, sc);
+    }
+    if (q4)
+        tgo_matmul_q4k((const uint8_t *)wo, ao, output, embed, q_dim);
+    else
+        tgo_matvec_f32((const float *)wo, ao, output, embed, q_dim);
+    free(q); free(k); free(v); free(qn); free(kn); free(ao); free(sc);
+}
+
+void tgo_attention_decode(const float *wq, const float *wk, const float *wv, const float *wo,
+                          const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v, int kv_len,
+                          int kv_max, const float *rope_cos, const float *rope_sin, const float *input,
+                          float *output, int embed, int n_heads, int n_kv_heads, int head_dim, int pos) {
+    attn_decode(0, wq, wk, wv, wo, q_norm_w, k_norm_w, kv_k, kv_v, kv_len, kv_max, rope_cos, rope_sin, input, output,
+                embed, n_heads, n_kv_heads, head_dim, pos);
+}
+
+void tgo_attention_decode_q4(const uint8_t *wq, const uint8_t *wk, const uint16_t *wv, const uint8_t *wo,
+                             const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v, int kv_len,
+                             int kv_max, const float *rope_cos, const float *rope_sin, const float *input,
+                             float *output, int embed, int n_heads, int n_kv_heads, int head_dim, int pos) {
+    attn_decode(1, wq, wk, wv, wo, q_norm_w, k_norm_w, kv_k, kv_v, kv_len, kv_max, rope_cos, rope_sin, input, output,
+                embed, n_heads, n_kv_heads, head_dim, pos);
+}
+
+/* tg_transformer_layer, libtinygiant.c:662-702: RMS norm (attn_norm_w),
+ * f32 attention, x += attn; RMS norm (ffn_norm_w), the experts' forward
+ * (down_is_f16[e] as the down format) accumulated from zero, x += moe. */
+void tgo_transformer_layer(const float *wq, const float *wk, const float *wv, const float *wo,
+                           const float *attn_norm_w, const float *q_norm_w, const float *k_norm_w,
+                           const float *ffn_norm_w, float *kv_k, float *kv_v, int kv_len, int kv_max,
+                           const float *rope_cos, const float *rope_sin, const uint8_t *const *gate_ptrs,
+                           const uint8_t *const *up_ptrs, const void *const *down_ptrs, const int *down_is_f16,
+                           const float *expert_weights, int n_active, float *x, int embed, int inter, int n_heads,
+                           int n_kv_heads, int head_dim, int pos) {
+    float *nrm = (float *)malloc(sizeof(float) * (size_t)embed), *ao = (float *)malloc(sizeof(float) * (size_t)embed);
+    float *mo = (float *)malloc(sizeof(float) * (size_t)embed);
+    tgo_rms_norm(x, attn_norm_w, nrm, embed, 1e-6f);
+    tgo_attention_decode(wq, wk, wv, wo, q_norm_w, k_norm_w, kv_k, kv_v, kv_len, kv_max, rope_cos, rope_sin, nrm, ao,
+                         embed, n_heads, n_kv_heads, head_dim, pos);
+    for (int i = 0; i < embed; i++) x[i] = x[i] + ao[i];
+    tgo_rms_norm(x, ffn_norm_w, nrm, embed, 1e-6f);
+    for (int i = 0; i < embed; i++) mo[i] = 0.0f;
+    for (int e = 0; e < n_active; e++)
+        tgo_expert_forward_mixed(gate_ptrs[e], up_ptrs[e], down_ptrs[e], down_is_f16[e], nrm, mo, expert_weights[e],
+                                 embed, inter);
+    for (int i = 0; i < embed; i++) x[i] = x[i] + mo[i];
+    free(nrm); free(ao); free(mo);
+}
+
 int tgo_set_threads(int n) {
 #ifdef _OPENMP
     if (n > 0) omp_set_num_threads(n);

@@ -117,6 +117,28 @@ void  tgo_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y,
 void  tgo_dequant_q4k_block(const uint8_t *block, float *out);
 void  tgo_dequant_q6k_block(const uint8_t *block, float *out);
 
+void  tgo_rope(float *x, int n_heads, int head_dim, const float *cos_t, const float *sin_t, int pos);
+void  tgo_attention_decode(const float *wq, const float *wk, const float *wv, const float *wo,
+                           const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v,
+                           int kv_len, int kv_max, const float *rope_cos, const float *rope_sin,
+                           const float *input, float *output, int embed, int n_heads,
+                           int n_kv_heads, int head_dim, int pos);
+void  tgo_attention_decode_q4(const uint8_t *wq, const uint8_t *wk, const uint16_t *wv,
+                              const uint8_t *wo, const float *q_norm_w, const float *k_norm_w,
+                              float *kv_k, float *kv_v, int kv_len, int kv_max,
+                              const float *rope_cos, const float *rope_sin, const float *input,
+                              float *output, int embed, int n_heads, int n_kv_heads,
+                              int head_dim, int pos);
+void  tgo_transformer_layer(const float *wq, const float *wk, const float *wv, const float *wo,
+                            const float *attn_norm_w, const float *q_norm_w,
+                            const float *k_norm_w, const float *ffn_norm_w, float *kv_k,
+                            float *kv_v, int kv_len, int kv_max, const float *rope_cos,
+                            const float *rope_sin, const uint8_t *const *gate_ptrs,
+                            const uint8_t *const *up_ptrs, const void *const *down_ptrs,
+                            const int *down_is_f16, const float *expert_weights, int n_active,
+                            float *x, int embed, int inter, int n_heads, int n_kv_heads,
+                            int head_dim, int pos);
+
 /* ---- threading for the CPU baseline (no effect on results) ---- */
 int   tgo_set_threads(int n);
 int   tgo_max_threads(void);

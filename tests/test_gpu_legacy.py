@@ -194,3 +194,78 @@ def test_moe_forward(O, L):
     L.tg_moe_forward(ptrs, ptr(w), n, ptr(x), ptr(out), embed, inter)
     ref = O.moe_forward_q4k(experts, w, x, embed, inter)
     assert_exact(out, ref, "moe_forward")
+
+
+# ---------------------------------------------------------------- attention
+
+def attn_case(rng, q4, embed, n_heads, n_kv, hd, kv_max):
+    from tests.test_oracle_attention import rope_tables
+    q_dim, kv_dim = n_heads * hd, n_kv * hd
+    if q4:
+        wq = q4k_matrix(rng, q_dim, embed // 256)
+        wk = q4k_matrix(rng, kv_dim, embed // 256)
+        wv = f16_matrix(rng, kv_dim, embed)
+        wo = q4k_matrix(rng, embed, q_dim // 256)
+    else:
+        wq = rng.normal(0, 0.03, q_dim * embed).astype(np.float32)
+        wk = rng.normal(0, 0.03, kv_dim * embed).astype(np.float32)
+        wv = rng.normal(0, 0.03, kv_dim * embed).astype(np.float32)
+        wo = rng.normal(0, 0.03, embed * q_dim).astype(np.float32)
+    qn = rng.normal(1.0, 0.1, hd).astype(np.float32)
+    kn = rng.normal(1.0, 0.1, hd).astype(np.float32)
+    c, s = rope_tables(kv_max, hd // 2)
+    kv_k = rng.normal(0, 1, (n_kv, kv_max, hd)).astype(np.float32)
+    kv_v = rng.normal(0, 1, (n_kv, kv_max, hd)).astype(np.float32)
+    x = rng.normal(0, 1, embed).astype(np.float32)
+    return wq, wk, wv, wo, qn, kn, c, s, kv_k, kv_v, x
+
+
+@pytest.mark.parametrize("q4", [False, True])
+@pytest.mark.parametrize("embed,n_heads,n_kv,hd,kv_max,kv_len",
+                         [(512, 4, 2, 64, 16, 0), (512, 4, 2, 64, 16, 9), (2048, 32, 4, 128, 300, 257),
+                          (256, 2, 1, 130, 8, 7)])
+def test_attention_decode(O, L, q4, embed, n_heads, n_kv, hd, kv_max, kv_len):
+    if q4 and (n_heads * hd) % 256:
+        pytest.skip("Q4_K output projection needs q_dim % 256 == 0")
+    gpu_note(f"tg_attention_decode{'_q4' if q4 else ''} E={embed} H={n_heads}/{n_kv} hd={hd} kv_len={kv_len}")
+    rng = np.random.default_rng(embed + 7 * kv_len + q4)
+    wq, wk, wv, wo, qn, kn, c, s, kv_k, kv_v, x = attn_case(rng, q4, embed, n_heads, n_kv, hd, kv_max)
+    gk, gv = kv_k.copy(), kv_v.copy()
+    out = np.zeros(embed, np.float32)
+    fn = L.tg_attention_decode_q4 if q4 else L.tg_attention_decode
+    fn(ptr(wq), ptr(wk), ptr(wv), ptr(wo), ptr(qn), ptr(kn), ptr(gk), ptr(gv), kv_len, kv_max, ptr(c), ptr(s),
+       ptr(x), ptr(out), embed, n_heads, n_kv, hd, kv_len)
+    rk, rv = kv_k.copy(), kv_v.copy()
+    ref = O.attention_decode(q4, wq, wk, wv, wo, qn, kn, rk, rv, kv_len, kv_max, c, s, x, embed, n_heads, n_kv, hd,
+                             kv_len)
+    assert_exact(out, ref, "attention output")
+    assert np.array_equal(gk.view(np.uint32), rk.view(np.uint32)), "key cache"
+    assert np.array_equal(gv.view(np.uint32), rv.view(np.uint32)), "value cache"
+
+
+def test_transformer_layer(O, L):
+    """tg_transformer_layer: attention + experts (Q4_K and f16 down) on one
+    token, x and the caches updated in place, against the oracle."""
+    gpu_note("tg_transformer_layer E=2048 H=32/4 hd=128 kv_len=40, 4 experts")
+    rng = np.random.default_rng(123)
+    embed, n_heads, n_kv, hd, kv_max, kv_len, inter = 2048, 32, 4, 128, 64, 40, 768
+    wq, wk, wv, wo, qn, kn, c, s, kv_k, kv_v, x = attn_case(rng, False, embed, n_heads, n_kv, hd, kv_max)
+    an = rng.normal(1.0, 0.1, embed).astype(np.float32)
+    fn_ = rng.normal(1.0, 0.1, embed).astype(np.float32)
+    fmts = [0, 1, 0, 1]
+    ex = [expert_operands(rng, embed, inter, f) for f in fmts]
+    ew = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    gx, gk, gv = x.copy(), kv_k.copy(), kv_v.copy()
+    n = len(ex)
+    arr = lambda lst: (ctypes.c_void_p * n)(*[a.ctypes.data for a in lst])
+    dif = np.array(fmts, np.int32)
+    L.tg_transformer_layer(ptr(wq), ptr(wk), ptr(wv), ptr(wo), ptr(an), ptr(qn), ptr(kn), ptr(fn_), ptr(gk), ptr(gv),
+                           kv_len, kv_max, ptr(c), ptr(s), arr([e[0] for e in ex]), arr([e[1] for e in ex]),
+                           arr([e[2] for e in ex]), ptr(dif), ptr(ew), n, ptr(gx), embed, inter, n_heads, n_kv, hd,
+                           kv_len)
+    rx, rk, rv = x.copy(), kv_k.copy(), kv_v.copy()
+    O.transformer_layer(wq, wk, wv, wo, an, qn, kn, fn_, rk, rv, kv_len, kv_max, c, s, [e[0] for e in ex],
+                        [e[1] for e in ex], [e[2] for e in ex], fmts, ew, rx, embed, inter, n_heads, n_kv, hd, kv_len)
+    assert_exact(gx, rx, "transformer layer x")
+    assert np.array_equal(gk.view(np.uint32), rk.view(np.uint32)), "key cache"
+    assert np.array_equal(gv.view(np.uint32), rv.view(np.uint32)), "value cache"

@@ -944,20 +944,15 @@ extern "C" int tg_mlock(const void *addr, size_t len) {
 // ================================================================ legacy ABI
 // The reference's legacy entry points keep its conventions: synchronous
 // calls on caller-owned host pointers, no error returns.  Q4_K / Q6_K / f16
-// / f32 products, the RMS norm and the expert forward run on the GPU
-// (tg_legacy.hip): each call copies its operands into one device scratch
-// buffer (grown as needed, kept for the process), runs the kernels on one
-// stream and copies the result back.  A failure (no device, out of memory)
-// is reported loudly: tg_last_error(), one line on stderr per symbol, and
-// NaN in every output element.  Attention and the transformer layer are not
-// on the GPU in this build and fail the same way.
+// / f32 products, the RMS norm, the expert forward, attention decode and the
+// transformer layer run on the GPU (tg_legacy.hip): each call copies its
+// operands into one device scratch buffer (grown as needed, kept for the
+// process), runs the kernels on one stream and copies the result back (and
+// the new KV cache rows into the caller's caches).  A failure (no device,
+// out of memory, an invalid geometry) is reported loudly: tg_last_error(),
+// one line on stderr per symbol, and NaN in every output element.
 static void legacy_fail(const char *name, std::atomic<bool> &warned) {
     if (!warned.exchange(true)) fprintf(stderr, "libtinygiant (gfx950): %s: %s\n", name, g_err.c_str());
-}
-
-static void legacy_unavailable(const char *name, std::atomic<bool> &warned) {
-    set_err(TG_E_UNSUPPORTED, "%s: not available on the GPU in this build", name);
-    legacy_fail(name, warned);
 }
 
 static void fill_nan(float *p, long n) {
@@ -1299,27 +1294,259 @@ extern "C" void tg_rms_norm(const float *x, const float *weight, float *out, int
     }
 }
 
-extern "C" void tg_attention_decode(const float *, const float *, const float *, const float *, const float *,
-                                    const float *, float *, float *, int, int, const float *, const float *,
-                                    const float *, float *output, int embed_dim, int, int, int, int) {
-    legacy_unavailable("tg_attention_decode", warned_attention_decode);
-    fill_nan(output, embed_dim);
+// ---------------------------------------------------------------- attention
+// Geometry of one attention decode step (libtinygiant.c:365-551).
+struct LgAttn {
+    int embed, n_heads, n_kv, hd, kv_len, kv_max, pos;
+    int q_dim() const { return n_heads * hd; }
+    int kv_dim() const { return n_kv * hd; }
+    int seq() const { return kv_len + 1; }
+    bool ok() const {
+        return embed > 0 && n_heads > 0 && n_kv > 0 && n_heads % n_kv == 0 && hd > 0 && hd % 2 == 0 && hd <= 512 &&
+               kv_len >= 0 && kv_len < kv_max && pos >= 0;
+    }
+};
+
+// Device buffers of one attention step (weights excluded).
+struct LgAttnBufs {
+    float *x, *q, *k, *v, *qn, *kn, *ao, *out, *kc, *vc, *scr, *cs, *sn;
+    void *xq, *aq;
+};
+
+static LgAttnBufs lg_attn_bufs(LgCarve &c, const LgAttn &g) {
+    LgAttnBufs b;
+    const size_t cache = 4 * (size_t)g.n_kv * g.seq() * g.hd;
+    b.x = c.take<float>(4 * (size_t)g.embed);
+    b.q = c.take<float>(4 * (size_t)g.q_dim());
+    b.k = c.take<float>(4 * (size_t)g.kv_dim());
+    b.v = c.take<float>(4 * (size_t)g.kv_dim());
+    b.qn = c.take<float>(4 * (size_t)g.q_dim());
+    b.kn = c.take<float>(4 * (size_t)g.kv_dim());
+    b.ao = c.take<float>(4 * (size_t)g.q_dim());
+    b.out = c.take<float>(4 * (size_t)g.embed);
+    b.kc = c.take<float>(cache);
+    b.vc = c.take<float>(cache);
+    b.scr = c.take<float>(4 * (size_t)g.n_heads * g.seq());
+    b.cs = c.take<float>(4 * (size_t)(g.hd / 2));
+    b.sn = c.take<float>(4 * (size_t)(g.hd / 2));
+    b.xq = c.take<uint8_t>((size_t)(g.embed / tg::LG_QK) * tg::LG_Q8K_BYTES);
+    b.aq = c.take<uint8_t>((size_t)(g.q_dim() / tg::LG_QK) * tg::LG_Q8K_BYTES);
+    return b;
 }
 
-extern "C" void tg_attention_decode_q4(const uint8_t *, const uint8_t *, const uint16_t *, const uint8_t *,
-                                       const float *, const float *, float *, float *, int, int, const float *,
-                                       const float *, const float *, float *output, int embed_dim, int, int, int,
-                                       int) {
-    legacy_unavailable("tg_attention_decode_q4", warned_attention_decode_q4);
-    fill_nan(output, embed_dim);
+// Host cache rows 0 .. kv_len-1 of every kv head into the device caches
+// [n_kv][seq][hd], and this position's RoPE table rows.
+static int lg_attn_in(const LgAttn &g, const LgAttnBufs &b, const float *kv_k, const float *kv_v,
+                      const float *rope_cos, const float *rope_sin) {
+    const size_t row = 4 * (size_t)g.hd, half = 4 * (size_t)(g.hd / 2);
+    if (g.kv_len > 0) {
+        HIP_TRY(hipMemcpy2DAsync(b.kc, row * g.seq(), kv_k, row * g.kv_max, row * g.kv_len, g.n_kv,
+                                 hipMemcpyHostToDevice, g_lg_st));
+        HIP_TRY(hipMemcpy2DAsync(b.vc, row * g.seq(), kv_v, row * g.kv_max, row * g.kv_len, g.n_kv,
+                                 hipMemcpyHostToDevice, g_lg_st));
+    }
+    int rc;
+    if ((rc = lg_h2d(b.cs, rope_cos + (size_t)g.pos * (g.hd / 2), half)) ||
+        (rc = lg_h2d(b.sn, rope_sin + (size_t)g.pos * (g.hd / 2), half)))
+        return rc;
+    return TG_OK;
 }
 
-extern "C" void tg_transformer_layer(const float *, const float *, const float *, const float *, const float *,
-                                     const float *, const float *, const float *, float *, float *, int, int,
-                                     const float *, const float *, const uint8_t **, const uint8_t **,
-                                     const void **, const int *, const float *, int, float *x, int embed_dim, int,
-                                     int, int, int, int) {
-    legacy_unavailable("tg_transformer_layer", warned_transformer_layer);
-    fill_nan(x, embed_dim);
+// The new cache rows (row kv_len of every kv head) back to the host caches.
+static int lg_attn_out(const LgAttn &g, const LgAttnBufs &b, float *kv_k, float *kv_v) {
+    const size_t row = 4 * (size_t)g.hd;
+    HIP_TRY(hipMemcpy2DAsync(kv_k + (size_t)g.kv_len * g.hd, row * g.kv_max, b.kc + (size_t)g.kv_len * g.hd,
+                             row * g.seq(), row, g.n_kv, hipMemcpyDeviceToHost, g_lg_st));
+    HIP_TRY(hipMemcpy2DAsync(kv_v + (size_t)g.kv_len * g.hd, row * g.kv_max, b.vc + (size_t)g.kv_len * g.hd,
+                             row * g.seq(), row, g.n_kv, hipMemcpyDeviceToHost, g_lg_st));
+    return TG_OK;
+}
+
+// The attention step on device operands (input b.x, output b.out): q/k/v
+// projections (q4: Q4_K q, k, o and f16 v; else f32), per-head RMS norms of
+// q and k (eps 1e-6), RoPE, the new rows into the caches, GQA attention,
+// output projection.
+static int lg_attn_core(bool q4, const void *wq, const void *wk, const void *wv, const void *wo, const float *qnw,
+                        const float *knw, const LgAttn &g, const LgAttnBufs &b) {
+    hipStream_t st = g_lg_st;
+    const int ebpr = g.embed / tg::LG_QK;
+    if (q4) {
+        PROFILED("lg_quant", st, tg::launch_quantize_q8k(b.x, b.xq, ebpr, st));
+        PROFILED("lg_q4k_attn", st,
+                 tg::launch_matmul_q4k(static_cast<const uint8_t *>(wq), b.xq, b.q, g.q_dim(), ebpr, st));
+        PROFILED("lg_q4k_attn", st,
+                 tg::launch_matmul_q4k(static_cast<const uint8_t *>(wk), b.xq, b.k, g.kv_dim(), ebpr, st));
+        PROFILED("lg_f16", st, tg::launch_matvec_two_acc(wv, true, b.x, b.v, g.kv_dim(), g.embed, st));
+    } else {
+        PROFILED("lg_f32", st, tg::launch_matvec_two_acc(wq, false, b.x, b.q, g.q_dim(), g.embed, st));
+        PROFILED("lg_f32", st, tg::launch_matvec_two_acc(wk, false, b.x, b.k, g.kv_dim(), g.embed, st));
+        PROFILED("lg_f32", st, tg::launch_matvec_two_acc(wv, false, b.x, b.v, g.kv_dim(), g.embed, st));
+    }
+    PROFILED("lg_rms", st, tg::launch_rms_norm_rows(b.q, qnw, b.qn, g.hd, g.n_heads, 1e-6f, st));
+    PROFILED("lg_rms", st, tg::launch_rms_norm_rows(b.k, knw, b.kn, g.hd, g.n_kv, 1e-6f, st));
+    PROFILED("lg_rope", st, tg::launch_rope(b.qn, g.n_heads, g.hd, b.cs, b.sn, st));
+    PROFILED("lg_rope", st, tg::launch_rope(b.kn, g.n_kv, g.hd, b.cs, b.sn, st));
+    PROFILED("lg_kv", st, tg::launch_kv_append(b.kn, b.v, b.kc, b.vc, g.n_kv, g.seq(), g.hd, g.kv_len, st));
+    const float inv_sqrt = 1.0f / sqrtf((float)g.hd);
+    PROFILED("lg_attn", st,
+             tg::launch_attn_heads(b.qn, b.kc, b.vc, b.scr, b.ao, g.n_heads, g.seq(), g.hd, g.n_heads / g.n_kv,
+                                   inv_sqrt, st));
+    if (q4) {
+        const int abpr = g.q_dim() / tg::LG_QK;
+        PROFILED("lg_quant", st, tg::launch_quantize_q8k(b.ao, b.aq, abpr, st));
+        PROFILED("lg_q4k_attn", st,
+                 tg::launch_matmul_q4k(static_cast<const uint8_t *>(wo), b.aq, b.out, g.embed, abpr, st));
+    } else {
+        PROFILED("lg_f32", st, tg::launch_matvec_two_acc(wo, false, b.ao, b.out, g.embed, g.q_dim(), st));
+    }
+    return TG_OK;
+}
+
+// Bytes of the four projection weights.
+static void lg_attn_wbytes(bool q4, const LgAttn &g, size_t &bq, size_t &bk, size_t &bv, size_t &bo) {
+    if (q4) {
+        bq = (size_t)g.q_dim() * (g.embed / tg::LG_QK) * tg::LG_Q4K_BYTES;
+        bk = (size_t)g.kv_dim() * (g.embed / tg::LG_QK) * tg::LG_Q4K_BYTES;
+        bv = (size_t)g.kv_dim() * g.embed * 2;
+        bo = (size_t)g.embed * (g.q_dim() / tg::LG_QK) * tg::LG_Q4K_BYTES;
+    } else {
+        bq = 4 * (size_t)g.q_dim() * g.embed;
+        bk = bv = 4 * (size_t)g.kv_dim() * g.embed;
+        bo = 4 * (size_t)g.embed * g.q_dim();
+    }
+}
+
+static int lg_attention(bool q4, const void *wq, const void *wk, const void *wv, const void *wo, const float *qnw,
+                        const float *knw, float *kv_k, float *kv_v, const float *rope_cos, const float *rope_sin,
+                        const float *input, float *output, const LgAttn &g) {
+    if (!g.ok()) return set_err(TG_E_INVALID, "attention geometry");
+    size_t bq, bk, bv, bo;
+    lg_attn_wbytes(q4, g, bq, bk, bv, bo);
+    const size_t nb = 4 * (size_t)g.hd;
+    for (int pass = 0; pass < 2; pass++) {
+        LgCarve c{pass ? g_lg_buf : nullptr};
+        uint8_t *dq = c.take<uint8_t>(bq), *dk = c.take<uint8_t>(bk), *dv = c.take<uint8_t>(bv);
+        uint8_t *dwo = c.take<uint8_t>(bo);
+        float *dqn = c.take<float>(nb), *dkn = c.take<float>(nb);
+        const LgAttnBufs b = lg_attn_bufs(c, g);
+        if (!pass) {
+            int rc = lg_reserve(c.off);
+            if (rc) return rc;
+            continue;
+        }
+        int rc;
+        if ((rc = lg_h2d(dq, wq, bq)) || (rc = lg_h2d(dk, wk, bk)) || (rc = lg_h2d(dv, wv, bv)) ||
+            (rc = lg_h2d(dwo, wo, bo)) || (rc = lg_h2d(dqn, qnw, nb)) || (rc = lg_h2d(dkn, knw, nb)) ||
+            (rc = lg_h2d(b.x, input, 4 * (size_t)g.embed)) || (rc = lg_attn_in(g, b, kv_k, kv_v, rope_cos, rope_sin)) ||
+            (rc = lg_attn_core(q4, dq, dk, dv, dwo, dqn, dkn, g, b)) || (rc = lg_attn_out(g, b, kv_k, kv_v)))
+            return rc;
+        return lg_finish(output, b.out, 4 * (size_t)g.embed);
+    }
+    return TG_OK;
+}
+
+extern "C" void tg_attention_decode(const float *wq, const float *wk, const float *wv, const float *wo,
+                                    const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v,
+                                    int kv_len, int kv_max, const float *rope_cos, const float *rope_sin,
+                                    const float *input, float *output, int embed_dim, int n_heads, int n_kv_heads,
+                                    int head_dim, int pos) {
+    if (embed_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const LgAttn g{embed_dim, n_heads, n_kv_heads, head_dim, kv_len, kv_max, pos};
+    if (lg_attention(false, wq, wk, wv, wo, q_norm_w, k_norm_w, kv_k, kv_v, rope_cos, rope_sin, input, output, g)) {
+        legacy_fail("tg_attention_decode", warned_attention_decode);
+        fill_nan(output, embed_dim);
+    }
+}
+
+extern "C" void tg_attention_decode_q4(const uint8_t *wq_q4, const uint8_t *wk_q4, const uint16_t *wv_f16,
+                                       const uint8_t *wo_q4, const float *q_norm_w, const float *k_norm_w,
+                                       float *kv_k, float *kv_v, int kv_len, int kv_max, const float *rope_cos,
+                                       const float *rope_sin, const float *input, float *output, int embed_dim,
+                                       int n_heads, int n_kv_heads, int head_dim, int pos) {
+    if (embed_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const LgAttn g{embed_dim, n_heads, n_kv_heads, head_dim, kv_len, kv_max, pos};
+    if (lg_attention(true, wq_q4, wk_q4, wv_f16, wo_q4, q_norm_w, k_norm_w, kv_k, kv_v, rope_cos, rope_sin, input,
+                     output, g)) {
+        legacy_fail("tg_attention_decode_q4", warned_attention_decode_q4);
+        fill_nan(output, embed_dim);
+    }
+}
+
+// tg_transformer_layer (libtinygiant.c:662-702): RMS norm, f32 attention,
+// x += attn; RMS norm, the experts' forward (down_is_f16[e] as the down
+// format) accumulated from zero, x += moe.
+static int lg_transformer_layer(const float *wq, const float *wk, const float *wv, const float *wo,
+                                const float *attn_norm_w, const float *q_norm_w, const float *k_norm_w,
+                                const float *ffn_norm_w, float *kv_k, float *kv_v, const float *rope_cos,
+                                const float *rope_sin, const uint8_t **gate_ptrs, const uint8_t **up_ptrs,
+                                const void **down_ptrs, const int *down_is_f16, const float *expert_weights,
+                                int n_active, float *x, int inter, const LgAttn &g) {
+    if (!g.ok() || inter <= 0 || n_active < 0) return set_err(TG_E_INVALID, "transformer layer geometry");
+    size_t bq, bk, bv, bo;
+    lg_attn_wbytes(false, g, bq, bk, bv, bo);
+    const int embed = g.embed;
+    const size_t gb = (size_t)inter * (embed / tg::LG_QK) * tg::LG_Q4K_BYTES;
+    size_t dbmax = 0;
+    for (int e = 0; e < n_active; e++) dbmax = std::max(dbmax, down_bytes(down_is_f16[e], embed, inter));
+    const size_t nb = 4 * (size_t)g.hd, ev = 4 * (size_t)embed;
+    for (int pass = 0; pass < 2; pass++) {
+        LgCarve c{pass ? g_lg_buf : nullptr};
+        uint8_t *dq = c.take<uint8_t>(bq), *dk = c.take<uint8_t>(bk), *dv = c.take<uint8_t>(bv);
+        uint8_t *dwo = c.take<uint8_t>(bo);
+        float *dqn = c.take<float>(nb), *dkn = c.take<float>(nb), *dan = c.take<float>(ev), *dfn = c.take<float>(ev);
+        float *dx = c.take<float>(ev), *dmo = c.take<float>(ev);
+        uint8_t *dg = c.take<uint8_t>(gb), *du = c.take<uint8_t>(gb), *dd = c.take<uint8_t>(dbmax);
+        const LgAttnBufs b = lg_attn_bufs(c, g);
+        const LgExpertBufs eb = lg_expert_bufs(c, embed, inter);
+        if (!pass) {
+            int rc = lg_reserve(c.off);
+            if (rc) return rc;
+            continue;
+        }
+        hipStream_t st = g_lg_st;
+        int rc;
+        if ((rc = lg_h2d(dq, wq, bq)) || (rc = lg_h2d(dk, wk, bk)) || (rc = lg_h2d(dv, wv, bv)) ||
+            (rc = lg_h2d(dwo, wo, bo)) || (rc = lg_h2d(dqn, q_norm_w, nb)) || (rc = lg_h2d(dkn, k_norm_w, nb)) ||
+            (rc = lg_h2d(dan, attn_norm_w, ev)) || (rc = lg_h2d(dfn, ffn_norm_w, ev)) || (rc = lg_h2d(dx, x, ev)) ||
+            (rc = lg_attn_in(g, b, kv_k, kv_v, rope_cos, rope_sin)))
+            return rc;
+        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, dan, b.x, embed, 1e-6f, st));
+        if ((rc = lg_attn_core(false, dq, dk, dv, dwo, dqn, dkn, g, b))) return rc;
+        PROFILED("lg_add", st, tg::launch_add_vec(dx, b.out, embed, st));
+        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, dfn, b.x, embed, 1e-6f, st));
+        HIP_TRY(hipMemsetAsync(dmo, 0, ev, st));  // moe_out starts at zero
+        for (int e = 0; e < n_active; e++) {
+            // one expert's operands at a time (the copies wait for the previous expert's kernels)
+            const int fmt = down_is_f16[e];
+            if ((rc = lg_h2d(dg, gate_ptrs[e], gb)) || (rc = lg_h2d(du, up_ptrs[e], gb)) ||
+                (rc = lg_h2d(dd, down_ptrs[e], down_bytes(fmt, embed, inter))) ||
+                (rc = lg_expert(dg, du, dd, fmt, b.x, dmo, expert_weights[e], embed, inter, eb)))
+                return rc;
+        }
+        PROFILED("lg_add", st, tg::launch_add_vec(dx, dmo, embed, st));
+        if ((rc = lg_attn_out(g, b, kv_k, kv_v))) return rc;
+        return lg_finish(x, dx, ev);
+    }
+    return TG_OK;
+}
+
+extern "C" void tg_transformer_layer(const float *wq, const float *wk, const float *wv, const float *wo,
+                                     const float *attn_norm_w, const float *q_norm_w, const float *k_norm_w,
+                                     const float *ffn_norm_w, float *kv_k, float *kv_v, int kv_len, int kv_max,
+                                     const float *rope_cos, const float *rope_sin, const uint8_t **gate_ptrs,
+                                     const uint8_t **up_ptrs, const void **down_ptrs, const int *down_is_f16,
+                                     const float *expert_weights, int n_active, float *x, int embed_dim,
+                                     int inter_dim, int n_heads, int n_kv_heads, int head_dim, int pos) {
+    if (embed_dim <= 0) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const LgAttn g{embed_dim, n_heads, n_kv_heads, head_dim, kv_len, kv_max, pos};
+    if (lg_transformer_layer(wq, wk, wv, wo, attn_norm_w, q_norm_w, k_norm_w, ffn_norm_w, kv_k, kv_v, rope_cos,
+                             rope_sin, gate_ptrs, up_ptrs, down_ptrs, down_is_f16, expert_weights, n_active, x,
+                             inter_dim, g)) {
+        legacy_fail("tg_transformer_layer", warned_transformer_layer);
+        fill_nan(x, embed_dim);
+    }
 }
 

@@ -130,6 +130,15 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *out, int dim, 
 hipError_t launch_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y, int nrows, int bpr, hipStream_t st);
 hipError_t launch_silu_mul_vec(const float *g, const float *u, float *h, int n, hipStream_t st);
 hipError_t launch_acc_scaled(float *out, const float *v, float w, int n, hipStream_t st);
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
+                                hipStream_t st);
+hipError_t launch_rope(float *x, int n_heads, int hd, const float *c, const float *sn, hipStream_t st);
+hipError_t launch_kv_append(const float *kn, const float *v, float *kc, float *vc, int n_kv, int seq, int hd, int row,
+                            hipStream_t st);
+// caches [n_kv][seq][hd]; scr: n_heads * seq floats; hd <= 512
+hipError_t launch_attn_heads(const float *q, const float *kc, const float *vc, float *scr, float *out, int n_heads,
+                             int seq, int hd, int ratio, float inv_sqrt, hipStream_t st);
+hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st);
 
 // One-token layer with routing inside (k_layer_dec) and the prologue that
 // forms the first layer's router partials (k_dec_part).  part buffers hold

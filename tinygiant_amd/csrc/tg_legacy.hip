@@ -260,12 +260,15 @@ __global__ __launch_bounds__(256) void k_matvec_two_acc(const void *__restrict__
 // --------------------------------------------------------------- RMS norm
 // tg_rms_norm, libtinygiant.c:322-340: four fma chains of squares over
 // steps of 4, ss = (v0 + v1) + (v2 + v3), the tail one product and add at a
-// time, scale = 1 / sqrt(ss / dim + eps), out = (x * scale) * w.  One block.
+// time, scale = 1 / sqrt(ss / dim + eps), out = (x * scale) * w.  One block
+// per row (row b at x + b * dim, the same weight w).
 __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
                                                   float *__restrict__ out, int dim, float eps) {
     __shared__ float v[4];
     __shared__ float scale;
     const int tid = threadIdx.x, n4 = dim & ~3;
+    x += (size_t)blockIdx.x * dim;
+    out += (size_t)blockIdx.x * dim;
     if (tid < 4) {
         float a = 0.0f;
         for (int i = 0; i < n4; i += 4) a = __builtin_fmaf(x[i + tid], x[i + tid], a);
@@ -328,6 +331,101 @@ __global__ __launch_bounds__(256) void k_acc_scaled(float *__restrict__ out, con
     if (i < n) out[i] = out[i] + w * v[i];
 }
 
+// -------------------------------------------------------------- attention
+// apply_rope_inplace, libtinygiant.c:344-361, at one position (c, s: the
+// tables' row): x1' = x1 c - x2 s (products rounded, then the difference:
+// vmlsq_f32), x2' = fma(x1, s, x2 c) (vfmaq_f32 on the rounded x2 c).  One
+// thread per pair (head h, i < half).
+__global__ __launch_bounds__(256) void k_rope(float *__restrict__ x, int n_heads, int hd, const float *__restrict__ c,
+                                              const float *__restrict__ sn) {
+    const int half = hd / 2, p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= n_heads * half) return;
+    const int h = p / half, i = p - h * half;
+    float *xh = x + (size_t)h * hd;
+    const float x1 = xh[i], x2 = xh[half + i];
+    const float a = x1 * c[i], b = x2 * sn[i];
+    xh[i] = a - b;
+    xh[half + i] = __builtin_fmaf(x1, sn[i], x2 * c[i]);
+}
+
+// The new key and value rows into the caches [n_kv][seq][hd] at row `row`
+// (libtinygiant.c:395-401).
+__global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ kn, const float *__restrict__ v,
+                                                   float *__restrict__ kc, float *__restrict__ vc, int n_kv, int seq,
+                                                   int hd, int row) {
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= n_kv * hd) return;
+    const int h = p / hd, d = p - h * hd;
+    kc[((size_t)h * seq + row) * hd + d] = kn[p];
+    vc[((size_t)h * seq + row) * hd + d] = v[p];
+}
+
+// One head's attention over seq cached positions (libtinygiant.c:405-446):
+// score_t = dot(q, k_t) * inv_sqrt, the dot in four fma lanes over steps of 4
+// added as (l0 + l1) + (l2 + l3) with the tail one product and add at a time;
+// e_t = exp(score_t - max); sum = e_0 + e_1 + ... in order; out[d] = fma
+// chain over t of (e_t * (1 / sum)) v_t[d] (the tail d unfused).  One block
+// per head (kv head h / ratio); sc: this head's seq scores (device scratch).
+__global__ __launch_bounds__(256) void k_attn_head(const float *__restrict__ q, const float *__restrict__ kc,
+                                                   const float *__restrict__ vc, float *__restrict__ scr,
+                                                   float *__restrict__ out, int seq, int hd, int ratio,
+                                                   float inv_sqrt) {
+    __shared__ float qs[512];
+    __shared__ float red[256];
+    __shared__ float inv_sum;
+    const int h = blockIdx.x, tid = threadIdx.x, kh = h / ratio, hd4 = hd & ~3;
+    const float *qh = q + (size_t)h * hd;
+    const float *kch = kc + (size_t)kh * seq * hd, *vch = vc + (size_t)kh * seq * hd;
+    float *sc = scr + (size_t)h * seq;
+    for (int d = tid; d < hd; d += 256) qs[d] = qh[d];
+    __syncthreads();
+    float mx = -1e30f;
+    for (int t = tid; t < seq; t += 256) {
+        const float *kt = kch + (size_t)t * hd;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int d = 0; d < hd4; d += 4) {
+#pragma unroll
+            for (int l = 0; l < 4; l++) acc[l] = __builtin_fmaf(qs[d + l], kt[d + l], acc[l]);
+        }
+        float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (int d = hd4; d < hd; d++) dot = dot + qs[d] * kt[d];
+        const float s = dot * inv_sqrt;
+        sc[t] = s;
+        mx = s > mx ? s : mx;
+    }
+    red[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = red[tid + o] > red[tid] ? red[tid + o] : red[tid];
+        __syncthreads();
+    }
+    mx = red[0];
+    for (int t = tid; t < seq; t += 256) sc[t] = expf_tg(sc[t] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < seq; t++) sum = sum + sc[t];
+        inv_sum = 1.0f / sum;
+    }
+    __syncthreads();
+    const float is = inv_sum;
+    for (int d = tid; d < hd; d += 256) {
+        float o = 0.0f;
+        if (d < hd4) {
+            for (int t = 0; t < seq; t++) o = __builtin_fmaf(sc[t] * is, vch[(size_t)t * hd + d], o);
+        } else {
+            for (int t = 0; t < seq; t++) o = o + (sc[t] * is) * vch[(size_t)t * hd + d];
+        }
+        out[(size_t)h * hd + d] = o;
+    }
+}
+
+// x[i] += a[i] (libtinygiant.c:682,700)
+__global__ __launch_bounds__(256) void k_add_vec(float *__restrict__ x, const float *__restrict__ a, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = x[i] + a[i];
+}
+
 // ------------------------------------------------------------- launchers
 static unsigned lg_cdiv(long n, long d) { return (unsigned)((n + d - 1) / d); }
 
@@ -363,8 +461,13 @@ hipError_t launch_matvec_two_acc(const void *A, bool half, const float *x, float
 }
 
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int dim, float eps, hipStream_t st) {
-    if (dim <= 0) return hipSuccess;
-    TG_LAUNCH(k_rms_norm, dim3(1), dim3(256), 0, st, x, w, out, dim, eps);
+    return launch_rms_norm_rows(x, w, out, dim, 1, eps, st);
+}
+
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
+                                hipStream_t st) {
+    if (dim <= 0 || rows <= 0) return hipSuccess;
+    TG_LAUNCH(k_rms_norm, dim3(rows), dim3(256), 0, st, x, w, out, dim, eps);
     return hipGetLastError();
 }
 
@@ -377,6 +480,33 @@ hipError_t launch_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y, 
 hipError_t launch_silu_mul_vec(const float *g, const float *u, float *h, int n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     TG_LAUNCH(k_silu_mul_vec, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, g, u, h, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float *x, int n_heads, int hd, const float *c, const float *sn, hipStream_t st) {
+    const int n = n_heads * (hd / 2);
+    if (n <= 0) return hipSuccess;
+    TG_LAUNCH(k_rope, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, x, n_heads, hd, c, sn);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const float *kn, const float *v, float *kc, float *vc, int n_kv, int seq, int hd, int row,
+                            hipStream_t st) {
+    if (n_kv * hd <= 0) return hipSuccess;
+    TG_LAUNCH(k_kv_append, dim3(lg_cdiv((long)n_kv * hd, 256)), dim3(256), 0, st, kn, v, kc, vc, n_kv, seq, hd, row);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_heads(const float *q, const float *kc, const float *vc, float *scr, float *out, int n_heads,
+                             int seq, int hd, int ratio, float inv_sqrt, hipStream_t st) {
+    if (hd > 512 || n_heads <= 0) return hipErrorInvalidValue;
+    TG_LAUNCH(k_attn_head, dim3(n_heads), dim3(256), 0, st, q, kc, vc, scr, out, seq, hd, ratio, inv_sqrt);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    TG_LAUNCH(k_add_vec, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, x, a, n);
     return hipGetLastError();
 }
 
