@@ -365,33 +365,105 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ kn,
 // added as (l0 + l1) + (l2 + l3) with the tail one product and add at a time;
 // e_t = exp(score_t - max); sum = e_0 + e_1 + ... in order; out[d] = fma
 // chain over t of (e_t * (1 / sum)) v_t[d] (the tail d unfused).  One block
-// per head (kv head h / ratio); sc: this head's seq scores (device scratch).
+// per head (kv head h / ratio), 256 threads; scr: this head's seq scores
+// (device scratch).  Rows of K and V pass through LDS in chunks of ATT_TC(hd)
+// rows (K rows padded to hd + 1 floats, so the lanes reading different rows
+// use different banks): per chunk two threads share a row's dot (lanes 0-1
+// and 2-3), and in the weighted sum each thread carries its element's chain
+// across the chunks.
+__host__ __device__ inline int att_tc(int hd) {
+    int tc = 16384 / (hd + 1);
+    tc = tc > 128 ? 128 : tc;
+    return tc & ~1;
+}
+
+__host__ __device__ inline size_t att_lds_bytes(int hd) { return 4 * ((size_t)att_tc(hd) * (hd + 1) + 1024); }
+
+// n rows of hd floats (contiguous at src) into LDS rows of `stride` floats:
+// every thread's loads of a round are in flight together (16 float4 when hd
+// is a multiple of 4, else 16 floats), then stored.
+TG_DEV void att_stage(float *dst, int stride, const float *__restrict__ src, int n, int hd) {
+    const int tid = threadIdx.x, total = n * hd;
+    if ((hd & 3) == 0) {
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        const int t4 = total >> 2, h4 = hd >> 2;
+        for (int base = 0; base < t4; base += 256 * 16) {
+            float4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int i = base + u * 256 + tid;
+                v[u] = i < t4 ? s4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int i = base + u * 256 + tid;
+                if (i < t4) {
+                    const int rr = i / h4, c = 4 * (i - rr * h4);
+                    float *o = dst + rr * stride + c;
+                    o[0] = v[u].x; o[1] = v[u].y; o[2] = v[u].z; o[3] = v[u].w;
+                }
+            }
+        }
+    } else {
+        for (int base = 0; base < total; base += 256 * 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int i = base + u * 256 + tid;
+                v[u] = i < total ? src[i] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int i = base + u * 256 + tid;
+                if (i < total) {
+                    const int rr = i / hd;
+                    dst[rr * stride + i - rr * hd] = v[u];
+                }
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_attn_head(const float *__restrict__ q, const float *__restrict__ kc,
                                                    const float *__restrict__ vc, float *__restrict__ scr,
                                                    float *__restrict__ out, int seq, int hd, int ratio,
                                                    float inv_sqrt) {
+    extern __shared__ __align__(16) float lds[];  // [TC][hd + 1] rows, then 1024 floats of weights
     __shared__ float qs[512];
     __shared__ float red[256];
     __shared__ float inv_sum;
-    const int h = blockIdx.x, tid = threadIdx.x, kh = h / ratio, hd4 = hd & ~3;
+    const int h = blockIdx.x, tid = threadIdx.x, kh = h / ratio, hd4 = hd & ~3, TC = att_tc(hd), ks = hd + 1;
     const float *qh = q + (size_t)h * hd;
     const float *kch = kc + (size_t)kh * seq * hd, *vch = vc + (size_t)kh * seq * hd;
     float *sc = scr + (size_t)h * seq;
+    float *wl = lds + (size_t)TC * ks;
     for (int d = tid; d < hd; d += 256) qs[d] = qh[d];
-    __syncthreads();
+    // 1. scores, a chunk of TC rows at a time: thread pair (row tid / 2, lanes 2 (tid % 2) .. +1)
     float mx = -1e30f;
-    for (int t = tid; t < seq; t += 256) {
-        const float *kt = kch + (size_t)t * hd;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int d = 0; d < hd4; d += 4) {
-#pragma unroll
-            for (int l = 0; l < 4; l++) acc[l] = __builtin_fmaf(qs[d + l], kt[d + l], acc[l]);
+    const int r = tid >> 1, hf = tid & 1;
+    for (int t0 = 0; t0 < seq; t0 += TC) {
+        const int n = min(TC, seq - t0);
+        __syncthreads();  // the previous chunk's rows are read
+        att_stage(lds, ks, kch + (size_t)t0 * hd, n, hd);
+        __syncthreads();
+        float a0 = 0.0f, a1 = 0.0f;
+        if (r < n) {
+            const float *kt = lds + r * ks;
+#pragma unroll 8
+            for (int d = 2 * hf; d < hd4; d += 4) {
+                a0 = __builtin_fmaf(qs[d], kt[d], a0);
+                a1 = __builtin_fmaf(qs[d + 1], kt[d + 1], a1);
+            }
         }
-        float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        for (int d = hd4; d < hd; d++) dot = dot + qs[d] * kt[d];
-        const float s = dot * inv_sqrt;
-        sc[t] = s;
-        mx = s > mx ? s : mx;
+        const float mine = a0 + a1, other = __shfl_xor(mine, 1, WAVE);
+        if (r < n && hf == 0) {
+            float dot = mine + other;  // (l0 + l1) + (l2 + l3)
+            const float *kt = lds + r * ks;
+            for (int d = hd4; d < hd; d++) dot = dot + qs[d] * kt[d];
+            const float sv = dot * inv_sqrt;
+            sc[t0 + r] = sv;
+            mx = sv > mx ? sv : mx;
+        }
     }
     red[tid] = mx;
     __syncthreads();
@@ -400,24 +472,51 @@ __global__ __launch_bounds__(256) void k_attn_head(const float *__restrict__ q, 
         __syncthreads();
     }
     mx = red[0];
-    for (int t = tid; t < seq; t += 256) sc[t] = expf_tg(sc[t] - mx);
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        for (int t = 0; t < seq; t++) sum = sum + sc[t];
-        inv_sum = 1.0f / sum;
+    // 2. e_t (each score was written by thread 2 (t % TC) of its chunk)
+    for (int t0 = 0; t0 < seq; t0 += TC) {
+        const int t = t0 + r;
+        if (r < min(TC, seq - t0) && hf == 0) sc[t] = expf_tg(sc[t] - mx);
     }
+    __syncthreads();
+    // 3. sum in order, 1024 values at a time through LDS
+    float sum = 0.0f;
+    for (int t0 = 0; t0 < seq; t0 += 1024) {
+        const int n = min(1024, seq - t0);
+        for (int i = tid; i < n; i += 256) wl[i] = sc[t0 + i];
+        __syncthreads();
+        if (tid == 0) {
+#pragma unroll 16
+            for (int i = 0; i < n; i++) sum = sum + wl[i];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) inv_sum = 1.0f / sum;
     __syncthreads();
     const float is = inv_sum;
-    for (int d = tid; d < hd; d += 256) {
-        float o = 0.0f;
-        if (d < hd4) {
-            for (int t = 0; t < seq; t++) o = __builtin_fmaf(sc[t] * is, vch[(size_t)t * hd + d], o);
-        } else {
-            for (int t = 0; t < seq; t++) o = o + (sc[t] * is) * vch[(size_t)t * hd + d];
+    // 4. weighted values: chunks of TC rows of V and their weights in LDS
+    float o0 = 0.0f, o1 = 0.0f;  // elements tid and tid + 256
+    for (int t0 = 0; t0 < seq; t0 += TC) {
+        const int n = min(TC, seq - t0);
+        att_stage(lds, hd, vch + (size_t)t0 * hd, n, hd);
+        for (int i = tid; i < n; i += 256) wl[i] = sc[t0 + i] * is;
+        __syncthreads();
+#pragma unroll 8
+        for (int t = 0; t < n; t++) {
+            const float w = wl[t];
+            const float *vt = lds + t * hd;
+            if (tid < hd4)
+                o0 = __builtin_fmaf(w, vt[tid], o0);
+            else if (tid < hd)
+                o0 = o0 + w * vt[tid];
+            if (tid + 256 < hd4)
+                o1 = __builtin_fmaf(w, vt[tid + 256], o1);
+            else if (tid + 256 < hd)
+                o1 = o1 + w * vt[tid + 256];
         }
-        out[(size_t)h * hd + d] = o;
+        __syncthreads();
     }
+    if (tid < hd) out[(size_t)h * hd + tid] = o0;
+    if (tid + 256 < hd) out[(size_t)h * hd + tid + 256] = o1;
 }
 
 // x[i] += a[i] (libtinygiant.c:682,700)
@@ -499,8 +598,16 @@ hipError_t launch_kv_append(const float *kn, const float *v, float *kc, float *v
 
 hipError_t launch_attn_heads(const float *q, const float *kc, const float *vc, float *scr, float *out, int n_heads,
                              int seq, int hd, int ratio, float inv_sqrt, hipStream_t st) {
-    if (hd > 512 || n_heads <= 0) return hipErrorInvalidValue;
-    TG_LAUNCH(k_attn_head, dim3(n_heads), dim3(256), 0, st, q, kc, vc, scr, out, seq, hd, ratio, inv_sqrt);
+    if (hd > 512 || hd < 2 || n_heads <= 0) return hipErrorInvalidValue;
+    static bool lds_set = false;  // the largest chunk (any hd) fits 70 KB of dynamic LDS
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_attn_head, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 72 * 1024);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    TG_LAUNCH(k_attn_head, dim3(n_heads), dim3(256), att_lds_bytes(hd), st, q, kc, vc, scr, out, seq, hd, ratio,
+              inv_sqrt);
     return hipGetLastError();
 }
 
