@@ -365,6 +365,9 @@ def run_batched(args, torch, call):
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     gu_name = "gateup_mfma" if "gateup_mfma" in kern else "gateup_grouped"
+    # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries
+    gu_kernel = (("k_mfma_small" if T * K_TOP <= 16 * E else "k_mfma_grouped") if gu_name == "gateup_mfma"
+                 else "k_gateup_grouped")
     n_gu, ms_gu = kern[gu_name]
     achieved = n_uniq * GATEUP_BYTES_PER_EXPERT / (ms_gu / n_gu * 1e-3)
 
@@ -396,10 +399,10 @@ def run_batched(args, torch, call):
         "hbm_gbps_expert_weights": round(gbps, 1),
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": "k_mfma_grouped (gate/up)" if gu_name == "gateup_mfma"
-                     else "k_gateup_grouped", "bytes_per_launch": round(n_uniq * GATEUP_BYTES_PER_EXPERT),
+        "roofline": {"bound": "hbm", "kernel": gu_kernel + " (gate/up)",
+                     "bytes_per_launch": round(n_uniq * GATEUP_BYTES_PER_EXPERT),
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(gu_kernel + "/gate_up")},
         "cpu_baseline": cpu,
     }
     del outs
@@ -653,7 +656,8 @@ def run_prefill(args, torch, call):
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "mfma", "kernel": "k_mfma_grouped (gate/up)", "ops_per_launch": gu_ops,
                      "achieved": round(achieved / 1e12, 1), "peak": MFMA_INT8_PEAK / 1e12, "unit": "TOPS",
-                     "frac": round(achieved / MFMA_INT8_PEAK, 4), "traffic": None},
+                     "frac": round(achieved / MFMA_INT8_PEAK, 4),
+                     "traffic": profiled_traffic("k_mfma_grouped/gate_up")},
         "cpu_baseline": cpu,
     }
 
@@ -735,7 +739,7 @@ def run_legacy_moe(args, torch, call):
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": "k_matmul_q4k (gate/up)", "bytes_per_launch": q_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic("k_matmul_q4k/gate_up")},
         "cpu_baseline": cpu,
     }
 
@@ -826,7 +830,7 @@ def run_legacy_layer(args, torch, call):
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": "k_attn_head", "bytes_per_launch": attn_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic("k_attn_head")},
         "cpu_baseline": cpu,
     }
 
