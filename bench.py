@@ -792,8 +792,8 @@ def run_legacy_layer(args, torch, call):
     for _ in range(4):
         step()
     call("tg_prof_enable", 0)
-    kern = kernel_times(call, ("lg_f32", "lg_rms", "lg_rope", "lg_kv", "lg_attn", "lg_add", "lg_quant", "lg_q4k",
-                               "lg_silu", "lg_q4k_down", "lg_acc"))
+    kern = kernel_times(call, ("lg_f32", "lg_rms", "lg_rope", "lg_kv", "lg_attn_sc", "lg_attn_sm", "lg_attn", "lg_add",
+                               "lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     n_a, ms_a = kern["lg_attn"]
     attn_bytes = 2 * KV * (kv_len + 1) * hd * 4  # the cache rows each kv head's query heads read

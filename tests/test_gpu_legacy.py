@@ -223,7 +223,17 @@ def attn_case(rng, q4, embed, n_heads, n_kv, hd, kv_max):
 @pytest.mark.parametrize("q4", [False, True])
 @pytest.mark.parametrize("embed,n_heads,n_kv,hd,kv_max,kv_len",
                          [(512, 4, 2, 64, 16, 0), (512, 4, 2, 64, 16, 9), (2048, 32, 4, 128, 300, 257),
-                          (256, 2, 1, 130, 8, 7)])
+                          (256, 2, 1, 130, 8, 7),
+                          # 12 query heads per kv head (two head groups), 1031 positions (three chunks)
+                          (768, 12, 1, 64, 1100, 1030),
+                          # one query head per kv head
+                          (512, 4, 4, 128, 40, 33),
+                          # hd not a multiple of 4 over two chunks, 3 heads per kv head
+                          (256, 6, 2, 130, 600, 520),
+                          # the largest head
+                          (1024, 2, 1, 512, 20, 17),
+                          # 2091 positions: the softmax runs over two chunks
+                          (256, 2, 1, 128, 2100, 2090)])
 def test_attention_decode(O, L, q4, embed, n_heads, n_kv, hd, kv_max, kv_len):
     if q4 and (n_heads * hd) % 256:
         pytest.skip("Q4_K output projection needs q_dim % 256 == 0")

@@ -1326,7 +1326,7 @@ static LgAttnBufs lg_attn_bufs(LgCarve &c, const LgAttn &g) {
     b.out = c.take<float>(4 * (size_t)g.embed);
     b.kc = c.take<float>(cache);
     b.vc = c.take<float>(cache);
-    b.scr = c.take<float>(4 * (size_t)g.n_heads * g.seq());
+    b.scr = c.take<float>(sizeof(float) * tg::attn_scratch_floats(g.n_heads, g.seq()));
     b.cs = c.take<float>(4 * (size_t)(g.hd / 2));
     b.sn = c.take<float>(4 * (size_t)(g.hd / 2));
     b.xq = c.take<uint8_t>((size_t)(g.embed / tg::LG_QK) * tg::LG_Q8K_BYTES);
@@ -1388,9 +1388,10 @@ static int lg_attn_core(bool q4, const void *wq, const void *wk, const void *wv,
     PROFILED("lg_rope", st, tg::launch_rope(b.kn, g.n_kv, g.hd, b.cs, b.sn, st));
     PROFILED("lg_kv", st, tg::launch_kv_append(b.kn, b.v, b.kc, b.vc, g.n_kv, g.seq(), g.hd, g.kv_len, st));
     const float inv_sqrt = 1.0f / sqrtf((float)g.hd);
-    PROFILED("lg_attn", st,
-             tg::launch_attn_heads(b.qn, b.kc, b.vc, b.scr, b.ao, g.n_heads, g.seq(), g.hd, g.n_heads / g.n_kv,
-                                   inv_sqrt, st));
+    PROFILED("lg_attn_sc", st,
+             tg::launch_attn_scores(b.qn, b.kc, b.scr, g.n_heads, g.seq(), g.hd, g.n_heads / g.n_kv, inv_sqrt, st));
+    PROFILED("lg_attn_sm", st, tg::launch_attn_softmax(b.scr, g.n_heads, g.seq(), st));
+    PROFILED("lg_attn", st, tg::launch_attn_wv(b.scr, b.vc, b.ao, g.n_heads, g.seq(), g.hd, g.n_heads / g.n_kv, st));
     if (q4) {
         const int abpr = g.q_dim() / tg::LG_QK;
         PROFILED("lg_quant", st, tg::launch_quantize_q8k(b.ao, b.aq, abpr, st));

@@ -135,9 +135,26 @@ hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int 
 hipError_t launch_rope(float *x, int n_heads, int hd, const float *c, const float *sn, hipStream_t st);
 hipError_t launch_kv_append(const float *kn, const float *v, float *kc, float *vc, int n_kv, int seq, int hd, int row,
                             hipStream_t st);
-// caches [n_kv][seq][hd]; scr: n_heads * seq floats; hd <= 512
-hipError_t launch_attn_heads(const float *q, const float *kc, const float *vc, float *scr, float *out, int n_heads,
-                             int seq, int hd, int ratio, float inv_sqrt, hipStream_t st);
+// Attention of n_heads query heads over seq cached positions, caches
+// [n_kv][seq][hd] (ratio = n_heads / n_kv query heads per kv head), hd <= 512,
+// in three launches: scores and per-block maxima, the softmax weights of each
+// head, the weighted sum of V into out.  scr holds attn_scratch_floats()
+// floats: [n_heads][seq] scores, [n_heads][nblk] maxima, then (from a 16-byte
+// boundary) [n_heads][seq rounded up to 4] weights.
+constexpr int ATT_HB = 8;   // query heads of one kv head per block
+constexpr int ATT_TP = 16;  // positions per scores block
+inline int attn_score_blocks(int seq) { return (seq + ATT_TP - 1) / ATT_TP; }
+inline size_t attn_w_offset(int n_heads, int seq) {
+    return ((size_t)n_heads * ((size_t)seq + attn_score_blocks(seq)) + 3) & ~(size_t)3;
+}
+inline size_t attn_scratch_floats(int n_heads, int seq) {
+    return attn_w_offset(n_heads, seq) + (size_t)n_heads * (((size_t)seq + 3) & ~(size_t)3);
+}
+hipError_t launch_attn_scores(const float *q, const float *kc, float *scr, int n_heads, int seq, int hd, int ratio,
+                              float inv_sqrt, hipStream_t st);
+hipError_t launch_attn_softmax(float *scr, int n_heads, int seq, hipStream_t st);
+hipError_t launch_attn_wv(const float *scr, const float *vc, float *out, int n_heads, int seq, int hd, int ratio,
+                          hipStream_t st);
 hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st);
 
 // One-token layer with routing inside (k_layer_dec) and the prologue that

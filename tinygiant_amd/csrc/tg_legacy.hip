@@ -360,28 +360,29 @@ __global__ __launch_bounds__(256) void k_kv_append(const float *__restrict__ kn,
     vc[((size_t)h * seq + row) * hd + d] = v[p];
 }
 
-// One head's attention over seq cached positions (libtinygiant.c:405-446):
-// score_t = dot(q, k_t) * inv_sqrt, the dot in four fma lanes over steps of 4
-// added as (l0 + l1) + (l2 + l3) with the tail one product and add at a time;
-// e_t = exp(score_t - max); sum = e_0 + e_1 + ... in order; out[d] = fma
-// chain over t of (e_t * (1 / sum)) v_t[d] (the tail d unfused).  One block
-// per head (kv head h / ratio), 256 threads; scr: this head's seq scores
-// (device scratch).  Rows of K and V pass through LDS in chunks of ATT_TC(hd)
-// rows (K rows padded to hd + 1 floats, so the lanes reading different rows
-// use different banks): per chunk two threads share a row's dot (lanes 0-1
-// and 2-3), and in the weighted sum each thread carries its element's chain
-// across the chunks.
-__host__ __device__ inline int att_tc(int hd) {
-    int tc = 16384 / (hd + 1);
-    tc = tc > 128 ? 128 : tc;
-    return tc & ~1;
+// Attention over seq cached positions (libtinygiant.c:405-446), the head's
+// arithmetic in the reference's order: score_t = dot(q, k_t) * inv_sqrt, the
+// dot in four fma lanes over steps of 4 added as (l0 + l1) + (l2 + l3) with
+// the tail one product and add at a time; e_t = exp(score_t - max); sum =
+// e_0 + e_1 + ... in order; out[d] = fma chain over t of (e_t * (1 / sum))
+// v_t[d] (the tail d unfused).  The scores and the max are free of order,
+// the two sums are not: the first launch spreads the dots over (kv head,
+// 16 positions) blocks that share the K rows among the kv head's query heads;
+// the second gives each (head group, 16 elements of d) block the sequential
+// sums, with the V slice shared by the group's heads.
+//
+// A group is up to ATT_HB query heads of one kv head: group hg of kv head
+// g = hg / ngrp starts at head g * ratio + (hg % ngrp) * ATT_HB.
+TG_DEV void att_group(int hg, int ratio, int ngrp, int &g, int &h0, int &nh) {
+    g = hg / ngrp;
+    const int sub = hg - g * ngrp;
+    h0 = g * ratio + sub * ATT_HB;
+    nh = min(ATT_HB, ratio - sub * ATT_HB);
 }
-
-__host__ __device__ inline size_t att_lds_bytes(int hd) { return 4 * ((size_t)att_tc(hd) * (hd + 1) + 1024); }
 
 // n rows of hd floats (contiguous at src) into LDS rows of `stride` floats:
 // every thread's loads of a round are in flight together (16 float4 when hd
-// is a multiple of 4, else 16 floats), then stored.
+// is a multiple of 4, else 16 floats), then stored.  256 threads.
 TG_DEV void att_stage(float *dst, int stride, const float *__restrict__ src, int n, int hd) {
     const int tid = threadIdx.x, total = n * hd;
     if ((hd & 3) == 0) {
@@ -424,99 +425,280 @@ TG_DEV void att_stage(float *dst, int stride, const float *__restrict__ src, int
     }
 }
 
-__global__ __launch_bounds__(256) void k_attn_head(const float *__restrict__ q, const float *__restrict__ kc,
-                                                   const float *__restrict__ vc, float *__restrict__ scr,
-                                                   float *__restrict__ out, int seq, int hd, int ratio,
-                                                   float inv_sqrt) {
-    extern __shared__ __align__(16) float lds[];  // [TC][hd + 1] rows, then 1024 floats of weights
-    __shared__ float qs[512];
-    __shared__ float red[256];
-    __shared__ float inv_sum;
-    const int h = blockIdx.x, tid = threadIdx.x, kh = h / ratio, hd4 = hd & ~3, TC = att_tc(hd), ks = hd + 1;
-    const float *qh = q + (size_t)h * hd;
-    const float *kch = kc + (size_t)kh * seq * hd, *vch = vc + (size_t)kh * seq * hd;
-    float *sc = scr + (size_t)h * seq;
-    float *wl = lds + (size_t)TC * ks;
-    for (int d = tid; d < hd; d += 256) qs[d] = qh[d];
-    // 1. scores, a chunk of TC rows at a time: thread pair (row tid / 2, lanes 2 (tid % 2) .. +1)
-    float mx = -1e30f;
-    const int r = tid >> 1, hf = tid & 1;
-    for (int t0 = 0; t0 < seq; t0 += TC) {
-        const int n = min(TC, seq - t0);
-        __syncthreads();  // the previous chunk's rows are read
-        att_stage(lds, ks, kch + (size_t)t0 * hd, n, hd);
-        __syncthreads();
-        float a0 = 0.0f, a1 = 0.0f;
-        if (r < n) {
-            const float *kt = lds + r * ks;
-#pragma unroll 8
-            for (int d = 2 * hf; d < hd4; d += 4) {
-                a0 = __builtin_fmaf(qs[d], kt[d], a0);
-                a1 = __builtin_fmaf(qs[d + 1], kt[d + 1], a1);
+// Scores of one group's heads at positions [16 blockIdx.x, +16): a thread
+// pair per (head, position), lanes 0-1 and 2-3 of the dot, K rows padded to
+// hd + 1 floats in LDS.  scr: [n_heads][seq] scores, then [n_heads][nblk]
+// maxima of each block's scores (starting from -1e30 and passing over NaN,
+// as the reference's running max does).
+template <bool VEC>  // VEC: hd % 4 == 0, q and K rows loaded as float4 in one round
+__global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q, const float *__restrict__ kc,
+                                                     float *__restrict__ scr, int n_heads, int seq, int hd, int ratio,
+                                                     int ngrp, float inv_sqrt) {
+    extern __shared__ __align__(16) float lds[];  // [ATT_HB][hd] q rows, then [ATT_TP][hd + 1] K rows
+    int g, h0, nh;
+    att_group(blockIdx.y, ratio, ngrp, g, h0, nh);
+    const int tid = threadIdx.x, t0 = blockIdx.x * ATT_TP, n = min(ATT_TP, seq - t0), ks = hd + 1, hd4 = hd & ~3;
+    float *qs = lds, *kr = lds + ATT_HB * hd;
+    const float *qg = q + (size_t)h0 * hd, *kg = kc + ((size_t)g * seq + t0) * hd;
+    if constexpr (VEC) {
+        // hd <= 512: at most 4 float4 of q and 8 of K per thread, all in flight
+        // (addresses clamped into the rows, not branched around)
+        const int h4 = hd >> 2, nq = nh * h4, nk = n * h4;
+        float4 qv[4], kv[8];
+#pragma unroll
+        for (int u = 0; u < 4; u++) qv[u] = reinterpret_cast<const float4 *>(qg)[min(tid + 256 * u, nq - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) kv[u] = reinterpret_cast<const float4 *>(kg)[min(tid + 256 * u, nk - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = tid + 256 * u;
+            if (i < nq) reinterpret_cast<float4 *>(qs)[i] = qv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = tid + 256 * u;
+            if (i < nk) {
+                const int rr = i / h4, c = 4 * (i - rr * h4);
+                float *o = kr + rr * ks + c;
+                o[0] = kv[u].x; o[1] = kv[u].y; o[2] = kv[u].z; o[3] = kv[u].w;
             }
         }
-        const float mine = a0 + a1, other = __shfl_xor(mine, 1, WAVE);
-        if (r < n && hf == 0) {
-            float dot = mine + other;  // (l0 + l1) + (l2 + l3)
-            const float *kt = lds + r * ks;
-            for (int d = hd4; d < hd; d++) dot = dot + qs[d] * kt[d];
-            const float sv = dot * inv_sqrt;
-            sc[t0 + r] = sv;
-            mx = sv > mx ? sv : mx;
+    } else {
+        att_stage(qs, hd, qg, nh, hd);
+        att_stage(kr, ks, kg, n, hd);
+    }
+    __syncthreads();
+    const int j = tid >> 1, hf = tid & 1, hl = j / ATT_TP, p = j - hl * ATT_TP;
+    const bool ok = hl < nh && p < n;
+    const float *qh = qs + hl * hd, *kt = kr + p * ks;
+    float a0 = 0.0f, a1 = 0.0f;
+    if (ok) {
+#pragma unroll 8
+        for (int d = 2 * hf; d < hd4; d += 4) {
+            a0 = __builtin_fmaf(qh[d], kt[d], a0);
+            a1 = __builtin_fmaf(qh[d + 1], kt[d + 1], a1);
         }
     }
-    red[tid] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) red[tid] = red[tid + o] > red[tid] ? red[tid + o] : red[tid];
-        __syncthreads();
+    const float mine = a0 + a1, other = __shfl_xor(mine, 1, WAVE);
+    float m = -1e30f;
+    if (ok && hf == 0) {
+        float dot = mine + other;  // (l0 + l1) + (l2 + l3)
+        for (int d = hd4; d < hd; d++) dot = dot + qh[d] * kt[d];
+        const float sv = dot * inv_sqrt;
+        scr[(size_t)(h0 + hl) * seq + t0 + p] = sv;
+        m = sv > m ? sv : m;
     }
-    mx = red[0];
-    // 2. e_t (each score was written by thread 2 (t % TC) of its chunk)
-    for (int t0 = 0; t0 < seq; t0 += TC) {
-        const int t = t0 + r;
-        if (r < min(TC, seq - t0) && hf == 0) sc[t] = expf_tg(sc[t] - mx);
+    // a head's 16 positions are 32 consecutive lanes
+#pragma unroll
+    for (int s = 1; s < 32; s <<= 1) {
+        const float o = __shfl_xor(m, s, WAVE);
+        m = o > m ? o : m;
     }
+    if ((tid & 31) == 0 && hl < nh)
+        scr[(size_t)n_heads * seq + (size_t)(h0 + hl) * gridDim.x + blockIdx.x] = m;
+}
+
+// Softmax weights of one head (blockIdx.x): max over the scores blocks'
+// maxima, e_t = exp(score_t - max), sum = e_0 + e_1 + ... in order (one
+// lane's add chain through LDS, the next 16 values read while 16 are added),
+// w_t = e_t * (1 / sum) into the weights rows.  Positions go through LDS in
+// chunks of ATT_SC; with a single chunk the e_t stay there for the weights.
+constexpr int ATT_SC = 2048;
+
+__global__ __launch_bounds__(256) void k_attn_softmax(float *__restrict__ scr, int n_heads, int seq, int nblk,
+                                                      size_t woff) {
+    __shared__ __align__(16) float e[ATT_SC];
+    __shared__ float red[4];
+    __shared__ float bc;
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const float *sc = scr + (size_t)h * seq;
+    const float *pm = scr + (size_t)n_heads * seq + (size_t)h * nblk;
+    float *w = scr + woff + (size_t)h * ((seq + 3) & ~3);
+    constexpr int SU = ATT_SC / 256;
+    float v[SU];
+    // the first chunk's scores, then the maxima: all in flight together
+#pragma unroll
+    for (int u = 0; u < SU; u++) v[u] = sc[min(tid + 256 * u, seq - 1)];
+    float mx = -1e30f;
+    for (int b = tid; b < nblk; b += 256) {
+        const float p = pm[b];
+        mx = p > mx ? p : mx;
+    }
+#pragma unroll
+    for (int s = 1; s < WAVE; s <<= 1) {
+        const float o = __shfl_xor(mx, s, WAVE);
+        mx = o > mx ? o : mx;
+    }
+    if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = mx;
     __syncthreads();
-    // 3. sum in order, 1024 values at a time through LDS
+#pragma unroll
+    for (int i = 0; i < 4; i++) mx = red[i] > mx ? red[i] : mx;
     float sum = 0.0f;
-    for (int t0 = 0; t0 < seq; t0 += 1024) {
-        const int n = min(1024, seq - t0);
-        for (int i = tid; i < n; i += 256) wl[i] = sc[t0 + i];
+    for (int t0 = 0; t0 < seq; t0 += ATT_SC) {
+        const int n = min(ATT_SC, seq - t0);
+        if (t0 > 0) {
+            __syncthreads();  // the previous chunk is summed
+#pragma unroll
+            for (int u = 0; u < SU; u++) v[u] = sc[min(t0 + tid + 256 * u, seq - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int i = tid + 256 * u;
+            if (i < n) e[i] = expf_tg(v[u] - mx);
+        }
         __syncthreads();
         if (tid == 0) {
-#pragma unroll 16
-            for (int i = 0; i < n; i++) sum = sum + wl[i];
+            // 16 values a step in two register sets taken in turn: one set's
+            // reads are in flight while the other's values are added
+            const float4 *e4 = reinterpret_cast<const float4 *>(e);
+            const int n16 = n >> 4;
+            float4 a[4], b[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) a[k] = e4[k];
+            int s16 = 0;
+            for (; s16 + 2 <= n16; s16 += 2) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) b[k] = e4[4 * (s16 + 1) + k];
+#pragma unroll
+                for (int k = 0; k < 4; k++) sum = ((sum + a[k].x) + a[k].y + a[k].z) + a[k].w;
+                const int nx = 4 * min(s16 + 2, n16 - 1);
+#pragma unroll
+                for (int k = 0; k < 4; k++) a[k] = e4[nx + k];
+#pragma unroll
+                for (int k = 0; k < 4; k++) sum = ((sum + b[k].x) + b[k].y + b[k].z) + b[k].w;
+            }
+            if (s16 < n16) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) sum = ((sum + a[k].x) + a[k].y + a[k].z) + a[k].w;
+            }
+            for (int i = 16 * n16; i < n; i++) sum = sum + e[i];
+            bc = 1.0f / sum;
         }
-        __syncthreads();
     }
-    if (tid == 0) inv_sum = 1.0f / sum;
     __syncthreads();
-    const float is = inv_sum;
-    // 4. weighted values: chunks of TC rows of V and their weights in LDS
-    float o0 = 0.0f, o1 = 0.0f;  // elements tid and tid + 256
-    for (int t0 = 0; t0 < seq; t0 += TC) {
-        const int n = min(TC, seq - t0);
-        att_stage(lds, hd, vch + (size_t)t0 * hd, n, hd);
-        for (int i = tid; i < n; i += 256) wl[i] = sc[t0 + i] * is;
-        __syncthreads();
-#pragma unroll 8
-        for (int t = 0; t < n; t++) {
-            const float w = wl[t];
-            const float *vt = lds + t * hd;
-            if (tid < hd4)
-                o0 = __builtin_fmaf(w, vt[tid], o0);
-            else if (tid < hd)
-                o0 = o0 + w * vt[tid];
-            if (tid + 256 < hd4)
-                o1 = __builtin_fmaf(w, vt[tid + 256], o1);
-            else if (tid + 256 < hd)
-                o1 = o1 + w * vt[tid + 256];
-        }
-        __syncthreads();
+    const float is = bc;
+    if (seq <= ATT_SC) {
+        for (int i = tid; i < seq; i += 256) w[i] = e[i] * is;
+    } else {
+        for (int i = tid; i < seq; i += 256) w[i] = expf_tg(sc[i] - mx) * is;
     }
-    if (tid < hd) out[(size_t)h * hd + tid] = o0;
-    if (tid + 256 < hd) out[(size_t)h * hd + tid + 256] = o1;
+}
+
+// Weighted sum of one group's heads for d in [16 blockIdx.x, +16): thread
+// (hl = tid / 16, r = tid % 16) carries out[h0 + hl][d0 + r] as one fma
+// chain over the positions.  Weights and the V slice go through LDS in
+// chunks of ATT_CH positions, the next chunk loaded into registers while the
+// current one is summed; the LDS reads of the chain run 8 positions ahead.
+constexpr int ATT_DS = 16, ATT_CH = 512, ATT_VU = ATT_CH * ATT_DS / 4 / 128, ATT_WU = ATT_HB * ATT_CH / 4 / 128;
+
+template <bool VEC>  // VEC: hd % 4 == 0, the V slice read as float4
+__global__ __launch_bounds__(128) void k_attn_wv(const float *__restrict__ scr, const float *__restrict__ vc,
+                                                 float *__restrict__ out, int seq, int hd, int ratio, int ngrp,
+                                                 size_t woff) {
+    __shared__ __align__(16) float wl[ATT_HB][ATT_CH + 4];  // rows 16-byte aligned, 4 banks apart
+    __shared__ __align__(16) float vs[ATT_CH * ATT_DS];
+    int g, h0, nh;
+    att_group(blockIdx.y, ratio, ngrp, g, h0, nh);
+    const int tid = threadIdx.x, hl = tid >> 4, r = tid & 15, d0 = blockIdx.x * ATT_DS, hd4 = hd & ~3;
+    const int seq4 = (seq + 3) & ~3;
+    const float *wg = scr + woff + (size_t)h0 * seq4;
+    const float *vg = vc + (size_t)g * seq * hd;
+    float4 vr[ATT_VU], wr[ATT_WU];
+    // Loads without branches or selects (either makes the compiler wait for
+    // the load where it stands): each address is clamped into its buffer.  A
+    // clamped position (t >= seq), element (d >= hd) or head (>= nh) holds a
+    // copy of a valid value that no chain reads and no output stores.
+    auto load = [&](int t0) {
+        t0 = min(t0, seq - 1);  // a prefetch past the end reads the last chunk again
+        const int n = min(ATT_CH, seq - t0);
+#pragma unroll
+        for (int u = 0; u < ATT_VU; u++) {
+            const int i = tid + 128 * u, row = min(i >> 2, n - 1), c = d0 + 4 * (i & 3);
+            const float *src = vg + (size_t)(t0 + row) * hd;
+            if constexpr (VEC) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + min(c, hd - 4));
+                vr[u].x = v.x;  // by component: a whole-float4 copy keeps the array out of registers
+                vr[u].y = v.y;
+                vr[u].z = v.z;
+                vr[u].w = v.w;
+            } else {
+                vr[u].x = src[min(c, hd - 1)];
+                vr[u].y = src[min(c + 1, hd - 1)];
+                vr[u].z = src[min(c + 2, hd - 1)];
+                vr[u].w = src[min(c + 3, hd - 1)];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < ATT_WU; u++) {
+            const int i = tid + 128 * u, row = min(i / (ATT_CH / 4), nh - 1);
+            const int p = min(t0 + 4 * (i & (ATT_CH / 4 - 1)), seq4 - 4);
+            const float4 v = *reinterpret_cast<const float4 *>(wg + (size_t)row * seq4 + p);
+            wr[u].x = v.x;
+            wr[u].y = v.y;
+            wr[u].z = v.z;
+            wr[u].w = v.w;
+        }
+    };
+    load(0);
+    const int d = d0 + r;
+    float o = 0.0f;
+    for (int t0 = 0; t0 < seq; t0 += ATT_CH) {
+        const int n = min(ATT_CH, seq - t0);
+        lds_barrier();  // the previous chunk is consumed
+#pragma unroll
+        for (int u = 0; u < ATT_VU; u++)
+            *reinterpret_cast<float4 *>(vs + 4 * (tid + 128 * u)) = make_float4(vr[u].x, vr[u].y, vr[u].z, vr[u].w);
+#pragma unroll
+        for (int u = 0; u < ATT_WU; u++) {
+            const int i = tid + 128 * u;
+            *reinterpret_cast<float4 *>(&wl[i / (ATT_CH / 4)][4 * (i & (ATT_CH / 4 - 1))]) =
+                make_float4(wr[u].x, wr[u].y, wr[u].z, wr[u].w);
+        }
+        load(t0 + ATT_CH);  // past the end: harmless reloads, no branch
+        lds_barrier();
+        const float *w = wl[hl];
+        if (d < hd4) {
+            // 8 positions a step in two register sets taken in turn: one
+            // set's LDS reads are in flight while the other's fmas run
+            const float4 *w4 = reinterpret_cast<const float4 *>(w);
+            const float *v = vs + r;
+            const int n8 = n >> 3;
+            float4 wa0, wa1, wb0, wb1;
+            float va[8], vb[8];
+            wa0 = w4[0]; wa1 = w4[1];
+#pragma unroll
+            for (int k = 0; k < 8; k++) va[k] = v[k * ATT_DS];
+            int s8 = 0;
+            for (; s8 + 2 <= n8; s8 += 2) {
+                const int nb = 8 * (s8 + 1);
+                wb0 = w4[nb >> 2]; wb1 = w4[(nb >> 2) + 1];
+#pragma unroll
+                for (int k = 0; k < 8; k++) vb[k] = v[(nb + k) * ATT_DS];
+                o = __builtin_fmaf(wa0.x, va[0], o); o = __builtin_fmaf(wa0.y, va[1], o);
+                o = __builtin_fmaf(wa0.z, va[2], o); o = __builtin_fmaf(wa0.w, va[3], o);
+                o = __builtin_fmaf(wa1.x, va[4], o); o = __builtin_fmaf(wa1.y, va[5], o);
+                o = __builtin_fmaf(wa1.z, va[6], o); o = __builtin_fmaf(wa1.w, va[7], o);
+                const int na = 8 * min(s8 + 2, n8 - 1);
+                wa0 = w4[na >> 2]; wa1 = w4[(na >> 2) + 1];
+#pragma unroll
+                for (int k = 0; k < 8; k++) va[k] = v[(na + k) * ATT_DS];
+                o = __builtin_fmaf(wb0.x, vb[0], o); o = __builtin_fmaf(wb0.y, vb[1], o);
+                o = __builtin_fmaf(wb0.z, vb[2], o); o = __builtin_fmaf(wb0.w, vb[3], o);
+                o = __builtin_fmaf(wb1.x, vb[4], o); o = __builtin_fmaf(wb1.y, vb[5], o);
+                o = __builtin_fmaf(wb1.z, vb[6], o); o = __builtin_fmaf(wb1.w, vb[7], o);
+            }
+            if (s8 < n8) {
+                o = __builtin_fmaf(wa0.x, va[0], o); o = __builtin_fmaf(wa0.y, va[1], o);
+                o = __builtin_fmaf(wa0.z, va[2], o); o = __builtin_fmaf(wa0.w, va[3], o);
+                o = __builtin_fmaf(wa1.x, va[4], o); o = __builtin_fmaf(wa1.y, va[5], o);
+                o = __builtin_fmaf(wa1.z, va[6], o); o = __builtin_fmaf(wa1.w, va[7], o);
+            }
+            for (int t = 8 * n8; t < n; t++) o = __builtin_fmaf(w[t], vs[t * ATT_DS + r], o);
+        } else if (d < hd) {
+            for (int t = 0; t < n; t++) o = o + w[t] * vs[t * ATT_DS + r];
+        }
+    }
+    if (hl < nh && d < hd) out[(size_t)(h0 + hl) * hd + d] = o;
 }
 
 // x[i] += a[i] (libtinygiant.c:682,700)
@@ -596,18 +778,38 @@ hipError_t launch_kv_append(const float *kn, const float *v, float *kc, float *v
     return hipGetLastError();
 }
 
-hipError_t launch_attn_heads(const float *q, const float *kc, const float *vc, float *scr, float *out, int n_heads,
-                             int seq, int hd, int ratio, float inv_sqrt, hipStream_t st) {
-    if (hd > 512 || hd < 2 || n_heads <= 0) return hipErrorInvalidValue;
-    static bool lds_set = false;  // the largest chunk (any hd) fits 70 KB of dynamic LDS
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_attn_head, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 72 * 1024);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
-    TG_LAUNCH(k_attn_head, dim3(n_heads), dim3(256), att_lds_bytes(hd), st, q, kc, vc, scr, out, seq, hd, ratio,
-              inv_sqrt);
+static int att_ngrp(int ratio) { return (ratio + ATT_HB - 1) / ATT_HB; }
+
+hipError_t launch_attn_scores(const float *q, const float *kc, float *scr, int n_heads, int seq, int hd, int ratio,
+                              float inv_sqrt, hipStream_t st) {
+    if (hd > 512 || hd < 2 || n_heads <= 0 || seq <= 0 || ratio <= 0 || n_heads % ratio) return hipErrorInvalidValue;
+    const int ngrp = att_ngrp(ratio), n_kv = n_heads / ratio;
+    const size_t lds = sizeof(float) * ((size_t)ATT_HB * hd + (size_t)ATT_TP * (hd + 1));
+    const dim3 grid(attn_score_blocks(seq), n_kv * ngrp);
+    if (hd % 4 == 0)
+        TG_LAUNCH(k_attn_scores<true>, grid, dim3(256), lds, st, q, kc, scr, n_heads, seq, hd, ratio, ngrp, inv_sqrt);
+    else
+        TG_LAUNCH(k_attn_scores<false>, grid, dim3(256), lds, st, q, kc, scr, n_heads, seq, hd, ratio, ngrp, inv_sqrt);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_softmax(float *scr, int n_heads, int seq, hipStream_t st) {
+    if (n_heads <= 0 || seq <= 0) return hipErrorInvalidValue;
+    TG_LAUNCH(k_attn_softmax, dim3(n_heads), dim3(256), 0, st, scr, n_heads, seq, attn_score_blocks(seq),
+              attn_w_offset(n_heads, seq));
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_wv(const float *scr, const float *vc, float *out, int n_heads, int seq, int hd, int ratio,
+                          hipStream_t st) {
+    if (hd > 512 || hd < 2 || n_heads <= 0 || seq <= 0 || ratio <= 0 || n_heads % ratio) return hipErrorInvalidValue;
+    const int ngrp = att_ngrp(ratio), n_kv = n_heads / ratio;
+    const dim3 grid(lg_cdiv(hd, ATT_DS), n_kv * ngrp);
+    const size_t woff = attn_w_offset(n_heads, seq);
+    if (hd % 4 == 0)
+        TG_LAUNCH(k_attn_wv<true>, grid, dim3(128), 0, st, scr, vc, out, seq, hd, ratio, ngrp, woff);
+    else
+        TG_LAUNCH(k_attn_wv<false>, grid, dim3(128), 0, st, scr, vc, out, seq, hd, ratio, ngrp, woff);
     return hipGetLastError();
 }
 
