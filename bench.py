@@ -795,9 +795,15 @@ def run_legacy_layer(args, torch, call):
     kern = kernel_times(call, ("lg_f32", "lg_rms", "lg_rope", "lg_kv", "lg_attn_sc", "lg_attn_sm", "lg_attn", "lg_add",
                                "lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    n_a, ms_a = kern["lg_attn"]
-    attn_bytes = 2 * KV * (kv_len + 1) * hd * 4  # the cache rows each kv head's query heads read
-    achieved = attn_bytes / (ms_a / n_a * 1e-3)
+    # dominant kernel: the f32 q / k / v / o projections (k_matvec_two_acc),
+    # bytes per launch = weights + input averaged over the four launches
+    n_f, ms_f = kern["lg_f32"]
+    proj_shapes = ((Hh * hd, H), (KV * hd, H), (KV * hd, H), (H, Hh * hd))
+    proj_bytes = sum(4 * (r * c + c + r) for r, c in proj_shapes) / len(proj_shapes)
+    achieved = proj_bytes / (ms_f / n_f * 1e-3)
+    # attention proper: scores, softmax weights, weighted sum of V
+    attn_bytes = 2 * KV * (kv_len + 1) * hd * 4  # the K and V cache rows, each read once
+    attn_us = sum(kern[k][1] / kern[k][0] * 1e3 for k in ("lg_attn_sc", "lg_attn_sm", "lg_attn") if k in kern)
 
     cpu = None
     if not args.no_cpu:
@@ -828,9 +834,12 @@ def run_legacy_layer(args, torch, call):
         "config": {"workload": "legacy-transformer-layer", "hidden": H, "heads": Hh, "kv_heads": KV, "head_dim": hd,
                    "kv_len": kv_len, "experts": K_TOP, "moe_intermediate": I},
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": "k_attn_head", "bytes_per_launch": attn_bytes,
-                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic("k_attn_head")},
+        "roofline": {"bound": "hbm", "kernel": "k_matvec_two_acc (f32 projections)",
+                     "bytes_per_launch": round(proj_bytes), "achieved": round(achieved / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": profiled_traffic("k_matvec_two_acc/f32")},
+        "attention": {"kernels": "k_attn_scores + k_attn_softmax + k_attn_wv", "us": round(attn_us, 3),
+                      "cache_bytes": attn_bytes, "gbps": round(attn_bytes / (attn_us * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
     }
 

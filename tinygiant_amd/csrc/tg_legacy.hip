@@ -261,19 +261,36 @@ __global__ __launch_bounds__(256) void k_matvec_two_acc(const void *__restrict__
 // tg_rms_norm, libtinygiant.c:322-340: four fma chains of squares over
 // steps of 4, ss = (v0 + v1) + (v2 + v3), the tail one product and add at a
 // time, scale = 1 / sqrt(ss / dim + eps), out = (x * scale) * w.  One block
-// per row (row b at x + b * dim, the same weight w).
+// per row (row b at x + b * dim, the same weight w).  The row passes
+// through LDS in chunks of 4096 values, loaded by all threads with their
+// loads in flight together, so the four chains (threads 0-3) read LDS
+// rather than wait on a global load per step.
+constexpr int RMS_CH = 4096;
+
 __global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
                                                   float *__restrict__ out, int dim, float eps) {
+    __shared__ float xs[RMS_CH];
     __shared__ float v[4];
     __shared__ float scale;
     const int tid = threadIdx.x, n4 = dim & ~3;
     x += (size_t)blockIdx.x * dim;
     out += (size_t)blockIdx.x * dim;
-    if (tid < 4) {
-        float a = 0.0f;
-        for (int i = 0; i < n4; i += 4) a = __builtin_fmaf(x[i + tid], x[i + tid], a);
-        v[tid] = a;
+    float a = 0.0f;
+    for (int c0 = 0; c0 < n4; c0 += RMS_CH) {
+        const int n = min(RMS_CH, n4 - c0);
+        float xv[RMS_CH / 256];
+#pragma unroll
+        for (int u = 0; u < RMS_CH / 256; u++) xv[u] = x[c0 + min(tid + 256 * u, n - 1)];
+        __syncthreads();  // the previous chunk is read
+#pragma unroll
+        for (int u = 0; u < RMS_CH / 256; u++) xs[tid + 256 * u] = xv[u];
+        __syncthreads();
+        if (tid < 4) {
+#pragma unroll 8
+            for (int i = tid; i < n; i += 4) a = __builtin_fmaf(xs[i], xs[i], a);
+        }
     }
+    if (tid < 4) v[tid] = a;
     __syncthreads();
     if (tid == 0) {
         float ss = (v[0] + v[1]) + (v[2] + v[3]);
