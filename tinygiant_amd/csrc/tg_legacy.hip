@@ -220,31 +220,70 @@ __global__ __launch_bounds__(256) void k_matmul_q6k(const uint8_t *__restrict__ 
 // matvec_f16 / tg_f32_matvec, libtinygiant.c:277-318: eight fma chains over
 // steps of 8 elements (chain c takes elements i + c), t_c = chain c + chain
 // c + 4, sum = (t0 + t1) + (t2 + t3), then the tail (ncols % 8) one product
-// and one add at a time.  Eight lanes per row.
+// and one add at a time.  Eight lanes per row (lane c carries chain c).
+// x passes through LDS in chunks of MV_XS columns; each lane's weights are
+// loaded MV_D steps at a time into two register sets taken in turn, so one
+// set's loads are in flight while the other's fmas run.  Addresses are
+// clamped into the row instead of branched around (a branch or select on a
+// load makes the compiler wait for it in place); clamped steps are not added.
+constexpr int MV_D = 16, MV_XS = 8192;
+
 template <bool HALF>
 __global__ __launch_bounds__(256) void k_matvec_two_acc(const void *__restrict__ A, const float *__restrict__ x,
                                                         float *__restrict__ y, int nrows, int ncols) {
-    const int c = threadIdx.x & 7, row = (blockIdx.x * 256 + threadIdx.x) >> 3;
+    __shared__ float xs[MV_XS];
+    const int tid = threadIdx.x, c = tid & 7, row = (blockIdx.x * 256 + tid) >> 3;
     const bool on = row < nrows;
     const int n8 = ncols & ~7;
     auto wat = [&](size_t i) -> float {
         return HALF ? h2f(reinterpret_cast<const uint16_t *>(A)[i]) : reinterpret_cast<const float *>(A)[i];
     };
-    const size_t r0 = (size_t)(on ? row : 0) * ncols;
+    const size_t r0 = (size_t)(on ? row : nrows - 1) * ncols;
     float a = 0.0f;
-    if (on) {
-        int i = 0;
-        for (; i + 32 <= n8; i += 32) {  // four steps' operands loaded ahead of the chain
-            float w4[4], x4[4];
+    for (int x0 = 0; x0 < n8; x0 += MV_XS) {
+        const int nx = min(MV_XS, n8 - x0), ns = nx >> 3;
+        __syncthreads();  // the previous chunk of x is read
+        for (int i0 = 0; i0 < nx; i0 += 256 * 8) {
+            float t[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                w4[u] = wat(r0 + i + 8 * u + c);
-                x4[u] = x[i + 8 * u + c];
+            for (int u = 0; u < 8; u++) t[u] = x[x0 + min(i0 + tid + 256 * u, nx - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + tid + 256 * u;
+                if (i < nx) xs[i] = t[u];
             }
-#pragma unroll
-            for (int u = 0; u < 4; u++) a = __builtin_fmaf(w4[u], x4[u], a);
         }
-        for (; i < n8; i += 8) a = __builtin_fmaf(wat(r0 + i + c), x[i + c], a);
+        __syncthreads();
+        const size_t wb = r0 + x0 + c;
+        float pa[MV_D], pb[MV_D], xa[MV_D], xb[MV_D];
+        auto ld = [&](float *p, float *q, int s0) {  // weights from HBM, x from LDS
+#pragma unroll
+            for (int k = 0; k < MV_D; k++) {
+                const int sk = min(s0 + k, ns - 1);
+                p[k] = wat(wb + 8 * (size_t)sk);
+                q[k] = xs[8 * sk + c];
+            }
+        };
+        auto run = [&](const float *p, const float *q) {
+#pragma unroll
+            for (int k = 0; k < MV_D; k++) a = __builtin_fmaf(p[k], q[k], a);
+        };
+        int st = 0;
+        ld(pa, xa, 0);
+        for (; st + 2 * MV_D <= ns; st += 2 * MV_D) {
+            ld(pb, xb, st + MV_D);
+            run(pa, xa);
+            ld(pa, xa, st + 2 * MV_D);
+            run(pb, xb);
+        }
+        // fewer than 2 MV_D steps remain: pa holds steps st.., pb the next MV_D
+        ld(pb, xb, st + MV_D);
+#pragma unroll
+        for (int k = 0; k < MV_D; k++)
+            if (st + k < ns) a = __builtin_fmaf(pa[k], xa[k], a);
+#pragma unroll
+        for (int k = 0; k < MV_D; k++)
+            if (st + MV_D + k < ns) a = __builtin_fmaf(pb[k], xb[k], a);
     }
     const float t = a + __shfl_xor(a, 4, WAVE);  // lanes c < 4: chain c + chain c + 4
     const float t1 = __shfl_xor(t, 1, WAVE);
