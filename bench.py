@@ -25,6 +25,8 @@ Other workloads (--workload):
   legacy-layer the reference's tg_transformer_layer on the same buffers: f32
                attention (32 heads / 4 kv heads of 128, 1024 cached positions)
                and 8 Q4_K experts, one token.
+  output-head  the step after the layers: logits of the 151936 x 2048 fp32
+               head (resident) and the greedy token, one call per step.
 
 Prints one JSON line: tok/s (value), expert-weight HBM GB/s, the roofline
 of the dominant kernel (HIP events on its launch stream) and the CPU oracle
@@ -886,10 +888,84 @@ def run_hbm_ceiling(args, torch, call):
             "cpu_baseline": None}
 
 
+def run_output_head(args, torch, call):
+    """The output head after the layers (engine.py:262-266,359): logits =
+    W @ rms_norm(x) with the Qwen3-30B-A3B head W 151936 x 2048 fp32 (1.24 GB,
+    resident in HBM behind tg_head_create), then the greedy token.  One step =
+    one tg_head_forward call: the 8 KB input copied in, norm, matvec, argmax,
+    the token copied back (the logits stay on the device)."""
+    from tinygiant_amd._lib import require_lib
+    lib = require_lib()
+    V = 151936
+    rng = np.random.default_rng(args.seed)
+    log(f"head weights {V} x {H} fp32 ({V * H * 4 / 1e9:.2f} GB)")
+    W = rng.standard_normal((V, H), dtype=np.float32) * np.float32(0.02)
+    nw = rng.normal(1.0, 0.1, H).astype(np.float32)
+    xs = [rng.normal(0, 1, H).astype(np.float32) for _ in range(8)]
+    h = lib.tg_head_create(W.ctypes.data, nw.ctypes.data, V, H)
+    if not h:
+        raise RuntimeError(f"tg_head_create: {lib.tg_last_error().decode()}")
+    tok = ctypes.c_int32()
+    K, W_ = args.steps or 200, 10 if args.warmup is None else args.warmup
+
+    def step(i):
+        rc = lib.tg_head_forward(h, xs[i % len(xs)].ctypes.data, 1e-6, None, ctypes.byref(tok))
+        if rc:
+            raise RuntimeError(f"tg_head_forward: {lib.tg_last_error().decode()}")
+
+    log(f"warmup {W_} calls")
+    for i in range(W_):
+        step(i)
+    log(f"timing {K} calls")
+    t0 = time.perf_counter()
+    for i in range(K):
+        step(i)
+    wall = time.perf_counter() - t0
+    call("tg_prof_enable", 1)
+    for i in range(16):
+        step(i)
+    call("tg_prof_enable", 0)
+    kern = kernel_times(call, ("head_rms", "head_mv", "head_argmax"))
+    kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    n_m, ms_m = kern["head_mv"]
+    mv_bytes = 4 * (V * H + H + V)
+    achieved = mv_bytes / (ms_m / n_m * 1e-3)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        from oracle import oracle as O  # the checker, timed as the CPU baseline
+        logits, ref_tok = O.output_head(W, nw, xs[0], 1e-6)
+        step(0)
+        assert tok.value == ref_tok, "GPU head token differs from the oracle"
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0):
+            O.output_head(W, nw, xs[n % len(xs)], 1e-6)
+            n += 1
+        cpu_s = (time.perf_counter() - t1) / n
+        cpu = {"value": round(1.0 / cpu_s, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"{n} output-head calls (norm + 151936 x 2048 fp32 matvec + argmax) through the C oracle, "
+                         "one thread; same token as the GPU call"}
+    lib.tg_head_destroy(h)
+    return {
+        "metric": "output head tok/s (151936 x 2048 fp32 logits + greedy token, weights resident)",
+        "value": round(K / wall, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W_,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (N(0, 0.02) fp32 head, N(0, 1) inputs)",
+        "config": {"workload": "qwen3-30b-a3b-output-head", "vocab": V, "hidden": H},
+        "kernel_avg_us": kern_us,
+        "roofline": {"bound": "hbm", "kernel": "k_matvec_two_acc (head)", "bytes_per_launch": mv_bytes,
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic("k_matvec_two_acc/head")},
+        "cpu_baseline": cpu,
+    }
+
+
 WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill": run_prefill,
              "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
              "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
-             "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe, "legacy-layer": run_legacy_layer}
+             "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe, "legacy-layer": run_legacy_layer,
+             "output-head": run_output_head}
 
 
 def main() -> int:

@@ -273,6 +273,20 @@ int tg_synth_normal_dev(uint64_t seed, uint64_t stream_id, float sigma,
 int tg_synth_q40_dev(uint64_t seed, uint64_t stream_id, float sigma,
                      int rows, int cols, void *planar_out, void *stream);
 
+/* Output head, the step after the layers (tinygiant/engine.py:262-266 forms
+ * logits = output_weight @ rms_norm(x, output_norm) in numpy, and :359 takes
+ * the greedy token np.argmax(logits)).  W [vocab][embed] fp32 and the norm
+ * weight are copied to HBM once; each forward copies x in, runs the norm
+ * (tg_rms_norm's order), the fp32 matvec (tg_f32_matvec's order,
+ * libtinygiant.c:299-318) and the argmax (first index of the largest value,
+ * NaN largest), and returns the token and, when logits is not NULL, the
+ * vocab logits.  Create returns NULL on failure (tg_last_error() says why);
+ * forward returns 0 or a negative TG_E_* code. */
+typedef struct tg_head tg_head;
+tg_head *tg_head_create(const float *W, const float *norm_w, int vocab, int embed);
+int tg_head_forward(tg_head *h, const float *x, float eps, float *logits, int32_t *token);
+void tg_head_destroy(tg_head *h);
+
 #ifdef __cplusplus
 }
 #endif

@@ -379,6 +379,15 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return out
 
 
+def output_head(W: np.ndarray, norm_w: np.ndarray, x: np.ndarray, eps: float = 1e-6):
+    """(logits, greedy token) of tinygiant/engine.py:262-266,359: logits =
+    W @ rms_norm(x, norm_w) with the product in tg_f32_matvec's order
+    (libtinygiant.c:299-318), token = np.argmax(logits) (first index of the
+    largest value, NaN largest)."""
+    logits = matvec_f32(W, rms_norm(x, norm_w, eps))
+    return logits, int(np.argmax(logits))
+
+
 def expert_forward_mixed(gate, up, down, down_format, x, out, weight, embed, inter):
     lib().tgo_expert_forward_mixed(_p(gate), _p(up), _p(down), down_format,
                                    _p(np.ascontiguousarray(x, dtype=np.float32)), _p(out),

@@ -279,3 +279,45 @@ def test_transformer_layer(O, L):
     assert_exact(gx, rx, "transformer layer x")
     assert np.array_equal(gk.view(np.uint32), rk.view(np.uint32)), "key cache"
     assert np.array_equal(gv.view(np.uint32), rv.view(np.uint32)), "value cache"
+
+
+@pytest.mark.parametrize("vocab,embed,case", [(1000, 256, "plain"), (5003, 2048, "tie"), (4097, 1001, "nan"),
+                                              (151936, 2048, "plain")])
+def test_output_head(O, L, vocab, embed, case):
+    """tg_head_forward: logits bit-identical to the oracle's norm + fp32
+    matvec, token = numpy's argmax (ties to the first index, NaN largest)."""
+    gpu_note(f"tg_head_forward vocab={vocab} embed={embed} {case}")
+    rng = np.random.default_rng(vocab + embed)
+    W = rng.standard_normal((vocab, embed), dtype=np.float32) * np.float32(0.02)
+    nw = rng.normal(1.0, 0.1, embed).astype(np.float32)
+    x = rng.normal(0, 1, embed).astype(np.float32)
+    if case == "tie":
+        best = int(np.argmax(O.output_head(W, nw, x)[0]))
+        W[vocab - 1] = W[best]
+        W[3] = W[best]
+    elif case == "nan":
+        W[vocab // 2, 5] = np.nan
+        W[vocab - 2, 0] = np.nan
+    ref, ref_tok = O.output_head(W, nw, x, 1e-6)
+    h = L.tg_head_create(ptr(W), ptr(nw), vocab, embed)
+    assert h, L.tg_last_error()
+    try:
+        out = np.zeros(vocab, np.float32)
+        tok = ctypes.c_int32(-1)
+        assert L.tg_head_forward(h, ptr(x), 1e-6, ptr(out), ctypes.byref(tok)) == 0, L.tg_last_error()
+        if case == "nan":  # NaN rows: same positions; every other logit bit-identical
+            nan = np.isnan(ref)
+            assert np.array_equal(np.isnan(out), nan)
+            assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+        else:
+            assert_exact(out, ref, "logits")
+        assert tok.value == ref_tok
+        tok2 = ctypes.c_int32(-1)  # the token alone, logits not copied back
+        assert L.tg_head_forward(h, ptr(x), 1e-6, None, ctypes.byref(tok2)) == 0, L.tg_last_error()
+        assert tok2.value == ref_tok
+    finally:
+        L.tg_head_destroy(h)
+    if case == "tie":
+        assert ref_tok == 3
+    if case == "nan":
+        assert ref_tok == vocab // 2

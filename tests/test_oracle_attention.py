@@ -234,3 +234,28 @@ def test_transformer_layer_composition(O):
     assert np.array_equal(x_layer.view(np.uint32), xr.view(np.uint32))
     assert np.array_equal(kv_k.view(np.uint32), kk.view(np.uint32))
     assert np.array_equal(kv_v.view(np.uint32), vv.view(np.uint32))
+
+
+def test_output_head_oracle(O):
+    """The output head composes the pinned norm and matvec; its product
+    agrees with numpy's W @ x (the reference's own op, in BLAS order) to fp32
+    rounding, and its token is numpy's argmax of the same logits, ties to the
+    first index."""
+    rng = np.random.default_rng(11)
+    vocab, embed = 3001, 512
+    W = rng.normal(0, 0.02, (vocab, embed)).astype(np.float32)
+    nw = rng.normal(1, 0.1, embed).astype(np.float32)
+    x = rng.normal(0, 1, embed).astype(np.float32)
+    logits, tok = O.output_head(W, nw, x, 1e-6)
+    xn = O.rms_norm(x, nw, 1e-6)
+    ref = W.astype(np.float64) @ xn.astype(np.float64)
+    bound = 4 * embed * np.finfo(np.float32).eps * (np.abs(W).astype(np.float64) @ np.abs(xn).astype(np.float64))
+    assert np.all(np.abs(logits - ref) <= bound)
+    assert np.all(np.abs(logits - W @ xn) <= bound)
+    assert tok == int(np.argmax(logits))
+    # a tie: two rows equal to the best one, the first index wins
+    W2 = W.copy()
+    W2[7] = W2[tok]
+    W2[2900] = W2[tok]
+    _, tok2 = O.output_head(W2, nw, x, 1e-6)
+    assert tok2 == min(7, tok)

@@ -85,6 +85,9 @@ NEW_SYMBOLS = [
     ("tg_stream_read_dev", CI, [VP, SZ, CI, VP, VP]),
     ("tg_synth_normal_dev", CI, [U64, U64, CF, SZ, VP, VP]),
     ("tg_synth_q40_dev", CI, [U64, U64, CF, CI, CI, VP, VP]),
+    ("tg_head_create", VP, [VP, VP, CI, CI]),
+    ("tg_head_forward", CI, [VP, VP, CF, VP, VP]),
+    ("tg_head_destroy", None, [VP]),
 ]
 
 ALL_SYMBOLS = LEGACY_SYMBOLS + UNREGISTERED_SYMBOLS + NEW_SYMBOLS

@@ -1551,3 +1551,74 @@ extern "C" void tg_transformer_layer(const float *wq, const float *wk, const flo
     }
 }
 
+
+// ------------------------------------------------------------- output head
+// The step after the layers (engine.py:262-266,359): logits = W ·
+// rms_norm(x, output_norm) with W [vocab][embed] fp32, then the greedy token
+// argmax(logits).  The reference keeps W in a numpy array and multiplies with
+// `@`; here W stays resident in HBM behind a handle, the product follows the
+// reference's own fp32 matvec order (tg_f32_matvec, libtinygiant.c:299-318)
+// and the norm tg_rms_norm's (:322-340).
+struct tg_head {
+    int vocab, embed, dev;
+    float *W, *nw, *x, *xn, *logits, *pv;
+    int *pi, *tok;
+};
+
+static void head_free(tg_head *h) {
+    if (!h) return;
+    for (void *p : {(void *)h->W, (void *)h->nw, (void *)h->x, (void *)h->xn, (void *)h->logits, (void *)h->pv,
+                    (void *)h->pi, (void *)h->tok})
+        if (p) (void)hipFree(p);
+    delete h;
+}
+
+extern "C" tg_head *tg_head_create(const float *W, const float *norm_w, int vocab, int embed) {
+    if (!W || !norm_w || vocab <= 0 || embed <= 0) {
+        set_err(TG_E_INVALID, "tg_head_create: vocab %d, embed %d", vocab, embed);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (lg_reserve(0)) return nullptr;
+    tg_head *h = new tg_head{vocab, embed, g_lg_dev, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             nullptr};
+    const size_t wb = sizeof(float) * (size_t)vocab * embed, eb = sizeof(float) * (size_t)embed;
+    auto alloc = [&](void **p, size_t n) { return hipMalloc(p, n) == hipSuccess; };
+    if (!alloc((void **)&h->W, wb) || !alloc((void **)&h->nw, eb) || !alloc((void **)&h->x, eb) ||
+        !alloc((void **)&h->xn, eb) || !alloc((void **)&h->logits, sizeof(float) * (size_t)vocab) ||
+        !alloc((void **)&h->pv, sizeof(float) * tg::ARGMAX_BLOCKS) ||
+        !alloc((void **)&h->pi, sizeof(int) * tg::ARGMAX_BLOCKS) || !alloc((void **)&h->tok, sizeof(int))) {
+        (void)hipGetLastError();
+        head_free(h);
+        set_err(TG_E_NOMEM, "tg_head_create: %zu bytes of output weights", wb);
+        return nullptr;
+    }
+    if (hipMemcpy(h->W, W, wb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(h->nw, norm_w, eb, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        head_free(h);
+        set_err(TG_E_HIP, "tg_head_create: copy of the output weights failed");
+        return nullptr;
+    }
+    return h;
+}
+
+extern "C" void tg_head_destroy(tg_head *h) { head_free(h); }
+
+// x (embed floats, host) -> logits (vocab floats, host; may be null) and the
+// greedy token.  Returns 0 or a negative TG_E_* code.
+extern "C" int tg_head_forward(tg_head *h, const float *x, float eps, float *logits, int32_t *token) {
+    if (!h || !x || !token) return set_err(TG_E_INVALID, "tg_head_forward: null handle, input or token");
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    int rc = lg_reserve(0);
+    if (rc) return rc;
+    if (g_lg_dev != h->dev) return set_err(TG_E_INVALID, "tg_head_forward: handle of device %d", h->dev);
+    hipStream_t st = g_lg_st;
+    const size_t eb = sizeof(float) * (size_t)h->embed;
+    if ((rc = lg_h2d(h->x, x, eb))) return rc;
+    PROFILED("head_rms", st, tg::launch_rms_norm(h->x, h->nw, h->xn, h->embed, eps, st));
+    PROFILED("head_mv", st, tg::launch_matvec_two_acc(h->W, false, h->xn, h->logits, h->vocab, h->embed, st));
+    PROFILED("head_argmax", st, tg::launch_argmax(h->logits, h->vocab, h->pv, h->pi, h->tok, st));
+    if (logits) HIP_TRY(hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)h->vocab, hipMemcpyDeviceToHost, st));
+    return lg_finish(token, h->tok, sizeof(int32_t));
+}

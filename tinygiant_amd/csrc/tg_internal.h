@@ -156,6 +156,10 @@ hipError_t launch_attn_softmax(float *scr, int n_heads, int seq, hipStream_t st)
 hipError_t launch_attn_wv(const float *scr, const float *vc, float *out, int n_heads, int seq, int hd, int ratio,
                           hipStream_t st);
 hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st);
+// first index of the largest of x[0..n) (NaN largest) into out[0]; pv / pi
+// hold ARGMAX_BLOCKS partials
+constexpr int ARGMAX_BLOCKS = 256;
+hipError_t launch_argmax(const float *x, int n, float *pv, int *pi, int *out, hipStream_t st);
 
 // One-token layer with routing inside (k_layer_dec) and the prologue that
 // forms the first layer's router partials (k_dec_part).  part buffers hold

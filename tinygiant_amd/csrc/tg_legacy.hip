@@ -763,6 +763,57 @@ __global__ __launch_bounds__(256) void k_add_vec(float *__restrict__ x, const fl
     if (i < n) x[i] = x[i] + a[i];
 }
 
+// ----------------------------------------------------------------- argmax
+// Greedy next token (engine.py:359, np.argmax): the first index of the
+// largest value, NaN above every number (numpy returns the first NaN).
+// Blocks reduce grid-strided slices to (value, index) partials; one block
+// reduces the partials in index order of the slices.
+TG_DEV bool am_better(float av, int ai, float bv, int bi) {
+    const bool an = av != av, bn = bv != bv;
+    if (an || bn) return an && (!bn || ai < bi);
+    return av > bv || (av == bv && ai < bi);
+}
+
+TG_DEV void am_block(float &v, int &i) {
+    __shared__ float sv[256 / WAVE];
+    __shared__ int si[256 / WAVE];
+#pragma unroll
+    for (int s = 1; s < WAVE; s <<= 1) {
+        const float ov = __shfl_xor(v, s, WAVE);
+        const int oi = __shfl_xor(i, s, WAVE);
+        if (am_better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+    const int tid = threadIdx.x;
+    if ((tid & (WAVE - 1)) == 0) { sv[tid / WAVE] = v; si[tid / WAVE] = i; }
+    __syncthreads();
+    v = sv[0]; i = si[0];
+#pragma unroll
+    for (int w = 1; w < 256 / WAVE; w++)
+        if (am_better(sv[w], si[w], v, i)) { v = sv[w]; i = si[w]; }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ x, int n, float *__restrict__ pv,
+                                                     int *__restrict__ pi) {
+    float v = x[0];
+    int i = 0;
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+        const float xv = x[j];
+        if (am_better(xv, j, v, i)) { v = xv; i = j; }
+    }
+    am_block(v, i);
+    if (threadIdx.x == 0) { pv[blockIdx.x] = v; pi[blockIdx.x] = i; }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(const float *__restrict__ pv, const int *__restrict__ pi, int nb,
+                                                      int *__restrict__ out) {
+    float v = pv[0];
+    int i = pi[0];
+    for (int b = threadIdx.x; b < nb; b += 256)
+        if (am_better(pv[b], pi[b], v, i)) { v = pv[b]; i = pi[b]; }
+    am_block(v, i);
+    if (threadIdx.x == 0) out[0] = i;
+}
+
 // ------------------------------------------------------------- launchers
 static unsigned lg_cdiv(long n, long d) { return (unsigned)((n + d - 1) / d); }
 
@@ -866,6 +917,14 @@ hipError_t launch_attn_wv(const float *scr, const float *vc, float *out, int n_h
         TG_LAUNCH(k_attn_wv<true>, grid, dim3(128), 0, st, scr, vc, out, seq, hd, ratio, ngrp, woff);
     else
         TG_LAUNCH(k_attn_wv<false>, grid, dim3(128), 0, st, scr, vc, out, seq, hd, ratio, ngrp, woff);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *x, int n, float *pv, int *pi, int *out, hipStream_t st) {
+    if (n <= 0) return hipErrorInvalidValue;
+    const int nb = (int)std::min<long>(ARGMAX_BLOCKS, (long)lg_cdiv(n, 256));
+    TG_LAUNCH(k_argmax_part, dim3(nb), dim3(256), 0, st, x, n, pv, pi);
+    TG_LAUNCH(k_argmax_final, dim3(1), dim3(256), 0, st, pv, pi, nb, out);
     return hipGetLastError();
 }
 
