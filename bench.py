@@ -6,8 +6,12 @@ MoE stack, 48 layers of H=2048, I=768, 128 Q4_0 experts, top-8 with
 renormalised softmax, decode batch 1.  One step = one token through all 48
 layers (x <- x + MoE_l(rms_norm(x))).  Weights are synthetic N(0, 0.02)
 quantized to Q4_0 (16.3 GB resident in HBM) with fp32 N(0, 0.02) routers;
-every step uses a fresh N(0, 1) token.  The timed region starts with all
-inputs in HBM.
+every step copies a fresh N(0, 1) token into the stack's hidden-state
+buffer and replays the stack's HIP graph.  The timed region starts with all
+inputs in HBM.  The same line carries a "prefill" object: 2048 tokens through
+the same 48-layer stack on the grouped int8-MFMA path (BASELINE's second
+half: int8 TOPS against the MFMA peak), with its own roofline and CPU
+baseline.  Step times are also reported as the median of the timed steps.
 
 Other workloads (--workload):
   batched      one layer per step, 64 tokens per step, router skewed so that
@@ -52,7 +56,7 @@ H, I, E, K_TOP = 2048, 768, 128, 8
 HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
 EXPERT_Q4_BYTES = 3 * I * (H // 32) * 18          # 2,654,208
 ROUTER_BYTES = E * H * 4                           # 1,048,576 (fp32 router of one layer)
-DECODE_PATHS = {"auto": 0, "persistent": 1, "per-layer": 2, "fused": 3, "routed": 4}
+DECODE_PATHS = {"auto": 0, "per-layer": 2, "fused": 3, "routed": 4}
 GATEUP_BYTES_PER_EXPERT = 2 * I * (H // 32) * 18  # 1,769,472
 
 
@@ -100,6 +104,41 @@ def kernel_times(call, names):
     return out
 
 
+def step_stats(events):
+    """Median / min / max step time (ms) from HIP events recorded before each
+    step and after the last one, on the stream the steps run on."""
+    ms = np.array([events[i].elapsed_time(events[i + 1]) for i in range(len(events) - 1)])
+    return {"median": round(float(np.median(ms)), 4), "min": round(float(ms.min()), 4),
+            "max": round(float(ms.max()), 4), "n": int(ms.size)}
+
+
+def host_copy_gbps(threads, nbytes=1 << 30, reps=5):
+    """STREAM-style copy on this host's cores: dst[:] = src[:] over nbytes,
+    split over `threads` threads (numpy releases the GIL for the copy);
+    bytes read + written per second, best of `reps`."""
+    from concurrent.futures import ThreadPoolExecutor
+    src = np.ones(nbytes // 4, np.float32)
+    dst = np.zeros_like(src)
+    cuts = np.linspace(0, src.size, threads + 1).astype(np.int64)
+    parts = [(int(cuts[i]), int(cuts[i + 1])) for i in range(threads)]
+    best = float("inf")
+    with ThreadPoolExecutor(threads) as ex:
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            list(ex.map(lambda ab: np.copyto(dst[ab[0]:ab[1]], src[ab[0]:ab[1]]), parts))
+            best = min(best, time.perf_counter() - t0)
+    return 2 * nbytes / best / 1e9
+
+
+def cpu_roofline(value_gbps, cores):
+    """The CPU baseline's expert-byte rate against this host's copy rate."""
+    copy_n = host_copy_gbps(cores)
+    copy_1 = host_copy_gbps(1)
+    return {"expert_gbps": round(value_gbps, 2), "host_copy_gbps": round(copy_n, 1),
+            "host_copy_gbps_1thread": round(copy_1, 1), "frac": round(value_gbps / copy_n, 4),
+            "note": "STREAM-style copy (read + write bytes) on the same cores"}
+
+
 # ----------------------------------------------------------------- CPU legs
 
 def cpu_baseline_stack(arena, seed, n_layers_total, seconds, gpu_check, shape=(H, I, E, K_TOP), n_sample=4):
@@ -131,8 +170,10 @@ def cpu_baseline_stack(arena, seed, n_layers_total, seconds, gpu_check, shape=(H
     O.set_threads(cores)
     v1, tok1, dt1 = res[1]
     vn, tokn, dtn = res[cores]
+    EBt = 3 * I * (H // 32) * 18
     return {
         "value": round(vn, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+        "roofline": cpu_roofline(vn * n_layers_total * K_TOP * EBt / 1e9, cores),
         "sample": (f"C oracle, {tokn} tokens x {n_s} of {n_layers_total} layers "
                    f"({dtn:.1f} s, {cores} OpenMP threads), per-layer time extrapolated to "
                    f"{n_layers_total} layers"),
@@ -197,24 +238,30 @@ def run_decode_stack(args, torch, call):
     X = torch.empty((W + K, H), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
     X0 = X.clone()
+    xt = torch.empty((1, H), dtype=torch.float32, device="cuda")  # the token's hidden state
     torch.cuda.synchronize()
     blk = MoEBlock(arena)
 
+    # every step copies its token into the same buffer, so the stack call
+    # replays the one HIP graph captured in the warmup
     log(f"warmup {W} tokens")
     for i in range(W):
-        blk.step(X[i:i + 1])
+        xt.copy_(X[i:i + 1])
+        blk.step(xt)
     torch.cuda.synchronize()
     log(f"timing {K} tokens x {L} layers")
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0.record()
     for i in range(W, W + K):
-        blk.step(X[i:i + 1])
-    ev1.record()
+        evs[i - W].record()
+        xt.copy_(X[i:i + 1])
+        blk.step(xt)
+    evs[K].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     arena.status()
+    steps_ms = step_stats(evs)
     ms_step = wall * 1e3 / K
     tok_s = K / wall
     bytes_per_tok = L * K_TOP * EXPERT_Q4_BYTES
@@ -226,11 +273,12 @@ def run_decode_stack(args, torch, call):
     torch.cuda.synchronize()
     call("tg_prof_enable", 1)
     for i in range(W, W + K):
-        blk.step(X[i:i + 1])
+        xt.copy_(X[i:i + 1])
+        blk.step(xt)
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     arena.status()
-    kern = kernel_times(call, ("persist", "dec_part", "layer", "route", "experts", "gateup", "down"))
+    kern = kernel_times(call, ("dec_part", "layer", "route", "experts", "gateup", "down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     if "layer" in kern:
         # one launch = routing, gate/up and down of one layer (expert weights
@@ -239,12 +287,6 @@ def run_decode_stack(args, torch, call):
         avg = ms_x / max(n_x, 1) * 1e-3
         roof_kernel, roof_bytes = "k_layer_dec", K_TOP * EXPERT_Q4_BYTES + ROUTER_BYTES
         path = "routed"
-    elif "persist" in kern:
-        # one launch = one token through all L layers
-        n_p, ms_p = kern["persist"]
-        avg = ms_p / n_p * 1e-3
-        roof_kernel, roof_bytes = "k_persist", L * K_TOP * EXPERT_Q4_BYTES
-        path = "persistent"
     elif "experts" in kern:
         # one launch = gate/up and down of the token's k experts in one layer
         n_x, ms_x = kern["experts"]
@@ -269,6 +311,11 @@ def run_decode_stack(args, torch, call):
         torch.cuda.synchronize()
         cpu = cpu_baseline_stack(arena, args.seed, L, args.cpu_seconds, (xt, xg.cpu().numpy()))
 
+    prefill = None
+    if not args.no_prefill:
+        log("prefill leg: 2048 tokens through the same stack")
+        prefill = prefill_leg(args, torch, call, arena, L, K=20, W=2)
+
     out = {
         "metric": "MoE-layer decode tok/s (48-layer Q4_0 stack, batch 1)",
         "value": round(tok_s, 2),
@@ -286,13 +333,15 @@ def run_decode_stack(args, torch, call):
                    "experts": E, "moe_intermediate": I, "top_k": K_TOP, "batch": 1, "tokens": K},
         "hbm_gbps_expert_weights": round(gbps, 1),
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
-        "event_ms_per_step": round(ev0.elapsed_time(ev1) / K, 4),
+        "event_ms_per_step": round(evs[0].elapsed_time(evs[K]) / K, 4),
+        "step_ms": steps_ms,
         "kernel_avg_us": kern_us,
         "decode_path": path,
         "roofline": {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(roof_kernel)},
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     arena.close()
     return out
@@ -580,42 +629,48 @@ def run_235b(args, torch, call, T):
 MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA, ops/s
 
 
-def run_prefill(args, torch, call):
-    """Config 4: 2048 tokens through the 48-layer stack on the grouped int8
-    MFMA path (uniform-ish routing from the N(0, 0.02) routers)."""
-    from tinygiant_amd.arena import HBMExpertArena
+def prefill_leg(args, torch, call, arena, L, K=20, W=2):
+    """Config 4 on an arena that holds L synthetic 30B layers: 2048 tokens
+    through the stack on the grouped int8-MFMA path (routing uniform-ish from
+    the N(0, 0.02) routers).  Returns the prefill object of the bench line:
+    int8 TOPS (median step), the MFMA fraction, the roofline of the gate/up
+    MFMA kernel and the CPU oracle on a one-layer sample."""
     from tinygiant_amd.moe import MoEBlock
     from tinygiant_amd.synth import stream_id
 
-    T, L = 2048, args.layers
-    K, W = args.steps or 5, 1 if args.warmup is None else args.warmup
+    T = 2048
     ops_layer = 2 * T * K_TOP * 3 * H * I  # 154,618,822,656
-    log(f"arena: {L} layers x {E} experts ({L * E * EXPERT_Q4_BYTES / 1e9:.2f} GB Q4_0)")
-    arena = HBMExpertArena(L, E, H, I, K_TOP)
-    for l in range(L):
-        arena.synth_layer(l, args.seed)
     arena.set_batch_path(arena.BATCH_GROUPED)
     stream = torch.cuda.current_stream().cuda_stream
     X = torch.empty((W + K, T, H), dtype=torch.float32, device="cuda")
-    call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
+    call("tg_synth_normal_dev", args.seed, stream_id(0, 1, 4), 1.0, X.numel(), X.data_ptr(), stream)
+    xb = torch.empty((T, H), dtype=torch.float32, device="cuda")  # the batch's hidden states
     torch.cuda.synchronize()
     blk = MoEBlock(arena)
     log(f"warmup {W} prefills")
     for i in range(W):
-        blk.step(X[i])
+        xb.copy_(X[i])
+        blk.step(xb)
     torch.cuda.synchronize()
     log(f"timing {K} prefills of {T} tokens x {L} layers")
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
     t0 = time.perf_counter()
     for i in range(W, W + K):
-        blk.step(X[i])
+        evs[i - W].record()
+        xb.copy_(X[i])
+        blk.step(xb)
+    evs[K].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = wall * 1e3 / K
-    tops = ops_layer * L / (wall / K) / 1e12
+    steps_ms = step_stats(evs)
+    tops_mean = ops_layer * L / (wall / K) / 1e12
+    tops = ops_layer * L / (steps_ms["median"] * 1e-3) / 1e12
 
     log("kernel timing pass")
     call("tg_prof_enable", 1)
-    blk.step(X[W])
+    for i in range(W, W + min(K, 4)):
+        xb.copy_(X[i])
+        blk.step(xb)
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "combine")
@@ -624,44 +679,60 @@ def run_prefill(args, torch, call):
     n_gu, ms_gu = kern["gateup_mfma"]
     gu_ops = 2 * T * K_TOP * 2 * H * I
     achieved = gu_ops / (ms_gu / n_gu * 1e-3)
+    layer_us = sum(kern_us.values())
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (oracle)")
-        from oracle import oracle as O
+        log("prefill cpu baseline (oracle, one layer, 64 tokens)")
+        from oracle import oracle as O  # the checker, timed as the CPU baseline
         lb = arena.read_layer(0)
         router = O.synth_normal(args.seed, O.stream_id(0, 0, 3), 0.02, E * H).reshape(E, H)
         Xs = X[W][:64].cpu().numpy()
         out = blk.forward(0, X[W][:64].contiguous())
-        c = cpu_baseline_layer(lb, router, [Xs], args.cpu_seconds, (Xs, out.cpu().numpy()))
+        c = cpu_baseline_layer(lb, router, [Xs], args.cpu_seconds / 2, (Xs, out.cpu().numpy()))
         c["value_int_ops"] = round(c["value"] * 2 * K_TOP * 3 * H * I / 1e12, 4)
         c["unit_int_ops"] = "TOPS"
         cpu = c
 
+    arena.set_batch_path(arena.BATCH_AUTO)
     return {
         "metric": "MoE prefill int8 TOPS (2048 tokens x 48-layer Q4_0 stack, grouped int8 MFMA)",
-        "value": round(tops, 2),
-        "unit": "TOPS",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(ms_step, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "value": round(tops, 2), "unit": "TOPS", "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 3), "step_ms": steps_ms, "value_mean_steps": round(tops_mean, 2),
         "dtype": "q4_0 x q8_0 (int8 MFMA, fp32 accumulate)",
-        "data": "synthetic (N(0,0.02) Q4_0 experts and fp32 routers, N(0,1) tokens)",
         "config": {"workload": "qwen3-30b-a3b-moe-prefill", "tokens": T, "layers": L, "hidden": H,
                    "experts": E, "moe_intermediate": I, "top_k": K_TOP, "ops_per_layer": ops_layer,
-                   "us_per_layer": round(ms_step * 1e3 / L, 2)},
+                   "us_per_layer": round(steps_ms["median"] * 1e3 / L, 2)},
         "mfma_frac": round(tops * 1e12 / MFMA_INT8_PEAK, 4),
         "kernel_avg_us": kern_us,
+        "layer_kernel_us": round(layer_us, 2),
         "roofline": {"bound": "mfma", "kernel": "k_mfma_grouped (gate/up)", "ops_per_launch": gu_ops,
                      "achieved": round(achieved / 1e12, 1), "peak": MFMA_INT8_PEAK / 1e12, "unit": "TOPS",
                      "frac": round(achieved / MFMA_INT8_PEAK, 4),
                      "traffic": profiled_traffic("k_mfma_grouped/gate_up")},
         "cpu_baseline": cpu,
     }
+
+
+def run_prefill(args, torch, call):
+    """Config 4 alone: 2048 tokens through the 48-layer stack."""
+    from tinygiant_amd.arena import HBMExpertArena
+
+    L = args.layers
+    K, W = args.steps or 20, 2 if args.warmup is None else args.warmup
+    log(f"arena: {L} layers x {E} experts ({L * E * EXPERT_Q4_BYTES / 1e9:.2f} GB Q4_0)")
+    arena = HBMExpertArena(L, E, H, I, K_TOP)
+    for l in range(L):
+        arena.synth_layer(l, args.seed)
+    p = prefill_leg(args, torch, call, arena, L, K=K, W=W)
+    arena.close()
+    out = {"metric": p.pop("metric"), "value": p.pop("value"), "unit": p.pop("unit"), "n_gpus": 1,
+           "steps": p.pop("steps"), "warmup": p.pop("warmup"), "ms_per_step": p.pop("ms_per_step"),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": p.pop("dtype"),
+           "data": "synthetic (N(0,0.02) Q4_0 experts and fp32 routers, N(0,1) tokens)",
+           "config": p.pop("config")}
+    out.update(p)
+    return out
 
 
 def q4k_blocks(rng, n):
@@ -978,6 +1049,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="default workload: skip the prefill leg")
     ap.add_argument("--path", choices=list(DECODE_PATHS), default="auto",
                     help="decode path of one-token stack calls")
     args = ap.parse_args()

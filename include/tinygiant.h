@@ -142,9 +142,13 @@ void tg_matmul_q4k_scalar(const uint8_t *q4_matrix, const float *input,
 /* ------------------------------------------------------------------ */
 typedef struct tg_arena tg_arena;
 
-/* Reserve device memory for n_layers layers of n_experts Q4_0 experts
- * (embed_dim = H, inter_dim = I, both multiples of 32) plus one fp32 router
- * [n_experts x H] per layer.  Returns NULL on error (see tg_last_error).
+/* Reserve device memory for n_layers layers of n_experts Q4_0 experts plus
+ * one fp32 router [n_experts x H] and one fp32 FFN norm weight [H] (all ones
+ * until tg_arena_load_norm) per layer.  embed_dim = H must be a multiple of
+ * 256 and inter_dim = I a multiple of 32, both at most 8192; n_experts a
+ * multiple of 4 up to 252; top_k in 1..min(32, n_experts); the kernels'
+ * LDS limits can refuse a shape within these bounds, and the error message
+ * then says so.  Returns NULL on error (see tg_last_error).
  * Role: tinygiant/cache.py:14-57 (ExpertCache over index.json). */
 tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim,
                           int inter_dim, int top_k);
@@ -163,6 +167,13 @@ int tg_arena_load_layer(tg_arena *a, int layer, const void *host_bytes,
 /* Upload one layer's fp32 router [n_experts x H] (host memory). */
 int tg_arena_load_router(tg_arena *a, int layer, const float *host_router,
                          size_t count);
+/* Upload one layer's FFN norm weight [H] (host memory): the MoE block of
+ * that layer runs on rms_norm(x) * w, as engine.py:229-230 does with
+ * ffn_norms[i] (tg_rms_norm, csrc/libtinygiant.c:322-340).  The router is
+ * applied as s * ((router * w) . x), the norm weight folded into the
+ * router's columns once, here and in tg_arena_load_router. */
+int tg_arena_load_norm(tg_arena *a, int layer, const float *host_norm,
+                       size_t count);
 /* Read one layer back in the relayout layout (host memory). */
 int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes,
                         size_t nbytes);
@@ -175,10 +186,10 @@ int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float sigma);
 /* MoE block: norm -> router -> top-k -> experts -> combine             */
 /* (engine.py:229-258 with Q4_0 experts)                                */
 /* ------------------------------------------------------------------ */
-/* For each of n_tokens tokens x[t] (fp32, H): xn = x / rms(x) (eps),
- * logits = router xn, top-k with renormalised softmax, moe_out[t] =
- * sum_j w_j * expert_j(Q8_0(xn)).  topk_idx / topk_w ([n_tokens x k],
- * descending logit) may be NULL. */
+/* For each of n_tokens tokens x[t] (fp32, H): xn = (x / rms(x)) * g (eps;
+ * g the layer's norm weight), logits = router xn, top-k with renormalised
+ * softmax, moe_out[t] = sum_j w_j * expert_j(Q8_0(xn)).  topk_idx / topk_w
+ * ([n_tokens x k], descending logit) may be NULL. */
 int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x,
                          float *moe_out, int n_tokens, int32_t *topk_idx,
                          float *topk_w, float eps, void *stream);
@@ -200,12 +211,19 @@ int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
  * routes, from router partial sums the layer before it leaves; stack
  * calls add one small prologue launch and replay as a HIP graph), FUSED
  * (per layer a routing kernel and one launch for gate/up and down),
- * PER_LAYER (routing, gate/up and down as three kernels per layer),
- * PERSISTENT (one cooperative launch over every layer of a stack call;
- * error when the shape / device does not allow it), AUTO (ROUTED where
- * the shape allows it, else FUSED, else PER_LAYER). */
+ * PER_LAYER (routing, gate/up and down as three kernels per layer), AUTO
+ * (ROUTED where the shape allows it, else FUSED, else PER_LAYER).  Value 1
+ * is not a path (TG_E_INVALID).
+ *
+ * The ROUTED and FUSED launches hand data between their own blocks through
+ * device memory (bounded polls), so they need every block of the launch
+ * resident at once: H / rd blocks of 1024 threads, rd the smallest row
+ * count that keeps the grid within the device's CUs (one block per CU).  Work that another stream
+ * keeps on the same device can hold CUs for the whole launch; the polls then
+ * run out of tries, the affected rows come back NaN and tg_arena_status()
+ * reports the failure.  Run nothing else on the device beside these
+ * launches. */
 #define TG_DECODE_AUTO 0
-#define TG_DECODE_PERSISTENT 1
 #define TG_DECODE_PER_LAYER 2
 #define TG_DECODE_FUSED 3
 #define TG_DECODE_ROUTED 4
@@ -222,20 +240,9 @@ int tg_arena_set_decode_path(tg_arena *a, int path);
 #define TG_BATCH_PER_TOKEN 2
 #define TG_BATCH_GROUPED_DOT 3
 int tg_arena_set_batch_path(tg_arena *a, int path);
-/* Timeline of the persistent decode kernel (tracing): while set, every
- * persistent launch writes wall-clock stamps [n_layers][blocks][8] into
- * dev_words (device memory, at least the size tg_timeline_info gives):
- * per block and layer, slot 0 layer start, 1 routing known / expert ids
- * received, 2 Q8_0 x published / received, 3 h block published, 4 down
- * loads issued, 5 h received, 6 next layer's partials published (unset
- * slots keep their contents).  n_words = 0 switches it off.  The clock
- * runs at clock_khz kHz. */
-int tg_arena_set_timeline(tg_arena *a, uint64_t *dev_words, size_t n_words);
-int tg_timeline_info(const tg_arena *a, int n_layers, size_t *n_words,
-                     int *blocks, int *clock_khz);
 /* Waits for the device and reports a device-side failure of an earlier
- * asynchronous call on this arena (a persistent-kernel wait that ran out of
- * tries). */
+ * asynchronous call on this arena (a hand-off poll of the ROUTED or FUSED
+ * launch that ran out of tries). */
 int tg_arena_status(tg_arena *a);
 
 /* ------------------------------------------------------------------ */

@@ -72,8 +72,9 @@ def lib():
             "tgo_topk_softmax": (None, [_P, _I, _I, _P, _P]),
             "tgo_silu_mul": (_F, [_F, _F]),
             "tgo_expert_q40": (None, [_P, _I, _I, _P, _P, _P, _P, _P, _P]),
-            "tgo_moe_layer_q40": (None, [_P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P, _P, _P]),
-            "tgo_moe_stack_q40": (None, [_P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P]),
+            "tgo_router_dot_g": (_F, [_P, _P, _P, _I]),
+            "tgo_moe_layer_q40": (None, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P, _P, _P]),
+            "tgo_moe_stack_q40": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P]),
             "tgo_group_by_expert": (_I, [_P, _I, _I, _I, _P, _P, _P]),
             "tgo_quantize_q8k": (None, [_P, _P, _I]),
             "tgo_scale_min_k4": (None, [_I, _P, _P, _P]),
@@ -281,29 +282,48 @@ def expert(ex: np.ndarray, H: int, I: int, xq: np.ndarray):
     return dict(gate=g, up=u, h=h, hq=hq, down=d)
 
 
+def router_dot_g(w: np.ndarray, g, x: np.ndarray) -> float:
+    """Grouped dot (w * g) . x, the norm weight folded into the router column."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if g is None:
+        return lib().tgo_router_dot_g(_p(w), None, _p(x), w.size)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    return lib().tgo_router_dot_g(_p(w), _p(g), _p(x), w.size)
+
+
 def moe_layer(layer: np.ndarray, Wr: np.ndarray, H: int, I: int, E: int, k: int,
-              x: np.ndarray, eps: float = 1e-6):
+              x: np.ndarray, eps: float = 1e-6, norm=None):
+    """One MoE block over the rows of x; norm is the FFN norm weight (None: unit)."""
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, H)
     T = x.shape[0]
     out = np.empty((T, H), np.float32)
     idx = np.empty((T, k), np.int32)
     w = np.empty((T, k), np.float32)
     xq = np.empty((T, H // QK * Q80_BYTES), np.uint8)
+    g = None if norm is None else np.ascontiguousarray(norm, dtype=np.float32).reshape(H)
     lib().tgo_moe_layer_q40(_p(np.ascontiguousarray(layer)), _p(np.ascontiguousarray(Wr, dtype=np.float32)),
-                            H, I, E, k, eps, _p(x), T, _p(out), _p(idx), _p(w), _p(xq))
+                            None if g is None else _p(g), H, I, E, k, eps, _p(x), T, _p(out), _p(idx), _p(w),
+                            _p(xq))
     return out, idx, w, xq
 
 
-def moe_stack(layers, routers, H: int, I: int, E: int, k: int, x: np.ndarray, eps: float = 1e-6):
-    """x <- x + MoE_l(x) over the layers; returns (x, idx_trace)."""
+def moe_stack(layers, routers, H: int, I: int, E: int, k: int, x: np.ndarray, eps: float = 1e-6, norms=None):
+    """x <- x + MoE_l(x) over the layers; returns (x, idx_trace).  norms:
+    per-layer FFN norm weights (None: unit)."""
     n = len(layers)
     x = np.array(x, dtype=np.float32, copy=True).reshape(-1, H)
     T = x.shape[0]
     keep = [np.ascontiguousarray(a) for a in layers] + [np.ascontiguousarray(r, dtype=np.float32) for r in routers]
     lp = (ctypes.c_void_p * n)(*[_p(a) for a in keep[:n]])
     rp = (ctypes.c_void_p * n)(*[_p(a) for a in keep[n:]])
+    npp = None
+    if norms is not None:
+        keep += [np.ascontiguousarray(g, dtype=np.float32).reshape(H) for g in norms]
+        npp = (ctypes.c_void_p * n)(*[_p(a) for a in keep[2 * n:]])
     trace = np.empty((n, T, k), np.int32)
     lib().tgo_moe_stack_q40(ctypes.cast(lp, ctypes.c_void_p), ctypes.cast(rp, ctypes.c_void_p),
+                            None if npp is None else ctypes.cast(npp, ctypes.c_void_p),
                             n, H, I, E, k, eps, _p(x), T, _p(trace))
     return x, trace
 

@@ -437,6 +437,26 @@ void tgo_router_logits(const float *Wr, int E, int H, const float *x, float s,
     for (int e = 0; e < E; e++) logits[e] = tgo_router_dot(Wr + (size_t)e * H, x, H) * s;
 }
 
+/* Router over rms_norm(x) * g (engine.py:229-231 with ffn_norms[i]):
+ * routers @ ((x * s) * g) evaluated as s * ((w * g) . x), the norm weight
+ * folded into each router column with one rounding (w[i] * g[i]) and the
+ * dot in the grouped order of tgo_router_dot.  g = NULL is the unit
+ * weight.  Pinned by tests/test_oracle_math.py::test_norm_weight_*. */
+float tgo_router_dot_g(const float *w, const float *g, const float *x, int n) {
+    if (!g) return tgo_router_dot(w, x, n);
+    float tot = 0.0f;
+    for (int gi = 0; gi < n / 32; gi++) {
+        float a = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            const int j = 32 * gi + i;
+            const float wg = w[j] * g[j];
+            a = fmaf(wg, x[j], a);
+        }
+        tot = tot + a;
+    }
+    return tot;
+}
+
 /* numpy's pairwise float32 sum (np.sum as used at engine.py:236) for the
  * short arrays that occur here (n <= 128). */
 static float np_pairwise_sum(const float *a, int n) {
@@ -526,14 +546,16 @@ void tgo_expert_q40(const uint8_t *expert, int H, int I, const uint8_t *xq,
 }
 
 /* One MoE block for n_tokens independent tokens (engine.py:229-258 with
- * Q4_0 experts): xn = x / rms(x) (unit weight, eps), logits = Wr xn,
- * top-k + softmax, Q8_0(xn), the k experts, moe_out = sum_j w_j down_j in
- * ascending logit order.  Work is split over rows so the result does not
- * depend on the thread count.  idx/w/xq_out may be NULL. */
-void tgo_moe_layer_q40(const uint8_t *layer, const float *Wr, int H, int I,
-                       int E, int k, float eps, const float *x, int n_tokens,
-                       float *moe_out, int32_t *idx_out, float *w_out,
-                       uint8_t *xq_out) {
+ * Q4_0 experts): xn = (x * s) * g with s = 1 / rms(x) (eps) and g the FFN
+ * norm weight (tg_rms_norm's order, libtinygiant.c:332-339; g = NULL is
+ * the unit weight), logits = Wr xn (tgo_router_dot_g), top-k + softmax,
+ * Q8_0(xn), the k experts, moe_out = sum_j w_j down_j in ascending logit
+ * order.  Work is split over rows so the result does not depend on the
+ * thread count.  idx/w/xq_out may be NULL. */
+void tgo_moe_layer_q40(const uint8_t *layer, const float *Wr, const float *g,
+                       int H, int I, int E, int k, float eps, const float *x,
+                       int n_tokens, float *moe_out, int32_t *idx_out,
+                       float *w_out, uint8_t *xq_out) {
     int nbh = H / TGO_QK, nbi = I / TGO_QK;
     size_t gate_bytes = (size_t)I * nbh * TGO_Q40_BYTES;
     size_t down_bytes = (size_t)H * nbi * TGO_Q40_BYTES;
@@ -549,8 +571,11 @@ void tgo_moe_layer_q40(const uint8_t *layer, const float *Wr, int H, int I,
     for (int t = 0; t < n_tokens; t++) {
         const float *xt = x + (size_t)t * H;
         float s = tgo_rms_scale(xt, H, eps);
-        for (int i = 0; i < H; i++) xn[i] = xt[i] * s;
-        tgo_router_logits(Wr, E, H, xt, s, logits);
+        for (int i = 0; i < H; i++) {
+            const float v = xt[i] * s;
+            xn[i] = g ? v * g[i] : v;
+        }
+        for (int e = 0; e < E; e++) logits[e] = tgo_router_dot_g(Wr + (size_t)e * H, g, xt, H) * s;
         tgo_topk_softmax(logits, E, k, idx, w);
         tgo_quantize_q8_0(xn, (size_t)H, xq);
         if (idx_out) memcpy(idx_out + (size_t)t * k, idx, sizeof(int32_t) * (size_t)k);
@@ -588,14 +613,16 @@ void tgo_moe_layer_q40(const uint8_t *layer, const float *Wr, int H, int I,
 }
 
 /* Layer stack (D7): x <- x + MoE_l(x) for l = 0..n_layers-1, each token
- * independent (engine.py:199-258 without attention).  idx_trace (may be
+ * independent (engine.py:199-258 without attention).  norms (may be NULL,
+ * as may each entry) holds each layer's FFN norm weight.  idx_trace (may be
  * NULL) receives [n_layers][n_tokens][k] expert ids. */
 void tgo_moe_stack_q40(const uint8_t *const *layers, const float *const *routers,
-                       int n_layers, int H, int I, int E, int k, float eps,
-                       float *x, int n_tokens, int32_t *idx_trace) {
+                       const float *const *norms, int n_layers, int H, int I,
+                       int E, int k, float eps, float *x, int n_tokens,
+                       int32_t *idx_trace) {
     float *mo = (float *)malloc(sizeof(float) * (size_t)H * n_tokens);
     for (int l = 0; l < n_layers; l++) {
-        tgo_moe_layer_q40(layers[l], routers[l], H, I, E, k, eps, x, n_tokens, mo,
+        tgo_moe_layer_q40(layers[l], routers[l], norms ? norms[l] : NULL, H, I, E, k, eps, x, n_tokens, mo,
                           idx_trace ? idx_trace + (size_t)l * n_tokens * k : NULL,
                           NULL, NULL);
         for (size_t i = 0; i < (size_t)H * n_tokens; i++) x[i] = x[i] + mo[i];

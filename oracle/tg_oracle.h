@@ -77,12 +77,15 @@ float   tgo_silu_mul(float g, float u);
 void    tgo_expert_q40(const uint8_t *expert, int H, int I,
                        const uint8_t *xq, float *gate, float *up,
                        float *h, uint8_t *hq, float *down);
+float   tgo_router_dot_g(const float *w, const float *g, const float *x, int n);
 void    tgo_moe_layer_q40(const uint8_t *layer, const float *Wr,
-                          int H, int I, int E, int k, float eps,
-                          const float *x, int n_tokens, float *moe_out,
-                          int32_t *idx, float *w, uint8_t *xq_out);
+                          const float *g, int H, int I, int E, int k,
+                          float eps, const float *x, int n_tokens,
+                          float *moe_out, int32_t *idx, float *w,
+                          uint8_t *xq_out);
 void    tgo_moe_stack_q40(const uint8_t *const *layers,
-                          const float *const *routers, int n_layers,
+                          const float *const *routers,
+                          const float *const *norms, int n_layers,
                           int H, int I, int E, int k, float eps,
                           float *x, int n_tokens, int32_t *idx_trace);
 int     tgo_group_by_expert(const int32_t *idx, int n_tokens, int k, int E,

@@ -109,7 +109,9 @@ def test_matmul_q6k(O, L, nrows, ncols):
 
 
 @pytest.mark.parametrize("half", [True, False])
-@pytest.mark.parametrize("nrows,ncols", [(2048, 768), (3, 7), (129, 777), (16, 8)])
+# (33, 8200) and (9, 16391) stage x through LDS in more than one chunk of
+# 8192 columns, the last one ragged
+@pytest.mark.parametrize("nrows,ncols", [(2048, 768), (3, 7), (129, 777), (16, 8), (33, 8200), (9, 16391)])
 def test_matvec_f16_f32(O, L, half, nrows, ncols):
     gpu_note(f"tg_{'f16' if half else 'f32'}_matvec {nrows}x{ncols}")
     rng = np.random.default_rng(nrows + ncols + half)
@@ -126,7 +128,9 @@ def test_matvec_f16_f32(O, L, half, nrows, ncols):
     assert_exact(out, ref, f"matvec half={half} {nrows}x{ncols}")
 
 
-@pytest.mark.parametrize("dim", [2048, 1001, 3])
+# 6150 and 8195 stage the row in more than one chunk of 4096 (6150: the
+# second chunk ragged), 4099 and 8195 leave a tail of 3
+@pytest.mark.parametrize("dim", [2048, 1001, 3, 4099, 6150, 8195])
 def test_rms_norm(O, L, dim):
     gpu_note(f"tg_rms_norm {dim}")
     rng = np.random.default_rng(dim)
@@ -282,7 +286,7 @@ def test_transformer_layer(O, L):
 
 
 @pytest.mark.parametrize("vocab,embed,case", [(1000, 256, "plain"), (5003, 2048, "tie"), (4097, 1001, "nan"),
-                                              (151936, 2048, "plain")])
+                                              (151936, 2048, "plain"), (700, 8300, "plain")])
 def test_output_head(O, L, vocab, embed, case):
     """tg_head_forward: logits bit-identical to the oracle's norm + fp32
     matvec, token = numpy's argmax (ties to the first index, NaN largest)."""

@@ -64,6 +64,7 @@ NEW_SYMBOLS = [
     ("tg_arena_expert_offset", CI, [VP, CI, VP, VP, VP, VP]),
     ("tg_arena_load_layer", CI, [VP, CI, VP, SZ]),
     ("tg_arena_load_router", CI, [VP, CI, VP, SZ]),
+    ("tg_arena_load_norm", CI, [VP, CI, VP, SZ]),
     ("tg_arena_read_layer", CI, [VP, CI, VP, SZ]),
     ("tg_arena_synth_layer", CI, [VP, CI, U64, CF]),
     ("tg_moe_layer_q40_dev", CI, [VP, CI, VP, VP, CI, VP, VP, CF, VP]),
@@ -74,8 +75,6 @@ NEW_SYMBOLS = [
     ("tg_arena_set_decode_path", CI, [VP, CI]),
     ("tg_arena_set_batch_path", CI, [VP, CI]),
     ("tg_arena_status", CI, [VP]),
-    ("tg_arena_set_timeline", CI, [VP, VP, SZ]),
-    ("tg_timeline_info", CI, [VP, CI, VP, VP, VP]),
     ("tg_q40_quantize_q8_0_dev", CI, [VP, VP, CI, VP]),
     ("tg_q40_to_planar_dev", CI, [VP, VP, CI, CI, VP]),
     ("tg_q40_from_planar_dev", CI, [VP, VP, CI, CI, VP]),

@@ -66,17 +66,16 @@ class HBMExpertArena:
             pass
 
     # ------------------------------------------------------------ decode path
-    DECODE_AUTO, DECODE_PERSISTENT, DECODE_PER_LAYER, DECODE_FUSED, DECODE_ROUTED = 0, 1, 2, 3, 4
+    DECODE_AUTO, DECODE_PER_LAYER, DECODE_FUSED, DECODE_ROUTED = 0, 2, 3, 4
 
     def set_decode_path(self, path: int) -> None:
         """One-token calls.  ROUTED: one launch per layer that also routes
         (from router partial sums the layer before it leaves, plus one
         prologue launch per call); FUSED: per layer a routing kernel and
         one launch for gate/up and down; PER_LAYER: routing, gate/up and
-        down as three kernels; PERSISTENT: one cooperative launch over
-        every layer of a stack call (error where the shape / device does
-        not allow it); AUTO: ROUTED, else FUSED, else PER_LAYER, as the
-        shape allows."""
+        down as three kernels; AUTO: ROUTED, else FUSED, else PER_LAYER, as
+        the shape allows.  ROUTED and FUSED need every block of their launch
+        resident at once: run nothing else on the device beside them."""
         call("tg_arena_set_decode_path", self.handle, int(path))
 
     BATCH_AUTO, BATCH_GROUPED, BATCH_PER_TOKEN, BATCH_GROUPED_DOT = 0, 1, 2, 3
@@ -90,7 +89,7 @@ class HBMExpertArena:
 
     def status(self) -> None:
         """Wait for the device; raise if an earlier asynchronous call failed
-        on the device (a persistent-kernel wait that ran out of tries)."""
+        on the device (a hand-off poll that ran out of tries)."""
         call("tg_arena_status", self.handle)
 
     # ------------------------------------------------------------ contents
@@ -103,6 +102,12 @@ class HBMExpertArena:
     def load_router(self, layer: int, router: np.ndarray) -> None:
         r = np.ascontiguousarray(router, dtype=np.float32)
         call("tg_arena_load_router", self.handle, layer, r.ctypes.data, r.size)
+
+    def load_norm(self, layer: int, norm: np.ndarray) -> None:
+        """Upload one layer's FFN norm weight [H] (engine.py:229-230's
+        ffn_norms[i]); until then a layer runs on a unit weight."""
+        g = np.ascontiguousarray(norm, dtype=np.float32)
+        call("tg_arena_load_norm", self.handle, layer, g.ctypes.data, g.size)
 
     def read_layer(self, layer: int) -> np.ndarray:
         out = np.empty(self.layer_bytes, dtype=np.uint8)
@@ -137,7 +142,8 @@ class HBMExpertArena:
     @classmethod
     def from_cache_dir(cls, cache_dir, top_k: int | None = None) -> "HBMExpertArena":
         """Load a Q4_0 relayout cache (index.json + layer_NNN.q4.bin +
-        router_NNN.f32.bin) written by tinygiant_amd.relayout."""
+        router_NNN.f32.bin [+ norm_NNN.f32.bin]) written by
+        tinygiant_amd.relayout."""
         cache_dir = Path(cache_dir)
         index = json.loads((cache_dir / "index.json").read_text())
         if index.get("dtype") != "q4_0":
@@ -157,4 +163,6 @@ class HBMExpertArena:
             a.load_layer(L, data)
             router = np.fromfile(cache_dir / info["router_file"], dtype=np.float32)
             a.load_router(L, router)
+            if "norm_file" in info:
+                a.load_norm(L, np.fromfile(cache_dir / info["norm_file"], dtype=np.float32))
         return a

@@ -179,7 +179,9 @@ struct tg_arena {
     Shape s;
     int L = 0;
     uint8_t *experts = nullptr;   // L * LB bytes, tensor-planar per tensor
-    float *routers = nullptr;     // L * E * H
+    float *routers = nullptr;     // L * E * H, the router as loaded times the norm weight (per column)
+    float *routers_raw = nullptr; // L * E * H, the router as loaded
+    float *norms = nullptr;       // L * H, FFN norm weight (ones until loaded)
     uint8_t *staging = nullptr;   // LB bytes, relayout form for load/read
     // per-call scratch, grown on demand
     int cap_T = 0;
@@ -222,15 +224,8 @@ struct tg_arena {
     };
     std::vector<Graph> graphs;
     hipStream_t capture = nullptr;
-    // one-launch decode (T = 1): exchange buffers and sync words
     int decode_path = TG_DECODE_AUTO;
     int n_cu = 0;
-    bool coop = false;
-    uint8_t *ps_scratch = nullptr;
-    uint32_t *ps_sync = nullptr;
-    uint32_t ps_gen = 0;          // launch generation of the tagged exchange words
-    uint64_t *tl = nullptr;       // optional persistent-kernel timeline (caller's device buffer)
-    size_t tl_words = 0;
 };
 
 static void drop_graphs(tg_arena *a) {
@@ -264,6 +259,8 @@ static void arena_free(tg_arena *a) {
     if (a->capture) (void)hipStreamDestroy(a->capture);
     dfree(a->experts);
     dfree(a->routers);
+    dfree(a->routers_raw);
+    dfree(a->norms);
     dfree(a->staging);
     dfree(a->raw);
     dfree(a->dec);
@@ -272,8 +269,6 @@ static void arena_free(tg_arena *a) {
     dfree(a->xbuf);
     dfree(a->obuf);
     dfree(a->grp);
-    dfree(a->ps_scratch);
-    dfree(a->ps_sync);
     delete a;
 }
 
@@ -294,14 +289,21 @@ extern "C" tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim,
         int dev = 0, v = 0;
         (void)hipGetDevice(&dev);
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) a->n_cu = v;
-        v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess) a->coop = v != 0;
     }
     size_t eb = a->s.LB * (size_t)n_layers;
     size_t rb = sizeof(float) * (size_t)n_experts * embed_dim * n_layers;
-    if (hipMalloc(&a->experts, eb) != hipSuccess || hipMalloc(&a->routers, rb) != hipSuccess) {
+    size_t nb = sizeof(float) * (size_t)embed_dim * n_layers;
+    if (hipMalloc(&a->experts, eb) != hipSuccess || hipMalloc(&a->routers, rb) != hipSuccess ||
+        hipMalloc(&a->routers_raw, rb) != hipSuccess || hipMalloc(&a->norms, nb) != hipSuccess) {
         (void)hipGetLastError();
-        set_err(TG_E_NOMEM, "hipMalloc of %.2f GB expert arena failed", (eb + rb) / 1e9);
+        set_err(TG_E_NOMEM, "hipMalloc of %.2f GB expert arena failed", (eb + 2 * rb + nb) / 1e9);
+        arena_free(a);
+        return nullptr;
+    }
+    // unit norm weight until tg_arena_load_norm
+    if (tg::launch_fill(a->norms, 1.0f, (size_t)embed_dim * n_layers, nullptr) != hipSuccess ||
+        hipStreamSynchronize(nullptr) != hipSuccess) {
+        set_err(TG_E_HIP, "initialising the norm weights failed");
         arena_free(a);
         return nullptr;
     }
@@ -362,23 +364,43 @@ extern "C" int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes, siz
     return TG_OK;
 }
 
+static const float *norm_of(const tg_arena *a, int layer) { return a->norms + (size_t)layer * a->s.H; }
+
+// The kernels use router * g (per column), recomputed from the router as
+// loaded whenever either changes.
+static int arena_refresh_router(tg_arena *a, int layer) {
+    const size_t n = (size_t)a->s.E * a->s.H;
+    HIP_TRY(tg::launch_scale_router(a->routers_raw + (size_t)layer * n, norm_of(a, layer),
+                                    a->routers + (size_t)layer * n, a->s.E, a->s.H, nullptr));
+    HIP_TRY(hipStreamSynchronize(nullptr));
+    return TG_OK;
+}
+
 extern "C" int tg_arena_load_router(tg_arena *a, int layer, const float *host_router, size_t count) {
     int rc = arena_layer_check(a, layer);
     if (rc) return rc;
     size_t n = (size_t)a->s.E * a->s.H;
     if (!host_router || count != n) return set_err(TG_E_INVALID, "router needs %zu floats (got %zu)", n, count);
-    HIP_TRY(hipMemcpy(a->routers + (size_t)layer * n, host_router, n * sizeof(float), hipMemcpyHostToDevice));
-    return TG_OK;
+    HIP_TRY(hipMemcpy(a->routers_raw + (size_t)layer * n, host_router, n * sizeof(float), hipMemcpyHostToDevice));
+    return arena_refresh_router(a, layer);
+}
+
+extern "C" int tg_arena_load_norm(tg_arena *a, int layer, const float *host_norm, size_t count) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    const size_t n = (size_t)a->s.H;
+    if (!host_norm || count != n) return set_err(TG_E_INVALID, "norm weight needs %zu floats (got %zu)", n, count);
+    HIP_TRY(hipMemcpy(a->norms + (size_t)layer * n, host_norm, n * sizeof(float), hipMemcpyHostToDevice));
+    return arena_refresh_router(a, layer);
 }
 
 extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float sigma) {
     int rc = arena_layer_check(a, layer);
     if (rc) return rc;
     HIP_TRY(tg::launch_synth_layer(a->experts + (size_t)layer * a->s.LB,
-                                   a->routers + (size_t)layer * a->s.E * a->s.H, a->s, layer, seed, sigma,
+                                   a->routers_raw + (size_t)layer * a->s.E * a->s.H, a->s, layer, seed, sigma,
                                    nullptr));
-    HIP_TRY(hipStreamSynchronize(nullptr));
-    return TG_OK;
+    return arena_refresh_router(a, layer);
 }
 
 static size_t dec_words_bytes(const Shape &s, int T) {
@@ -485,7 +507,8 @@ static int layer_kernels_grouped(tg_arena *a, int layer, const float *x, float *
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
     PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
     PROFILED("route_q8", st,
-             tg::launch_route_q8(a->raw, x, T, s.E, s.H, s.k, eps, a->idx, a->w, a->xq, a->xd, a->xs, st));
+             tg::launch_route_q8(a->raw, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, a->idx, a->w, a->xq, a->xd,
+                                 a->xs, st));
     const int n = T * s.k;
     if (mfma_usable(a, T)) {
         const int mt = tg::mfma_tiles(s, T), ch = 32 * mt, wmax = tg::group_work_max(s, n, ch);
@@ -539,7 +562,7 @@ static int routed_layers(tg_arena *a, int l0, int n, const float *x, float *out,
         const int l = l0 + j;
         const float *wr_next = j + 1 < n ? router_of(a, l + 1) : nullptr;
         PROFILED("layer", st,
-                 tg::launch_layer_dec(a->experts + (size_t)l * s.LB, s, a->n_cu, j == 0 ? x : out,
+                 tg::launch_layer_dec(a->experts + (size_t)l * s.LB, s, a->n_cu, j == 0 ? x : out, norm_of(a, l),
                                       a->dec_part + (size_t)(j & 1) * half, wr_next,
                                       a->dec_part + (size_t)((j + 1) & 1) * half, a->dec_hw, a->dec_ow, a->dec_ctl,
                                       (uint32_t)(n - 1 - j), a->dec_err, j == 0 ? resid : out, out,
@@ -555,8 +578,8 @@ static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, con
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
     PROFILED("route", st,
-             tg::launch_route_dec(router_of(a, layer), x, T, s, eps, a->dec_lw, a->dec_ctl, a->dec_err, a->idx, a->w,
-                                  a->xq, a->xd, a->xs, st));
+             tg::launch_route_dec(router_of(a, layer), x, norm_of(a, layer), T, s, eps, a->dec_lw, a->dec_ctl,
+                                  a->dec_err, a->idx, a->w, a->xq, a->xd, a->xs, st));
     if (fused_usable(a, T)) {
         PROFILED("experts", st,
                  tg::launch_experts_fused(lp, s, a->n_cu, a->idx, a->w, a->xq, a->xd, a->xs, a->dec_hw, a->dec_ctl,
@@ -597,51 +620,10 @@ static bool graphs_enabled() {
     return on == 1 && !g_prof_on;
 }
 
-// The persistent path runs when asked for; AUTO keeps the per-layer graph,
-// which is the faster of the two on MI355X today (profiles/).
-static bool persist_usable(tg_arena *a, int T) {
-    return T == 1 && a->decode_path == TG_DECODE_PERSISTENT && a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s);
-}
-
-static int persist_buffers(tg_arena *a) {
-    if (!a->ps_scratch) {
-        size_t n = tg::persist_scratch_bytes(a->s);
-        if (hipMalloc(&a->ps_scratch, n) != hipSuccess) {
-            (void)hipGetLastError();
-            return set_err(TG_E_NOMEM, "persistent decode exchange buffers");
-        }
-        HIP_TRY(hipMemset(a->ps_scratch, 0, n));  // tag 0 never matches a launch
-    }
-    if (!a->ps_sync) {
-        if (hipMalloc(&a->ps_sync, 64) != hipSuccess) {
-            (void)hipGetLastError();
-            return set_err(TG_E_NOMEM, "persistent decode sync words");
-        }
-        HIP_TRY(hipMemset(a->ps_sync, 0, 64));
-    }
-    return TG_OK;
-}
-
-// One cooperative launch for the whole layer range (one token).
-static int persist_run(tg_arena *a, float *x, int l0, int n, float eps, int32_t *idx_out, float *w_out,
-                       hipStream_t st) {
-    int rc = persist_buffers(a);
-    if (rc) return rc;
-    a->ps_gen = a->ps_gen + 1 >= (1u << 24) ? 1u : a->ps_gen + 1;
-    PROFILED("persist", st,
-             tg::launch_persist(a->experts, a->routers, a->s, l0, n, eps, x, a->ps_scratch, a->ps_sync, a->ps_gen,
-                                idx_out, w_out, a->tl, a->tl_words, a->n_cu, st));
-    return TG_OK;
-}
-
-// Decode of one token (T = 1) runs as one persistent launch when the shape
-// and device allow it.  Otherwise the stack is replayed as a HIP graph
-// captured on first use for this (x, T, layer range, eps), or launched
-// layer by layer while kernel timing is on.
+// A stack call is replayed as a HIP graph captured on first use for this
+// (x, T, layer range, eps), or launched layer by layer while kernel timing
+// is on.
 static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
-    if (persist_usable(a, T)) return persist_run(a, x, l0, n, eps, nullptr, nullptr, st);
-    if (T == 1 && a->decode_path == TG_DECODE_PERSISTENT)
-        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     if (!graphs_enabled()) return stack_launch(a, x, T, l0, n, eps, st);
     for (auto &g : a->graphs)
         if (g.x == x && g.T == T && g.layer0 == l0 && g.n == n && g.eps == eps) {
@@ -727,9 +709,6 @@ extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int
     if (rc) return rc;
     if (!topk_idx || !topk_w) return set_err(TG_E_INVALID, "topk_idx / topk_w is NULL");
     hipStream_t st = as_stream(stream);
-    if (persist_usable(a, 1)) return persist_run(a, x, layer0, n_layers, eps, topk_idx, topk_w, st);
-    if (a->decode_path == TG_DECODE_PERSISTENT)
-        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     const size_t k = (size_t)a->s.k;
     if (routed_usable(a, 1)) return routed_layers(a, layer0, n_layers, x, x, x, eps, topk_idx, topk_w, (int)k, st);
     for (int l = 0; l < n_layers; l++) {
@@ -754,11 +733,9 @@ extern "C" int tg_arena_set_batch_path(tg_arena *a, int path) {
 
 extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
-    if (path != TG_DECODE_AUTO && path != TG_DECODE_PERSISTENT && path != TG_DECODE_PER_LAYER &&
-        path != TG_DECODE_FUSED && path != TG_DECODE_ROUTED)
+    if (path != TG_DECODE_AUTO && path != TG_DECODE_PER_LAYER && path != TG_DECODE_FUSED &&
+        path != TG_DECODE_ROUTED)
         return set_err(TG_E_INVALID, "unknown decode path %d", path);
-    if (path == TG_DECODE_PERSISTENT && !(a->coop && a->n_cu > 0 && tg::persist_shape_ok(a->s)))
-        return set_err(TG_E_UNSUPPORTED, "persistent decode is not available for this shape / device");
     if (path == TG_DECODE_FUSED && !tg::experts_fused_ok(a->s, a->n_cu))
         return set_err(TG_E_UNSUPPORTED, "the fused expert launch is not available for this shape");
     if (path == TG_DECODE_ROUTED && !tg::layer_dec_ok(a->s, a->n_cu))
@@ -768,38 +745,11 @@ extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     return TG_OK;
 }
 
-extern "C" int tg_arena_set_timeline(tg_arena *a, uint64_t *dev_words, size_t n_words) {
-    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
-    a->tl = n_words ? dev_words : nullptr;
-    a->tl_words = dev_words ? n_words : 0;
-    return TG_OK;
-}
-
-extern "C" int tg_timeline_info(const tg_arena *a, int n_layers, size_t *n_words, int *blocks, int *clock_khz) {
-    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
-    int rc = ensure_device();
-    if (rc) return rc;
-    if (n_words) *n_words = tg::persist_timeline_words(n_layers, a->n_cu);
-    if (blocks) *blocks = a->n_cu;
-    if (clock_khz) {
-        int dev = 0, v = 0;
-        HIP_TRY(hipGetDevice(&dev));
-        HIP_TRY(hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, dev));
-        *clock_khz = v;
-    }
-    return TG_OK;
-}
-
 extern "C" int tg_arena_status(tg_arena *a) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
     int rc = ensure_device();
     if (rc) return rc;
     HIP_TRY(hipDeviceSynchronize());
-    if (a->ps_sync) {
-        uint32_t w[4] = {0, 0, 0, 0};
-        HIP_TRY(hipMemcpy(w, a->ps_sync, sizeof w, hipMemcpyDeviceToHost));
-        if (w[1] != 0u) return set_err(TG_E_HIP, "persistent decode: a device-side poll ran out of tries");
-    }
     if (a->dec_err) {
         uint32_t v = 0;
         HIP_TRY(hipMemcpy(&v, a->dec_err, sizeof v, hipMemcpyDeviceToHost));

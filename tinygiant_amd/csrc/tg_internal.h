@@ -81,6 +81,11 @@ constexpr int MAX_K = 32;        // top-k
 constexpr int MAX_E = 256;       // experts per layer (one thread per expert)
 constexpr int MAX_NB = 256;      // blocks per row (H, I <= 8192)
 
+// router[e][i] = raw[e][i] * g[i] (the FFN norm weight folded into the
+// router: s * (router . x) is then the router applied to (x * s) * g)
+hipError_t launch_scale_router(const float *raw, const float *g, float *router, int E, int H, hipStream_t st);
+// every one of the n floats at p set to v
+hipError_t launch_fill(float *p, float v, size_t n, hipStream_t st);
 hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, int layer,
                               uint64_t seed, float sigma, hipStream_t st);
 hipError_t launch_synth_q40(uint8_t *pl, uint64_t key, float sigma, int rows, int nb, hipStream_t st);
@@ -104,9 +109,10 @@ bool decode_shape_ok(const Shape &s);
 // (word 1: generation of the token's last routing; zero before first use),
 // err set to nonzero when a poll ran out of tries; writes idx, w [T][k]
 // and the Q8_0 activations xq [T][H], xd / xs [T][H/32]
-hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape &s, float eps, uint64_t *lw,
-                            uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                            hipStream_t st);
+// (gn: the FFN norm weight, H floats; the expert input is Q8_0((x * s) * gn))
+hipError_t launch_route_dec(const float *Wr, const float *x, const float *gn, int T, const Shape &s, float eps,
+                            uint64_t *lw, uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd,
+                            int *xs, hipStream_t st);
 // gate/up + SwiGLU -> Q8_0 h [T][k][I] (hd / hs [T][k][I/32])
 hipError_t launch_gateup(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const int8_t *xq,
                          const float *xd, const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);
@@ -170,10 +176,10 @@ size_t dec_part_floats(const Shape &s);
 size_t dec_ow_words(const Shape &s);
 hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, float *part, uint32_t *ctl, int n_layers,
                            hipStream_t st);
-hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *part_in,
-                            const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow, const uint32_t *ctl,
-                            uint32_t back, uint32_t *err, const float *resid, float *out, int32_t *idx, float *w,
-                            float eps, hipStream_t st);
+hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *gn,
+                            const float *part_in, const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow,
+                            const uint32_t *ctl, uint32_t back, uint32_t *err, const float *resid, float *out,
+                            int32_t *idx, float *w, float eps, hipStream_t st);
 hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_cu, const int32_t *idx, const float *w,
                                 const int8_t *xq, const float *xd, const int *xs, uint64_t *hw, const uint32_t *ctl,
                                 uint32_t *err, const float *resid, float *out, hipStream_t st);
@@ -186,8 +192,8 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *s
 
 // grouped (batched decode / prefill) MoE layer pieces
 bool grouped_shape_ok(const Shape &s);
-hipError_t launch_route_q8(const float *raw, const float *x, int T, int E, int H, int k, float eps, int32_t *idx,
-                           float *w, int8_t *xq, float *xd, int *xs, hipStream_t st);
+hipError_t launch_route_q8(const float *raw, const float *x, const float *gn, int T, int E, int H, int k, float eps,
+                           int32_t *idx, float *w, int8_t *xq, float *xd, int *xs, hipStream_t st);
 // work list: at most group_work_max(s, n) items per list, two lists
 int group_work_max(const Shape &s, int n);
 int group_work_max(const Shape &s, int n, int ch);
@@ -212,17 +218,5 @@ hipError_t launch_down_grouped(const uint8_t *layer_pl, const Shape &s, int n, c
                                const int *hs, float *D, hipStream_t st);
 hipError_t launch_combine(const float *D, const float *w, int T, int H, int k, const float *resid, float *out,
                           hipStream_t st);
-
-// one-token decode of a layer range in one cooperative launch
-bool persist_shape_ok(const Shape &s);
-size_t persist_scratch_bytes(const Shape &s);
-// gen: launch generation in 1 .. 2^24 - 1, different from the previous
-// launch on the same scratch
-// timeline: optional [nl][blocks][8] wall-clock stamps (used when
-// timeline_words covers nl * blocks * 8)
-hipError_t launch_persist(const uint8_t *experts, const float *routers, const Shape &s, int layer0, int nl, float eps,
-                          float *x, void *scratch, uint32_t *sync, uint32_t gen, int32_t *idx_out, float *w_out,
-                          uint64_t *timeline, size_t timeline_words, int n_cu, hipStream_t st);
-size_t persist_timeline_words(int nl, int n_cu);
 
 }  // namespace tg

@@ -111,6 +111,19 @@ __global__ __launch_bounds__(256) void k_synth_normal(float *__restrict__ out, u
     if (g < n) out[g] = sigma * normal_at(key, g);
 }
 
+// router[e][i] = raw[e][i] * g[i]: one rounding per weight, so a unit g
+// leaves the router's bits unchanged.
+__global__ __launch_bounds__(256) void k_scale_router(const float *__restrict__ raw, const float *__restrict__ g,
+                                                      float *__restrict__ router, int H, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) router[i] = raw[i] * g[i % (size_t)H];
+}
+
+__global__ __launch_bounds__(256) void k_fill(float *__restrict__ p, float v, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
 // ================================================================= repack
 // relayout 18-byte blocks <-> tensor-planar, one thread per block.
 TG_DEV void aos_to_planar_block(const uint8_t *src, uint8_t *qs_dst, uint16_t *d_dst) {
@@ -357,6 +370,18 @@ hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, 
         TG_LAUNCH(k_synth_normal, dim3(cdiv(n, 256)), dim3(256), 0, st, router,
                            host_stream_key(seed, stream_id(layer, 0, 3)), sigma, n);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_router(const float *raw, const float *g, float *router, int E, int H, hipStream_t st) {
+    const size_t n = (size_t)E * H;
+    TG_LAUNCH(k_scale_router, dim3(cdiv(n, 256)), dim3(256), 0, st, raw, g, router, H, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(float *p, float v, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    TG_LAUNCH(k_fill, dim3(cdiv(n, 256)), dim3(256), 0, st, p, v, n);
     return hipGetLastError();
 }
 

@@ -429,8 +429,7 @@ __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 // Block (e, t): the raw router dot of expert e for token t (grouped sums as
 // k_route) and, from the same x, the token's RMS scale s (grouped sums of
 // squares as route_token), so logit = raw * s as in route_token.  Thread 0
-// publishes the logit as a tagged word (see tg_persist.hip; relaxed
-// agent-scope atomics).  Block (0, t) also ranks the token: it forms
+// publishes the logit as a tagged word (relaxed agent-scope atomics).  Block (0, t) also ranks the token: it forms
 // Q8_0(x * s), reads the E logits (bounded polls on the tags), ranks them,
 // forms the softmax weights, and writes idx / w / xq / xd / xs for the
 // expert kernels.
@@ -493,7 +492,8 @@ TG_DEV float topk_softmax_lane(const float *slog, const int *sidx, int k) {
 }
 
 __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restrict__ Wr, const float *__restrict__ x,
-                                                          int E, int H, int k, float eps, uint64_t *__restrict__ lw,
+                                                          const float *__restrict__ gn, int E, int H, int k, float eps,
+                                                          uint64_t *__restrict__ lw,
                                                           uint32_t *__restrict__ ctl, uint32_t *__restrict__ err,
                                                           int32_t *__restrict__ idx, float *__restrict__ w,
                                                           int8_t *__restrict__ xq, float *__restrict__ xd,
@@ -556,15 +556,17 @@ __global__ __launch_bounds__(RD_THREADS) void k_route_dec(const float *__restric
     if (e != 0) return;
     __syncthreads();
 
-    // ---- block (0, t): Q8_0(x * s), then the E logits
+    // ---- block (0, t): Q8_0((x * s) * g), then the E logits
     const float sc = ssc;
     {
         const int i0 = tid * 8;
         if (i0 < H) {  // H / 8 is a multiple of 32: whole 4-lane groups
             const float4 a4 = *reinterpret_cast<const float4 *>(xt + i0);
             const float4 b4 = *reinterpret_cast<const float4 *>(xt + i0 + 4);
-            const float v[8] = {a4.x * sc, a4.y * sc, a4.z * sc, a4.w * sc,
-                                b4.x * sc, b4.y * sc, b4.z * sc, b4.w * sc};
+            const float4 ga = *reinterpret_cast<const float4 *>(gn + i0);
+            const float4 gb = *reinterpret_cast<const float4 *>(gn + i0 + 4);
+            const float v[8] = {(a4.x * sc) * ga.x, (a4.y * sc) * ga.y, (a4.z * sc) * ga.z, (a4.w * sc) * ga.w,
+                                (b4.x * sc) * gb.x, (b4.y * sc) * gb.y, (b4.z * sc) * gb.z, (b4.w * sc) * gb.w};
             q8_group8(v, true, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
         }
     }
@@ -1103,6 +1105,7 @@ constexpr int LD_PC = 16;  // float4 of partials per load round of one thread
 struct LdArgs {
     const uint8_t *layer_pl;
     const float *x;         // this layer's input row (H)
+    const float *gn;        // this layer's FFN norm weight (H)
     const float *part_in;   // [E + 1][G] partials of x for this layer's router
     const float *wr_next;   // next layer's router [E][H], or null (no partials out)
     float *part_out;        // [E + 1][G] partials of out for the next layer
@@ -1186,13 +1189,15 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     //    residual rows, (owners) the next router's columns of the group, then
     //    the partials
     // x is read by the threads that quantize it (waves 1.., H / 8 of them)
-    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa;
+    float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa, ga = xa, gb = xa;
     const int u0 = role.rank;  // first gate/up unit
     const int qt = tid - WAVE;
     const bool qon = u0 < ng && qt >= 0 && qt < H / 8;
     if (qon) {
         xa = reinterpret_cast<const float4 *>(A.x)[2 * qt];
         xb = reinterpret_cast<const float4 *>(A.x)[2 * qt + 1];
+        ga = reinterpret_cast<const float4 *>(A.gn)[2 * qt];
+        gb = reinterpret_cast<const float4 *>(A.gn)[2 * qt + 1];
     }
     float rv = 0.0f;
     if (A.resid && tid < RD) rv = A.resid[r0 + tid];
@@ -1234,12 +1239,13 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     __syncthreads();
     rank_topk(keys, E, k, sidx, rcnt);  // ends with a barrier: sidx is set
     // the first unit's weights are in flight while wave 0 forms the softmax
-    // and waves 1..4 Q8_0(x * s) into the gate/up LDS layout; x * s is
-    // formed (and pinned) before the unit loads are issued, so the Q8_0
-    // waits for no load
+    // and waves 1..4 Q8_0((x * s) * g) into the gate/up LDS layout; the
+    // normed x is formed (and pinned) before the unit loads are issued, so
+    // the Q8_0 waits for no load
     float xsv[8];
     if (qon) {
-        const float v[8] = {xa.x * sc, xa.y * sc, xa.z * sc, xa.w * sc, xb.x * sc, xb.y * sc, xb.z * sc, xb.w * sc};
+        const float v[8] = {(xa.x * sc) * ga.x, (xa.y * sc) * ga.y, (xa.z * sc) * ga.z, (xa.w * sc) * ga.w,
+                            (xb.x * sc) * gb.x, (xb.y * sc) * gb.y, (xb.z * sc) * gb.z, (xb.w * sc) * gb.w};
 #pragma unroll
         for (int c = 0; c < 8; c++) xsv[c] = __uint_as_float(at_use(__float_as_uint(v[c])));
     }
@@ -1445,7 +1451,7 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 //
 //   k_route          raw router dots (as above)
 //   k_route_q8       grid (T): routing of token t (route_token), its top-k
-//                    ids and weights, and Q8_0(x_t * s_t) to global
+//                    ids and weights, and Q8_0((x_t * s_t) * g) to global
 //   k_group          one block: per-expert counts, offsets, and the entry
 //                    list (entry i = t * k + j) of every expert
 //   k_gateup_grouped grid (I/32, E): rows [32m, 32m+32) of gate and up of
@@ -1463,7 +1469,8 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 // to the per-token path bit for bit.
 
 __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ x,
-                                                         int E, int H, int k, float eps, int32_t *__restrict__ idx,
+                                                         const float *__restrict__ gn, int E, int H, int k, float eps,
+                                                         int32_t *__restrict__ idx,
                                                          float *__restrict__ w, int8_t *__restrict__ xq,
                                                          float *__restrict__ xd, int *__restrict__ xs) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1485,8 +1492,14 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
         const int i0 = ps * RO_THREADS * 8 + tid * 8;
         if (ps * RO_THREADS * 8 < H) {
             float v[8];
+            float4 ga = make_float4(0.f, 0.f, 0.f, 0.f), gb = ga;
+            if (i0 < H) {
+                ga = *reinterpret_cast<const float4 *>(gn + i0);
+                gb = *reinterpret_cast<const float4 *>(gn + i0 + 4);
+            }
+            const float g8[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
-            for (int c = 0; c < 8; c++) v[c] = xv[ps][c] * sc;
+            for (int c = 0; c < 8; c++) v[c] = (xv[ps][c] * sc) * g8[c];
             q8_group8(v, i0 < H, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
         }
     }
@@ -1933,11 +1946,11 @@ hipError_t launch_topk(const float *raw, const float *x, int T, int E, int H, in
     return hipGetLastError();
 }
 
-hipError_t launch_route_dec(const float *Wr, const float *x, int T, const Shape &s, float eps, uint64_t *lw,
-                            uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                            hipStream_t st) {
+hipError_t launch_route_dec(const float *Wr, const float *x, const float *gn, int T, const Shape &s, float eps,
+                            uint64_t *lw, uint32_t *ctl, uint32_t *err, int32_t *idx, float *w, int8_t *xq, float *xd,
+                            int *xs, hipStream_t st) {
     if (!decode_shape_ok(s)) return hipErrorInvalidValue;
-    TG_LAUNCH(k_route_dec, dim3(s.E, T), dim3(RD_THREADS), 0, st, Wr, x, s.E, s.H, s.k, eps, lw, ctl, err, idx,
+    TG_LAUNCH(k_route_dec, dim3(s.E, T), dim3(RD_THREADS), 0, st, Wr, x, gn, s.E, s.H, s.k, eps, lw, ctl, err, idx,
                        w, xq, xd, xs);
     return hipGetLastError();
 }
@@ -2070,13 +2083,13 @@ static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *part_in,
-                            const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow, const uint32_t *ctl,
-                            uint32_t back, uint32_t *err, const float *resid, float *out, int32_t *idx, float *w,
-                            float eps, hipStream_t st) {
+hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *gn,
+                            const float *part_in, const float *wr_next, float *part_out, uint64_t *hw, uint64_t *ow,
+                            const uint32_t *ctl, uint32_t back, uint32_t *err, const float *resid, float *out,
+                            int32_t *idx, float *w, float eps, hipStream_t st) {
     if (!layer_dec_ok(s, n_cu)) return hipErrorInvalidValue;
     const int rd = ld_rows(s, n_cu);
-    const LdArgs A{layer_pl, x, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
+    const LdArgs A{layer_pl, x, gn, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
     if (ug <= 4 && ld_ud(s, rd) <= 2) return ld_go<4, 2>(A, s, st);
     return ld_go<8, 6>(A, s, st);
@@ -2090,12 +2103,12 @@ bool grouped_shape_ok(const Shape &s) {
            gu_grouped_lds(s.nbH) <= 160 * 1024 && dn_grouped_lds(s.nbI, s.I) <= 160 * 1024;
 }
 
-hipError_t launch_route_q8(const float *raw, const float *x, int T, int E, int H, int k, float eps, int32_t *idx,
-                           float *w, int8_t *xq, float *xd, int *xs, hipStream_t st) {
+hipError_t launch_route_q8(const float *raw, const float *x, const float *gn, int T, int E, int H, int k, float eps,
+                           int32_t *idx, float *w, int8_t *xq, float *xd, int *xs, hipStream_t st) {
     size_t lds = route_lds_bytes(H);
     hipError_t e = allow_lds((const void *)k_route_q8, lds);
     if (e != hipSuccess) return e;
-    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, E, H, k, eps, idx, w, xq, xd, xs);
+    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, gn, E, H, k, eps, idx, w, xq, xd, xs);
     return hipGetLastError();
 }
 

@@ -3,15 +3,15 @@
 Host-side mirror of the reference's per-layer MoE step
 (tinygiant/engine.py:229-258):
 
-    normed = rms_norm(x)                       engine.py:229-230
+    normed = rms_norm(x, ffn_norms[i])         engine.py:229-230
     logits = router @ normed                   engine.py:231
     top_k_idx, softmax over the top k          engine.py:232-236
     moe_out = sum_j w_j * expert_j(normed)     engine.py:238-257
     x += moe_out                               engine.py:258
 
 Every step runs in libtinygiant.so's gfx950 kernels on weights resident in
-an HBMExpertArena; torch is used only to hold device buffers and name the
-current stream.
+an HBMExpertArena (the layer's norm weight from HBMExpertArena.load_norm);
+torch is used only to hold device buffers and name the current stream.
 """
 from __future__ import annotations
 

@@ -7,7 +7,9 @@ expert's offset and sizes (relayout.py:142-157, 276-299).  The reference
 derives in_dim from Q4_K super-blocks (relayout.py:101-102); for Q4_0 a row
 of in_dim weights is in_dim / 32 blocks of 18 bytes.  The router of each
 layer is stored next to it as router_NNN.f32.bin ([n_experts x embed_dim]
-fp32), which the reference instead reads from the GGUF.
+fp32), and, when given, its FFN norm weight as norm_NNN.f32.bin
+([embed_dim] fp32); the reference reads both from the GGUF
+(engine.py:103-117).
 """
 from __future__ import annotations
 
@@ -35,9 +37,10 @@ def expert_sizes(embed_dim: int, inter_dim: int) -> dict:
             "down": q40_tensor_bytes(embed_dim, inter_dim)}
 
 
-def write_layer(out_dir, layer: int, experts: list, router: np.ndarray) -> dict:
+def write_layer(out_dir, layer: int, experts: list, router: np.ndarray, norm=None) -> dict:
     """experts: list of dicts {gate, up, down} of uint8 arrays (relayout
-    order).  Returns the layer's index entry."""
+    order); norm: the layer's FFN norm weight or None.  Returns the layer's
+    index entry."""
     out_dir = Path(out_dir)
     fname = f"layer_{layer:03d}.q4.bin"
     offsets = {}
@@ -54,8 +57,13 @@ def write_layer(out_dir, layer: int, experts: list, router: np.ndarray) -> dict:
             offsets[str(e)] = {"offset": start, "sizes": sizes}
     rname = f"router_{layer:03d}.f32.bin"
     np.ascontiguousarray(router, dtype=np.float32).tofile(out_dir / rname)
-    return {"file": fname, "router_file": rname, "total_bytes": cur, "expert_offsets": offsets,
-            "tensor_formats": {k: "q4_0" for k in EXPERT_KEYS}}
+    entry = {"file": fname, "router_file": rname, "total_bytes": cur, "expert_offsets": offsets,
+             "tensor_formats": {k: "q4_0" for k in EXPERT_KEYS}}
+    if norm is not None:
+        nname = f"norm_{layer:03d}.f32.bin"
+        np.ascontiguousarray(norm, dtype=np.float32).tofile(out_dir / nname)
+        entry["norm_file"] = nname
+    return entry
 
 
 def split_layer_bytes(data: np.ndarray, n_experts: int, embed_dim: int, inter_dim: int) -> list:
@@ -73,8 +81,11 @@ def split_layer_bytes(data: np.ndarray, n_experts: int, embed_dim: int, inter_di
     return out
 
 
-def write_cache(out_dir, layers: list, routers: list, n_experts_used: int, model: str = "synthetic") -> dict:
-    """Write a full Q4_0 cache: layers = list of per-layer byte arrays."""
+def write_cache(out_dir, layers: list, routers: list, n_experts_used: int, model: str = "synthetic",
+                norms=None) -> dict:
+    """Write a full Q4_0 cache: layers = list of per-layer byte arrays,
+    routers their [n_experts x embed_dim] fp32 routers, norms (optional)
+    their FFN norm weights."""
     out_dir = Path(out_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
     E, H = np.asarray(routers[0]).shape
@@ -89,6 +100,7 @@ def write_cache(out_dir, layers: list, routers: list, n_experts_used: int, model
              "tensor_formats": {k: "q4_0" for k in EXPERT_KEYS}, "layers": {}}
     for L, (data, router) in enumerate(zip(layers, routers)):
         experts = split_layer_bytes(np.asarray(data, dtype=np.uint8), E, H, I)
-        index["layers"][str(L)] = write_layer(out_dir, L, experts, router)
+        index["layers"][str(L)] = write_layer(out_dir, L, experts, router,
+                                              None if norms is None else norms[L])
     (out_dir / "index.json").write_text(json.dumps(index, indent=2))
     return index

@@ -36,3 +36,24 @@ def fit_zipf_exponent(idx: np.ndarray, n_experts: int) -> float:
     if m.sum() < 2:
         return float("nan")
     return float(-np.polyfit(np.log(r[m]), np.log(f[m]), 1)[0])
+
+
+def zipf_skew(rng: np.random.Generator, n_experts: int, embed_dim: int, sigma: float = 0.02):
+    """Zipf(1.1)-skewed routing for one layer fed tokens x = N(0, 1) + shift.
+
+    Returns (router, shift): router = N(0, sigma) plus, along a unit
+    direction u that every token shares, the per-expert offsets of
+    zipf_router_bias scaled to the logit noise; shift = c u with
+    c = sqrt(H) / 2 is the component each token carries along u.  The
+    reference's router has no bias term (engine.py:231), so the skew lives
+    in the weights and the activations."""
+    H, E = embed_dim, n_experts
+    u = rng.standard_normal(H)
+    u /= np.linalg.norm(u)
+    c = 0.5 * np.sqrt(H)
+    rms = np.sqrt(1.0 + c * c / H)
+    noise_std = sigma * np.sqrt(H) / rms
+    bias = zipf_router_bias(E, 0.54 * noise_std / 0.905)
+    router = (rng.standard_normal((E, H)) * sigma).astype(np.float32)
+    router += (bias[:, None] * (rms / c) * u[None, :]).astype(np.float32)
+    return router, (c * u).astype(np.float32)
