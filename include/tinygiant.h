@@ -196,6 +196,22 @@ int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x,
 int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out,
                      int n_tokens, int32_t *topk_idx, float *topk_w,
                      float eps);
+/* tg_moe_layer_q40_dev that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as tg_moe_layer_q40_dev;
+ * its scratch is a fixed 16 MiB device array per GPU, held until the
+ * process ends, instead of the arena's.  Calls whose scratch would exceed it
+ * fail with TG_E_INVALID (the message gives the largest n_tokens at the
+ * arena's shape).  tg_gpu_init must have
+ * run.  Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU (other streams, other threads) race.  A call whose shape or
+ * n_tokens differs from the previous call's on that GPU first clears the
+ * array's exchange words with a kernel on `stream`. */
+int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float *x,
+                                 float *moe_out, int n_tokens,
+                                 int32_t *topk_idx, float *topk_w, float eps,
+                                 void *stream);
 /* x <- x + MoE_l(x) for l = layer0 .. layer0+n_layers-1, in place.  The
  * decode path of one-token calls is chosen by tg_arena_set_decode_path. */
 int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int layer0,

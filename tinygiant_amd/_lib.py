@@ -69,6 +69,7 @@ NEW_SYMBOLS = [
     ("tg_arena_synth_layer", CI, [VP, CI, U64, CF]),
     ("tg_moe_layer_q40_dev", CI, [VP, CI, VP, VP, CI, VP, VP, CF, VP]),
     ("tg_moe_layer_q40", CI, [VP, CI, VP, VP, CI, VP, VP, CF]),
+    ("tg_moe_layer_q40_noalloc_dev", CI, [VP, CI, VP, VP, CI, VP, VP, CF, VP]),
     ("tg_moe_stack_q40_dev", CI, [VP, VP, CI, CI, CI, CF, VP]),
     ("tg_moe_stack_q40", CI, [VP, VP, CI, CI, CI, CF]),
     ("tg_moe_stack_q40_trace_dev", CI, [VP, VP, CI, CI, CF, VP, VP, VP]),

@@ -53,6 +53,8 @@ extern "C" const char *tg_version(void) { return "tinygiant-gfx950 0.1"; }
 static std::mutex g_dev_mu;
 static int g_dev = -1;
 
+static int noalloc_setup(int device);
+
 extern "C" int tg_gpu_init(int device) {
     std::lock_guard<std::mutex> lk(g_dev_mu);
     int n = 0;
@@ -61,6 +63,8 @@ extern "C" int tg_gpu_init(int device) {
     if (device < 0 || device >= n) return set_err(TG_E_INVALID, "device %d out of range (0..%d)", device, n - 1);
     HIP_TRY(hipSetDevice(device));
     HIP_TRY(hipFree(nullptr));
+    int rc = noalloc_setup(device);
+    if (rc) return rc;
     g_dev = device;
     return TG_OK;
 }
@@ -174,34 +178,28 @@ extern "C" int tg_prof_read(const char *kernel, int *launches, double *total_ms)
                            __LINE__);                                                          \
     } while (0)
 
-// ================================================================ arena
-struct tg_arena {
-    Shape s;
-    int L = 0;
-    uint8_t *experts = nullptr;   // L * LB bytes, tensor-planar per tensor
-    float *routers = nullptr;     // L * E * H, the router as loaded times the norm weight (per column)
-    float *routers_raw = nullptr; // L * E * H, the router as loaded
-    float *norms = nullptr;       // L * H, FFN norm weight (ones until loaded)
-    uint8_t *staging = nullptr;   // LB bytes, relayout form for load/read
-    // per-call scratch, grown on demand
-    int cap_T = 0;
+// ================================================================ scratch
+// Device memory of one MoE call beyond its inputs and outputs, for T tokens
+// of one shape.  Every piece starts on a 256-byte boundary.
+struct Scratch {
     float *raw = nullptr;         // T * E raw router dots
     // decode exchange words: tagged logits [T][E] u64 | tagged h blocks of
-    // the fused expert launch | counter, generation [T][2] u32 | error word
+    // the fused expert launch | generation [T][2] u32 | error word; then two
+    // router-partial buffers and the group hand-off words of the routed
+    // one-token launch.  Tags and generations start at zero (tag 0 never
+    // matches).
     uint8_t *dec = nullptr;
+    size_t dec_bytes = 0;
     uint64_t *dec_lw = nullptr;
     uint64_t *dec_hw = nullptr;
     uint32_t *dec_ctl = nullptr;
     uint32_t *dec_err = nullptr;
-    float *dec_part = nullptr;    // two router-partial buffers of the routed one-token path
-    uint64_t *dec_ow = nullptr;   // its group hand-off words
+    float *dec_part = nullptr;
+    uint64_t *dec_ow = nullptr;
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
-    float *xbuf = nullptr;        // T * H (host-pointer entry points)
-    float *obuf = nullptr;        // T * H
-    // grouped (batched) path, carved from one allocation
-    uint8_t *grp = nullptr;
-    int8_t *xq = nullptr;         // T * H      Q8_0 x * s per token
+    // grouped (batched) path
+    int8_t *xq = nullptr;         // T * H      Q8_0 of the normed x per token
     float *xd = nullptr;          // T * nbH
     int *xs = nullptr;            // T * nbH
     int32_t *counts = nullptr;    // E
@@ -213,6 +211,69 @@ struct tg_arena {
     float *hd = nullptr;          // T * k * nbI
     int *hs = nullptr;            // T * k * nbI
     float *D = nullptr;           // T * k * H  down rows per (token, slot)
+};
+
+static size_t dec_words_bytes(const Shape &s, int T) {
+    return 8 * ((size_t)T * s.E + tg::experts_fused_words(s)) + 8 * (size_t)T + 16;
+}
+
+// Lays the scratch of T tokens out from base (base may be null: sizes only)
+// and returns its size in bytes.  The decode exchange words come first, so
+// they sit at the same place for every T of one shape.
+static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> uint8_t * {
+        const size_t o = (off + 255) & ~(size_t)255;
+        off = o + bytes;
+        return base ? base + o : nullptr;
+    };
+    const size_t n = (size_t)T * s.k;
+    const size_t wmax = (size_t)tg::group_work_max(s, (int)n);
+    Scratch c;
+    uint8_t *dec0 = take(dec_words_bytes(s, T));
+    c.dec_part = reinterpret_cast<float *>(take(4 * tg::dec_part_floats(s)));
+    c.dec_ow = reinterpret_cast<uint64_t *>(take(8 * tg::dec_ow_words(s)));
+    c.dec = dec0;
+    c.dec_bytes = off;
+    c.dec_lw = reinterpret_cast<uint64_t *>(dec0);
+    c.dec_hw = c.dec_lw ? c.dec_lw + (size_t)T * s.E : nullptr;
+    c.dec_ctl = c.dec_hw ? reinterpret_cast<uint32_t *>(c.dec_hw + tg::experts_fused_words(s)) : nullptr;
+    c.dec_err = c.dec_ctl ? c.dec_ctl + 2 * (size_t)T : nullptr;
+    c.raw = reinterpret_cast<float *>(take(4 * (size_t)T * s.E));
+    c.idx = reinterpret_cast<int32_t *>(take(4 * n));
+    c.w = reinterpret_cast<float *>(take(4 * n));
+    c.xq = reinterpret_cast<int8_t *>(take((size_t)T * s.H));
+    c.xd = reinterpret_cast<float *>(take(4 * (size_t)T * s.nbH));
+    c.xs = reinterpret_cast<int *>(take(4 * (size_t)T * s.nbH));
+    c.counts = reinterpret_cast<int32_t *>(take(4 * (size_t)s.E));
+    c.offsets = reinterpret_cast<int32_t *>(take(4 * ((size_t)s.E + 1)));
+    c.entries = reinterpret_cast<int32_t *>(take(4 * n));
+    c.hq = reinterpret_cast<int8_t *>(take(n * s.I));
+    c.hd = reinterpret_cast<float *>(take(4 * n * s.nbI));
+    c.hs = reinterpret_cast<int *>(take(4 * n * s.nbI));
+    c.D = reinterpret_cast<float *>(take(4 * n * s.H));
+    c.work = reinterpret_cast<int32_t *>(take(4 * 2 * 3 * wmax));
+    c.work_n = reinterpret_cast<int32_t *>(take(4 * 2));
+    if (sc) *sc = c;
+    return (off + 255) & ~(size_t)255;
+}
+
+// ================================================================ arena
+struct tg_arena {
+    Shape s;
+    int L = 0;
+    uint8_t *experts = nullptr;   // L * LB bytes, tensor-planar per tensor
+    float *routers = nullptr;     // L * E * H, the router as loaded times the norm weight (per column)
+    float *routers_raw = nullptr; // L * E * H, the router as loaded
+    float *norms = nullptr;       // L * H, FFN norm weight (ones until loaded)
+    uint8_t *staging = nullptr;   // LB bytes, relayout form for load/read
+    // per-call scratch, grown on demand (one allocation, laid out by
+    // scratch_layout), and the host-pointer entry points' x / out buffers
+    int cap_T = 0;
+    uint8_t *sc_mem = nullptr;
+    Scratch sc;
+    float *xbuf = nullptr;        // T * H (host-pointer entry points)
+    float *obuf = nullptr;        // T * H
     int batch_path = TG_BATCH_AUTO;
     // captured stacks, replayed as HIP graphs
     struct Graph {
@@ -262,13 +323,9 @@ static void arena_free(tg_arena *a) {
     dfree(a->routers_raw);
     dfree(a->norms);
     dfree(a->staging);
-    dfree(a->raw);
-    dfree(a->dec);
-    dfree(a->idx);
-    dfree(a->w);
+    dfree(a->sc_mem);
     dfree(a->xbuf);
     dfree(a->obuf);
-    dfree(a->grp);
     delete a;
 }
 
@@ -403,73 +460,21 @@ extern "C" int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float
     return arena_refresh_router(a, layer);
 }
 
-static size_t dec_words_bytes(const Shape &s, int T) {
-    return 8 * ((size_t)T * s.E + tg::experts_fused_words(s)) + 8 * (size_t)T + 16;
-}
-
-static size_t dec_part_off(const Shape &s, int T) { return (dec_words_bytes(s, T) + 255) & ~(size_t)255; }
-
-static size_t dec_ow_off(const Shape &s, int T) {
-    return (dec_part_off(s, T) + 4 * tg::dec_part_floats(s) + 255) & ~(size_t)255;
-}
-
-static size_t dec_bytes(const Shape &s, int T) { return dec_ow_off(s, T) + 8 * tg::dec_ow_words(s); }
-
 static int arena_scratch(tg_arena *a, int T) {
     if (T <= a->cap_T) return TG_OK;
     drop_graphs(a);  // captured graphs point at the old buffers
-    dfree(a->raw); dfree(a->dec); dfree(a->idx); dfree(a->w); dfree(a->xbuf); dfree(a->obuf); dfree(a->grp);
-    a->raw = nullptr; a->dec = nullptr; a->idx = nullptr; a->w = nullptr;
-    a->dec_lw = nullptr; a->dec_hw = nullptr; a->dec_ctl = nullptr; a->dec_err = nullptr; a->dec_part = nullptr;
-    a->dec_ow = nullptr;
-    a->xbuf = nullptr; a->obuf = nullptr; a->grp = nullptr;
+    dfree(a->sc_mem); dfree(a->xbuf); dfree(a->obuf);
+    a->sc_mem = nullptr; a->xbuf = nullptr; a->obuf = nullptr;
+    a->sc = Scratch();
     a->cap_T = 0;
     const Shape &s = a->s;
-    bool ok = hipMalloc(&a->raw, sizeof(float) * (size_t)T * s.E) == hipSuccess &&
-              hipMalloc(&a->dec, dec_bytes(s, T)) == hipSuccess &&
-              hipMalloc(&a->idx, sizeof(int32_t) * (size_t)T * s.k) == hipSuccess &&
-              hipMalloc(&a->w, sizeof(float) * (size_t)T * s.k) == hipSuccess &&
+    const size_t bytes = scratch_layout(s, T, nullptr, nullptr);
+    bool ok = hipMalloc(&a->sc_mem, bytes) == hipSuccess &&
               hipMalloc(&a->xbuf, sizeof(float) * (size_t)T * s.H) == hipSuccess &&
               hipMalloc(&a->obuf, sizeof(float) * (size_t)T * s.H) == hipSuccess;
     if (ok) {
-        // counters, generations and tags start at zero (tag 0 never matches)
-        ok = hipMemset(a->dec, 0, dec_bytes(s, T)) == hipSuccess;
-        a->dec_lw = reinterpret_cast<uint64_t *>(a->dec);
-        a->dec_hw = a->dec_lw + (size_t)T * s.E;
-        a->dec_ctl = reinterpret_cast<uint32_t *>(a->dec_hw + tg::experts_fused_words(s));
-        a->dec_err = a->dec_ctl + 2 * (size_t)T;
-        a->dec_part = reinterpret_cast<float *>(a->dec + dec_part_off(s, T));
-        a->dec_ow = reinterpret_cast<uint64_t *>(a->dec + dec_ow_off(s, T));
-    }
-    if (ok) {
-        // grouped path: every piece 256-byte aligned
-        const size_t n = (size_t)T * s.k;
-        const size_t wmax = (size_t)tg::group_work_max(s, (int)n);
-        size_t sizes[] = {(size_t)T * s.H,     4 * (size_t)T * s.nbH,  4 * (size_t)T * s.nbH,
-                          4 * (size_t)s.E,     4 * ((size_t)s.E + 1), 4 * n,
-                          n * s.I,             4 * n * s.nbI,          4 * n * s.nbI,
-                          4 * n * s.H,         4 * 2 * 3 * wmax,       4 * 2};
-        size_t off[12], tot = 0;
-        for (int i = 0; i < 12; i++) {
-            off[i] = tot;
-            tot += (sizes[i] + 255) & ~(size_t)255;
-        }
-        ok = hipMalloc(&a->grp, tot) == hipSuccess;
-        if (ok) {
-            uint8_t *b = a->grp;
-            a->xq = reinterpret_cast<int8_t *>(b + off[0]);
-            a->xd = reinterpret_cast<float *>(b + off[1]);
-            a->xs = reinterpret_cast<int *>(b + off[2]);
-            a->counts = reinterpret_cast<int32_t *>(b + off[3]);
-            a->offsets = reinterpret_cast<int32_t *>(b + off[4]);
-            a->entries = reinterpret_cast<int32_t *>(b + off[5]);
-            a->hq = reinterpret_cast<int8_t *>(b + off[6]);
-            a->hd = reinterpret_cast<float *>(b + off[7]);
-            a->hs = reinterpret_cast<int *>(b + off[8]);
-            a->D = reinterpret_cast<float *>(b + off[9]);
-            a->work = reinterpret_cast<int32_t *>(b + off[10]);
-            a->work_n = reinterpret_cast<int32_t *>(b + off[11]);
-        }
+        scratch_layout(s, T, a->sc_mem, &a->sc);
+        ok = hipMemset(a->sc_mem, 0, a->sc.dec_bytes) == hipSuccess;  // tags and generations start at zero
     }
     if (!ok) {
         (void)hipGetLastError();
@@ -501,37 +506,37 @@ static bool mfma_usable(tg_arena *a, int T) {
 
 // One MoE block over T tokens grouped by expert: every selected expert's
 // weights stream once for all its tokens.
-static int layer_kernels_grouped(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T,
+static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const float *x, float *out, const float *resid, int T,
                                  float eps, hipStream_t st) {
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
-    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, a->raw, st));
+    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, c.raw, st));
     PROFILED("route_q8", st,
-             tg::launch_route_q8(a->raw, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, a->idx, a->w, a->xq, a->xd,
-                                 a->xs, st));
+             tg::launch_route_q8(c.raw, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, c.idx, c.w, c.xq, c.xd,
+                                 c.xs, st));
     const int n = T * s.k;
     if (mfma_usable(a, T)) {
         const int mt = tg::mfma_tiles(s, T), ch = 32 * mt, wmax = tg::group_work_max(s, n, ch);
         PROFILED("group", st,
-                 tg::launch_group_chunked(s, a->idx, n, ch, a->counts, a->offsets, a->entries, a->work, a->work_n,
+                 tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
                                           st));
         PROFILED("gateup_mfma", st,
-                 tg::launch_gateup_mfma(lp, s, mt, wmax, a->work, a->work_n, a->entries, a->xq, a->xd, a->xs, a->hq,
-                                        a->hd, a->hs, st));
+                 tg::launch_gateup_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.xq, c.xd, c.xs, c.hq,
+                                        c.hd, c.hs, st));
         PROFILED("down_mfma", st,
-                 tg::launch_down_mfma(lp, s, mt, wmax, a->work, a->work_n, a->entries, a->hq, a->hd, a->hs, a->D,
+                 tg::launch_down_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.hq, c.hd, c.hs, c.D,
                                       st));
-        PROFILED("combine", st, tg::launch_combine(a->D, a->w, T, s.H, s.k, resid, out, st));
+        PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
         return TG_OK;
     }
     PROFILED("group", st,
-             tg::launch_group(s, a->idx, n, a->counts, a->offsets, a->entries, a->work, a->work_n, st));
+             tg::launch_group(s, c.idx, n, c.counts, c.offsets, c.entries, c.work, c.work_n, st));
     PROFILED("gateup_grouped", st,
-             tg::launch_gateup_grouped(lp, s, n, a->work, a->work_n, a->entries, a->xq, a->xd, a->xs, a->hq, a->hd,
-                                       a->hs, st));
+             tg::launch_gateup_grouped(lp, s, n, c.work, c.work_n, c.entries, c.xq, c.xd, c.xs, c.hq, c.hd,
+                                       c.hs, st));
     PROFILED("down_grouped", st,
-             tg::launch_down_grouped(lp, s, n, a->work, a->work_n, a->entries, a->hq, a->hd, a->hs, a->D, st));
-    PROFILED("combine", st, tg::launch_combine(a->D, a->w, T, s.H, s.k, resid, out, st));
+             tg::launch_down_grouped(lp, s, n, c.work, c.work_n, c.entries, c.hq, c.hd, c.hs, c.D, st));
+    PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
     return TG_OK;
 }
 
@@ -553,59 +558,59 @@ static bool fused_usable(tg_arena *a, int T) {
 // j reads the partials buffer j % 2 and leaves the next layer's in the
 // other.  Layer j's top-k ids / weights go to idx + j * k_step (k_step 0:
 // every layer overwrites the same k entries).
-static int routed_layers(tg_arena *a, int l0, int n, const float *x, float *out, const float *resid, float eps,
+static int routed_layers(tg_arena *a, const Scratch &c, int l0, int n, const float *x, float *out, const float *resid, float eps,
                          int32_t *idx, float *w, int k_step, hipStream_t st) {
     const Shape &s = a->s;
     const size_t half = tg::dec_part_floats(s) / 2;
-    PROFILED("dec_part", st, tg::launch_dec_part(router_of(a, l0), x, s, a->dec_part, a->dec_ctl, n, st));
+    PROFILED("dec_part", st, tg::launch_dec_part(router_of(a, l0), x, s, c.dec_part, c.dec_ctl, n, st));
     for (int j = 0; j < n; j++) {
         const int l = l0 + j;
         const float *wr_next = j + 1 < n ? router_of(a, l + 1) : nullptr;
         PROFILED("layer", st,
                  tg::launch_layer_dec(a->experts + (size_t)l * s.LB, s, a->n_cu, j == 0 ? x : out, norm_of(a, l),
-                                      a->dec_part + (size_t)(j & 1) * half, wr_next,
-                                      a->dec_part + (size_t)((j + 1) & 1) * half, a->dec_hw, a->dec_ow, a->dec_ctl,
-                                      (uint32_t)(n - 1 - j), a->dec_err, j == 0 ? resid : out, out,
+                                      c.dec_part + (size_t)(j & 1) * half, wr_next,
+                                      c.dec_part + (size_t)((j + 1) & 1) * half, c.dec_hw, c.dec_ow, c.dec_ctl,
+                                      (uint32_t)(n - 1 - j), c.dec_err, j == 0 ? resid : out, out,
                                       idx + (size_t)j * k_step, w + (size_t)j * k_step, eps, st));
     }
     return TG_OK;
 }
 
-static int layer_kernels(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T, float eps,
+static int layer_kernels(tg_arena *a, const Scratch &c, int layer, const float *x, float *out, const float *resid, int T, float eps,
                          hipStream_t st) {
-    if (grouped_usable(a, T)) return layer_kernels_grouped(a, layer, x, out, resid, T, eps, st);
-    if (routed_usable(a, T)) return routed_layers(a, layer, 1, x, out, resid, eps, a->idx, a->w, 0, st);
+    if (grouped_usable(a, T)) return layer_kernels_grouped(a, c, layer, x, out, resid, T, eps, st);
+    if (routed_usable(a, T)) return routed_layers(a, c, layer, 1, x, out, resid, eps, c.idx, c.w, 0, st);
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
     PROFILED("route", st,
-             tg::launch_route_dec(router_of(a, layer), x, norm_of(a, layer), T, s, eps, a->dec_lw, a->dec_ctl,
-                                  a->dec_err, a->idx, a->w, a->xq, a->xd, a->xs, st));
+             tg::launch_route_dec(router_of(a, layer), x, norm_of(a, layer), T, s, eps, c.dec_lw, c.dec_ctl,
+                                  c.dec_err, c.idx, c.w, c.xq, c.xd, c.xs, st));
     if (fused_usable(a, T)) {
         PROFILED("experts", st,
-                 tg::launch_experts_fused(lp, s, a->n_cu, a->idx, a->w, a->xq, a->xd, a->xs, a->dec_hw, a->dec_ctl,
-                                          a->dec_err, resid, out, st));
+                 tg::launch_experts_fused(lp, s, a->n_cu, c.idx, c.w, c.xq, c.xd, c.xs, c.dec_hw, c.dec_ctl,
+                                          c.dec_err, resid, out, st));
         return TG_OK;
     }
-    PROFILED("gateup", st, tg::launch_gateup(lp, s, T, a->idx, a->xq, a->xd, a->xs, a->hq, a->hd, a->hs, st));
-    PROFILED("down", st, tg::launch_down(lp, s, T, a->idx, a->w, a->hq, a->hd, a->hs, resid, out, st));
+    PROFILED("gateup", st, tg::launch_gateup(lp, s, T, c.idx, c.xq, c.xd, c.xs, c.hq, c.hd, c.hs, st));
+    PROFILED("down", st, tg::launch_down(lp, s, T, c.idx, c.w, c.hq, c.hd, c.hs, resid, out, st));
     return TG_OK;
 }
 
-static int moe_layer_launch(tg_arena *a, int layer, const float *x, float *out, const float *resid, int T,
+static int moe_layer_launch(tg_arena *a, const Scratch &c, int layer, const float *x, float *out, const float *resid, int T,
                             int32_t *idx_out, float *w_out, float eps, hipStream_t st) {
     const Shape &s = a->s;
-    int rc = layer_kernels(a, layer, x, out, resid, T, eps, st);
+    int rc = layer_kernels(a, c, layer, x, out, resid, T, eps, st);
     if (rc) return rc;
-    if (idx_out) HIP_TRY(hipMemcpyAsync(idx_out, a->idx, sizeof(int32_t) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
-    if (w_out) HIP_TRY(hipMemcpyAsync(w_out, a->w, sizeof(float) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
+    if (idx_out) HIP_TRY(hipMemcpyAsync(idx_out, c.idx, sizeof(int32_t) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
+    if (w_out) HIP_TRY(hipMemcpyAsync(w_out, c.w, sizeof(float) * (size_t)T * s.k, hipMemcpyDeviceToDevice, st));
     return TG_OK;
 }
 
 // x <- x + MoE_l(x) for layers [l0, l0+n), in place.
-static int stack_launch(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
-    if (routed_usable(a, T)) return routed_layers(a, l0, n, x, x, x, eps, a->idx, a->w, 0, st);
+static int stack_launch(tg_arena *a, const Scratch &c, float *x, int T, int l0, int n, float eps, hipStream_t st) {
+    if (routed_usable(a, T)) return routed_layers(a, c, l0, n, x, x, x, eps, c.idx, c.w, 0, st);
     for (int l = l0; l < l0 + n; l++) {
-        int rc = layer_kernels(a, l, x, x, x, T, eps, st);
+        int rc = layer_kernels(a, c, l, x, x, x, T, eps, st);
         if (rc) return rc;
     }
     return TG_OK;
@@ -624,7 +629,7 @@ static bool graphs_enabled() {
 // (x, T, layer range, eps), or launched layer by layer while kernel timing
 // is on.
 static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
-    if (!graphs_enabled()) return stack_launch(a, x, T, l0, n, eps, st);
+    if (!graphs_enabled()) return stack_launch(a, a->sc, x, T, l0, n, eps, st);
     for (auto &g : a->graphs)
         if (g.x == x && g.T == T && g.layer0 == l0 && g.n == n && g.eps == eps) {
             HIP_TRY(hipGraphLaunch(g.exec, st));
@@ -633,7 +638,7 @@ static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hip
     if (!a->capture) HIP_TRY(hipStreamCreateWithFlags(&a->capture, hipStreamNonBlocking));
     tg_arena::Graph g{x, T, l0, n, eps, nullptr, nullptr};
     HIP_TRY(hipStreamBeginCapture(a->capture, hipStreamCaptureModeRelaxed));
-    int rc = stack_launch(a, x, T, l0, n, eps, a->capture);
+    int rc = stack_launch(a, a->sc, x, T, l0, n, eps, a->capture);
     hipError_t ec = hipStreamEndCapture(a->capture, &g.graph);
     if (rc) return rc;
     if (ec != hipSuccess) return set_err(TG_E_HIP, "graph capture failed: %s", hipGetErrorString(ec));
@@ -664,7 +669,7 @@ extern "C" int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x, floa
     if ((rc = check_tokens(n_tokens))) return rc;
     if (!x || !moe_out) return set_err(TG_E_INVALID, "x / moe_out is NULL");
     if ((rc = arena_scratch(a, n_tokens))) return rc;
-    return moe_layer_launch(a, layer, x, moe_out, nullptr, n_tokens, topk_idx, topk_w, eps, as_stream(stream));
+    return moe_layer_launch(a, a->sc, layer, x, moe_out, nullptr, n_tokens, topk_idx, topk_w, eps, as_stream(stream));
 }
 
 extern "C" int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out, int n_tokens,
@@ -677,11 +682,11 @@ extern "C" int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *m
     const Shape &s = a->s;
     size_t nx = (size_t)n_tokens * s.H;
     HIP_TRY(hipMemcpy(a->xbuf, x, nx * sizeof(float), hipMemcpyHostToDevice));
-    if ((rc = moe_layer_launch(a, layer, a->xbuf, a->obuf, nullptr, n_tokens, nullptr, nullptr, eps, nullptr)))
+    if ((rc = moe_layer_launch(a, a->sc, layer, a->xbuf, a->obuf, nullptr, n_tokens, nullptr, nullptr, eps, nullptr)))
         return rc;
     HIP_TRY(hipMemcpy(moe_out, a->obuf, nx * sizeof(float), hipMemcpyDeviceToHost));
-    if (topk_idx) HIP_TRY(hipMemcpy(topk_idx, a->idx, sizeof(int32_t) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
-    if (topk_w) HIP_TRY(hipMemcpy(topk_w, a->w, sizeof(float) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
+    if (topk_idx) HIP_TRY(hipMemcpy(topk_idx, a->sc.idx, sizeof(int32_t) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
+    if (topk_w) HIP_TRY(hipMemcpy(topk_w, a->sc.w, sizeof(float) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
     return TG_OK;
 }
 
@@ -710,11 +715,11 @@ extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int
     if (!topk_idx || !topk_w) return set_err(TG_E_INVALID, "topk_idx / topk_w is NULL");
     hipStream_t st = as_stream(stream);
     const size_t k = (size_t)a->s.k;
-    if (routed_usable(a, 1)) return routed_layers(a, layer0, n_layers, x, x, x, eps, topk_idx, topk_w, (int)k, st);
+    if (routed_usable(a, 1)) return routed_layers(a, a->sc, layer0, n_layers, x, x, x, eps, topk_idx, topk_w, (int)k, st);
     for (int l = 0; l < n_layers; l++) {
-        if ((rc = layer_kernels(a, layer0 + l, x, x, x, 1, eps, st))) return rc;
-        HIP_TRY(hipMemcpyAsync(topk_idx + l * k, a->idx, sizeof(int32_t) * k, hipMemcpyDeviceToDevice, st));
-        HIP_TRY(hipMemcpyAsync(topk_w + l * k, a->w, sizeof(float) * k, hipMemcpyDeviceToDevice, st));
+        if ((rc = layer_kernels(a, a->sc, layer0 + l, x, x, x, 1, eps, st))) return rc;
+        HIP_TRY(hipMemcpyAsync(topk_idx + l * k, a->sc.idx, sizeof(int32_t) * k, hipMemcpyDeviceToDevice, st));
+        HIP_TRY(hipMemcpyAsync(topk_w + l * k, a->sc.w, sizeof(float) * k, hipMemcpyDeviceToDevice, st));
     }
     return TG_OK;
 }
@@ -745,15 +750,100 @@ extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
     return TG_OK;
 }
 
+// ================================================================ no-alloc layer call
+// tg_moe_layer_q40_noalloc_dev runs tg_moe_layer_q40_dev's kernels with
+// their scratch in `scratch`, a fixed device array (each GPU holds its own
+// copy until the process ends), so the call allocates nothing.  In host code
+// the array's name is not a device address: each device's address comes
+// from hipGetSymbolAddress at set-up (tg_gpu_init, with that device
+// current) and only that address is used.  The array keeps the last call's
+// contents; the tagged exchange words and generations must start at zero
+// for a layout (shape, token count), so a call whose layout differs from the
+// previous call's on that device clears them first with a fill kernel on
+// its stream.  Calls that overlap on one device race.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+constexpr int NOALLOC_MAX_DEV = 64;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+struct NoAllocDev {
+    uint8_t *ptr = nullptr;  // this device's copy of `scratch`
+    uint64_t key = 0;        // layout of the last call (0: none since set-up)
+    size_t err_off = 0;      // its error word
+};
+static std::mutex g_na_mu;
+static NoAllocDev g_na[NOALLOC_MAX_DEV];
+
+// With `device` current: its address of the array.
+static int noalloc_setup(int device) {
+    if (device < 0 || device >= NOALLOC_MAX_DEV) return TG_OK;  // the no-alloc call refuses such devices
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (g_na[device].ptr) return TG_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_err(TG_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    g_na[device].ptr = static_cast<uint8_t *>(p);
+    g_na[device].key = 0;
+    return TG_OK;
+}
+
+static uint64_t noalloc_key(const Shape &s, int T) {
+    return (1ull << 63) | ((uint64_t)s.H << 46) | ((uint64_t)s.I << 32) | ((uint64_t)s.E << 24) |
+           ((uint64_t)s.k << 16) | (uint64_t)T;
+}
+
+extern "C" int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float *x, float *moe_out, int n_tokens,
+                                            int32_t *topk_idx, float *topk_w, float eps, void *stream) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    if (layer < 0 || layer >= a->L) return set_err(TG_E_INVALID, "layer %d out of range 0..%d", layer, a->L - 1);
+    int rc = check_tokens(n_tokens);
+    if (rc) return rc;
+    if (!x || !moe_out) return set_err(TG_E_INVALID, "x / moe_out is NULL");
+    const int dev = g_dev;
+    if (dev < 0) return set_err(TG_E_NODEVICE, "no device initialised (tg_gpu_init)");
+    if (dev >= NOALLOC_MAX_DEV) return set_err(TG_E_UNSUPPORTED, "device %d: no-alloc scratch covers devices 0..%d",
+                                               dev, NOALLOC_MAX_DEV - 1);
+    int cur = -1;
+    HIP_TRY(hipGetDevice(&cur));
+    if (cur != dev) HIP_TRY(hipSetDevice(dev));
+    if (!g_na[dev].ptr && (rc = noalloc_setup(dev))) return rc;
+    const size_t need = scratch_layout(a->s, n_tokens, nullptr, nullptr);
+    if (need > NOALLOC_SCRATCH_BYTES) {
+        int tmax = 0;
+        while (tmax < 65535 && scratch_layout(a->s, tmax + 1, nullptr, nullptr) <= NOALLOC_SCRATCH_BYTES) tmax++;
+        return set_err(TG_E_INVALID,
+                       "no-alloc layer call: %d tokens need %zu bytes of scratch, above its %zu (at most %d tokens at "
+                       "this shape)",
+                       n_tokens, need, NOALLOC_SCRATCH_BYTES, tmax);
+    }
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    NoAllocDev &d = g_na[dev];
+    Scratch c;
+    scratch_layout(a->s, n_tokens, d.ptr, &c);
+    hipStream_t st = as_stream(stream);
+    const uint64_t key = noalloc_key(a->s, n_tokens);
+    if (d.key != key) {  // exchange words of another layout: back to zero (a kernel, not a memset node)
+        HIP_TRY(tg::launch_fill(reinterpret_cast<float *>(d.ptr), 0.0f, c.dec_bytes / 4, st));
+        d.key = key;
+        d.err_off = (size_t)(reinterpret_cast<uint8_t *>(c.dec_err) - d.ptr);
+    }
+    return moe_layer_launch(a, c, layer, x, moe_out, nullptr, n_tokens, topk_idx, topk_w, eps, st);
+}
+
 extern "C" int tg_arena_status(tg_arena *a) {
     if (!a) return set_err(TG_E_INVALID, "arena is NULL");
     int rc = ensure_device();
     if (rc) return rc;
     HIP_TRY(hipDeviceSynchronize());
-    if (a->dec_err) {
+    if (a->sc.dec_err) {
         uint32_t v = 0;
-        HIP_TRY(hipMemcpy(&v, a->dec_err, sizeof v, hipMemcpyDeviceToHost));
+        HIP_TRY(hipMemcpy(&v, a->sc.dec_err, sizeof v, hipMemcpyDeviceToHost));
         if (v != 0u) return set_err(TG_E_HIP, "decode routing: a device-side poll ran out of tries");
+    }
+    if (g_dev >= 0 && g_dev < NOALLOC_MAX_DEV && g_na[g_dev].key) {  // the no-alloc call's error word
+        uint32_t v = 0;
+        HIP_TRY(hipMemcpy(&v, g_na[g_dev].ptr + g_na[g_dev].err_off, sizeof v, hipMemcpyDeviceToHost));
+        if (v != 0u) return set_err(TG_E_HIP, "no-alloc layer call: a device-side poll ran out of tries");
     }
     return TG_OK;
 }
