@@ -40,9 +40,13 @@ def build() -> Path:
 def lib():
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            build()
-        L = ctypes.CDLL(str(LIB_PATH))
+        alt = os.environ.get("TG_ORACLE_LIB")  # a sanitizer build of the same source (tests/test_sanitizers.py)
+        if alt:
+            L = ctypes.CDLL(alt)
+        else:
+            if not LIB_PATH.exists():
+                build()
+            L = ctypes.CDLL(str(LIB_PATH))
         sigs = {
             "tgo_f16_to_f32": (_F, [ctypes.c_uint16]),
             "tgo_f16_to_f32_n": (None, [_P, _SZ, _P]),

@@ -14,6 +14,7 @@ the MoE path can silently run without the GPU kernels.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 VP = ctypes.c_void_p
@@ -141,7 +142,10 @@ def require_lib():
     """The loaded library, or an ImportError naming the missing build."""
     global _LIB
     if _LIB is None:
-        path = find_library()
+        # TINYGIANT_LIB names another build of this library (the sanitizer
+        # build of tests/test_sanitizers.py); find_library keeps the
+        # reference's search order
+        path = os.environ.get("TINYGIANT_LIB") or find_library()
         if path is None:
             raise ImportError(
                 "libtinygiant.so (gfx950) is not built; run "

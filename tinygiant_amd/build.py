@@ -69,5 +69,30 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+SAN = PKG / "_san"
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """The library with AddressSanitizer and UndefinedBehaviorSanitizer on
+    its host code only (the gfx950 code is built as usual, without them),
+    into _san/.  For tests/test_sanitizers.py, which preloads clang's shared
+    ASan runtime.  Rebuilt only when a source is newer than the library."""
+    SAN.mkdir(exist_ok=True)
+    lib = SAN / "libtinygiant.so"
+    deps = [CSRC / f for f in SOURCES] + list(CSRC.glob("*.h")) + [ROOT / "include" / "tinygiant.h", Path(__file__)]
+    if lib.exists() and lib.stat().st_mtime > max(d.stat().st_mtime for d in deps):
+        return lib
+    host = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+            "-Xarch_host", "-g", "-Xarch_host", "-shared-libsan"]
+    objs = []
+    for src in SOURCES:
+        obj = SAN / (Path(src).stem + ".o")
+        _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), *host, "-c", CSRC / src, "-o", obj], verbose)
+        objs.append(obj)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *host, *objs, "-o", lib], verbose)
+    return lib
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
