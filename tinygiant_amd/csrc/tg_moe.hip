@@ -1101,6 +1101,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
 // generation `back` steps before it.  Polls are bounded; when one runs out
 // the block sets *err and writes NaN rows (and NaN partials).
 constexpr int LD_PC = 16;  // float4 of partials per load round of one thread
+constexpr int LD_EMAX = 128;  // experts per layer of the routed launch (keys padded to this)
 
 struct LdArgs {
     const uint8_t *layer_pl;
@@ -1157,17 +1158,79 @@ TG_DEV LdRole ld_role(int b, int NB, int GQ) {
 }
 
 // LDS: the gate/up part, then the down part (k_experts' layout for rd rows),
-// the group's RG combined rows and the next router's columns [E][RG + 1].
+// the group's RG combined rows and the next router's columns [E][RG + 1] ...
+// ... and one arrival flag per gate/up unit (nonzero once that unit's h
+// block is in LDS).
 __host__ __device__ inline size_t ld_lds_bytes(const Shape &s, int rd) {
-    return fx_down_off(s) + fx_down_lds_bytes(s.k, s.I, s.nbI, rd) + 4 * (size_t)RG + 4 * (size_t)s.E * (RG + 1);
+    return fx_down_off(s) + fx_down_lds_bytes(s.k, s.I, s.nbI, rd) + 4 * (size_t)RG + 4 * (size_t)s.E * (RG + 1) +
+           4 * (size_t)s.k * s.nbI;
+}
+
+// Index maps of one thread's weight items, formed at launch (they do not
+// depend on the routing), so the phases after the routing only add the
+// selected expert's base and read LDS at precomputed offsets.  Gate/up
+// unit (m, j): item u is p = u * FX_THREADS + tid (clamped) of the unit's
+// 2 * GU_ROWS * nbH blocks, row rd = p >> lnbH (gate rows 0..31, up rows
+// 32..63), column block cb = p & (nbH - 1).
+template <int UG>
+struct LdGu {
+    uint32_t off[UG];  // byte offset of the nibbles inside the expert
+    uint32_t soff[UG]; // byte offset of the scale
+    uint32_t pk[UG];   // U index << 8 | cb
+};
+
+template <int UG>
+TG_DEV void ld_gu_map(const Shape &s, int m, int lnbh, int usth, LdGu<UG> &M) {
+    constexpr int RT = GU_ROWS;
+    const int nbh = s.nbH, items = 2 * RT * nbh, tid = threadIdx.x;
+    const uint32_t ntb = (uint32_t)s.I * nbh;
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        const int p = min(u * FX_THREADS + tid, items - 1);
+        const int rd = p >> lnbh, cb = p & (nbh - 1);
+        const int mat = rd >= RT ? 1 : 0;
+        const uint32_t idx = (uint32_t)((m * RT + rd - mat * RT) * nbh + cb);
+        const uint32_t tb = mat ? (uint32_t)s.GB : 0u;
+        M.off[u] = tb + 16u * idx;
+        M.soff[u] = tb + 16u * ntb + 2u * idx;
+        M.pk[u] = ((uint32_t)(rd * usth + cb) << 8) | (uint32_t)cb;
+    }
+}
+
+template <int UG>
+TG_DEV void ld_gu_load(const uint8_t *ex, const LdGu<UG> &M, FxGu<UG> &g) {
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        g.wv[u] = *reinterpret_cast<const uint4 *>(ex + M.off[u]);
+        g.dv[u] = *reinterpret_cast<const uint16_t *>(ex + M.soff[u]);
+    }
+}
+
+// The unit's block dots into U (LDS), at the precomputed offsets.
+template <int UG>
+TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uint8_t *smem) {
+    const int nbh = s.nbH, H = s.H, items = 2 * GU_ROWS * nbh, tid = threadIdx.x;
+    const int8_t *xq = reinterpret_cast<const int8_t *>(smem);
+    const int *xs = reinterpret_cast<const int *>(xq + H + 4 * round4(nbh));
+    float *U = reinterpret_cast<float *>(smem + H + 8 * round4(nbh));
+    lds_barrier();  // Q8_0 x in LDS; the previous unit's U read
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        if (u * FX_THREADS + tid < items) {
+            const int cb = (int)(M.pk[u] & 255u), ui = (int)(M.pk[u] >> 8);
+            const int S = dot_q4_q8(g.wv[u], reinterpret_cast<const int *>(xq + cb * QK)) - 8 * xs[cb];
+            U[ui] = (float)S * h2f((uint16_t)at_use(g.dv[u]));
+        }
+    }
+    lds_barrier();
 }
 
 template <int UG, int UD>
 __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ __align__(16) uint64_t keys[MAX_E];
-    __shared__ int rcnt[MAX_E];
-    __shared__ float slog[MAX_E];
+    __shared__ __align__(16) uint64_t keys[LD_EMAX];
+    __shared__ int rcnt[LD_EMAX];
+    __shared__ float slog[LD_EMAX];
     __shared__ int sidx[MAX_K];
     __shared__ float sw[MAX_K];
     __shared__ float ssc;
@@ -1175,7 +1238,8 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     const int tid = threadIdx.x, k = s.k, E = s.E, H = s.H, I = s.I, G = H / RG, RD = A.rd, GQ = RG / RD;
     const int lrd = __builtin_ctz(RD);  // RD is a power of two
     const int nb = s.nbI, nbp = round4(nb), ust = round4(nb) + 4;
-    const int ng = (I / GU_ROWS) * k, NB = gridDim.x;
+    const int lnbh = __builtin_ctz(s.nbH), usth = round4(s.nbH) + 4;  // nbH is a power of two
+    const int ng = (I / GU_ROWS) * k, NB = gridDim.x, mI = I / GU_ROWS;
     const LdRole role = ld_role(blockIdx.x, NB, GQ);
     const int r0 = role.chunk * RD;
     const uint32_t tag =
@@ -1185,10 +1249,9 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     uint64_t *ow = A.ow + (size_t)(tag & 1u) * H;
     const bool nx = role.owner && A.wr_next;
 
-    // 0. loads that depend on nothing: x (blocks with gate/up units), the
-    //    residual rows, (owners) the next router's columns of the group, then
-    //    the partials
-    // x is read by the threads that quantize it (waves 1.., H / 8 of them)
+    // 0. loads that depend on nothing: x and the norm weight (the threads
+    //    that quantize it, waves 1..), the residual rows, (owners) the next
+    //    router's columns of the group, then the partials
     float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa, ga = xa, gb = xa;
     const int u0 = role.rank;  // first gate/up unit
     const int qt = tid - WAVE;
@@ -1205,10 +1268,13 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     if (nx && tid < E * (RG / 4))
         wn = reinterpret_cast<const float4 *>(A.wr_next + (size_t)(tid >> 3) * H + (size_t)role.group * RG)[tid & 7];
     if (tid == 0) bad = 0;
+    // arrival flags of the h blocks (LDS starts undefined): cleared before
+    // the first barrier, set by the polling waves, read by the down dots
+    int *uflag = reinterpret_cast<int *>(smem + ld_lds_bytes(s, RD) - 4 * (size_t)ng);
+    for (int i = tid; i < ng; i += FX_THREADS) uflag[i] = 0;
 
     // 1. routing: thread e <= E adds row e of the partials in ascending group
-    //    order (LD_PC float4 loaded per round, all before the adds), then
-    //    scale, rank, softmax
+    //    order (LD_PC float4 loaded per round, all before the adds)
     if (tid <= E) {
         const float4 *row = reinterpret_cast<const float4 *>(A.part_in + (size_t)tid * G);
         float tot = 0.0f;
@@ -1227,19 +1293,64 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         else
             ssc = rms_scale(tot, H, A.eps);
     }
-    if (tid < k) sidx[tid] = 0;
+    // while the partials load: the index maps of this thread's weight items
+    // (with deep unit loads, UG > 4, the unit map is formed after the routing
+    // and the down map after the units, so the maps and the loads they
+    // address never hold registers at once)
+    constexpr bool DOWN_FIRST = UG <= 4;
+    LdGu<UG> gm;
+    if (DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
+    // down item u: byte offset of its row block; (slot * RD + row) << 16 | block.
+    // Every thread takes down items, the polling waves included: their polls
+    // then start when their down loads have landed (vmcnt retires in order),
+    // which keeps the poll traffic off the fabric while the down stream is
+    // in flight (measured faster than keeping the polling waves free).
+    const int items = k * RD * nb;
+    const int dthr = FX_THREADS, dt = tid;  // every thread; the polls wait for these loads, which thins them
+    uint32_t doff[UD], dpk[UD];
+    auto down_map = [&]() {
+#pragma unroll
+        for (int u = 0; u < UD; u++) {
+            const int p = min(u * dthr + max(dt, 0), items - 1);
+            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
+            const int row = r0 + (rdi & (RD - 1));
+            doff[u] = (uint32_t)(2 * s.GB) + 16u * (uint32_t)(row * nb + b);
+            dpk[u] = ((uint32_t)rdi << 16) | (uint32_t)b;
+        }
+    };
+    if (DOWN_FIRST) down_map();
     __syncthreads();
     const float sc = ssc;
-    if (tid < E) {
-        const float l = slog[tid] * sc;
-        slog[tid] = l;
-        keys[tid] = rank_key(l, tid);
+    // keys (the experts beyond E rank below every logit)
+    if (tid < LD_EMAX) {
+        uint64_t key = 0;
+        if (tid < E) {
+            const float l = slog[tid] * sc;
+            slog[tid] = l;
+            key = rank_key(l, tid);
+        }
+        keys[tid] = key;
         rcnt[tid] = 0;
     }
-    __syncthreads();
-    rank_topk(keys, E, k, sidx, rcnt);  // ends with a barrier: sidx is set
+    lds_barrier();
+    // rank = number of larger keys: thread (e, part) = (tid % 128, tid / 128)
+    // counts among keys [16 part, 16 part + 16), LDS broadcasts
+    {
+        const int e = tid & (LD_EMAX - 1), part = tid >> 7;
+        const uint64_t my = keys[e];
+        const ulonglong2 *kp = reinterpret_cast<const ulonglong2 *>(keys + 16 * part);
+        ulonglong2 kk[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) kk[q] = kp[q];
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) cnt += (kk[q].x > my ? 1 : 0) + (kk[q].y > my ? 1 : 0);
+        if (e < E && cnt) atomicAdd(rcnt + e, cnt);
+    }
+    lds_barrier();
+    if (tid < E && rcnt[tid] < k) sidx[rcnt[tid]] = tid;
     // the first unit's weights are in flight while wave 0 forms the softmax
-    // and waves 1..4 Q8_0((x * s) * g) into the gate/up LDS layout; the
+    // and waves 1.. Q8_0((x * s) * g) into the gate/up LDS layout; the
     // normed x is formed (and pinned) before the unit loads are issued, so
     // the Q8_0 waits for no load
     float xsv[8];
@@ -1253,8 +1364,29 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     // landed long ago: an explicit wait for them here leaves the unit's
     // loads as the only ones in flight, so nothing below waits for those
     __builtin_amdgcn_s_waitcnt(VMCNT0);
+    lds_barrier();  // sidx
+    // this block's down weights: issued after the first unit's publication
+    // with shallow unit loads (UG <= 4; issued with the unit's loads they
+    // slow the unit's stream by as much as they add), after the units with
+    // deep ones
+    const size_t ntb = (size_t)H * nb;
+    uint4 wv[UD];
+    uint32_t dv[UD];
+    auto down_loads = [&]() {
+        if (dt >= 0) {  // whole waves; clamped, unbranched loads inside
+#pragma unroll
+            for (int u = 0; u < UD; u++) {
+                const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
+                const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
+                dv[u] = reinterpret_cast<const uint16_t *>(ex + 2 * s.GB + ntb * 16)[bi];
+            }
+        }
+        __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
+    };
     FxGu<UG> g;
-    if (u0 < ng) fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
+    if (!DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
+    if (u0 < ng) ld_gu_load<UG>(A.layer_pl + (size_t)sidx[u0 / mI] * s.EB, gm, g);
     if (tid < WAVE) {
         const float wj = topk_softmax_lane(slog, sidx, k);
         if (tid < k) {
@@ -1270,42 +1402,24 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     float *xd = reinterpret_cast<float *>(xq + H);
     int *xs = reinterpret_cast<int *>(xd + round4(s.nbH));
     if (qon) q8_group8(xsv, true, qt * 8, xq, xd, xs);
-    lds_barrier();  // sw, Q8_0 x (the unit's loads stay in flight)
 
     if (u0 < ng) {
-        fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
+        ld_gu_dots<UG>(s, gm, g, smem);
         fx_gu_publish(s, u0, tag, hw, smem);
     }
-    // 2. this block's down weights (item p on thread p % FX_THREADS; the
-    //    polling waves' loads land long before the first h word does) and
-    //    further gate/up units.  With deep unit loads (UG > 4) the down loads
-    //    follow the units, so the two never hold registers at once.
-    const size_t ntb = (size_t)H * nb;
-    const int items = k * RD * nb;
-    uint4 wv[UD];
-    uint32_t dv[UD];
-    auto down_loads = [&]() {
-#pragma unroll
-        for (int u = 0; u < UD; u++) {  // clamped, unbranched loads (as k_gateup)
-            const int p = min(u * FX_THREADS + tid, items - 1);
-            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int jj = rdi >> lrd, row = r0 + (rdi - (jj << lrd));
-            const uint8_t *tb = A.layer_pl + (size_t)sidx[jj] * s.EB + 2 * s.GB;
-            const size_t o = (size_t)row * nb + b;
-            wv[u] = reinterpret_cast<const uint4 *>(tb)[o];
-            dv[u] = reinterpret_cast<const uint16_t *>(tb + ntb * 16)[o];
-        }
-        __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
-    };
-    constexpr bool DOWN_FIRST = UG <= 4;
     if (DOWN_FIRST) down_loads();
+    // 2. further gate/up units
     for (int unit = u0 + NB; unit < ng; unit += NB) {
-        fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
-        lds_barrier();  // wave 0 has read the previous unit's LDS
-        fx_gu_dots<UG>(nullptr, nullptr, nullptr, s, g, smem);
+        LdGu<UG> gm2;
+        ld_gu_map<UG>(s, unit % mI, lnbh, usth, gm2);
+        ld_gu_load<UG>(A.layer_pl + (size_t)sidx[unit / mI] * s.EB, gm2, g);
+        ld_gu_dots<UG>(s, gm2, g, smem);
         fx_gu_publish(s, unit, tag, hw, smem);
     }
-    if (!DOWN_FIRST) down_loads();
+    if (!DOWN_FIRST) {
+        down_map();
+        down_loads();
+    }
 
     // 3. waves 0..2 read h of every unit into LDS (after the gate/up part,
     //    which wave 0 may still be reading); then the down rows
@@ -1327,6 +1441,8 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
             hd[jj * nbp + b] = __uint_as_float(pay[8]);
             hs[jj * nbp + b] = (int)pay[9];
             if (!ok) bad = 1;
+            // release: the copies above are in LDS before the flag is
+            __hip_atomic_store(uflag + unit, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
     if (nx && tid < E * (RG / 4)) {
@@ -1336,25 +1452,53 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
         wl[e * (RG + 1) + c + 2] = wn.z;
         wl[e * (RG + 1) + c + 3] = wn.w;
     }
-    __syncthreads();
+    // each down dot starts once its unit's h block is in LDS, so the dots run
+    // while later units are still on their way.  The polling waves finish
+    // every poll of theirs (bounded) before their own dots, so each flag is
+    // set; the wait here is bounded too.
 #pragma unroll
     for (int u = 0; u < UD; u++) {
-        const int p = u * FX_THREADS + tid;
-        if (p < items) {
-            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int jj = rdi >> lrd;
-            const int S = dot_q4_q8(wv[u], reinterpret_cast<const int *>(hq + (size_t)jj * I + b * QK)) -
-                          8 * hs[jj * nbp + b];
-            U[rdi * ust + b] = (float)S * h2f((uint16_t)at_use(dv[u]));
+        if (dt >= 0 && u * dthr + dt < items) {
+            const int rdi = (int)(dpk[u] >> 16), b = (int)(dpk[u] & 0xFFFFu), jj = rdi >> lrd;
+            const int unit = (int)__umul24((uint32_t)jj, (uint32_t)nb) + b;
+            uint32_t tries = 0;
+            while (__hip_atomic_load(uflag + unit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
+                if (++tries >= RD_SPIN_LIMIT) {
+                    bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            const int4 *h4 = reinterpret_cast<const int4 *>(hq + __umul24((uint32_t)jj, (uint32_t)I) + b * QK);
+            const int4 ha = h4[0], hb = h4[1];
+            const int hx[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+            const int S = dot_q4_q8(wv[u], hx) - 8 * hs[(int)__umul24((uint32_t)jj, (uint32_t)nbp) + b];
+            U[(int)__umul24((uint32_t)rdi, (uint32_t)ust) + b] = (float)S * h2f((uint16_t)at_use(dv[u]));
         }
     }
-    __syncthreads();
-    if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid >> lrd) * nbp, nb);
-    __syncthreads();
-    // combine; a non-owner publishes its rows to the group's owner
+    lds_barrier();
+    // chains and combine: with k * RD <= 64 one wave holds every (slot, row)
+    // chain and gathers a row's k slots by lane shuffles
+    float o = 0.0f;
+    if (k * RD <= WAVE) {
+        if (tid < WAVE) {
+            const int t = tid < k * RD ? tid : 0;
+            const float dvl = chain4(U + t * ust, hd + (t >> lrd) * nbp, nb);
+            const int r = tid & (RD - 1);
+            float acc = 0.0f;
+            for (int c = k - 1; c >= 0; c--) acc = __builtin_fmaf(sw[c], __shfl(dvl, c * RD + r, WAVE), acc);
+            o = A.resid ? rv + acc : acc;
+        }
+    } else {
+        if (tid < k * RD) D[tid] = chain4(U + tid * ust, hd + (tid >> lrd) * nbp, nb);
+        lds_barrier();
+        if (tid < RD) {
+            const float acc = combine_slots(sw, D, RD, k, tid);
+            o = A.resid ? rv + acc : acc;
+        }
+    }
+    // a non-owner publishes its rows to the group's owner
     if (tid < RD) {
-        const float acc = combine_slots(sw, D, RD, k, tid);
-        float o = A.resid ? rv + acc : acc;
         if (bad) o = __builtin_nanf("");
         A.out[r0 + tid] = o;
         if (A.wr_next) {
@@ -2064,6 +2208,7 @@ bool layer_dec_ok(const Shape &s, int n_cu) {
     if (!rd) return false;
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
     return decode_shape_ok(s) && s.H % RG == 0 && (s.H / RG) % 4 == 0 && s.E * (RG / 4) <= FX_THREADS &&
+           s.E <= LD_EMAX && (s.nbH & (s.nbH - 1)) == 0 && s.nbH <= 256 && s.nbI < 65536 &&
            s.E < 256 && s.k * rd <= FX_THREADS && s.H / 8 + WAVE <= FX_THREADS && ug <= 8 && ld_ud(s, rd) <= 6 &&
            RG - rd <= FX_THREADS && ld_lds_bytes(s, rd) <= 160 * 1024;
 }
