@@ -31,6 +31,8 @@ Other workloads (--workload):
                and 8 Q4_K experts, one token.
   output-head  the step after the layers: logits of the 151936 x 2048 fp32
                head (resident) and the greedy token, one call per step.
+  sample       temperature / top-p sampling of the next token over 151936
+               resident logits, one call per step.
 
 Prints one JSON line: tok/s (value), expert-weight HBM GB/s, the roofline
 of the dominant kernel (HIP events on its launch stream) and the CPU oracle
@@ -1032,11 +1034,87 @@ def run_output_head(args, torch, call):
     }
 
 
+def run_sample(args, torch, call):
+    """Next-token sampling after the head (engine.py:348-357 with the
+    reference's defaults T 0.7, top_p 0.9) at the Qwen3 vocabulary 151936, on
+    logits resident in HBM: one step = one tg_sampler_run (its launches and
+    the token copied back).  Logits N(0, 2.5): about a hundred candidates.
+    The same call with top_p 1.0 (every token a candidate: the global-memory
+    sort) is timed beside it."""
+    from tinygiant_amd._lib import require_lib
+    from oracle import sample as S  # the checker, timed as the CPU baseline
+    lib = require_lib()
+    V, T, TOP_P = 151936, 0.7, 0.9
+    rng = np.random.default_rng(args.seed)
+    logits = [(rng.standard_normal(V) * 2.5).astype(np.float32) for _ in range(8)]
+    dl = [torch.from_numpy(l).to("cuda:0") for l in logits]
+    torch.cuda.synchronize()
+    s = lib.tg_sampler_create(V)
+    if not s:
+        raise RuntimeError(f"tg_sampler_create: {lib.tg_last_error().decode()}")
+    tok = ctypes.c_int32()
+    us = rng.random(64)
+
+    def step(i, top_p=TOP_P):
+        rc = lib.tg_sampler_run(s, ctypes.c_void_p(dl[i % 8].data_ptr()), 1, np.float32(T), top_p, us[i % 64],
+                                ctypes.byref(tok), None)
+        if rc:
+            raise RuntimeError(f"tg_sampler_run: {lib.tg_last_error().decode()}")
+        return tok.value
+
+    for i in range(8):  # the same tokens as the numpy restatement
+        ref = S.sample(logits[i], T, TOP_P, us[i])[0]
+        assert step(i) == ref, "GPU token differs from the restatement"
+    K, W_ = args.steps or 200, 10 if args.warmup is None else args.warmup
+    log(f"warmup {W_} calls")
+    for i in range(W_):
+        step(i)
+    log(f"timing {K} calls")
+    times = []
+    for i in range(K):
+        t0 = time.perf_counter()
+        step(i)
+        times.append(time.perf_counter() - t0)
+    times_all = []
+    for i in range(max(K // 4, 10)):
+        t0 = time.perf_counter()
+        step(i, 1.0)
+        times_all.append(time.perf_counter() - t0)
+    call("tg_prof_enable", 1)
+    for i in range(16):
+        step(i)
+    call("tg_prof_enable", 0)
+    kern = kernel_times(call, ("sample",))
+    n_k, ms_k = kern["sample"]
+    med = float(np.median(times))
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (numpy, the reference's sampling code restated)")
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0):
+            S.sample(logits[n % 8], T, TOP_P, us[n % 64], exp="numpy")
+            n += 1
+        cpu_s = (time.perf_counter() - t1) / n
+        cpu = {"value": round(1.0 / cpu_s, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"{n} draws of engine.py:348-357 in numpy (float32 exp, argsort of 151936) on this host"}
+    lib.tg_sampler_destroy(s)
+    return {
+        "metric": "next-token sampling tok/s (T 0.7, top_p 0.9, vocab 151936, logits resident)",
+        "value": round(1.0 / med, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W_,
+        "ms_per_step": round(med * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (N(0, 2.5) logits, uniform draws)",
+        "config": {"workload": "qwen3-sampling", "vocab": V, "temperature": T, "top_p": TOP_P},
+        "launches_us": round(ms_k / max(n_k, 1) * 1e3, 2),
+        "top_p_1_ms": round(float(np.median(times_all)) * 1e3, 4),
+        "cpu_baseline": cpu,
+    }
+
+
 WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill": run_prefill,
              "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
              "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
              "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe, "legacy-layer": run_legacy_layer,
-             "output-head": run_output_head}
+             "output-head": run_output_head, "sample": run_sample}
 
 
 def main() -> int:

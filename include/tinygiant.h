@@ -310,6 +310,32 @@ tg_head *tg_head_create(const float *W, const float *norm_w, int vocab, int embe
 int tg_head_forward(tg_head *h, const float *x, float eps, float *logits, int32_t *token);
 void tg_head_destroy(tg_head *h);
 
+/* Next-token sampling (tinygiant/engine.py:348-359, which samples in numpy
+ * with np.random.choice).  temperature > 0: probs = exp((logits - max) / T)
+ * normalised, the smallest prefix of the descending order (ties by
+ * ascending id) whose float32 running sum reaches top_p (the crossing token
+ * included; every token when it never does), those renormalised, and the
+ * first one whose float64 cdf exceeds u.  u is the draw's uniform in [0, 1):
+ * np.random.choice takes one RandomState.random_sample() per draw, so passing
+ * that value reproduces the reference's token.  exp is the correctly rounded
+ * fp32 value (numpy's float32 exp is within 2 ulp of it); every later step
+ * follows numpy's operations and summation orders.  temperature <= 0 or NaN:
+ * the greedy argmax (engine.py:359), and top_p, u and probs are unused.
+ * Vocabularies up to 524288 tokens.  logits are a device pointer when
+ * logits_on_device, else host memory; probs (host, vocab floats, may be NULL)
+ * receives the normalised probabilities.  Calls return 0 or a negative
+ * TG_E_* code: NaN or +inf logits, or all -inf, are TG_E_INVALID like a u
+ * outside [0, 1).  No counterpart function in the reference. */
+typedef struct tg_sampler tg_sampler;
+tg_sampler *tg_sampler_create(int vocab);
+int tg_sampler_run(tg_sampler *s, const float *logits, int logits_on_device, float temperature, double top_p,
+                   double u, int32_t *token, float *probs);
+void tg_sampler_destroy(tg_sampler *s);
+/* tg_head_forward's logits sampled on the device (no logits copy needed;
+ * logits may still be NULL or receive them). */
+int tg_head_sample(tg_head *h, const float *x, float eps, float temperature, double top_p, double u,
+                   float *logits, int32_t *token);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,7 @@ CI = ctypes.c_int
 CF = ctypes.c_float
 SZ = ctypes.c_size_t
 U64 = ctypes.c_uint64
+CD = ctypes.c_double
 
 # (name, restype, argtypes) of the reference ABI, tinygiant/_lib.py:39-74
 LEGACY_SYMBOLS = [
@@ -89,6 +90,10 @@ NEW_SYMBOLS = [
     ("tg_head_create", VP, [VP, VP, CI, CI]),
     ("tg_head_forward", CI, [VP, VP, CF, VP, VP]),
     ("tg_head_destroy", None, [VP]),
+    ("tg_sampler_create", VP, [CI]),
+    ("tg_sampler_run", CI, [VP, VP, CI, CF, CD, CD, VP, VP]),
+    ("tg_sampler_destroy", None, [VP]),
+    ("tg_head_sample", CI, [VP, VP, CF, CF, CD, CD, VP, VP]),
 ]
 
 ALL_SYMBOLS = LEGACY_SYMBOLS + UNREGISTERED_SYMBOLS + NEW_SYMBOLS

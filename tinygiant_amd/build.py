@@ -16,7 +16,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtinygiant.so"
-SOURCES = ["tg_kernels.hip", "tg_moe.hip", "tg_mfma.hip", "tg_legacy.hip", "tg_abi.hip"]
+SOURCES = ["tg_kernels.hip", "tg_moe.hip", "tg_mfma.hip", "tg_legacy.hip", "tg_sample.hip", "tg_abi.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("TG_OFFLOAD_ARCH", "gfx950")

@@ -1599,14 +1599,19 @@ extern "C" void tg_transformer_layer(const float *wq, const float *wk, const flo
 // `@`; here W stays resident in HBM behind a handle, the product follows the
 // reference's own fp32 matvec order (tg_f32_matvec, libtinygiant.c:299-318)
 // and the norm tg_rms_norm's (:322-340).
+struct tg_sampler;
+static void sampler_free(tg_sampler *s);
+
 struct tg_head {
     int vocab, embed, dev;
     float *W, *nw, *x, *xn, *logits, *pv;
     int *pi, *tok;
+    tg_sampler *smp;  // created by the first tg_head_sample
 };
 
 static void head_free(tg_head *h) {
     if (!h) return;
+    sampler_free(h->smp);
     for (void *p : {(void *)h->W, (void *)h->nw, (void *)h->x, (void *)h->xn, (void *)h->logits, (void *)h->pv,
                     (void *)h->pi, (void *)h->tok})
         if (p) (void)hipFree(p);
@@ -1621,7 +1626,7 @@ extern "C" tg_head *tg_head_create(const float *W, const float *norm_w, int voca
     std::lock_guard<std::mutex> lk(g_lg_mu);
     if (lg_reserve(0)) return nullptr;
     tg_head *h = new tg_head{vocab, embed, g_lg_dev, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                             nullptr};
+                             nullptr, nullptr};
     const size_t wb = sizeof(float) * (size_t)vocab * embed, eb = sizeof(float) * (size_t)embed;
     auto alloc = [&](void **p, size_t n) { return hipMalloc(p, n) == hipSuccess; };
     if (!alloc((void **)&h->W, wb) || !alloc((void **)&h->nw, eb) || !alloc((void **)&h->x, eb) ||
@@ -1661,4 +1666,152 @@ extern "C" int tg_head_forward(tg_head *h, const float *x, float eps, float *log
     PROFILED("head_argmax", st, tg::launch_argmax(h->logits, h->vocab, h->pv, h->pi, h->tok, st));
     if (logits) HIP_TRY(hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)h->vocab, hipMemcpyDeviceToHost, st));
     return lg_finish(token, h->tok, sizeof(int32_t));
+}
+
+// ------------------------------------------------------------- sampling
+// engine.py:348-359: the next token from the logits, by temperature and
+// top-p (tg_sample.hip) when temperature > 0, else the greedy argmax.  The
+// reference draws with np.random.choice; the caller passes that draw's
+// uniform u in [0, 1) (choice takes one RandomState.random_sample() per
+// draw), so the same u gives the reference's token.  Device buffers for one
+// vocabulary are allocated once per sampler.
+struct tg_sampler {
+    int vocab, dev;
+    tg::SmpBufs b;
+    float *dl;            // logits copied from the host
+    float *pv;            // greedy argmax partials
+    int *pi, *tok;
+    void *mem;
+    tg::SmpCtl *hctl;     // pinned host copy of b.ctl
+};
+
+static void sampler_free(tg_sampler *s) {
+    if (!s) return;
+    if (s->mem) (void)hipFree(s->mem);
+    if (s->hctl) (void)hipHostFree(s->hctl);
+    delete s;
+}
+
+// Caller holds g_lg_mu and has run lg_reserve.
+static int sampler_new(int vocab, tg_sampler **out) {
+    *out = nullptr;
+    if (vocab <= 0 || vocab > tg::SMP_VMAX)
+        return set_err(TG_E_INVALID, "sampler: vocab %d outside 1..%d", vocab, tg::SMP_VMAX);
+    static bool prepared = false;
+    if (!prepared) {
+        if (tg::sample_prepare() != hipSuccess) {
+            (void)hipGetLastError();
+            return set_err(TG_E_HIP, "sampler: LDS attribute of the sort kernel");
+        }
+        prepared = true;
+    }
+    tg_sampler *s = new tg_sampler{};
+    s->vocab = vocab;
+    s->dev = g_lg_dev;
+    size_t nk = 16384;
+    while (nk < (size_t)vocab) nk <<= 1;
+    const size_t V = (size_t)vocab;
+    LgCarve c{nullptr};
+    for (int pass = 0; pass < 2; pass++) {
+        c = LgCarve{pass ? (uint8_t *)s->mem : nullptr};
+        s->b.pmax = c.take<float>(sizeof(float) * 256);
+        s->b.pbad = c.take<int>(sizeof(int) * 256);
+        s->b.p = c.take<float>(sizeof(float) * V);
+        s->b.q = c.take<float>(sizeof(float) * V);
+        s->b.sums = c.take<float>(sizeof(float) * 64);
+        s->b.hcnt = c.take<uint32_t>(sizeof(uint32_t) * tg::SMP_BUCKETS);
+        s->b.hmass = c.take<unsigned long long>(sizeof(unsigned long long) * tg::SMP_BUCKETS);
+        s->b.keys = c.take<unsigned long long>(sizeof(unsigned long long) * nk);
+        s->b.sq = c.take<float>(sizeof(float) * V);
+        s->b.sid = c.take<uint32_t>(sizeof(uint32_t) * V);
+        s->b.ctl = c.take<tg::SmpCtl>(sizeof(tg::SmpCtl));
+        s->dl = c.take<float>(sizeof(float) * V);
+        s->pv = c.take<float>(sizeof(float) * tg::ARGMAX_BLOCKS);
+        s->pi = c.take<int>(sizeof(int) * tg::ARGMAX_BLOCKS);
+        s->tok = c.take<int>(sizeof(int));
+        if (!pass && (hipMalloc(&s->mem, c.off) != hipSuccess ||
+                      hipHostMalloc((void **)&s->hctl, sizeof(tg::SmpCtl), hipHostMallocDefault) != hipSuccess)) {
+            (void)hipGetLastError();
+            sampler_free(s);
+            return set_err(TG_E_NOMEM, "sampler: %zu bytes for vocab %d", c.off, vocab);
+        }
+    }
+    *out = s;
+    return TG_OK;
+}
+
+// Caller holds g_lg_mu; dl = device logits of s->vocab values.
+static int sampler_run(tg_sampler *s, const float *dl, float temperature, double top_p, double u, int32_t *token,
+                       float *probs) {
+    hipStream_t st = g_lg_st;
+    if (!(temperature > 0.0f)) {  // engine.py:358-359 (a NaN temperature is not > 0 either)
+        PROFILED("sample_argmax", st, tg::launch_argmax(dl, s->vocab, s->pv, s->pi, s->tok, st));
+        return lg_finish(token, s->tok, sizeof(int32_t));
+    }
+    if (!(u >= 0.0 && u < 1.0)) return set_err(TG_E_INVALID, "sample: u = %g is not in [0, 1)", u);
+    PROFILED("sample", st, tg::launch_sample_main(s->b, dl, s->vocab, temperature, top_p, u, st));
+    HIP_TRY(hipMemcpyAsync(s->hctl, s->b.ctl, sizeof(tg::SmpCtl), hipMemcpyDeviceToHost, st));
+    if (probs) HIP_TRY(hipMemcpyAsync(probs, s->b.q, sizeof(float) * (size_t)s->vocab, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    tg::SmpCtl c = *s->hctl;
+    if (c.bad || c.status == tg::SMP_ST_INPUT)
+        return set_err(TG_E_INVALID, "sample: the logits hold NaN or +inf, or every logit is -inf");
+    if (c.large) {
+        PROFILED("sample_large", st, tg::launch_sample_large(s->b, s->vocab, (int)c.C, top_p, u, st));
+        HIP_TRY(hipMemcpyAsync(s->hctl, s->b.ctl, sizeof(tg::SmpCtl), hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        c = *s->hctl;
+    }
+    if (c.status != tg::SMP_ST_OK || c.token < 0 || c.token >= s->vocab)
+        return set_err(TG_E_HIP, "sample: device status %d, token %d, %u candidates", c.status, c.token, c.C);
+    *token = c.token;
+    return TG_OK;
+}
+
+extern "C" tg_sampler *tg_sampler_create(int vocab) {
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (vocab <= 0 || vocab > tg::SMP_VMAX) {
+        set_err(TG_E_INVALID, "tg_sampler_create: vocab %d outside 1..%d", vocab, tg::SMP_VMAX);
+        return nullptr;
+    }
+    tg_sampler *s = nullptr;
+    if (lg_reserve(0) || sampler_new(vocab, &s)) return nullptr;
+    return s;
+}
+
+extern "C" void tg_sampler_destroy(tg_sampler *s) { sampler_free(s); }
+
+extern "C" int tg_sampler_run(tg_sampler *s, const float *logits, int logits_on_device, float temperature,
+                              double top_p, double u, int32_t *token, float *probs) {
+    if (!s || !logits || !token) return set_err(TG_E_INVALID, "tg_sampler_run: null handle, logits or token");
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    int rc = lg_reserve(0);
+    if (rc) return rc;
+    if (g_lg_dev != s->dev) return set_err(TG_E_INVALID, "tg_sampler_run: handle of device %d", s->dev);
+    const float *dl = logits;
+    if (!logits_on_device) {
+        if ((rc = lg_h2d(s->dl, logits, sizeof(float) * (size_t)s->vocab))) return rc;
+        dl = s->dl;
+    }
+    return sampler_run(s, dl, temperature, top_p, u, token, probs);
+}
+
+// The head's logits sampled on the device: x (embed floats, host) -> token.
+extern "C" int tg_head_sample(tg_head *h, const float *x, float eps, float temperature, double top_p, double u,
+                              float *logits, int32_t *token) {
+    if (!h || !x || !token) return set_err(TG_E_INVALID, "tg_head_sample: null handle, input or token");
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    int rc = lg_reserve(0);
+    if (rc) return rc;
+    if (g_lg_dev != h->dev) return set_err(TG_E_INVALID, "tg_head_sample: handle of device %d", h->dev);
+    if (temperature > 0.0f && !(u >= 0.0 && u < 1.0))
+        return set_err(TG_E_INVALID, "tg_head_sample: u = %g is not in [0, 1)", u);
+    if (!h->smp && (rc = sampler_new(h->vocab, &h->smp))) return rc;
+    hipStream_t st = g_lg_st;
+    const size_t eb = sizeof(float) * (size_t)h->embed;
+    if ((rc = lg_h2d(h->x, x, eb))) return rc;
+    PROFILED("head_rms", st, tg::launch_rms_norm(h->x, h->nw, h->xn, h->embed, eps, st));
+    PROFILED("head_mv", st, tg::launch_matvec_two_acc(h->W, false, h->xn, h->logits, h->vocab, h->embed, st));
+    if (logits) HIP_TRY(hipMemcpyAsync(logits, h->logits, sizeof(float) * (size_t)h->vocab, hipMemcpyDeviceToHost, st));
+    return sampler_run(h->smp, h->logits, temperature, top_p, u, token, nullptr);
 }

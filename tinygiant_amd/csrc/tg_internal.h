@@ -167,6 +167,43 @@ hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st);
 constexpr int ARGMAX_BLOCKS = 256;
 hipError_t launch_argmax(const float *x, int n, float *pv, int *pi, int *out, hipStream_t st);
 
+// Temperature / top-p sampling (tg_sample.hip).
+constexpr int SMP_VMAX = 1 << 19;        // largest vocabulary
+constexpr int SMP_BUCKETS = 4096;        // histogram over q's bits 30..19
+constexpr int SMP_BUCKET_SHIFT = 19;
+constexpr int SMP_SMALL = 8192;          // candidates sorted in one block's LDS
+constexpr int NP_BUFSIZE = 8192;         // np.sum reduces in buffers of this many values
+constexpr int SMP_ST_PENDING = -1, SMP_ST_OK = 0, SMP_ST_INPUT = 1, SMP_ST_BOUND = 2;
+struct SmpCtl {
+    float m, S;        // max logit, np.sum of p
+    int bad;           // a NaN or +inf logit, or every logit -inf
+    int bstar;         // lowest histogram bucket of the candidate prefix
+    uint32_t C;        // elements in buckets >= bstar
+    uint32_t n;        // compaction counter
+    uint32_t done;     // blocks of the histogram launch that have finished
+    int large;         // C > SMP_SMALL: the sort runs in global memory
+    int cut;           // candidates after the top-p cutoff
+    int token;
+    int status;        // SMP_ST_*
+};
+struct SmpBufs {
+    float *pmax;                  // 256 block maxima
+    int *pbad;                    // 256 block flags
+    float *p, *q;                 // vocab: exp values, probabilities
+    float *sums;                  // 64 buffer sums
+    uint32_t *hcnt;               // SMP_BUCKETS
+    unsigned long long *hmass;    // SMP_BUCKETS
+    unsigned long long *keys;     // next power of two >= max(vocab, 16384)
+    float *sq;                    // vocab: sorted probabilities (more than SMP_SMALL candidates)
+    uint32_t *sid;                // vocab: their token ids
+    SmpCtl *ctl;
+};
+hipError_t sample_prepare();
+// k_smp_max .. k_smp_small; afterwards ctl->large says whether launch_sample_large must finish
+hipError_t launch_sample_main(const SmpBufs &b, const float *logits, int V, float T, double top_p, double u,
+                              hipStream_t st);
+hipError_t launch_sample_large(const SmpBufs &b, int V, int C, double top_p, double u, hipStream_t st);
+
 // One-token layer with routing inside (k_layer_dec) and the prologue that
 // forms the first layer's router partials (k_dec_part).  part buffers hold
 // [E+1][H/32] floats, dec_part_floats() the size of two; the group hand-off
