@@ -751,8 +751,10 @@ def run_legacy_moe(args, torch, call):
     reference's engine would call it: 8 Q4_K experts of the 30B shape
     (gate | up | down, 2,654,208 bytes each) in host memory, one call per
     layer; rotates over 16 sets of experts.  The call copies its operands to
-    the device, so the rate is bound by the host-to-device copy; the roofline
-    is the Q4_K row-dot kernel's on its device operands."""
+    the device, so the rate is bound by the host-to-device copy; "pinned"
+    times the same calls after tg_mlock of every expert, which keeps an HBM
+    copy (the reference's cache locks its pinned experts the same way).  The
+    roofline is the Q4_K row-dot kernel's on its device operands."""
     from tinygiant_amd._lib import require_lib
     lib = require_lib()
     rng = np.random.default_rng(args.seed)
@@ -777,6 +779,19 @@ def run_legacy_moe(args, torch, call):
     for i in range(K):
         step(i)
     wall = time.perf_counter() - t0
+    # the same calls with every expert locked, as the reference's cache locks its pinned experts
+    # (cache.py:59-67): tg_mlock keeps an HBM copy and the calls read the experts from it
+    for st in sets:
+        for e in st:
+            lib.tg_mlock(ctypes.c_void_p(e.ctypes.data), ctypes.c_size_t(e.nbytes))
+    for i in range(W):
+        step(i)
+    t0 = time.perf_counter()
+    for i in range(K):
+        step(i)
+    wall_pin = time.perf_counter() - t0
+    mb, mr, mh, mm = ctypes.c_size_t(), ctypes.c_int(), ctypes.c_uint64(), ctypes.c_uint64()
+    lib.tg_mirror_stats(ctypes.byref(mb), ctypes.byref(mr), ctypes.byref(mh), ctypes.byref(mm))
     call("tg_prof_enable", 1)
     for i in range(8):
         step(i)
@@ -811,6 +826,9 @@ def run_legacy_moe(args, torch, call):
         "data": "synthetic (random Q4_K blocks, N(0,1) input)",
         "config": {"workload": "legacy-q4k-moe-forward", "hidden": H, "moe_intermediate": I, "experts": K_TOP,
                    "expert_bytes": eb, "note": "each call copies 21.2 MB of host operands to the device"},
+        "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4),
+                   "note": f"after tg_mlock of every expert: {mb.value / 1e6:.1f} MB in {mr.value} HBM copies, "
+                           f"{mh.value} operand reads from them, {mm.value} copied"},
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": "k_matmul_q4k (gate/up)", "bytes_per_launch": q_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",

@@ -114,8 +114,23 @@ void tg_attention_decode_q4(
 void tg_prefetch(const void *addr, size_t len);
 /* csrc/libtinygiant.c:752 */
 void tg_prefetch_batch(const void **addrs, const size_t *lens, int count);
-/* csrc/libtinygiant.c:761 */
+/* csrc/libtinygiant.c:761.  Returns mlock()'s result on the 16 KiB-aligned
+ * range, as the reference.  The range is also copied to HBM once (the
+ * reference locks pinned experts' mmap views, cache.py:59-67, and the
+ * attention weights, engine.py:134-139, all read-only from then on); the
+ * legacy entry points then read any weight operand lying inside it from HBM
+ * instead of copying it per call.  A range whose first or last 64 bytes
+ * change is copied again per call; TG_MLOCK_MIRROR=0 disables the copies. */
 int tg_mlock(const void *addr, size_t len);
+/* Release the HBM copies of every tg_mlock range overlapping
+ * [addr, addr + len) (all of them for NULL), e.g. before unmapping or
+ * rewriting it.  No counterpart in the reference (its locks live as long as
+ * the process). */
+void tg_mirror_drop(const void *addr, size_t len);
+/* Bytes and ranges held in HBM for tg_mlock ranges, and how many legacy
+ * weight operands were read from them (hits) or copied (misses).  Any
+ * pointer may be NULL.  No counterpart in the reference. */
+void tg_mirror_stats(size_t *bytes, int *ranges, uint64_t *hits, uint64_t *misses);
 /* csrc/libtinygiant.c:662 */
 void tg_transformer_layer(
     const float *wq, const float *wk, const float *wv, const float *wo,

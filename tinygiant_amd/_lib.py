@@ -94,6 +94,8 @@ NEW_SYMBOLS = [
     ("tg_sampler_run", CI, [VP, VP, CI, CF, CD, CD, VP, VP]),
     ("tg_sampler_destroy", None, [VP]),
     ("tg_head_sample", CI, [VP, VP, CF, CF, CD, CD, VP, VP]),
+    ("tg_mirror_drop", None, [VP, SZ]),
+    ("tg_mirror_stats", None, [VP, VP, VP, VP]),
 ]
 
 ALL_SYMBOLS = LEGACY_SYMBOLS + UNREGISTERED_SYMBOLS + NEW_SYMBOLS

@@ -18,6 +18,7 @@
 #include <sys/mman.h>
 
 #include <atomic>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -975,10 +976,16 @@ extern "C" void tg_prefetch_batch(const void **addrs, const size_t *lens, int co
     for (int i = 0; i < count; i++) tg_prefetch(addrs[i], lens[i]);
 }
 
+static void mirror_add(const void *addr, size_t len);
+
+// mlock of the 16 KiB-aligned range, as the reference; the range is also
+// mirrored in HBM for the legacy entry points (residency section below).
 extern "C" int tg_mlock(const void *addr, size_t len) {
     void *aligned = (void *)((uintptr_t)addr & kPageMask);
     size_t alen = len + ((uintptr_t)addr - (uintptr_t)aligned);
-    return mlock(aligned, alen);
+    const int rc = mlock(aligned, alen);
+    mirror_add(addr, len);
+    return rc;
 }
 
 // ================================================================ legacy ABI
@@ -1076,6 +1083,121 @@ static int lg_finish(void *host_dst, const void *dev_src, size_t n) {
     return TG_OK;
 }
 
+// ------------------------------------------------------------- residency
+// The reference keeps its hot experts resident by locking their pages: the
+// cache calls tg_mlock on each pinned expert's gate / up / down views
+// (cache.py:59-67) and the engine on every attention weight
+// (engine.py:134-139).  Those ranges are read-only from then on (mmap views
+// of the relayout files, weights loaded once).  Here tg_mlock also copies
+// the range to HBM once, and every legacy entry point reads a weight operand
+// that lies inside such a range from that copy instead of sending it over
+// PCIe per call.  A copy is used only on the device it was made on, and only
+// while the range still starts and ends with the bytes it had when locked
+// (64 bytes at each end, hashed: an address reused for other data drops the
+// copy).  tg_mirror_drop releases copies; TG_MLOCK_MIRROR=0 turns the mirror
+// off.  All of it under g_lg_mu.
+struct Mirror {
+    size_t len;
+    void *dev;
+    int device;
+    uint64_t fp;
+};
+static std::map<uintptr_t, Mirror> g_mirror;
+static size_t g_mirror_bytes = 0;
+static uint64_t g_mirror_hits = 0, g_mirror_misses = 0;
+
+static uint64_t range_fp(const void *p, size_t n) {
+    const uint8_t *b = static_cast<const uint8_t *>(p);
+    uint64_t h = 1469598103934665603ull ^ n;  // FNV-1a over both ends
+    const size_t e = n < 64 ? n : 64;
+    for (size_t i = 0; i < e; i++) h = (h ^ b[i]) * 1099511628211ull;
+    for (size_t i = n - e; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
+    return h;
+}
+
+static bool mirror_enabled() {
+    static const int on = [] {
+        const char *e = getenv("TG_MLOCK_MIRROR");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+static void mirror_erase(std::map<uintptr_t, Mirror>::iterator it) {
+    (void)hipFree(it->second.dev);
+    g_mirror_bytes -= it->second.len;
+    g_mirror.erase(it);
+}
+
+// The device copy of [host, host + n), or NULL.
+static const void *mirror_find(const void *host, size_t n) {
+    if (g_mirror.empty() || !host) return nullptr;
+    auto it = g_mirror.upper_bound((uintptr_t)host);
+    if (it == g_mirror.begin()) return nullptr;
+    --it;
+    const uintptr_t a = it->first;
+    const Mirror &m = it->second;
+    if ((uintptr_t)host + n > a + m.len || m.device != g_lg_dev) return nullptr;
+    if (range_fp((const void *)a, m.len) != m.fp) {  // the range holds other data now
+        mirror_erase(it);
+        return nullptr;
+    }
+    return static_cast<const uint8_t *>(m.dev) + ((uintptr_t)host - a);
+}
+
+static void mirror_add(const void *addr, size_t len) {
+    if (!addr || !len || !mirror_enabled()) return;
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const std::string err = g_err;  // best effort: the caller sees mlock's result only
+    if (lg_reserve(0) == TG_OK && !mirror_find(addr, len)) {
+        void *d = nullptr;
+        if (hipMalloc(&d, len) == hipSuccess) {
+            if (hipMemcpy(d, addr, len, hipMemcpyHostToDevice) == hipSuccess) {
+                auto it = g_mirror.find((uintptr_t)addr);
+                if (it != g_mirror.end()) mirror_erase(it);  // a shorter copy of the same start
+                g_mirror[(uintptr_t)addr] = Mirror{len, d, g_lg_dev, range_fp(addr, len)};
+                g_mirror_bytes += len;
+            } else {
+                (void)hipFree(d);
+            }
+        }
+        (void)hipGetLastError();
+    }
+    g_err = err;
+}
+
+extern "C" void tg_mirror_drop(const void *addr, size_t len) {
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    const uintptr_t lo = (uintptr_t)addr, hi = lo + len;
+    for (auto it = g_mirror.begin(); it != g_mirror.end();) {
+        auto nx = std::next(it);
+        if (!addr || (it->first < hi && it->first + it->second.len > lo)) mirror_erase(it);
+        it = nx;
+    }
+}
+
+extern "C" void tg_mirror_stats(size_t *bytes, int *ranges, uint64_t *hits, uint64_t *misses) {
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (bytes) *bytes = g_mirror_bytes;
+    if (ranges) *ranges = (int)g_mirror.size();
+    if (hits) *hits = g_mirror_hits;
+    if (misses) *misses = g_mirror_misses;
+}
+
+// A read-only operand of a legacy call: its HBM copy when tg_mlock made one,
+// else copied into dst.
+template <class T>
+static int lg_in(const void *host, size_t n, T *dst, const T **out) {
+    if (const void *m = mirror_find(host, n)) {
+        g_mirror_hits++;
+        *out = static_cast<const T *>(m);
+        return TG_OK;
+    }
+    g_mirror_misses++;
+    *out = dst;
+    return lg_h2d(dst, host, n);
+}
+
 static size_t down_bytes(int fmt, int embed, int inter) {
     if (fmt == 1) return (size_t)embed * inter * 2;
     if (fmt == 2) return (size_t)embed * (inter / tg::LG_QK) * tg::LG_Q6K_BYTES;
@@ -1140,9 +1262,10 @@ static int lg_expert_forward_mixed(const uint8_t *gate, const uint8_t *up, const
             continue;
         }
         int rc;
-        if ((rc = lg_h2d(dg, gate, gb)) || (rc = lg_h2d(du, up, gb)) || (rc = lg_h2d(dd, down, db)) ||
+        const uint8_t *pg, *pu, *pd;
+        if ((rc = lg_in(gate, gb, dg, &pg)) || (rc = lg_in(up, gb, du, &pu)) || (rc = lg_in(down, db, dd, &pd)) ||
             (rc = lg_h2d(dx, input, 4 * (size_t)embed)) || (rc = lg_h2d(dout, output, 4 * (size_t)embed)) ||
-            (rc = lg_expert(dg, du, dd, fmt, dx, dout, weight, embed, inter, b)))
+            (rc = lg_expert(pg, pu, pd, fmt, dx, dout, weight, embed, inter, b)))
             return rc;
         return lg_finish(output, dout, 4 * (size_t)embed);
     }
@@ -1194,9 +1317,11 @@ extern "C" void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights
             if (rc) return rc;
             HIP_TRY(hipMemsetAsync(dout, 0, 4 * (size_t)embed_dim, g_lg_st));  // the reference's memset
             for (int e = 0; e < n_experts; e++) {
-                // one expert's bytes at a time: the copy waits for the previous expert's kernels
-                if ((rc = lg_h2d(de, expert_ptrs[e], eb)) ||
-                    (rc = lg_expert(de, de + gb, de + 2 * gb, 0, dx, dout, weights[e], embed_dim, inter_dim, b)))
+                // one expert's bytes at a time: a copy waits for the previous expert's kernels
+                const uint8_t *pg, *pu, *pd, *src = expert_ptrs[e];
+                if ((rc = lg_in(src, gb, de, &pg)) || (rc = lg_in(src + gb, gb, de + gb, &pu)) ||
+                    (rc = lg_in(src + 2 * gb, eb - 2 * gb, de + 2 * gb, &pd)) ||
+                    (rc = lg_expert(pg, pu, pd, 0, dx, dout, weights[e], embed_dim, inter_dim, b)))
                     return rc;
             }
             return lg_finish(output, dout, 4 * (size_t)embed_dim);
@@ -1227,15 +1352,16 @@ static int lg_matmul_k(bool q6, const uint8_t *W, const float *input, float *out
             continue;
         }
         int rc;
-        if ((rc = lg_h2d(dw, W, wb)) || (rc = lg_h2d(dx, input, xb))) return rc;
+        const uint8_t *pw;
+        if ((rc = lg_in(W, wb, dw, &pw)) || (rc = lg_h2d(dx, input, xb))) return rc;
         if (scalar) {
-            HIP_TRY(tg::launch_matmul_q4k_scalar(dw, dx, dy, nrows, bpr, g_lg_st));
+            HIP_TRY(tg::launch_matmul_q4k_scalar(pw, dx, dy, nrows, bpr, g_lg_st));
         } else {
             HIP_TRY(tg::launch_quantize_q8k(dx, dq, bpr, g_lg_st));
             if (q6)
-                HIP_TRY(tg::launch_matmul_q6k(dw, dq, dy, nrows, bpr, g_lg_st));
+                HIP_TRY(tg::launch_matmul_q6k(pw, dq, dy, nrows, bpr, g_lg_st));
             else
-                HIP_TRY(tg::launch_matmul_q4k(dw, dq, dy, nrows, bpr, g_lg_st));
+                HIP_TRY(tg::launch_matmul_q4k(pw, dq, dy, nrows, bpr, g_lg_st));
         }
         return lg_finish(output, dy, 4 * (size_t)nrows);
     }
@@ -1283,8 +1409,9 @@ static int lg_matvec(bool half, const void *A, const float *x, float *out, int n
             continue;
         }
         int rc;
-        if ((rc = lg_h2d(da, A, ab)) || (rc = lg_h2d(dx, x, 4 * (size_t)ncols))) return rc;
-        HIP_TRY(tg::launch_matvec_two_acc(da, half, dx, dy, nrows, ncols, g_lg_st));
+        const uint8_t *pa;
+        if ((rc = lg_in(A, ab, da, &pa)) || (rc = lg_h2d(dx, x, 4 * (size_t)ncols))) return rc;
+        HIP_TRY(tg::launch_matvec_two_acc(pa, half, dx, dy, nrows, ncols, g_lg_st));
         return lg_finish(out, dy, 4 * (size_t)nrows);
     }
     return TG_OK;
@@ -1476,10 +1603,12 @@ static int lg_attention(bool q4, const void *wq, const void *wk, const void *wv,
             continue;
         }
         int rc;
-        if ((rc = lg_h2d(dq, wq, bq)) || (rc = lg_h2d(dk, wk, bk)) || (rc = lg_h2d(dv, wv, bv)) ||
-            (rc = lg_h2d(dwo, wo, bo)) || (rc = lg_h2d(dqn, qnw, nb)) || (rc = lg_h2d(dkn, knw, nb)) ||
+        const uint8_t *pq, *pk, *pv, *po;
+        const float *pqn, *pkn;
+        if ((rc = lg_in(wq, bq, dq, &pq)) || (rc = lg_in(wk, bk, dk, &pk)) || (rc = lg_in(wv, bv, dv, &pv)) ||
+            (rc = lg_in(wo, bo, dwo, &po)) || (rc = lg_in(qnw, nb, dqn, &pqn)) || (rc = lg_in(knw, nb, dkn, &pkn)) ||
             (rc = lg_h2d(b.x, input, 4 * (size_t)g.embed)) || (rc = lg_attn_in(g, b, kv_k, kv_v, rope_cos, rope_sin)) ||
-            (rc = lg_attn_core(q4, dq, dk, dv, dwo, dqn, dkn, g, b)) || (rc = lg_attn_out(g, b, kv_k, kv_v)))
+            (rc = lg_attn_core(q4, pq, pk, pv, po, pqn, pkn, g, b)) || (rc = lg_attn_out(g, b, kv_k, kv_v)))
             return rc;
         return lg_finish(output, b.out, 4 * (size_t)g.embed);
     }
@@ -1548,22 +1677,26 @@ static int lg_transformer_layer(const float *wq, const float *wk, const float *w
         }
         hipStream_t st = g_lg_st;
         int rc;
-        if ((rc = lg_h2d(dq, wq, bq)) || (rc = lg_h2d(dk, wk, bk)) || (rc = lg_h2d(dv, wv, bv)) ||
-            (rc = lg_h2d(dwo, wo, bo)) || (rc = lg_h2d(dqn, q_norm_w, nb)) || (rc = lg_h2d(dkn, k_norm_w, nb)) ||
-            (rc = lg_h2d(dan, attn_norm_w, ev)) || (rc = lg_h2d(dfn, ffn_norm_w, ev)) || (rc = lg_h2d(dx, x, ev)) ||
+        const uint8_t *pq, *pk, *pv, *po;
+        const float *pqn, *pkn, *pan, *pfn;
+        if ((rc = lg_in(wq, bq, dq, &pq)) || (rc = lg_in(wk, bk, dk, &pk)) || (rc = lg_in(wv, bv, dv, &pv)) ||
+            (rc = lg_in(wo, bo, dwo, &po)) || (rc = lg_in(q_norm_w, nb, dqn, &pqn)) ||
+            (rc = lg_in(k_norm_w, nb, dkn, &pkn)) || (rc = lg_in(attn_norm_w, ev, dan, &pan)) ||
+            (rc = lg_in(ffn_norm_w, ev, dfn, &pfn)) || (rc = lg_h2d(dx, x, ev)) ||
             (rc = lg_attn_in(g, b, kv_k, kv_v, rope_cos, rope_sin)))
             return rc;
-        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, dan, b.x, embed, 1e-6f, st));
-        if ((rc = lg_attn_core(false, dq, dk, dv, dwo, dqn, dkn, g, b))) return rc;
+        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, pan, b.x, embed, 1e-6f, st));
+        if ((rc = lg_attn_core(false, pq, pk, pv, po, pqn, pkn, g, b))) return rc;
         PROFILED("lg_add", st, tg::launch_add_vec(dx, b.out, embed, st));
-        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, dfn, b.x, embed, 1e-6f, st));
+        PROFILED("lg_rms", st, tg::launch_rms_norm(dx, pfn, b.x, embed, 1e-6f, st));
         HIP_TRY(hipMemsetAsync(dmo, 0, ev, st));  // moe_out starts at zero
         for (int e = 0; e < n_active; e++) {
-            // one expert's operands at a time (the copies wait for the previous expert's kernels)
+            // one expert's operands at a time (a copy waits for the previous expert's kernels)
             const int fmt = down_is_f16[e];
-            if ((rc = lg_h2d(dg, gate_ptrs[e], gb)) || (rc = lg_h2d(du, up_ptrs[e], gb)) ||
-                (rc = lg_h2d(dd, down_ptrs[e], down_bytes(fmt, embed, inter))) ||
-                (rc = lg_expert(dg, du, dd, fmt, b.x, dmo, expert_weights[e], embed, inter, eb)))
+            const uint8_t *pg, *pu, *pd;
+            if ((rc = lg_in(gate_ptrs[e], gb, dg, &pg)) || (rc = lg_in(up_ptrs[e], gb, du, &pu)) ||
+                (rc = lg_in(down_ptrs[e], down_bytes(fmt, embed, inter), dd, &pd)) ||
+                (rc = lg_expert(pg, pu, pd, fmt, b.x, dmo, expert_weights[e], embed, inter, eb)))
                 return rc;
         }
         PROFILED("lg_add", st, tg::launch_add_vec(dx, dmo, embed, st));
