@@ -708,10 +708,10 @@ def prefill_leg(args, torch, call, arena, L, K=20, W=2):
         "mfma_frac": round(tops * 1e12 / MFMA_INT8_PEAK, 4),
         "kernel_avg_us": kern_us,
         "layer_kernel_us": round(layer_us, 2),
-        "roofline": {"bound": "mfma", "kernel": "k_mfma_grouped (gate/up)", "ops_per_launch": gu_ops,
+        "roofline": {"bound": "mfma", "kernel": "k_mfma16<true> (gate/up)", "ops_per_launch": gu_ops,
                      "achieved": round(achieved / 1e12, 1), "peak": MFMA_INT8_PEAK / 1e12, "unit": "TOPS",
                      "frac": round(achieved / MFMA_INT8_PEAK, 4),
-                     "traffic": profiled_traffic("k_mfma_grouped/gate_up")},
+                     "traffic": profiled_traffic("k_mfma16/gate_up")},
         "cpu_baseline": cpu,
     }
 

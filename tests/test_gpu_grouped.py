@@ -177,3 +177,31 @@ def test_mfma_equals_dot_path(O, tglib, T):
         assert np.array_equal(bits(m), bits(d))
     finally:
         a.close()
+
+
+def test_mfma16_every_item_size(O, tglib):
+    """Prefill-sized batches run 16 x 16 int8 MFMA tiles on items of up to
+    160 entries (10 column tiles of 16).  A Zipf(1.1)-skewed router gives
+    groups from a handful of entries (one column tile) to experts split over
+    several items; the layer must equal the oracle bit for bit."""
+    from tinygiant_amd.moe import MoEBlock
+    from tinygiant_amd.synth import zipf_skew
+    H, I, E, k, T = 512, 256, 32, 8, 1000
+    gpu_note(f"mfma16 item sizes H={H} I={I} E={E} T={T} zipf")
+    rng = np.random.default_rng(5)
+    router, shift = zipf_skew(rng, E, H)
+    a, layers, routers = make_arena(O, 1, H, I, E, k, seed=29, routers=[router])
+    try:
+        a.set_batch_path(a.BATCH_GROUPED)
+        x = (O.synth_normal(29, O.stream_id(0, T, 4), 1.0, T * H).reshape(T, H) + shift[None, :]).astype(np.float32)
+        ref, ridx, rw, _ = O.moe_layer(layers[0], routers[0], H, I, E, k, x)
+        counts = np.bincount(ridx.reshape(-1), minlength=E)
+        # the sizes this test is about: one-tile groups, whole items, experts over several items
+        assert counts[counts > 0].min() <= 16 and counts.max() > 320, counts
+        assert np.any((counts > 32) & (counts < 160)), counts
+        out, idx, w = MoEBlock(a).forward(0, dev(x), return_routing=True)
+        assert np.array_equal(host(idx), ridx)
+        got = host(out)
+        assert np.array_equal(bits(got), bits(ref)), f"max |diff| {np.max(np.abs(got - ref)):.3e}"
+    finally:
+        a.close()

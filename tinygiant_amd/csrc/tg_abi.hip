@@ -517,7 +517,7 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
                                  c.xs, st));
     const int n = T * s.k;
     if (mfma_usable(a, T)) {
-        const int mt = tg::mfma_tiles(s, T), ch = 32 * mt, wmax = tg::group_work_max(s, n, ch);
+        const int mt = tg::mfma_tiles(s, T), ch = tg::mfma_item_entries(s, mt), wmax = tg::group_work_max(s, n, ch);
         PROFILED("group", st,
                  tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
                                           st));

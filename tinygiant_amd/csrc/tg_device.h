@@ -20,6 +20,15 @@ constexpr int WAVE = 64;
 
 // ---------------------------------------------------------------- halves
 TG_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// LDS written by some lanes of a wave and read by others of the same wave:
+// a wave's LDS operations complete in order; this keeps the compiler from
+// reordering them across the hand-off
+TG_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 // round to nearest even (v_cvt_f16_f32 in the default mode)
 TG_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 

@@ -239,6 +239,8 @@ hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int c
 // int8-MFMA grouped gate/up and down (mt = M-tiles of 32 entries per item)
 bool mfma_shape_ok(const Shape &s);
 int mfma_tiles(const Shape &s, int T);
+// entries per work item for the MFMA launches at mt M-tiles
+int mfma_item_entries(const Shape &s, int mt);
 hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                               const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
                               const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);

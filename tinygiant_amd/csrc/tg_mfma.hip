@@ -606,8 +606,380 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     }
 }
 
+// ================================================================ 16 x 16 tiles
+// The prefill / large-batch path.  Work item = (expert e, up to XT_CT * 16
+// entries).  A block of NW waves stages, per chunk of XT_KC Q4_0 blocks, the
+// item's activations and activation scales and every wave's weight rows and
+// their scales straight into LDS (global_load_lds, no registers on the way;
+// one wait and one barrier per chunk, the next chunk in flight meanwhile).
+// Each wave owns 32 weight rows (two 16-row tiles) across the item's entries
+// (16-entry column tiles) and runs one v_mfma_i32_16x16x32_i8 per (row
+// tile, column tile, block): K = 32 is one Q4_0 / Q8_0 block.
+//
+// Operands (lane l, g = l / 16, c = l % 16; measured on gfx950):
+//   A  row c of the row tile, block elements 8g .. 8g+7: the low (g < 2) or
+//      high (g >= 2) nibbles of bytes 8 (g & 1) .. 8 (g & 1) + 7 of the row's
+//      16, as 16 (q - 8) = ((q << 4) ^ 0x80) per byte (exact in int8)
+//   B  entry c of the column tile, block elements 8g .. 8g+7 (Q8_0 bytes)
+//   C  0x4B400000 for every element
+// so D = 0x4B400000 + 16 S, |16 S| <= 520192 < 2^22: D's bits are the float
+// 1.5 * 2^23 + 16 S exactly.  D's register r of lane l is (row 4g + r,
+// entry c) of the tile.
+// Epilogue per block, the row-dot definition bit for bit:
+//   u   = fma(float_bits(D), dw / 16, -1.5 * 2^23 * dw / 16) = round(S * dw)
+//         (dw / 16 and the constant are exact: dw is a half)
+//   acc = fma(u, dx, acc)
+// Each lane needs 4 row scales per row tile (its rows 4g .. 4g+3) and one
+// activation scale per column tile (entry c).  Gate/up: waves 2i / 2i + 1
+// take gate / up of the same 32 rows; the up wave hands its sums over in
+// LDS and the gate wave applies SwiGLU and Q8_0 (an entry's 32 rows sit in
+// lanes c, c + 16, c + 32, c + 48, 8 values each).  Down writes fp32 rows.
+constexpr int XT_NW = 4;     // waves per block
+constexpr int XT_KC = 4;     // Q4_0 blocks per chunk
+constexpr int XT_CT = 10;    // 16-entry column tiles per item (160 entries)
+constexpr int XT_RB = XT_KC * 32;   // activation bytes per row and chunk
+constexpr int XT_NP = XT_KC * 2;    // 16-byte pieces per row and chunk
+constexpr int XT_CS = 12;           // activation-scale row: the column tiles' scales, then unused words (12
+                                    // words apart, 16 consecutive rows' 16-byte reads fall on distinct banks)
+static_assert(XT_CS >= XT_CT && XT_CS % 4 == 0, "scale row");
+
+// LDS byte offsets of one block's buffers (two of each staged buffer)
+struct XtLds {
+    static constexpr int ROWS = XT_CT * 16;
+    static constexpr int ACT = 0;                                     // [2][ROWS][XT_RB], pieces swizzled
+    static constexpr int AXS = ACT + 2 * ROWS * XT_RB;                // [2][XT_KC][16][XT_CS] fp32
+    static constexpr int WQ = AXS + 2 * XT_KC * 16 * XT_CS * 4;       // [3][NW][32 rows][XT_KC][16 B]
+    static constexpr int WSR = WQ + 3 * XT_NW * 32 * XT_KC * 16;      // [3][NW][32 rows][XT_KC] halves
+    static constexpr int TAB = WSR + 3 * XT_NW * 32 * XT_KC * 2;      // [NW][XT_KC][2][2 rt][16] fp32
+    static constexpr int BYTES = TAB + XT_NW * XT_KC * 2 * 2 * 16 * 4;
+};
+static_assert(XtLds::ACT % 16 == 0 && XtLds::AXS % 16 == 0 && XtLds::WQ % 16 == 0 && XtLds::WSR % 16 == 0 &&
+              XtLds::TAB % 16 == 0, "LDS alignment");
+static_assert(XT_NP == 8, "piece swizzle assumes 8 pieces per row");
+static_assert((XT_NW / 2) * 64 * (2 * XT_CT * 4) * 4 <= XtLds::BYTES, "gate/up hand-off fits in the block's LDS");
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+TG_DEV uint32_t lds_addr(uint8_t *smem, int off) { return (uint32_t)(uintptr_t)(lds_u8 *)(smem + off); }
+// global -> LDS without registers: lane l's 16 (4) bytes land at LDS byte
+// address m0 + 16 l (4 l); m0 must be the same on every lane.  Written as the bare instructions so the
+// compiler's wait insertion does not treat them as writes it must wait for
+// before every later LDS read (it cannot tell the staged buffers apart from
+// the ones being read); the kernel waits for them itself (vmcnt, then a
+// barrier) before reading what they wrote.
+TG_DEV void lds_dma16(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
+TG_DEV void lds_dma4(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
+
+// 16-byte piece slot of piece p in activation row t (rows t and t + 2 fall
+// on the same banks; the slot spreads 16 consecutive rows over all 64)
+TG_DEV int xt_slot(int p, int t) { return p ^ ((t >> 1) & 7); }
+// 16-byte block slot of block bl in weight row r of a wave
+TG_DEV int xt_wslot(int bl, int r) { return bl ^ ((r >> 2) & 3); }
+
+// 16 (q - 8) as int8 from 8 nibble bytes: low nibbles (sh = 4) or high (sh = 0)
+TG_DEV long xt_unpack(uint2 w, int sh) {
+    const uint32_t lo = ((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
+    const uint32_t hi = ((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u;
+    return (long)(((uint64_t)hi << 32) | lo);
+}
+
+template <bool PAIR>
+__global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                       const int32_t *__restrict__ work,
+                                                       const int32_t *__restrict__ work_n,
+                                                       const int32_t *__restrict__ entries,
+                                                       const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                       int8_t *__restrict__ oq, float *__restrict__ od,
+                                                       int *__restrict__ os, float *__restrict__ D) {
+    constexpr int NW = XT_NW, ROWS = XtLds::ROWS;
+    constexpr int NACT = ROWS * XT_NP / 64;          // activation load instructions per chunk (full item)
+    constexpr int NAXS = XT_KC * 16 * XT_CS / 64;    // activation-scale load instructions per chunk
+    static_assert(NACT % NW == 0 && NAXS % NW == 0, "staging split");
+    extern __shared__ __align__(16) uint8_t smem[];
+    // blocks are dealt to the 8 XCDs in turn (block b on XCD b % 8): the gx
+    // blocks of one item get ids 8 apart, so they share one XCD's L2 (the
+    // item's activations are fetched into one L2, not eight)
+    const int gx = PAIR ? s.I / (32 * (NW / 2)) : s.H / (32 * NW), bid = (int)blockIdx.x, rest = bid >> 3;
+    const int bx = rest % gx, wi = (rest / gx) * 8 + (bid & 7);
+    if (wi >= work_n[0]) return;  // uniform over the block
+    const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, cl = lane & 15;
+    const int K = PAIR ? s.H : s.I, nb = K / QK, k = s.k;
+    const int nch = nb / XT_KC;
+    const int ct_n = (c + 15) >> 4;                  // column tiles holding entries
+
+    // activation row (token for gate/up, entry for down) of item entry t;
+    // rows past the item's last entry read its first row (never stored)
+    auto arow = [&](int t) -> int {
+        const int ent = entries[o + (t < c ? t : 0)];
+        return PAIR ? ent / k : ent;
+    };
+    // staging maps, fixed over the chunks: activation piece and scale sources
+    int aoff[NACT / NW], soff[NAXS / NW];
+#pragma unroll
+    for (int u = 0; u < NACT / NW; u++) {
+        const int j = u * NW + wave, i = j * 64 + lane, t = i / XT_NP, sl = i % XT_NP;
+        aoff[u] = arow(t) * K + xt_slot(sl, t) * 16;  // ^ is an involution: slot sl holds piece xt_slot(sl, t)
+    }
+#pragma unroll
+    for (int u = 0; u < NAXS / NW; u++) {
+        const int j = u * NW + wave, d = j * 64 + lane, bl = d / (16 * XT_CS), rem = d % (16 * XT_CS);
+        const int cs = rem % XT_CS, t = (cs < XT_CT ? cs : 0) * 16 + rem / XT_CS;  // padding words: any row
+        soff[u] = arow(t) * nb + bl;
+    }
+    // this wave's 32 weight rows
+    const int mat = PAIR ? (wave & 1) : 0;  // 0 gate / down, 1 up
+    const int rb = PAIR ? (bx * (NW / 2) + (wave >> 1)) * 32 : (bx * NW + wave) * 32;
+    const uint8_t *ex = layer_pl + (size_t)e * s.EB;
+    const uint8_t *tb = PAIR ? ex + (size_t)mat * s.GB : ex + 2 * s.GB;
+    const int rows = PAIR ? s.I : s.H;
+    const uint8_t *wrow = tb + (size_t)rb * nb * 16;
+    const uint8_t *wsc = tb + (size_t)rows * nb * 16 + (size_t)rb * nb * 2;
+    // weight staging: lane l -> row l / 4 (+16), slot l % 4; scales: row l / 2, half-pair l % 2
+    const int wr0 = lane >> 2, wsl = lane & 3;
+    const int woff0 = wr0 * nb * 16 + xt_wslot(wsl, wr0) * 16;
+    const int woff1 = (wr0 + 16) * nb * 16 + xt_wslot(wsl, wr0 + 16) * 16;
+    const int soffw = (lane >> 1) * nb * 2 + (lane & 1) * 4;
+
+    // activations and their scales: one chunk ahead, two buffers
+    auto stage_act = [&](int ch) {
+        const int q = ch & 1;
+#pragma unroll
+        for (int u = 0; u < NACT / NW; u++) {
+            const int j = u * NW + wave;
+            if (j * 64 < ct_n * 16 * XT_NP)  // rows of column tiles in use (uniform per instruction)
+                lds_dma16(aq + aoff[u] + ch * XT_RB, lds_addr(smem, XtLds::ACT + q * ROWS * XT_RB + j * 1024));
+        }
+#pragma unroll
+        for (int u = 0; u < NAXS / NW; u++) {
+            const int j = u * NW + wave;
+            lds_dma4(ad + soff[u] + ch * XT_KC, lds_addr(smem, XtLds::AXS + (q * XT_KC * 16 * XT_CS + j * 64) * 4));
+        }
+    };
+    // the wave's weight rows and their scales (streamed from HBM): two
+    // chunks ahead, three buffers; XT_WLOADS load instructions per thread
+    constexpr int XT_WLOADS = 3;
+    auto stage_w = [&](int ch) {
+        const int q = ch % 3;
+        const int wq = XtLds::WQ + (q * NW + wave) * 32 * XT_KC * 16;
+        lds_dma16(wrow + woff0 + ch * XT_KC * 16, lds_addr(smem, wq));
+        lds_dma16(wrow + woff1 + ch * XT_KC * 16, lds_addr(smem, wq + 1024));
+        lds_dma4(wsc + soffw + ch * XT_KC * 2, lds_addr(smem, XtLds::WSR + (q * NW + wave) * 32 * XT_KC * 2));
+    };
+
+    float acc[2][XT_CT][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < XT_CT; ct++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[rt][ct][r] = 0.0f;
+    v4i cmag;
+#pragma unroll
+    for (int r = 0; r < 4; r++) cmag[r] = (int)MAGIC_I;
+
+    float *tab = reinterpret_cast<float *>(smem + XtLds::TAB) + wave * XT_KC * 2 * 2 * 16;
+    const int sh = g < 2 ? 4 : 0;  // low nibbles for elements 0..15, high for 16..31
+
+    // issue order: w(0), act(0), w(1); then per chunk ch: act(ch + 1), w(ch + 2)
+    stage_w(0);
+    stage_act(0);
+    if (nch > 1) stage_w(1);
+    auto run = [&](auto ctv) {
+        constexpr int CT = decltype(ctv)::value;
+        for (int ch = 0; ch < nch; ch++) {
+            const int q = ch & 1, qw = ch % 3;
+            // this thread's loads of chunk ch are in LDS: everything but w(ch + 1), issued last, if issued
+            if (ch + 1 < nch)
+                __builtin_amdgcn_s_waitcnt(VMCNT0 | XT_WLOADS);
+            else
+                __builtin_amdgcn_s_waitcnt(VMCNT0);
+            __syncthreads();  // everyone's; and chunk ch - 1 is read by all
+            if (ch + 1 < nch) stage_act(ch + 1);
+            if (ch + 2 < nch) stage_w(ch + 2);
+            // row scales of the chunk: dw / 16 and -1.5 * 2^23 * dw / 16, by lanes 0..31 (row = lane)
+            if (lane < 32) {
+                const uint2 hv = *reinterpret_cast<const uint2 *>(smem + XtLds::WSR +
+                                                                  ((qw * NW + wave) * 32 + lane) * XT_KC * 2);
+                const uint16_t hs[4] = {(uint16_t)hv.x, (uint16_t)(hv.x >> 16), (uint16_t)hv.y,
+                                        (uint16_t)(hv.y >> 16)};
+#pragma unroll
+                for (int bl = 0; bl < XT_KC; bl++) {
+                    const float d16 = h2f(hs[bl]) * 0.0625f;
+                    float *tt = tab + bl * 64 + (lane >> 4) * 16 + (lane & 15);
+                    tt[0] = d16;
+                    tt[32] = -MAGIC_F * d16;
+                }
+            }
+            wave_lds_sync();
+            const uint8_t *act = smem + XtLds::ACT + q * ROWS * XT_RB;
+            const float *axs = reinterpret_cast<const float *>(smem + XtLds::AXS) + q * XT_KC * 16 * XT_CS;
+            const uint8_t *wq = smem + XtLds::WQ + (qw * NW + wave) * 32 * XT_KC * 16;
+            // one block's operands: raw weight bytes (unpacked on use), row scales, activation scales and bytes
+            struct Ops {
+                uint2 w[2];
+                float dw[2][4], cw[2][4];
+                float dx[XT_CS];
+                long b[CT];
+            };
+            auto load = [&](int bl, Ops &o) {
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++) {
+                    const int r = rt * 16 + cl;
+                    o.w[rt] = *reinterpret_cast<const uint2 *>(wq + r * XT_KC * 16 + xt_wslot(bl, r) * 16 + 8 * (g & 1));
+                    const float4 v = *reinterpret_cast<const float4 *>(tab + bl * 64 + rt * 16 + 4 * g);
+                    const float4 u = *reinterpret_cast<const float4 *>(tab + bl * 64 + 32 + rt * 16 + 4 * g);
+                    o.dw[rt][0] = v.x; o.dw[rt][1] = v.y; o.dw[rt][2] = v.z; o.dw[rt][3] = v.w;
+                    o.cw[rt][0] = u.x; o.cw[rt][1] = u.y; o.cw[rt][2] = u.z; o.cw[rt][3] = u.w;
+                }
+#pragma unroll
+                for (int c4 = 0; c4 < (CT + 3) / 4; c4++) {
+                    const float4 v = *reinterpret_cast<const float4 *>(axs + (bl * 16 + cl) * XT_CS + 4 * c4);
+                    o.dx[4 * c4] = v.x; o.dx[4 * c4 + 1] = v.y; o.dx[4 * c4 + 2] = v.z; o.dx[4 * c4 + 3] = v.w;
+                }
+                const int p = bl * 2 + (g >> 1);
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) {
+                    const int t = ct * 16 + cl;
+                    o.b[ct] = *reinterpret_cast<const long *>(act + t * XT_RB + xt_slot(p, t) * 16 + 8 * (g & 1));
+                }
+            };
+            auto compute = [&](const Ops &o) {
+                __builtin_amdgcn_sched_barrier(0);
+                const long a[2] = {xt_unpack(o.w[0], sh), xt_unpack(o.w[1], sh)};
+                // product i = (column tile i / 2, row tile i % 2); product i + 1
+                // is issued before product i's epilogue (two result sets)
+                v4i dq0, dq1;
+                dq0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[0], o.b[0], cmag, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 2 * CT; i++) {
+                    const int ct = i >> 1, rt = i & 1;
+                    // the scheduler keeps this order: MFMA i + 1, then product i's epilogue
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (i + 1 < 2 * CT) {
+                        const v4i nx = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[(i + 1) & 1], o.b[(i + 1) >> 1], cmag,
+                                                                             0, 0, 0);
+                        if (i & 1) dq0 = nx; else dq1 = nx;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    const v4i d = (i & 1) ? dq1 : dq0;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float u = __builtin_fmaf(__int_as_float(d[r]), o.dw[rt][r], o.cw[rt][r]);
+                        acc[rt][ct][r] = __builtin_fmaf(u, o.dx[ct], acc[rt][ct][r]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            // two operand sets in turn: block bl + 1's loads are in flight during block bl's products
+            static_assert(XT_KC % 2 == 0, "blocks per chunk in pairs");
+            Ops oa, ob;
+            load(0, oa);
+#pragma unroll
+            for (int bl = 0; bl < XT_KC; bl += 2) {
+                load(bl + 1, ob);
+                compute(oa);
+                if (bl + 2 < XT_KC) load(bl + 2, oa);
+                compute(ob);
+            }
+        }
+    };
+    // the item's column tiles, rounded up to an even count
+    if (ct_n > 8) run(Tiles<10>{});
+    else if (ct_n > 6) run(Tiles<8>{});
+    else if (ct_n > 4) run(Tiles<6>{});
+    else if (ct_n > 2) run(Tiles<4>{});
+    else run(Tiles<2>{});
+    __syncthreads();  // the staging buffers are free for the hand-off
+
+    if (PAIR) {
+        // up sums -> LDS, gate waves combine
+        float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * 64 * 2 * XT_CT * 4;
+        if (mat == 1) {
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int ct = 0; ct < XT_CT; ct++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) x[((rt * XT_CT + ct) * 4 + r) * 64 + lane] = acc[rt][ct][r];
+        }
+        __syncthreads();
+        if (mat == 1) return;
+        const int nt = rb >> 5;  // I-block of the 32 rows
+#pragma unroll
+        for (int ct = 0; ct < XT_CT; ct++) {
+            const int t = ct * 16 + cl;
+            const bool on = t < c;
+            float hv[2][4], a = 0.0f;
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    hv[rt][r] = on ? silu_mul(acc[rt][ct][r], x[((rt * XT_CT + ct) * 4 + r) * 64 + lane]) : 0.0f;
+                    const float v = fabsf(hv[rt][r]);
+                    a = v > a ? v : a;
+                }
+            float ao = __shfl_xor(a, 16, WAVE);
+            a = ao > a ? ao : a;
+            ao = __shfl_xor(a, 32, WAVE);
+            a = ao > a ? ao : a;
+            const float d = a / 127.0f;
+            const float inv = a > 0.0f ? 127.0f / a : 0.0f;
+            int qv[2][4], sum = 0;
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    qv[rt][r] = (int)__builtin_rintf(hv[rt][r] * inv);
+                    sum += qv[rt][r];
+                }
+            sum += __shfl_xor(sum, 16, WAVE);
+            sum += __shfl_xor(sum, 32, WAVE);
+            if (on) {
+                const int ent = entries[o + t];
+                int8_t *dst = oq + (size_t)ent * s.I + rb + 4 * g;
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++) {
+                    const uint32_t w = (uint32_t)(qv[rt][0] & 0xFF) | ((uint32_t)(qv[rt][1] & 0xFF) << 8) |
+                                       ((uint32_t)(qv[rt][2] & 0xFF) << 16) | ((uint32_t)(qv[rt][3] & 0xFF) << 24);
+                    *reinterpret_cast<uint32_t *>(dst + 16 * rt) = w;
+                }
+                if (g == 0) {
+                    od[(size_t)ent * s.nbI + nt] = h2f(f2h(d));
+                    os[(size_t)ent * s.nbI + nt] = sum;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int ct = 0; ct < XT_CT; ct++) {
+            const int t = ct * 16 + cl;
+            if (t < c) {
+                float *dst = D + (size_t)entries[o + t] * s.H + rb + 4 * g;
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++)
+                    *reinterpret_cast<float4 *>(dst + 16 * rt) =
+                        make_float4(acc[rt][ct][0], acc[rt][ct][1], acc[rt][ct][2], acc[rt][ct][3]);
+            }
+        }
+    }
+}
+
 // ================================================================ launchers
 static inline unsigned mf_cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+static bool x16_ok(const Shape &s, bool pair);
+
+// entries per work item of the MFMA path at mt M-tiles: the 16 x 16 kernels
+// take up to XT_CT * 16 (both of them must fit the shape)
+int mfma_item_entries(const Shape &s, int mt) {
+    return mt == 4 && x16_ok(s, true) && x16_ok(s, false) ? XT_CT * 16 : 32 * mt;
+}
 
 int mfma_tiles(const Shape &s, int T) {
     // entries per expert in a work item: up to 4 M-tiles of 32; fewer when
@@ -655,6 +1027,35 @@ static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
     return hipGetLastError();
 }
 
+// the 16 x 16 kernel: whole chunks of K, whole 32-row groups per block
+static bool x16_ok(const Shape &s, bool pair) {
+    static const bool on = [] {
+        const char *v = getenv("TG_MFMA16");
+        return !(v && v[0] == '0');
+    }();
+    const int nb = (pair ? s.H : s.I) / QK, rows = pair ? s.I : s.H;
+    return on && nb % XT_KC == 0 && rows % (pair ? 32 * (XT_NW / 2) : 32 * XT_NW) == 0;
+}
+
+template <bool PAIR>
+static hipError_t x16_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                         const int32_t *work_n, const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq,
+                         float *od, int *os, float *D, hipStream_t st) {
+    const unsigned gx = PAIR ? (unsigned)(s.I / (32 * (XT_NW / 2))) : (unsigned)(s.H / (32 * XT_NW));
+    static bool attr = false;
+    if (!attr && XtLds::BYTES > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma16<PAIR>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, XtLds::BYTES);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    // one dimension: gx blocks for each of wmax items, wmax rounded up to 8
+    const unsigned wm8 = (unsigned)((wmax + 7) / 8 * 8);
+    TG_LAUNCH((k_mfma16<PAIR>), dim3(gx * wm8), dim3(XT_NW * 64), XtLds::BYTES, st, layer_pl, s, work, work_n,
+              entries, aq, ad, oq, od, os, D);
+    return hipGetLastError();
+}
+
 hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                               const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
                               const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
@@ -662,6 +1063,8 @@ hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, i
     (void)xs;
     if (mt == 1) return ms_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
     if (mt == 2) return mf_go<2, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+    if (mfma_item_entries(s, mt) > 128)
+        return x16_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
     return mf_go<4, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
 }
 
@@ -674,6 +1077,8 @@ hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int
                                      D, st);
     if (mt == 2) return mf_go<2, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
                                         D, st);
+    if (mfma_item_entries(s, mt) > 128)
+        return x16_go<false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
     return mf_go<4, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
 }
 

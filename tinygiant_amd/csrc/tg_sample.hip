@@ -76,13 +76,6 @@ TG_DEV double rdl(double v, int i) {
     return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 }
 
-// LDS written by some lanes of a wave and read by others of the same wave
-TG_DEV void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // ------------------------------------------------ numpy's pairwise sum
 // Base case of numpy's pairwise summation, n <= 128 values v[0..n).
 TG_DEV float pw_leaf(const float *v, int n) {
