@@ -849,22 +849,27 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
                     o.b[ct] = *reinterpret_cast<const long *>(act + t * XT_RB + xt_slot(p, t) * 16 + 8 * (g & 1));
                 }
             };
-            auto compute = [&](const Ops &o) {
-                __builtin_amdgcn_sched_barrier(0);
-                const long a[2] = {xt_unpack(o.w[0], sh), xt_unpack(o.w[1], sh)};
-                // product i = (column tile i / 2, row tile i % 2); product i + 1
-                // is issued before product i's epilogue (two result sets)
-                v4i dq0, dq1;
-                dq0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[0], o.b[0], cmag, 0, 0, 0);
+            // block products: product i = (column tile i / 2, row tile i % 2);
+            // product i + 1 is issued before product i's epilogue (two result
+            // sets), and the next block's product 0 before this block's last
+            // epilogue (the last product is odd: it uses set 1, product 0 set 0)
+            v4i dq0, dq1;
+            long a[2];
+            auto compute = [&](const Ops &o, const Ops &nx, auto has_next) {
+                constexpr bool HN = decltype(has_next)::value != 0;
+                long an[2] = {0, 0};
 #pragma unroll
                 for (int i = 0; i < 2 * CT; i++) {
                     const int ct = i >> 1, rt = i & 1;
-                    // the scheduler keeps this order: MFMA i + 1, then product i's epilogue
                     __builtin_amdgcn_sched_barrier(0);
                     if (i + 1 < 2 * CT) {
-                        const v4i nx = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[(i + 1) & 1], o.b[(i + 1) >> 1], cmag,
-                                                                             0, 0, 0);
-                        if (i & 1) dq0 = nx; else dq1 = nx;
+                        const v4i m = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[(i + 1) & 1], o.b[(i + 1) >> 1], cmag,
+                                                                            0, 0, 0);
+                        if (i & 1) dq0 = m; else dq1 = m;
+                    } else if constexpr (HN) {
+                        an[0] = xt_unpack(nx.w[0], sh);
+                        an[1] = xt_unpack(nx.w[1], sh);
+                        dq0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(an[0], nx.b[0], cmag, 0, 0, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                     const v4i d = (i & 1) ? dq1 : dq0;
@@ -875,23 +880,34 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                a[0] = an[0];
+                a[1] = an[1];
             };
             // two operand sets in turn: block bl + 1's loads are in flight during block bl's products
             static_assert(XT_KC % 2 == 0, "blocks per chunk in pairs");
             Ops oa, ob;
             load(0, oa);
+            a[0] = xt_unpack(oa.w[0], sh);
+            a[1] = xt_unpack(oa.w[1], sh);
+            dq0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[0], oa.b[0], cmag, 0, 0, 0);
 #pragma unroll
             for (int bl = 0; bl < XT_KC; bl += 2) {
                 load(bl + 1, ob);
-                compute(oa);
-                if (bl + 2 < XT_KC) load(bl + 2, oa);
-                compute(ob);
+                compute(oa, ob, Tiles<1>{});
+                if (bl + 2 < XT_KC) {
+                    load(bl + 2, oa);
+                    compute(ob, oa, Tiles<1>{});
+                } else {
+                    compute(ob, oa, Tiles<0>{});
+                }
             }
         }
     };
-    // the item's column tiles, rounded up to an even count
-    if (ct_n > 8) run(Tiles<10>{});
-    else if (ct_n > 6) run(Tiles<8>{});
+    // the item's column tiles (below 6 rounded up to an even count)
+    if (ct_n > 9) run(Tiles<10>{});
+    else if (ct_n > 8) run(Tiles<9>{});
+    else if (ct_n > 7) run(Tiles<8>{});
+    else if (ct_n > 6) run(Tiles<7>{});
     else if (ct_n > 4) run(Tiles<6>{});
     else if (ct_n > 2) run(Tiles<4>{});
     else run(Tiles<2>{});
