@@ -348,18 +348,23 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
 // (lane h*32+n: weight row n), so lane l, register r of the result holds
 // (entry 8 (r/4) + 4h + r%4, weight row l % 32).  The weight scale is then one
 // value per lane, and the epilogue runs only the register groups (8 entries
-// each) that hold entries of the item.  Per block and entry group the same
-// steps as k_mfma_grouped: u = fma(D, dw, -1.5 * 2^23 * dw) = round(S * dw),
-// acc = fma(u, dx, acc), blocks in ascending order.  Gate/up: waves 2i / 2i+1
+// each) that hold entries of the item.  The weight bytes enter the MFMA as
+// 16 (q - 8) (as in the 16 x 16 kernel) against an inline zero accumulator,
+// so D = 16 S exactly; per block and entry group u16 = round(float(D) * dw)
+// = 16 round(S * dw) and acc = fma(u16, dx / 16, acc) = fma(round(S * dw),
+// dx, acc) bit for bit (powers of two scale exactly), blocks in ascending
+// order: the row-dot definition.  Gate/up: waves 2i / 2i+1
 // take gate / up of tile 2x + i, meet in LDS, and the gate wave applies
 // SwiGLU and Q8_0 to each entry's 32 rows (one per lane of a half-wave:
 // maximum and sum by row rotations and a swap of the rows).
 // Weights: per chunk of MF_KC = 8 blocks, lane (n, h) loads row n's blocks
 // 4h .. 4h+3 (64 contiguous bytes; the two lanes of a row cover its whole
 // 128-byte line) and, with nb % 8 == 0, the row's 8 scales in one 16-byte
-// load; the next chunk's loads are in flight while this one computes.  Block
-// bl's 16 bytes reach both lanes of the row through one lane-half swap.
+// load; the loads of the next two chunks are in flight while this one
+// computes.  Block bl's 16 bytes reach both lanes of the row through one
+// lane-half swap.
 constexpr int MS_NW = 4;    // waves per block
+constexpr int MS_PF = 2;    // weight chunks in flight per wave
 
 __host__ __device__ inline size_t ms_lds_bytes() { return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4; }
 
@@ -448,40 +453,45 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     const uint4 *q0 = reinterpret_cast<const uint4 *>(tb) + (size_t)R * nb;
     const uint16_t *s0 = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + (size_t)R * nb;
 
+    // activation staging: unconditional loads from clamped, in-bounds
+    // addresses (entries past the item and blocks past K select zero when
+    // committed), so the waits before the commit count exactly the loads
+    // issued after them and leave the weight loads in flight
     uint4 sv[NTP];
     float sd[NDX];
     auto stage = [&](int ch) {
 #pragma unroll
         for (int u = 0; u < NTP; u++) {
-            const int kb = ch * MF_KC * 32 + sp * 16;
-            sv[u] = make_uint4(0u, 0u, 0u, 0u);
-            if (toff[u] >= 0 && kb < K) sv[u] = *reinterpret_cast<const uint4 *>(aq + toff[u] + kb);
+            const int kb = min(ch * MF_KC * 32 + sp * 16, K - 16);
+            sv[u] = *reinterpret_cast<const uint4 *>(aq + max(toff[u], 0) + kb);
         }
 #pragma unroll
-        for (int u = 0; u < NDX; u++) {
-            const int b = ch * MF_KC + sb;
-            sd[u] = (doff[u] >= 0 && b < nb) ? ad[doff[u] + b] : 0.0f;
-        }
+        for (int u = 0; u < NDX; u++) sd[u] = ad[max(doff[u], 0) + min(ch * MF_KC + sb, nb - 1)];
     };
-    auto commit = [&](int q) {
+    auto commit = [&](int q, int ch) {
 #pragma unroll
         for (int u = 0; u < NTP; u++) {
             const int t = tid / TP + u * (NT / TP);
-            *reinterpret_cast<uint4 *>(tokl + ((size_t)q * M + t) * MF_TS + sp * 16) = sv[u];
+            const bool ok = toff[u] >= 0 && ch * MF_KC * 32 + sp * 16 < K;
+            *reinterpret_cast<uint4 *>(tokl + ((size_t)q * M + t) * MF_TS + sp * 16) =
+                ok ? sv[u] : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int u = 0; u < NDX; u++) {
             const int t = tid / MF_KC + u * (NT / MF_KC);
-            dxl[(q * MF_KC + sb) * M + t] = sd[u];
+            const bool ok = doff[u] >= 0 && ch * MF_KC + sb < nb;
+            dxl[(q * MF_KC + sb) * M + t] = ok ? sd[u] * 0.0625f : 0.0f;  // dx / 16, exact
         }
     };
     // row R's weights of chunk ch: blocks 8ch + 4h + i (clamped; blocks past
-    // nb are never used) and the chunk's 8 scales (packed halves)
+    // nb are never used) and the chunk's 8 scales (packed halves); chunks
+    // past the last load the last one again (unconditional loads keep the
+    // waits exact)
     auto wload = [&](int ch, uint4 (&w)[4], uint4 &sc) {
 #pragma unroll
         for (int i = 0; i < 4; i++) w[i] = q0[min(ch * MF_KC + 4 * h + i, nb - 1)];
         if (SCV) {
-            sc = *reinterpret_cast<const uint4 *>(s0 + ch * MF_KC);
+            sc = *reinterpret_cast<const uint4 *>(s0 + min(ch, nch - 1) * MF_KC);
         } else {
             uint32_t hv[MF_KC];
 #pragma unroll
@@ -494,71 +504,86 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
 
-    uint4 wc[4], sc;
-    wload(0, wc, sc);
+    // weights run MS_PF chunks ahead in MS_PF + 1 register sets, each with a
+    // fixed role per unrolled step (a copy between sets would wait for the
+    // loads in flight); the activations one chunk ahead, issued before the
+    // newer weight loads so the wait before their commit leaves those in
+    // flight
+    static_assert(MS_PF == 2, "three register sets");
+    uint4 wa[4], sa, wb[4], sbv, wcx[4], scx;
+    wload(0, wa, sa);
     stage(0);
-    commit(0);
-    v16i cmag;
-#pragma unroll
-    for (int r = 0; r < 16; r++) cmag[r] = (int)MAGIC_I;
+    wload(1, wb, sbv);
+    commit(0, 0);
+    const v16i czero = {};  // the accumulator operand: an inline 0, no registers
+    const int nsh = h ? 0 : 4;  // this half's nibble to the high half of each byte
     __syncthreads();
 
     // register groups holding entries of the item (8 entries per group)
     auto run = [&](auto ngc) {
         constexpr int NG = decltype(ngc)::value;
-        for (int ch = 0; ch < nch; ch++) {
+        // chunk ch from set w (scales sc); chunk ch + MS_PF loads into set wl
+        auto step = [&](int ch, uint4 (&w)[4], const uint4 &sc, uint4 (&wl)[4], uint4 &sl) {
             const int q = ch & 1;
-            uint4 wn[4], sn;
-            if (ch + 1 < nch) {
-                wload(ch + 1, wn, sn);
-                stage(ch + 1);
-            }
-            const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
-            const float *xq = dxl + q * MF_KC * M + 4 * h;
-            const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+            stage(ch + 1);
+            __builtin_amdgcn_sched_barrier(0);  // activations issued before the weights
+            wload(ch + MS_PF, wl, sl);
+            if (ch < nch) {  // uniform
+                const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
+                const float *xq = dxl + q * MF_KC * M + 4 * h;
+                const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-            for (int bl = 0; bl < MF_KC; bl++) {
-                const int b = ch * MF_KC + bl;
-                if (b < nb) {
-                    // block bl sits in wc[bl % 4] of the half bl / 4 lane: the swap
-                    // at bl < 4 yields block bl and keeps block bl + 4 in wc[bl]
-                    uint4 blk;
-                    if (bl < 4) {
-                        uint4 &w = wc[bl];
-                        half_split(w.x, blk.x, w.x);
-                        half_split(w.y, blk.y, w.y);
-                        half_split(w.z, blk.z, w.z);
-                        half_split(w.w, blk.w, w.w);
-                    } else {
-                        blk = wc[bl & 3];
-                    }
-                    const v4i wb = h ? nib_hi(blk) : nib_lo(blk);
-                    const v4i ta = *reinterpret_cast<const v4i *>(tq + bl * 32);
-                    const float dw = h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1))));
-                    const float cw = -MAGIC_F * dw;
-                    float4 dx[NG];
+                for (int bl = 0; bl < MF_KC; bl++) {
+                    const int b = ch * MF_KC + bl;
+                    if (b < nb) {
+                        // block bl sits in w[bl % 4] of the half bl / 4 lane: the swap
+                        // at bl < 4 yields block bl and keeps block bl + 4 in w[bl]
+                        uint4 blk;
+                        if (bl < 4) {
+                            uint4 &wr = w[bl];
+                            half_split(wr.x, blk.x, wr.x);
+                            half_split(wr.y, blk.y, wr.y);
+                            half_split(wr.z, blk.z, wr.z);
+                            half_split(wr.w, blk.w, wr.w);
+                        } else {
+                            blk = w[bl & 3];
+                        }
+                        // 16 (q - 8) per byte: ((q << 4) & 0xF0) ^ 0x80, exact in int8
+                        v4i wq;
+                        wq.x = (int)(((blk.x << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+                        wq.y = (int)(((blk.y << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+                        wq.z = (int)(((blk.z << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+                        wq.w = (int)(((blk.w << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+                        const v4i ta = *reinterpret_cast<const v4i *>(tq + bl * 32);
+                        const float dw = h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1))));
+                        float4 dx[NG];
 #pragma unroll
-                    for (int g = 0; g < NG; g++) dx[g] = *reinterpret_cast<const float4 *>(xq + bl * M + 8 * g);
-                    const v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ta, wb, cmag, 0, 0, 0);
+                        for (int g = 0; g < NG; g++) dx[g] = *reinterpret_cast<const float4 *>(xq + bl * M + 8 * g);
+                        // rc = 16 S exactly (|16 S| < 2^24): u16 = round(16 S * dw) =
+                        // 16 round(S * dw), and u16 * (dx / 16) = round(S * dw) * dx
+                        const v16i rc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ta, wq, czero, 0, 0, 0);
 #pragma unroll
-                    for (int g = 0; g < NG; g++) {
-                        const float dxa[4] = {dx[g].x, dx[g].y, dx[g].z, dx[g].w};
+                        for (int g = 0; g < NG; g++) {
+                            const float dxa[4] = {dx[g].x, dx[g].y, dx[g].z, dx[g].w};
 #pragma unroll
-                        for (int rr = 0; rr < 4; rr++) {
-                            const int r = 4 * g + rr;
-                            const float u = __builtin_fmaf(__int_as_float(rc[r]), dw, cw);
-                            acc[r] = __builtin_fmaf(u, dxa[rr], acc[r]);
+                            for (int rr = 0; rr < 4; rr++) {
+                                const int r = 4 * g + rr;
+                                const float u16 = (float)rc[r] * dw;
+                                acc[r] = __builtin_fmaf(u16, dxa[rr], acc[r]);
+                            }
                         }
                     }
                 }
             }
-            if (ch + 1 < nch) {
-                commit(q ^ 1);
-#pragma unroll
-                for (int i = 0; i < 4; i++) wc[i] = wn[i];
-                sc = sn;
-            }
+            // unconditional (zeros past the last chunk), so the activation
+            // loads stay ahead of the weight loads
+            commit(q ^ 1, ch + 1);
             __syncthreads();
+        };
+        for (int ch = 0; ch < nch; ch += 3) {
+            step(ch, wa, sa, wcx, scx);
+            step(ch + 1, wb, sbv, wa, sa);
+            step(ch + 2, wcx, scx, wb, sbv);
         }
     };
     const int ng = (c + 7) >> 3;
