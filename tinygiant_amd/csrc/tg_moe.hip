@@ -1485,8 +1485,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
             const int t = tid < k * RD ? tid : 0;
             const float dvl = chain4(U + t * ust, hd + (t >> lrd) * nbp, nb);
             const int r = tid & (RD - 1);
+            // k * RD <= 64 and RD >= 8: k <= 8 slots, all shuffled ahead of
+            // the chain (one LDS round trip instead of one per slot)
+            float dd[8], ww[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                dd[c] = __shfl(dvl, min(c, k - 1) * RD + r, WAVE);
+                ww[c] = sw[min(c, k - 1)];
+            }
             float acc = 0.0f;
-            for (int c = k - 1; c >= 0; c--) acc = __builtin_fmaf(sw[c], __shfl(dvl, c * RD + r, WAVE), acc);
+#pragma unroll
+            for (int c = 7; c >= 0; c--)
+                if (c < k) acc = __builtin_fmaf(ww[c], dd[c], acc);
             o = A.resid ? rv + acc : acc;
         }
     } else {
