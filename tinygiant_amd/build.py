@@ -52,7 +52,8 @@ def _run(cmd, verbose):
 
 # Per-source extra flags.  tg_mfma.hip: MFMA results in ordinary VGPRs, so the
 # fp32 epilogue reads them without a v_accvgpr_read per element.
-EXTRA_FLAGS = {"tg_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA_FLAGS = {"tg_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "tg_moe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def build(verbose: bool = False) -> Path:

@@ -1225,8 +1225,18 @@ TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uin
     lds_barrier();
 }
 
+// The leading arguments (the partials' address, E, G) arrive preloaded in
+// SGPRs (this file is built with kernarg preloading), so the first round of
+// partial loads is issued before any argument is read from memory.
 template <int UG, int UD>
-__global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
+__global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restrict__ part_in, int pe, int pg, LdArgs A,
+                                                          Shape s) {
+    float4 pv0[LD_PC];
+    if ((int)threadIdx.x <= pe) {
+        const float4 *row = reinterpret_cast<const float4 *>(part_in + (size_t)threadIdx.x * pg);
+#pragma unroll
+        for (int q = 0; q < LD_PC; q++) pv0[q] = row[min(q, pg / 4 - 1)];
+    }
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ __align__(16) uint64_t keys[LD_EMAX];
     __shared__ int rcnt[LD_EMAX];
@@ -1276,12 +1286,12 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(LdArgs A, Shape s) {
     // 1. routing: thread e <= E adds row e of the partials in ascending group
     //    order (LD_PC float4 loaded per round, all before the adds)
     if (tid <= E) {
-        const float4 *row = reinterpret_cast<const float4 *>(A.part_in + (size_t)tid * G);
+        const float4 *row = reinterpret_cast<const float4 *>(part_in + (size_t)tid * G);
         float tot = 0.0f;
         for (int c = 0; c < G / 4; c += LD_PC) {
             float4 pv[LD_PC];
 #pragma unroll
-            for (int q = 0; q < LD_PC; q++) pv[q] = row[min(c + q, G / 4 - 1)];
+            for (int q = 0; q < LD_PC; q++) pv[q] = c == 0 ? pv0[q] : row[min(c + q, G / 4 - 1)];
 #pragma unroll
             for (int q = 0; q < LD_PC; q++)
                 if (c + q < G / 4) {
@@ -2234,7 +2244,7 @@ static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
     const size_t lds = ld_lds_bytes(s, A.rd);
     hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD>, lds);
     if (e != hipSuccess) return e;
-    TG_LAUNCH((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A, s);
+    TG_LAUNCH((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG, A, s);
     return hipGetLastError();
 }
 
