@@ -51,9 +51,15 @@ def _run(cmd, verbose):
 
 
 # Per-source extra flags.  tg_mfma.hip: MFMA results in ordinary VGPRs, so the
-# fp32 epilogue reads them without a v_accvgpr_read per element.
-EXTRA_FLAGS = {"tg_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "tg_moe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+# fp32 epilogue reads them without a v_accvgpr_read per element.  Every source:
+# the leading scalar and pointer kernel arguments arrive preloaded in SGPRs, so
+# a kernel's first loads need no round trip to the argument buffer (the code
+# object keeps the argument loads for firmware without the feature).
+EXTRA_FLAGS = {"tg_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=16"],
+               "tg_moe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+               "tg_kernels.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+               "tg_legacy.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+               "tg_sample.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def build(verbose: bool = False) -> Path:
