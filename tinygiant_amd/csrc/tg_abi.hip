@@ -511,10 +511,17 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
                                  float eps, hipStream_t st) {
     const Shape &s = a->s;
     const uint8_t *lp = a->experts + (size_t)layer * s.LB;
-    PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, c.raw, st));
+    // few tokens: the router's group chains go to the down rows' buffer (free
+    // until the down kernel; G T E <= T k H floats when E <= 32 k) and
+    // route_q8 adds them; otherwise the router dots
+    const bool chains = tg::route_chains_usable(T, s.E, s.H) && (size_t)s.E <= 32 * (size_t)s.k;
+    if (chains)
+        PROFILED("route", st, tg::launch_route_chains(router_of(a, layer), x, T, s.E, s.H, c.D, st));
+    else
+        PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, c.raw, st));
     PROFILED("route_q8", st,
-             tg::launch_route_q8(c.raw, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, c.idx, c.w, c.xq, c.xd,
-                                 c.xs, st));
+             tg::launch_route_q8(c.raw, chains ? c.D : nullptr, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, c.idx,
+                                 c.w, c.xq, c.xd, c.xs, st));
     const int n = T * s.k;
     if (mfma_usable(a, T)) {
         const int mt = tg::mfma_tiles(s, T), ch = tg::mfma_item_entries(s, mt), wmax = tg::group_work_max(s, n, ch);

@@ -229,8 +229,14 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *s
 
 // grouped (batched decode / prefill) MoE layer pieces
 bool grouped_shape_ok(const Shape &s);
-hipError_t launch_route_q8(const float *raw, const float *x, const float *gn, int T, int E, int H, int k, float eps,
-                           int32_t *idx, float *w, int8_t *xq, float *xd, int *xs, hipStream_t st);
+// raw [T][E] router dots, or chains [H/32][T][E] (non-null: summed first)
+hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
+                           int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
+                           hipStream_t st);
+// Few tokens: the router's per-group fma chains [H/32][T][E], for
+// launch_route_q8 to add (T < 128, E <= 128 and a multiple of 32).
+bool route_chains_usable(int T, int E, int H);
+hipError_t launch_route_chains(const float *Wr, const float *x, int T, int E, int H, float *chains, hipStream_t st);
 // work list: at most group_work_max(s, n) items per list, two lists
 int group_work_max(const Shape &s, int n);
 int group_work_max(const Shape &s, int n, int ch);

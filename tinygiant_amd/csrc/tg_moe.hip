@@ -135,6 +135,69 @@ __global__ __launch_bounds__(1024) void k_route_small(const float *__restrict__ 
     }
 }
 
+// Few tokens, first half of the routing: block (g, tile) forms, for the
+// RC_T tokens of its tile and every expert, the fma chain of group g (its 32
+// elements in order, from 0) and writes it to chains[g][t][e]; k_route_q8
+// adds a token's chains in ascending group order, so the logits are k_route's
+// bit for bit.  Every router and x element is read once (group g's columns
+// staged in LDS).  Thread (ti, ej): tokens 4 ti .. 4 ti + 3, experts
+// ej + 32 b (b < 4; E <= 128), so a wave's router reads are 32 consecutive
+// rows (conflict-free at the 9-float4 row stride) and its stores coalesce.
+constexpr int RC_T = 32;
+constexpr int RC_THREADS = 256;
+
+__host__ __device__ inline bool route_chains_ok(int E, int H) { return E <= 128 && E % 32 == 0 && H % RG == 0; }
+
+__global__ __launch_bounds__(RC_THREADS) void k_route_chains(const float *__restrict__ Wr, const float *__restrict__ x,
+                                                             int T, int E, int H, float *__restrict__ chains) {
+    constexpr int Q = RG / 4, QS = Q + 1;  // float4 per group row, padded stride
+    __shared__ float4 xs[RC_T * QS];
+    __shared__ float4 ws[128 * QS];
+    const int g = blockIdx.x, t0 = blockIdx.y * RC_T, tid = threadIdx.x;
+    {
+        const int r = tid / Q, q = tid % Q, t = t0 + r;  // RC_T * Q == RC_THREADS
+        xs[r * QS + q] = t < T ? reinterpret_cast<const float4 *>(x + (size_t)t * H + (size_t)g * RG)[q]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int e = r + RC_T * v;
+            if (e < E) ws[e * QS + q] = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + (size_t)g * RG)[q];
+        }
+    }
+    __syncthreads();
+    const int ti = tid >> 5, ej = tid & 31;
+    float acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        float4 xv[4], wv[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) xv[a] = xs[(4 * ti + a) * QS + q];
+#pragma unroll
+        for (int b = 0; b < 4; b++) wv[b] = ws[min(ej + 32 * b, E - 1) * QS + q];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                acc[a][b] = __builtin_fmaf(wv[b].x, xv[a].x, acc[a][b]);
+                acc[a][b] = __builtin_fmaf(wv[b].y, xv[a].y, acc[a][b]);
+                acc[a][b] = __builtin_fmaf(wv[b].z, xv[a].z, acc[a][b]);
+                acc[a][b] = __builtin_fmaf(wv[b].w, xv[a].w, acc[a][b]);
+            }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int t = t0 + 4 * ti + a;
+        if (t < T)
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                if (ej + 32 * b < E) chains[((size_t)g * T + t) * E + ej + 32 * b] = acc[a][b];
+    }
+}
+
 // Many tokens: block = 32 tokens x 32 experts, 256 threads, each thread 2
 // tokens x 2 experts.  Four groups (128 consecutive elements) of x and of the
 // router rows are staged in LDS per step, the next step's loads in flight
@@ -1632,17 +1695,41 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 // token in its own slot order, so every output is deterministic and equal
 // to the per-token path bit for bit.
 
-__global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ x,
+// raw: the router dots [T][E], or (chains != null) the group chains of
+// k_route_chains [G][T][E], which thread e adds in ascending group order
+// first (the same sums as k_route's).
+__global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ chains,
+                                                         int T, const float *__restrict__ x,
                                                          const float *__restrict__ gn, int E, int H, int k, float eps,
                                                          int32_t *__restrict__ idx,
                                                          float *__restrict__ w, int8_t *__restrict__ xq,
                                                          float *__restrict__ xd, int *__restrict__ xs) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float rsum[RO_THREADS];
     RouteLds L = route_lds(smem, H);
     const int t = blockIdx.x, tid = threadIdx.x, nbH = H / QK;
+    const float *rawt = raw + (size_t)t * E;
+    if (chains) {  // uniform
+        if (tid < E) {
+            const int G = H / RG;
+            const float *cp = chains + (size_t)t * E + tid;
+            const size_t gs = (size_t)T * E;
+            float tot = 0.0f;
+            for (int g0 = 0; g0 < G; g0 += 32) {  // 32 loads in flight, then the adds in order
+                float cv[32];
+#pragma unroll
+                for (int u = 0; u < 32; u++) cv[u] = cp[(size_t)min(g0 + u, G - 1) * gs];
+#pragma unroll
+                for (int u = 0; u < 32; u++)
+                    if (g0 + u < G) tot = tot + cv[u];
+            }
+            rsum[tid] = tot;
+        }
+        __syncthreads();
+        rawt = rsum;
+    }
     float xv[RO_MAXPASS][8];
-    route_token(x + (size_t)t * H, raw + (size_t)t * E, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx,
-                L.sred);
+    route_token(x + (size_t)t * H, rawt, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred);
     if (tid == 0) {
         topk_softmax(L.slog, L.sidx, k, L.sw, L.sex);
         for (int i = 0; i < k; i++) {
@@ -2268,12 +2355,22 @@ bool grouped_shape_ok(const Shape &s) {
            gu_grouped_lds(s.nbH) <= 160 * 1024 && dn_grouped_lds(s.nbI, s.I) <= 160 * 1024;
 }
 
-hipError_t launch_route_q8(const float *raw, const float *x, const float *gn, int T, int E, int H, int k, float eps,
-                           int32_t *idx, float *w, int8_t *xq, float *xd, int *xs, hipStream_t st) {
-    size_t lds = route_lds_bytes(H);
+hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
+                           int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
+                           hipStream_t st) {
+    const size_t lds = route_lds_bytes(H);
     hipError_t e = allow_lds((const void *)k_route_q8, lds);
     if (e != hipSuccess) return e;
-    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, x, gn, E, H, k, eps, idx, w, xq, xd, xs);
+    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd,
+              xs);
+    return hipGetLastError();
+}
+
+bool route_chains_usable(int T, int E, int H) { return T < 128 && route_chains_ok(E, H); }
+
+hipError_t launch_route_chains(const float *Wr, const float *x, int T, int E, int H, float *chains, hipStream_t st) {
+    if (!route_chains_usable(T, E, H)) return hipErrorInvalidValue;
+    TG_LAUNCH(k_route_chains, dim3(H / RG, cdiv((size_t)T, RC_T)), dim3(RC_THREADS), 0, st, Wr, x, T, E, H, chains);
     return hipGetLastError();
 }
 
