@@ -198,78 +198,105 @@ __global__ __launch_bounds__(RC_THREADS) void k_route_chains(const float *__rest
     }
 }
 
-// Many tokens: block = 32 tokens x 32 experts, 256 threads, each thread 2
-// tokens x 2 experts.  Four groups (128 consecutive elements) of x and of the
-// router rows are staged in LDS per step, the next step's loads in flight
-// while the current one is used; every (t, e) pair runs each group's fma
-// chain and adds it to its total in ascending group order, exactly as
-// k_route does.
-constexpr int RTT = 32;
-constexpr int RT_CH = 4;               // groups per staging step
-constexpr int RT_W = RT_CH * RG + 4;   // LDS row stride (floats)
+// Many tokens: block = 16 tokens x 32 experts, 256 threads (512 blocks at
+// 2048 tokens, two resident per CU).  Four groups (128 consecutive elements)
+// of x and of the router rows are staged in LDS per step, the next step's
+// loads in flight while the current one is used.  Wave w runs the fma chains
+// of group w of the step (with more groups per step, w + 4, ...) for all 512
+// pairs: lane (ti, ej) takes tokens
+// ti + 8 a (a < 2) and experts ej + 8 b (b < 4), 8 chains from 6 LDS values
+// per element (consecutive rows per lane, conflict-free), element by element
+// across the chains so consecutive fmas are independent.  The chains meet in
+// LDS and thread p adds them to the totals of pairs p and p + 256 in
+// ascending group order, exactly as k_route does.
+constexpr int RTT_T = 16, RTT_E = 32;
+constexpr int RT_CH = 4;                   // groups per staging step (a multiple of 4: waves take w, w + 4, ..)
+constexpr int RT_W = RT_CH * RG + 4;       // LDS row stride (floats)
+constexpr int RT_F4 = RT_CH * RG / 4;      // float4 per staged row and step
+constexpr int RT_PAIRS = RTT_T * RTT_E;    // 512
 
 __global__ __launch_bounds__(256) void k_route_tiled(const float *__restrict__ Wr, const float *__restrict__ x,
                                                      int T, int E, int H, float *__restrict__ raw) {
-    __shared__ __align__(16) float xs[RTT][RT_W];
-    __shared__ __align__(16) float ws[RTT][RT_W];
-    const int tid = threadIdx.x, t0 = blockIdx.x * RTT, e0 = blockIdx.y * RTT;
-    const int tt = (tid >> 4) * 2, ee = (tid & 15) * 2;  // this thread's 2 tokens, 2 experts
-    // staging: thread loads rows r = tid / 32 + 8 v (v < 4), float4 column c4
-    const int sr = tid >> 5, sc = (tid & 31) * 4;
-    float tot[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
-    const int G = H / RG, nst = G / RT_CH;
-    float4 xv[4], wv[4];
-    auto fetch = [&](int st) {
+    __shared__ __align__(16) float xs[RTT_T][RT_W];
+    __shared__ __align__(16) float ws[RTT_E][RT_W];
+    __shared__ float cs[RT_CH][RT_PAIRS];
+    const int tid = threadIdx.x, t0 = blockIdx.x * RTT_T, e0 = blockIdx.y * RTT_E;
+    const int gw = tid >> 6, ti = (tid >> 3) & 7, ej = tid & 7;
+    // staging: thread loads rows r = tid / 32 + 8 v, float4 column c4
+    const int sr = tid / RT_F4, sc = (tid % RT_F4) * 4;
+    constexpr int RS = 256 / RT_F4;  // rows per staging pass (8)
+    constexpr int TA = RTT_T / 8, TP = RT_PAIRS / 256;  // tokens per lane, pairs per thread
+    float tot[TP];                    // pairs tid + 256 j: token p / 32, expert p % 32
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int r = sr + 8 * v, t = t0 + r, e = e0 + r;
-            const size_t col = (size_t)st * RT_CH * RG + sc;
+    for (int j = 0; j < TP; j++) tot[j] = 0.0f;
+    const int G = H / RG, nst = G / RT_CH;
+    float4 xv[RTT_T / RS], wv[RTT_E / RS];
+    auto fetch = [&](int st) {
+        const size_t col = (size_t)st * RT_CH * RG + sc;
+#pragma unroll
+        for (int v = 0; v < RTT_T / RS; v++) {
+            const int t = t0 + sr + RS * v;
             xv[v] = t < T ? *reinterpret_cast<const float4 *>(x + (size_t)t * H + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int v = 0; v < RTT_E / RS; v++) {
+            const int e = e0 + sr + RS * v;
             wv[v] = e < E ? *reinterpret_cast<const float4 *>(Wr + (size_t)e * H + col) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     fetch(0);
     for (int st = 0; st < nst; st++) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            *reinterpret_cast<float4 *>(&xs[sr + 8 * v][sc]) = xv[v];
-            *reinterpret_cast<float4 *>(&ws[sr + 8 * v][sc]) = wv[v];
-        }
-        __syncthreads();
+        for (int v = 0; v < RTT_T / RS; v++) *reinterpret_cast<float4 *>(&xs[sr + RS * v][sc]) = xv[v];
+#pragma unroll
+        for (int v = 0; v < RTT_E / RS; v++) *reinterpret_cast<float4 *>(&ws[sr + RS * v][sc]) = wv[v];
+        __syncthreads();  // staged rows in; the previous step's chains read
         if (st + 1 < nst) fetch(st + 1);
 #pragma unroll
-        for (int gg = 0; gg < RT_CH; gg++) {
-            float a[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+        for (int h = 0; h < RT_CH / 4; h++) {
+        const int gl = gw + 4 * h;
+        float a[TA][4];
 #pragma unroll
-            for (int q = 0; q < RG / 4; q++) {
-                const int c = gg * RG + 4 * q;
-                const float4 x0 = *reinterpret_cast<const float4 *>(&xs[tt][c]);
-                const float4 x1 = *reinterpret_cast<const float4 *>(&xs[tt + 1][c]);
-                const float4 w0 = *reinterpret_cast<const float4 *>(&ws[ee][c]);
-                const float4 w1 = *reinterpret_cast<const float4 *>(&ws[ee + 1][c]);
-                const float xa[2][4] = {{x0.x, x0.y, x0.z, x0.w}, {x1.x, x1.y, x1.z, x1.w}};
-                const float wa[2][4] = {{w0.x, w0.y, w0.z, w0.w}, {w1.x, w1.y, w1.z, w1.w}};
+        for (int i = 0; i < TA; i++)
 #pragma unroll
-                for (int cc = 0; cc < 4; cc++)
+            for (int j = 0; j < 4; j++) a[i][j] = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 2; i++)
+        for (int q = 0; q < RG / 4; q++) {
+            const int c = gl * RG + 4 * q;
+            float xe[TA][4], we[4][4];
 #pragma unroll
-                        for (int j = 0; j < 2; j++) a[i][j] = __builtin_fmaf(wa[j][cc], xa[i][cc], a[i][j]);
+            for (int i = 0; i < TA; i++) {
+                const float4 v = *reinterpret_cast<const float4 *>(&xs[ti + 8 * i][c]);
+                xe[i][0] = v.x; xe[i][1] = v.y; xe[i][2] = v.z; xe[i][3] = v.w;
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int j = 0; j < 4; j++) {
+                const float4 v = *reinterpret_cast<const float4 *>(&ws[ej + 8 * j][c]);
+                we[j][0] = v.x; we[j][1] = v.y; we[j][2] = v.z; we[j][3] = v.w;
+            }
 #pragma unroll
-                for (int j = 0; j < 2; j++) tot[i][j] = tot[i][j] + a[i][j];
+            for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+                for (int i = 0; i < TA; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) a[i][j] = __builtin_fmaf(we[j][cc], xe[i][cc], a[i][j]);
         }
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TA; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) cs[gl][(ti + 8 * i) * RTT_E + ej + 8 * j] = a[i][j];
+        }
+        __syncthreads();  // the step's chains in
+#pragma unroll
+        for (int j = 0; j < TP; j++)
+#pragma unroll
+            for (int g = 0; g < RT_CH; g++) tot[j] = tot[j] + cs[g][tid + 256 * j];
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int t = t0 + tt + i, e = e0 + ee + j;
-            if (t < T && e < E) raw[(size_t)t * E + e] = tot[i][j];
-        }
+    for (int j = 0; j < TP; j++) {
+        const int p = tid + 256 * j, t = t0 + p / RTT_E, e = e0 + p % RTT_E;
+        if (t < T && e < E) raw[(size_t)t * E + e] = tot[j];
+    }
 }
 
 // NaN logits rank below every number (as -inf) and -0 equals +0, so the
@@ -2174,8 +2201,8 @@ bool decode_shape_ok(const Shape &s) {
 
 hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
     if (T >= 128 && (H / RG) % RT_CH == 0) {
-        TG_LAUNCH(k_route_tiled, dim3(cdiv((size_t)T, RTT), cdiv((size_t)E, RTT)), dim3(256), 0, st, Wr, x,
-                           T, E, H, raw);
+        TG_LAUNCH(k_route_tiled, dim3(cdiv((size_t)T, RTT_T), cdiv((size_t)E, RTT_E)), dim3(256), 0, st, Wr, x, T,
+                  E, H, raw);
     } else if (T >= RS_T && (H / RG) % (2 * RS_PARTS) == 0 && route_small_lds(H) <= 64 * 1024) {
         const size_t lds = route_small_lds(H);
         hipError_t e = allow_lds((const void *)k_route_small, lds);
