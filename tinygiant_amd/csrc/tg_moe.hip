@@ -1785,6 +1785,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
 
 constexpr int GR_THREADS = 1024;
 constexpr int GR_PER = 16;  // entries per thread per pass of k_group
+constexpr int GR_LDS_ENTRIES = 16384;  // entry lists staged in LDS up to this many entries
 
 // Exclusive prefix sums of N ints per thread over threads 0..255 (threads
 // >= n count as 0) with one pair of barriers: a shuffle scan per wave and
@@ -1936,6 +1937,11 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
     }
     __syncthreads();
     }
+    // entry lists: built in LDS when they fit (the dynamic buffer holds n
+    // ints), then written out in order, coalesced; scattered 4-byte stores
+    // to global memory cost one cache line each
+    extern __shared__ int ent_l[];
+    const bool in_lds = n <= GR_LDS_ENTRIES;
     for (int base = 0; base < n; base += GR_THREADS * GR_PER) {
         int ev[GR_PER];
 #pragma unroll
@@ -1949,9 +1955,16 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
             if (i < n) {
                 const int e = ev[u] < 0 ? 0 : (ev[u] >= E ? E - 1 : ev[u]);
                 const int pos = atomicAdd(&fill[e], 1);
-                entries[off[e] + pos] = i;
+                if (in_lds)
+                    ent_l[off[e] + pos] = i;
+                else
+                    entries[off[e] + pos] = i;
             }
         }
+    }
+    if (in_lds) {
+        __syncthreads();
+        for (int i = tid; i < n; i += GR_THREADS) entries[i] = ent_l[i];
     }
 }
 
@@ -2411,23 +2424,30 @@ int group_work_max(const Shape &s, int n) {
     return group_work_max(s, n, ch);
 }
 
+template <bool SORT>
+static hipError_t group_go(const int32_t *idx, int n, int E, int ch, int chd, int wmax, int32_t *counts,
+                           int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
+    const size_t lds = n <= GR_LDS_ENTRIES ? 4 * (size_t)n : 0;
+    hipError_t e = allow_lds((const void *)k_group<SORT>, lds);
+    if (e != hipSuccess) return e;
+    TG_LAUNCH(k_group<SORT>, dim3(1), dim3(GR_THREADS), lds, st, idx, n, E, ch, chd, wmax, counts, offsets, entries,
+              work, work_n);
+    return hipGetLastError();
+}
+
 hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
-    TG_LAUNCH(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, gu_chunk(s.nbH),
-                       dn_chunk(s.nbI, s.I), group_work_max(s, n), counts, offsets, entries, work, work_n);
-    return hipGetLastError();
+    return group_go<false>(idx, n, s.E, gu_chunk(s.nbH), dn_chunk(s.nbI, s.I), group_work_max(s, n), counts,
+                           offsets, entries, work, work_n, st);
 }
 
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
                                 int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
     // items of several M-tiles: largest first (one-tile items are all alike)
     if (ch > 32)
-        TG_LAUNCH(k_group<true>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
-                           group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
-    else
-        TG_LAUNCH(k_group<false>, dim3(1), dim3(GR_THREADS), 0, st, idx, n, s.E, ch, ch,
-                           group_work_max(s, n, ch), counts, offsets, entries, work, work_n);
-    return hipGetLastError();
+        return group_go<true>(idx, n, s.E, ch, ch, group_work_max(s, n, ch), counts, offsets, entries, work, work_n,
+                              st);
+    return group_go<false>(idx, n, s.E, ch, ch, group_work_max(s, n, ch), counts, offsets, entries, work, work_n, st);
 }
 
 template <int NT, int UNR>
