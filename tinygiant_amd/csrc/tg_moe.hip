@@ -1017,11 +1017,12 @@ TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, 
 // by one store, and is shared through the L2 by the blocks of an XCD), and
 // polls again only a word that still carries an old tag.  Bounded; false
 // when a poll ran out of tries.
-TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW]) {
-    constexpr int LAST = FX_QW - 1;
+template <int NW>
+TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW]) {
+    constexpr int LAST = NW - 1;
     uint32_t tries = 0;
 #pragma unroll
-    for (int i = 0; i < FX_QW; i++) pay[i] = 0u;
+    for (int i = 0; i < NW; i++) pay[i] = 0u;
     uint64_t v = ll_get(src + LAST);
     while ((uint32_t)(v >> 32) != tag) {
         if (++tries >= RD_SPIN_LIMIT) return false;
@@ -1056,6 +1057,10 @@ TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_Q
         __builtin_amdgcn_s_sleep(2);
     }
     return true;
+}
+
+TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW]) {
+    return fx_read_words<FX_QW>(src, tag, pay);
 }
 
 template <int UG, int UD>
@@ -1298,8 +1303,8 @@ TG_DEV void ld_gu_load(const uint8_t *ex, const LdGu<UG> &M, FxGu<UG> &g) {
 
 // The unit's block dots into U (LDS), at the precomputed offsets.
 template <int UG>
-TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uint8_t *smem) {
-    const int nbh = s.nbH, H = s.H, items = 2 * GU_ROWS * nbh, tid = threadIdx.x;
+TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uint8_t *smem, int rows = GU_ROWS) {
+    const int nbh = s.nbH, H = s.H, items = 2 * rows * nbh, tid = threadIdx.x;
     const int8_t *xq = reinterpret_cast<const int8_t *>(smem);
     const int *xs = reinterpret_cast<const int *>(xq + H + 4 * round4(nbh));
     float *U = reinterpret_cast<float *>(smem + H + 8 * round4(nbh));
@@ -1318,7 +1323,78 @@ TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uin
 // The leading arguments (the partials' address, E, G) arrive preloaded in
 // SGPRs (this file is built with kernarg preloading), so the first round of
 // partial loads is issued before any argument is read from memory.
-template <int UG, int UD>
+// Half units (the layer launch when a shape has more units than blocks):
+// half unit hu = 2 u + side takes rows [16 side, 16 side + 16) of unit u's
+// gate and of its up rows, so the 32 h values of a unit come from two
+// blocks and every block carries the same number of half units.  Item u of a
+// thread: p = u * FX_THREADS + tid of the half unit's 2 * 16 * nbH blocks, row
+// rd = p >> lnbH (gate 0..15, up 16..31), dotted into U row ubase + rd.
+constexpr int HU_ROWS = GU_ROWS / 2;
+constexpr int HU_QS = 16;  // tagged words per half unit: its 16 h values, one 128-byte line
+
+template <int UG>
+TG_DEV void ld_hu_map(const Shape &s, int m, int side, int ubase, int lnbh, int usth, LdGu<UG> &M) {
+    const int nbh = s.nbH, items = 2 * HU_ROWS * nbh, tid = threadIdx.x;
+    const uint32_t ntb = (uint32_t)s.I * nbh;
+#pragma unroll
+    for (int u = 0; u < UG; u++) {
+        const int p = min(u * FX_THREADS + tid, items - 1);
+        const int rd = p >> lnbh, cb = p & (nbh - 1);
+        const int mat = rd >= HU_ROWS ? 1 : 0;
+        const uint32_t idx = (uint32_t)((m * GU_ROWS + side * HU_ROWS + rd - mat * HU_ROWS) * nbh + cb);
+        const uint32_t tb = mat ? (uint32_t)s.GB : 0u;
+        M.off[u] = tb + 16u * idx;
+        M.soff[u] = tb + 16u * ntb + 2u * idx;
+        M.pk[u] = ((uint32_t)((ubase + rd) * usth + cb) << 8) | (uint32_t)cb;
+    }
+}
+
+// Wave 0: the chains of U rows 0..63 (half unit huA in rows 0..31, huB, if
+// >= 0, in rows 32..63), SwiGLU of each half's 16 rows, and the 16 h values
+// of each half published as tagged words (lanes 0..15: huA, 32..47: huB).
+// Readers form the Q8_0 block of a unit from its two halves.
+TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
+    const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
+    const float *xd = reinterpret_cast<const float *>(smem + H);
+    const float *U = xd + 2 * round4(nb);
+    if (tid < 64) {
+        const float a = chain4(U + tid * ust, xd, nb);
+        const float gv = __shfl(a, tid, WAVE), uv = __shfl(a, (tid + HU_ROWS) & (WAVE - 1), WAVE);
+        const int l = tid & 31, half = tid >> 5;
+        const int hu = half ? huB : huA;
+        if (l < HU_ROWS && hu >= 0) ll_put(hw + (size_t)hu * HU_QS + l, __float_as_uint(silu_mul(gv, uv)), tag);
+    }
+}
+
+// Q8_0 of a unit's 32 h values in one thread, the steps of q8_lane (the same
+// bits for finite values: the maximum of |v| does not depend on the order it
+// is taken in): the packed bytes, the scale as float(half(d)), the sum.
+TG_DEV void q8_block32(const float (&v)[32], uint32_t (&wq)[8], float &dscale, int &qsum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const float o = fabsf(v[i]);
+        a = o > a ? o : a;
+    }
+    const float d = a / 127.0f;
+    const float inv = a > 0.0f ? 127.0f / a : 0.0f;
+    int sum = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        uint32_t word = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int q = (int)__builtin_rintf(v[4 * w + b] * inv);
+            sum += q;
+            word |= (uint32_t)(q & 255) << (8 * b);
+        }
+        wq[w] = word;
+    }
+    dscale = h2f(f2h(d));
+    qsum = sum;
+}
+
+template <int UG, int UD, bool HU>
 __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restrict__ part_in, int pe, int pg, LdArgs A,
                                                           Shape s) {
     float4 pv0[LD_PC];
@@ -1340,12 +1416,13 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     const int nb = s.nbI, nbp = round4(nb), ust = round4(nb) + 4;
     const int lnbh = __builtin_ctz(s.nbH), usth = round4(s.nbH) + 4;  // nbH is a power of two
     const int ng = (I / GU_ROWS) * k, NB = gridDim.x, mI = I / GU_ROWS;
+    const int nu = HU ? 2 * ng : ng;  // work units: units, or half units
     const LdRole role = ld_role(blockIdx.x, NB, GQ);
     const int r0 = role.chunk * RD;
     const uint32_t tag =
         gen_back(__hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                  A.back);
-    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * FX_QS;
+    uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * (HU ? 2 * HU_QS : FX_QS);
     uint64_t *ow = A.ow + (size_t)(tag & 1u) * H;
     const bool nx = role.owner && A.wr_next;
 
@@ -1353,9 +1430,9 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     //    that quantize it, waves 1..), the residual rows, (owners) the next
     //    router's columns of the group, then the partials
     float4 xa = make_float4(0.f, 0.f, 0.f, 0.f), xb = xa, ga = xa, gb = xa;
-    const int u0 = role.rank;  // first gate/up unit
+    const int u0 = role.rank;  // first gate/up unit (half unit)
     const int qt = tid - WAVE;
-    const bool qon = u0 < ng && qt >= 0 && qt < H / 8;
+    const bool qon = u0 < nu && qt >= 0 && qt < H / 8;
     if (qon) {
         xa = reinterpret_cast<const float4 *>(A.x)[2 * qt];
         xb = reinterpret_cast<const float4 *>(A.x)[2 * qt + 1];
@@ -1485,8 +1562,27 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
     };
     FxGu<UG> g;
-    if (!DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
-    if (u0 < ng) ld_gu_load<UG>(A.layer_pl + (size_t)sidx[u0 / mI] * s.EB, gm, g);
+    // (half units) the first two: hu0 = u0 into U rows 0..31, hu1 = u0 + NB
+    // into rows 32..63, their loads in flight together
+    constexpr int UH = UG / 2 > 0 ? UG / 2 : 1;
+    LdGu<UH> hma, hmb;
+    FxGu<UH> hga, hgb;
+    const int hu1 = u0 + NB;
+    if constexpr (HU) {
+        if (u0 < nu) {
+            const int un = u0 >> 1;
+            ld_hu_map<UH>(s, un % mI, u0 & 1, 0, lnbh, usth, hma);
+            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hma, hga);
+        }
+        if (hu1 < nu) {
+            const int un = hu1 >> 1;
+            ld_hu_map<UH>(s, un % mI, hu1 & 1, GU_ROWS, lnbh, usth, hmb);
+            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hmb, hgb);
+        }
+    } else {
+        if (!DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
+        if (u0 < ng) ld_gu_load<UG>(A.layer_pl + (size_t)sidx[u0 / mI] * s.EB, gm, g);
+    }
     if (tid < WAVE) {
         const float wj = topk_softmax_lane(slog, sidx, k);
         if (tid < k) {
@@ -1503,18 +1599,35 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     int *xs = reinterpret_cast<int *>(xd + round4(s.nbH));
     if (qon) q8_group8(xsv, true, qt * 8, xq, xd, xs);
 
-    if (u0 < ng) {
-        ld_gu_dots<UG>(s, gm, g, smem);
-        fx_gu_publish(s, u0, tag, hw, smem);
-    }
-    if (DOWN_FIRST) down_loads();
-    // 2. further gate/up units
-    for (int unit = u0 + NB; unit < ng; unit += NB) {
-        LdGu<UG> gm2;
-        ld_gu_map<UG>(s, unit % mI, lnbh, usth, gm2);
-        ld_gu_load<UG>(A.layer_pl + (size_t)sidx[unit / mI] * s.EB, gm2, g);
-        ld_gu_dots<UG>(s, gm2, g, smem);
-        fx_gu_publish(s, unit, tag, hw, smem);
+    if constexpr (HU) {
+        if (u0 < nu) {  // uniform
+            ld_gu_dots<UH>(s, hma, hga, smem, HU_ROWS);
+            if (hu1 < nu) ld_gu_dots<UH>(s, hmb, hgb, smem, HU_ROWS);
+            fx_hu_publish(s, u0, hu1 < nu ? hu1 : -1, tag, hw, smem);
+        }
+        // 2. further half units, one at a time
+        for (int hu = u0 + 2 * NB; hu < nu; hu += NB) {
+            LdGu<UH> hm2;
+            const int un = hu >> 1;
+            ld_hu_map<UH>(s, un % mI, hu & 1, 0, lnbh, usth, hm2);
+            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hm2, hga);
+            ld_gu_dots<UH>(s, hm2, hga, smem, HU_ROWS);
+            fx_hu_publish(s, hu, -1, tag, hw, smem);
+        }
+    } else {
+        if (u0 < ng) {
+            ld_gu_dots<UG>(s, gm, g, smem);
+            fx_gu_publish(s, u0, tag, hw, smem);
+        }
+        if (DOWN_FIRST) down_loads();
+        // 2. further gate/up units
+        for (int unit = u0 + NB; unit < ng; unit += NB) {
+            LdGu<UG> gm2;
+            ld_gu_map<UG>(s, unit % mI, lnbh, usth, gm2);
+            ld_gu_load<UG>(A.layer_pl + (size_t)sidx[unit / mI] * s.EB, gm2, g);
+            ld_gu_dots<UG>(s, gm2, g, smem);
+            fx_gu_publish(s, unit, tag, hw, smem);
+        }
     }
     if (!DOWN_FIRST) {
         down_map();
@@ -1533,7 +1646,28 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     if (tid < FX_PT) {
         for (int unit = tid; unit < ng; unit += FX_PT) {
             uint32_t pay[FX_QW];
-            const bool ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
+            bool ok;
+            if constexpr (HU) {  // the unit's two halves, then its Q8_0 block here
+                uint32_t pa[HU_QS], pb[HU_QS];
+                ok = fx_read_words<HU_QS>(hw + (size_t)(2 * unit) * HU_QS, tag, pa);
+                ok = fx_read_words<HU_QS>(hw + (size_t)(2 * unit + 1) * HU_QS, tag, pb) && ok;
+                float v[2 * HU_QS];
+#pragma unroll
+                for (int i = 0; i < HU_QS; i++) {
+                    v[i] = __uint_as_float(pa[i]);
+                    v[HU_QS + i] = __uint_as_float(pb[i]);
+                }
+                uint32_t wq[8];
+                float dsc;
+                int qs;
+                q8_block32(v, wq, dsc, qs);
+#pragma unroll
+                for (int wd = 0; wd < 8; wd++) pay[wd] = wq[wd];
+                pay[8] = __float_as_uint(dsc);
+                pay[9] = (uint32_t)qs;
+            } else {
+                ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
+            }
             const int jj = unit / nb, b = unit - jj * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
 #pragma unroll
@@ -2309,7 +2443,9 @@ bool experts_fused_ok(const Shape &s, int n_cu) {
     return regs && s.H % rd == 0 && s.k * rd <= FX_THREADS && fx_lds_bytes(s, rd) <= 160 * 1024 && s.k <= MAX_K;
 }
 
-size_t experts_fused_words(const Shape &s) { return 2 * (size_t)s.k * s.nbI * FX_QS; }
+// (two parities; each holds a line per unit, or per half unit for the layer
+// launch's half units: 2 HU_QS words per unit = 2 FX_QS)
+size_t experts_fused_words(const Shape &s) { return 2 * 2 * (size_t)s.k * s.nbI * FX_QS; }
 
 template <int UG, int UD>
 static hipError_t experts_go(const FxArgs &A, const Shape &s, hipStream_t st) {
@@ -2350,6 +2486,15 @@ static int ld_rows(const Shape &s, int n_cu) {
 
 static int ld_ud(const Shape &s, int rd) { return (int)cdiv((size_t)s.k * rd * s.nbI, FX_THREADS); }
 
+// TG_LD_HALF=0 keeps whole units on shapes with more units than blocks
+static bool ld_half_units() {
+    static const bool on = [] {
+        const char *v = getenv("TG_LD_HALF");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 bool layer_dec_ok(const Shape &s, int n_cu) {
     const int rd = n_cu > 0 ? ld_rows(s, n_cu) : 0;
     if (!rd) return false;
@@ -2366,12 +2511,13 @@ hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, floa
     return hipGetLastError();
 }
 
-template <int UG, int UD>
+template <int UG, int UD, bool HU>
 static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
     const size_t lds = ld_lds_bytes(s, A.rd);
-    hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD>, lds);
+    hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD, HU>, lds);
     if (e != hipSuccess) return e;
-    TG_LAUNCH((k_layer_dec<UG, UD>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG, A, s);
+    TG_LAUNCH((k_layer_dec<UG, UD, HU>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG, A,
+              s);
     return hipGetLastError();
 }
 
@@ -2383,8 +2529,12 @@ hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, c
     const int rd = ld_rows(s, n_cu);
     const LdArgs A{layer_pl, x, gn, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
-    if (ug <= 4 && ld_ud(s, rd) <= 2) return ld_go<4, 2>(A, s, st);
-    return ld_go<8, 6>(A, s, st);
+    if (ug <= 4 && ld_ud(s, rd) <= 2) return ld_go<4, 2, false>(A, s, st);
+    // more units than blocks: half units, so every block carries the same
+    // number (each half unit's items fit four loads per thread)
+    const int ng = (s.I / GU_ROWS) * s.k, nblk = s.H / rd;
+    if (ld_half_units() && ng > nblk && 2 * HU_ROWS * s.nbH <= 4 * FX_THREADS) return ld_go<8, 6, true>(A, s, st);
+    return ld_go<8, 6, false>(A, s, st);
 }
 
 size_t dec_part_floats(const Shape &s) { return 2 * (size_t)(s.H / RG) * (s.E + 1); }
