@@ -178,6 +178,26 @@ TG_DEV void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+TG_DEV uint32_t lds_addr(uint8_t *smem, int off) { return (uint32_t)(uintptr_t)(lds_u8 *)(smem + off); }
+// global -> LDS without registers: lane l's 16 (4) bytes land at LDS byte
+// address m0 + 16 l (4 l); m0 must be the same on every lane.  Written as the bare instructions so the
+// compiler's wait insertion does not treat them as writes it must wait for
+// before every later LDS read (it cannot tell the staged buffers apart from
+// the ones being read); the kernel waits for them itself (vmcnt, then a
+// barrier when other waves read them) before reading what they wrote.  The
+// compiler does not count them either: its own vmcnt waits stay correct
+// (a younger load in flight only makes a wait stricter), and a wait of
+// its for a load issued after them covers them, since loads retire in order.
+TG_DEV void lds_dma16(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
+TG_DEV void lds_dma4(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
+
 // Tagged words: a 32-bit payload and a 32-bit tag in one 64-bit word,
 // stored and loaded with relaxed agent-scope atomics, so a reader that sees
 // the tag it expects also sees the payload stored with it.

@@ -683,23 +683,6 @@ static_assert(XtLds::ACT % 16 == 0 && XtLds::AXS % 16 == 0 && XtLds::WQ % 16 == 
 static_assert(XT_NP == 8, "piece swizzle assumes 8 pieces per row");
 static_assert((XT_NW / 2) * 64 * (2 * XT_CT * 4) * 4 <= XtLds::BYTES, "gate/up hand-off fits in the block's LDS");
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-TG_DEV uint32_t lds_addr(uint8_t *smem, int off) { return (uint32_t)(uintptr_t)(lds_u8 *)(smem + off); }
-// global -> LDS without registers: lane l's 16 (4) bytes land at LDS byte
-// address m0 + 16 l (4 l); m0 must be the same on every lane.  Written as the bare instructions so the
-// compiler's wait insertion does not treat them as writes it must wait for
-// before every later LDS read (it cannot tell the staged buffers apart from
-// the ones being read); the kernel waits for them itself (vmcnt, then a
-// barrier) before reading what they wrote.
-TG_DEV void lds_dma16(const void *src, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
-                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
-}
-TG_DEV void lds_dma4(const void *src, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src),
-                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
-}
-
 // 16-byte piece slot of piece p in activation row t (rows t and t + 2 fall
 // on the same banks; the slot spreads 16 consecutive rows over all 64)
 TG_DEV int xt_slot(int p, int t) { return p ^ ((t >> 1) & 7); }

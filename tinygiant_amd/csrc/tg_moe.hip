@@ -1011,25 +1011,14 @@ TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, 
     }
 }
 
-// Reads the FX_QW tagged words of one unit (its line at src): polls the
-// last word with coherent loads until it carries `tag`, then reads the
-// others with plain loads (the line holds this unit's words only, written
-// by one store, and is shared through the L2 by the blocks of an XCD), and
-// polls again only a word that still carries an old tag.  Bounded; false
+// Words 0 .. NW-2 of a line whose last word already carries `tag`: plain
+// loads (the line holds one unit's words only, written by one store, and is
+// shared through the L2 by the blocks of an XCD), then coherent polls of a
+// word that still carries an old tag.  Bounded (tries counts on); false
 // when a poll ran out of tries.
 template <int NW>
-TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW]) {
+TG_DEV bool fx_read_rest(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW], uint32_t &tries) {
     constexpr int LAST = NW - 1;
-    uint32_t tries = 0;
-#pragma unroll
-    for (int i = 0; i < NW; i++) pay[i] = 0u;
-    uint64_t v = ll_get(src + LAST);
-    while ((uint32_t)(v >> 32) != tag) {
-        if (++tries >= RD_SPIN_LIMIT) return false;
-        __builtin_amdgcn_s_sleep(2);
-        v = ll_get(src + LAST);
-    }
-    pay[LAST] = (uint32_t)v;
     __asm__ volatile("" ::: "memory");  // the plain loads stay after the poll
     uint32_t pend = 0;
     uint64_t w[LAST];
@@ -1058,6 +1047,50 @@ TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW]
     }
     return true;
 }
+
+// Reads the NW tagged words of one unit (its line at src): polls the last
+// word with coherent loads until it carries `tag`, then the rest as above.
+// Bounded; false when a poll ran out of tries.
+template <int NW>
+TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW]) {
+    constexpr int LAST = NW - 1;
+    uint32_t tries = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) pay[i] = 0u;
+    uint64_t v = ll_get(src + LAST);
+    while ((uint32_t)(v >> 32) != tag) {
+        if (++tries >= RD_SPIN_LIMIT) return false;
+        __builtin_amdgcn_s_sleep(2);
+        v = ll_get(src + LAST);
+    }
+    pay[LAST] = (uint32_t)v;
+    return fx_read_rest<NW>(src, tag, pay, tries);
+}
+
+// The two half-unit lines of one unit: both last words are polled in the
+// same rounds (one poll latency for the two lines), then each line's rest.
+template <int NW>
+TG_DEV bool fx_read_pair(const uint64_t *sa, const uint64_t *sb, uint32_t tag, uint32_t (&pa)[NW],
+                         uint32_t (&pb)[NW]) {
+    constexpr int LAST = NW - 1;
+    uint32_t tries = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        pa[i] = 0u;
+        pb[i] = 0u;
+    }
+    uint64_t va = ll_get(sa + LAST), vb = ll_get(sb + LAST);
+    while ((uint32_t)(va >> 32) != tag || (uint32_t)(vb >> 32) != tag) {
+        if (++tries >= RD_SPIN_LIMIT) return false;
+        __builtin_amdgcn_s_sleep(2);
+        if ((uint32_t)(va >> 32) != tag) va = ll_get(sa + LAST);
+        if ((uint32_t)(vb >> 32) != tag) vb = ll_get(sb + LAST);
+    }
+    pa[LAST] = (uint32_t)va;
+    pb[LAST] = (uint32_t)vb;
+    return fx_read_rest<NW>(sa, tag, pa, tries) && fx_read_rest<NW>(sb, tag, pb, tries);
+}
+
 
 TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW]) {
     return fx_read_words<FX_QW>(src, tag, pay);
@@ -1357,10 +1390,11 @@ TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
     const float *xd = reinterpret_cast<const float *>(smem + H);
     const float *U = xd + 2 * round4(nb);
-    if (tid < 64) {
-        const float a = chain4(U + tid * ust, xd, nb);
-        const float gv = __shfl(a, tid, WAVE), uv = __shfl(a, (tid + HU_ROWS) & (WAVE - 1), WAVE);
-        const int l = tid & 31, half = tid >> 5;
+    if (tid >= FX_THREADS - WAVE) {  // the last wave: wave 0 polls first and should not wait for these stores
+        const int ln = tid - (FX_THREADS - WAVE);
+        const float a = chain4(U + ln * ust, xd, nb);
+        const float gv = __shfl(a, ln, WAVE), uv = __shfl(a, (ln + HU_ROWS) & (WAVE - 1), WAVE);
+        const int l = ln & 31, half = ln >> 5;
         const int hu = half ? huB : huA;
         if (l < HU_ROWS && hu >= 0) ll_put(hw + (size_t)hu * HU_QS + l, __float_as_uint(silu_mul(gv, uv)), tag);
     }
@@ -1439,8 +1473,22 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         ga = reinterpret_cast<const float4 *>(A.gn)[2 * qt];
         gb = reinterpret_cast<const float4 *>(A.gn)[2 * qt + 1];
     }
+    // deep unit loads (UG > 4): the unit map is formed after the routing and
+    // the down map after the units (the maps and the loads they address
+    // never hold registers at once), and the residual rows and the down
+    // scales go to LDS without registers (dsl: [UD][FX_THREADS] scale words,
+    // then the residual rows), since a loaded value the compiler spills is
+    // waited for on the spot
+    constexpr bool DOWN_FIRST = UG <= 4;
+    const int dsl_off = (int)ld_lds_bytes(s, RD);
+    const uint32_t *dsl = reinterpret_cast<const uint32_t *>(smem + dsl_off);
     float rv = 0.0f;
-    if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+    if constexpr (DOWN_FIRST) {
+        if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+    } else {
+        if (A.resid && tid < WAVE)  // wave 0; the wait before the unit loads retires it
+            lds_dma4(A.resid + r0 + min(tid, RD - 1), lds_addr(smem, dsl_off + 4 * UD * FX_THREADS));
+    }
     float4 wn = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nx && tid < E * (RG / 4))
         wn = reinterpret_cast<const float4 *>(A.wr_next + (size_t)(tid >> 3) * H + (size_t)role.group * RG)[tid & 7];
@@ -1471,10 +1519,6 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             ssc = rms_scale(tot, H, A.eps);
     }
     // while the partials load: the index maps of this thread's weight items
-    // (with deep unit loads, UG > 4, the unit map is formed after the routing
-    // and the down map after the units, so the maps and the loads they
-    // address never hold registers at once)
-    constexpr bool DOWN_FIRST = UG <= 4;
     LdGu<UG> gm;
     if (DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
     // down item u: byte offset of its row block; (slot * RD + row) << 16 | block.
@@ -1551,12 +1595,30 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     uint32_t dv[UD];
     auto down_loads = [&]() {
         if (dt >= 0) {  // whole waves; clamped, unbranched loads inside
+            if constexpr (DOWN_FIRST) {
 #pragma unroll
-            for (int u = 0; u < UD; u++) {
-                const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
-                wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
-                const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
-                dv[u] = reinterpret_cast<const uint16_t *>(ex + 2 * s.GB + ntb * 16)[bi];
+                for (int u = 0; u < UD; u++) {
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
+                    const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
+                    dv[u] = reinterpret_cast<const uint16_t *>(ex + 2 * s.GB + ntb * 16)[bi];
+                }
+            } else {
+                // the scales first (the word holding each: nb is even, so
+                // block b's scale is its high half when b is odd), then the
+                // nibbles: a wait for any nibble load covers every scale
+#pragma unroll
+                for (int u = 0; u < UD; u++) {
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
+                    lds_dma4(ex + 2 * s.GB + ntb * 16 + (size_t)(bi & ~1u) * 2,
+                             lds_addr(smem, dsl_off + 4 * (u * FX_THREADS + (tid & ~(WAVE - 1)))));
+                }
+#pragma unroll
+                for (int u = 0; u < UD; u++) {
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
+                }
             }
         }
         __asm__ volatile("" ::: "memory");  // keep the down loads in flight from here
@@ -1643,14 +1705,16 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     float *D = U + k * RD * ust;
     float *xo = D + k * RD;
     float *wl = xo + RG;  // [E][RG + 1]
+    // (half units: a unit's two lines are polled together; more polling
+    // waves were slower, the coherent poll traffic grows with them)
     if (tid < FX_PT) {
         for (int unit = tid; unit < ng; unit += FX_PT) {
             uint32_t pay[FX_QW];
             bool ok;
             if constexpr (HU) {  // the unit's two halves, then its Q8_0 block here
                 uint32_t pa[HU_QS], pb[HU_QS];
-                ok = fx_read_words<HU_QS>(hw + (size_t)(2 * unit) * HU_QS, tag, pa);
-                ok = fx_read_words<HU_QS>(hw + (size_t)(2 * unit + 1) * HU_QS, tag, pb) && ok;
+                ok = fx_read_pair<HU_QS>(hw + (size_t)(2 * unit) * HU_QS, hw + (size_t)(2 * unit + 1) * HU_QS, tag,
+                                         pa, pb);
                 float v[2 * HU_QS];
 #pragma unroll
                 for (int i = 0; i < HU_QS; i++) {
@@ -1689,7 +1753,10 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     // each down dot starts once its unit's h block is in LDS, so the dots run
     // while later units are still on their way.  The polling waves finish
     // every poll of theirs (bounded) before their own dots, so each flag is
-    // set; the wait here is bounded too.
+    // set; the wait here is bounded too.  (Deep unit loads: at most the UD
+    // nibble loads still in flight, so the older scale loads have landed;
+    // the flag's acquire keeps the scale reads after this wait.)
+    if constexpr (!DOWN_FIRST) __builtin_amdgcn_s_waitcnt(VMCNT0 | UD);
 #pragma unroll
     for (int u = 0; u < UD; u++) {
         if (dt >= 0 && u * dthr + dt < items) {
@@ -1707,7 +1774,12 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             const int4 ha = h4[0], hb = h4[1];
             const int hx[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
             const int S = dot_q4_q8(wv[u], hx) - 8 * hs[(int)__umul24((uint32_t)jj, (uint32_t)nbp) + b];
-            U[(int)__umul24((uint32_t)rdi, (uint32_t)ust) + b] = (float)S * h2f((uint16_t)at_use(dv[u]));
+            uint32_t sv;
+            if constexpr (DOWN_FIRST)
+                sv = at_use(dv[u]);
+            else
+                sv = dsl[u * FX_THREADS + tid] >> (16 * (b & 1));
+            U[(int)__umul24((uint32_t)rdi, (uint32_t)ust) + b] = (float)S * h2f((uint16_t)sv);
         }
     }
     lds_barrier();
@@ -1731,6 +1803,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
 #pragma unroll
             for (int c = 7; c >= 0; c--)
                 if (c < k) acc = __builtin_fmaf(ww[c], dd[c], acc);
+            if constexpr (!DOWN_FIRST) rv = __uint_as_float(dsl[UD * FX_THREADS + tid]);  // after the barrier above
             o = A.resid ? rv + acc : acc;
         }
     } else {
@@ -1738,6 +1811,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         lds_barrier();
         if (tid < RD) {
             const float acc = combine_slots(sw, D, RD, k, tid);
+            if constexpr (!DOWN_FIRST) rv = __uint_as_float(dsl[UD * FX_THREADS + tid]);
             o = A.resid ? rv + acc : acc;
         }
     }
@@ -2495,14 +2569,26 @@ static bool ld_half_units() {
     return on;
 }
 
+// dynamic LDS of the routed launch: the deep variant (<8, 6>) adds its
+// staged down scales and residual rows
+template <int UG, int UD>
+static size_t ld_launch_lds(const Shape &s, int rd) {
+    return ld_lds_bytes(s, rd) + (UG > 4 ? 4 * ((size_t)UD * FX_THREADS + WAVE) : 0);
+}
+
+static bool ld_shallow(const Shape &s, int rd) {
+    return cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS) <= 4 && ld_ud(s, rd) <= 2;
+}
+
 bool layer_dec_ok(const Shape &s, int n_cu) {
     const int rd = n_cu > 0 ? ld_rows(s, n_cu) : 0;
     if (!rd) return false;
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
+    const size_t lds = ld_shallow(s, rd) ? ld_launch_lds<4, 2>(s, rd) : ld_launch_lds<8, 6>(s, rd);
     return decode_shape_ok(s) && s.H % RG == 0 && (s.H / RG) % 4 == 0 && s.E * (RG / 4) <= FX_THREADS &&
            s.E <= LD_EMAX && (s.nbH & (s.nbH - 1)) == 0 && s.nbH <= 256 && s.nbI < 65536 &&
            s.E < 256 && s.k * rd <= FX_THREADS && s.H / 8 + WAVE <= FX_THREADS && ug <= 8 && ld_ud(s, rd) <= 6 &&
-           RG - rd <= FX_THREADS && ld_lds_bytes(s, rd) <= 160 * 1024;
+           RG - rd <= FX_THREADS && lds <= 160 * 1024;
 }
 
 hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, float *part, uint32_t *ctl, int n_layers,
@@ -2513,7 +2599,7 @@ hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, floa
 
 template <int UG, int UD, bool HU>
 static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
-    const size_t lds = ld_lds_bytes(s, A.rd);
+    const size_t lds = ld_launch_lds<UG, UD>(s, A.rd);
     hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD, HU>, lds);
     if (e != hipSuccess) return e;
     TG_LAUNCH((k_layer_dec<UG, UD, HU>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG, A,
@@ -2528,8 +2614,7 @@ hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, c
     if (!layer_dec_ok(s, n_cu)) return hipErrorInvalidValue;
     const int rd = ld_rows(s, n_cu);
     const LdArgs A{layer_pl, x, gn, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
-    const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
-    if (ug <= 4 && ld_ud(s, rd) <= 2) return ld_go<4, 2, false>(A, s, st);
+    if (ld_shallow(s, rd)) return ld_go<4, 2, false>(A, s, st);
     // more units than blocks: half units, so every block carries the same
     // number (each half unit's items fit four loads per thread)
     const int ng = (s.I / GU_ROWS) * s.k, nblk = s.H / rd;
