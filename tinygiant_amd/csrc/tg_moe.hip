@@ -930,6 +930,16 @@ struct FxGu {
     uint32_t dv[UG];
 };
 
+// Marks every register of a unit's loads as read (an empty asm taking them
+// all), after its dots: the dots skip clamped items, so without this the
+// compiler keeps such loads pending and waits for them when it reuses
+// their registers, which can land behind later loads.
+template <int UG>
+TG_DEV void fx_consume(const FxGu<UG> &g) {
+#pragma unroll
+    for (int i = 0; i < UG; i++) __asm__ volatile("" ::"v"(g.wv[i].x), "v"(g.wv[i].y), "v"(g.wv[i].z), "v"(g.wv[i].w), "v"(g.dv[i]));
+}
+
 // (eid: the block's clamped expert ids by slot, in LDS)
 template <int UG>
 TG_DEV void fx_gu_load(const uint8_t *layer_pl, const Shape &s, int unit, const int *eid, FxGu<UG> &g) {
@@ -1631,15 +1641,15 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     FxGu<UH> hga, hgb;
     const int hu1 = u0 + NB;
     if constexpr (HU) {
-        if (u0 < nu) {
+        if (u0 < nu) {  // nested like the dots below, so no path leaves a load unconsumed
             const int un = u0 >> 1;
             ld_hu_map<UH>(s, un % mI, u0 & 1, 0, lnbh, usth, hma);
             ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hma, hga);
-        }
-        if (hu1 < nu) {
-            const int un = hu1 >> 1;
-            ld_hu_map<UH>(s, un % mI, hu1 & 1, GU_ROWS, lnbh, usth, hmb);
-            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hmb, hgb);
+            if (hu1 < nu) {
+                const int un1 = hu1 >> 1;
+                ld_hu_map<UH>(s, un1 % mI, hu1 & 1, GU_ROWS, lnbh, usth, hmb);
+                ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un1 / mI] * s.EB, hmb, hgb);
+            }
         }
     } else {
         if (!DOWN_FIRST) ld_gu_map<UG>(s, u0 % mI, lnbh, usth, gm);
@@ -1664,7 +1674,11 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     if constexpr (HU) {
         if (u0 < nu) {  // uniform
             ld_gu_dots<UH>(s, hma, hga, smem, HU_ROWS);
-            if (hu1 < nu) ld_gu_dots<UH>(s, hmb, hgb, smem, HU_ROWS);
+            fx_consume<UH>(hga);
+            if (hu1 < nu) {
+                ld_gu_dots<UH>(s, hmb, hgb, smem, HU_ROWS);
+                fx_consume<UH>(hgb);
+            }
             fx_hu_publish(s, u0, hu1 < nu ? hu1 : -1, tag, hw, smem);
         }
         // 2. further half units, one at a time
@@ -1674,6 +1688,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             ld_hu_map<UH>(s, un % mI, hu & 1, 0, lnbh, usth, hm2);
             ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hm2, hga);
             ld_gu_dots<UH>(s, hm2, hga, smem, HU_ROWS);
+            fx_consume<UH>(hga);
             fx_hu_publish(s, hu, -1, tag, hw, smem);
         }
     } else {
