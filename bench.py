@@ -582,7 +582,8 @@ def run_235b(args, torch, call, T):
         roof = "k_gateup"
     else:
         rk, rb = "gateup_mfma", round(n_uniq * GATEUP5_BYTES)
-        roof = "k_mfma_grouped (gate/up)"
+        # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries
+        roof = "k_mfma_small/gate_up" if T * K5 <= 16 * E5 else "k_mfma_grouped/gate_up"
     n_r, ms_r = kern[rk]
     achieved = rb / (ms_r / n_r * 1e-3)
 
@@ -621,7 +622,7 @@ def run_235b(args, torch, call, T):
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": roof, "bytes_per_launch": rb, "achieved": round(achieved / 1e9, 1),
                      "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                     "traffic": profiled_traffic(roof)},
+                     "traffic": profiled_traffic(roof + "@235b")},  # this shape's own counter run
         "cpu_baseline": cpu,
     }
     arena.close()
