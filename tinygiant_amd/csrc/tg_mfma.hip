@@ -601,9 +601,11 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         }
         __syncthreads();
         if (mat == 1) return;
-        // SwiGLU, then Q8_0 over each entry's 32 rows (lanes of this half)
+        // SwiGLU, then Q8_0 over each entry's 32 rows (lanes of this half);
+        // register groups past the item's entries are skipped (uniform)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
+            if (r >= 4 * ng) break;
             const int t = 8 * (r >> 2) + 4 * h + (r & 3);
             const bool on = valid && t < c;
             const float hv = on ? silu_mul(acc[r], x[r * 64 + lane]) : 0.0f;
