@@ -924,21 +924,28 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
     __syncthreads();  // the staging buffers are free for the hand-off
 
     if (PAIR) {
-        // up sums -> LDS, gate waves combine
+        // the pair's sums meet in LDS and each wave applies SwiGLU and Q8_0
+        // to half of the item's column tiles, the gate wave to [0, hc) and the
+        // up wave to [hc, ct_n): each hands over its sums of the other half
+        // (the LDS slots of one whole hand-over)
         float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * 64 * 2 * XT_CT * 4;
-        if (mat == 1) {
+        const int hc = (ct_n + 1) >> 1;
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+        for (int ct = 0; ct < XT_CT; ct++) {
+            const bool give = mat == 0 ? (ct >= hc && ct < ct_n) : ct < hc;  // uniform
+            if (give) {
 #pragma unroll
-                for (int ct = 0; ct < XT_CT; ct++)
+                for (int rt = 0; rt < 2; rt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) x[((rt * XT_CT + ct) * 4 + r) * 64 + lane] = acc[rt][ct][r];
+            }
         }
         __syncthreads();
-        if (mat == 1) return;
         const int nt = rb >> 5;  // I-block of the 32 rows
 #pragma unroll
         for (int ct = 0; ct < XT_CT; ct++) {
+            const bool mine = mat == 0 ? ct < hc : (ct >= hc && ct < ct_n);  // uniform
+            if (!mine) continue;
             const int t = ct * 16 + cl;
             const bool on = t < c;
             float hv[2][4], a = 0.0f;
@@ -946,7 +953,8 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
             for (int rt = 0; rt < 2; rt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    hv[rt][r] = on ? silu_mul(acc[rt][ct][r], x[((rt * XT_CT + ct) * 4 + r) * 64 + lane]) : 0.0f;
+                    const float own = acc[rt][ct][r], other = x[((rt * XT_CT + ct) * 4 + r) * 64 + lane];
+                    hv[rt][r] = on ? silu_mul(mat == 0 ? own : other, mat == 0 ? other : own) : 0.0f;
                     const float v = fabsf(hv[rt][r]);
                     a = v > a ? v : a;
                 }
