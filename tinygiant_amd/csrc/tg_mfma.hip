@@ -593,22 +593,26 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     else run(Tiles<1>{});
 
     if (PAIR) {
-        // up sums -> LDS (over the activation buffers), gate waves combine
+        // the pair's sums meet in LDS (over the activation buffers) and each
+        // wave applies SwiGLU and Q8_0 to half of the entries: registers
+        // r % 4 < 2 the gate wave, the others the up wave; each hands over
+        // its sums of the other half.  Register groups past the item's
+        // entries are skipped (uniform).
         float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * 16 * 64;
-        if (mat == 1) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) x[r * 64 + lane] = acc[r];
+        for (int r = 0; r < 16; r++) {
+            const bool give = r < 4 * ng && (mat == 0) == ((r & 2) != 0);  // uniform
+            if (give) x[r * 64 + lane] = acc[r];
         }
         __syncthreads();
-        if (mat == 1) return;
-        // SwiGLU, then Q8_0 over each entry's 32 rows (lanes of this half);
-        // register groups past the item's entries are skipped (uniform)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             if (r >= 4 * ng) break;
+            if ((mat == 0) == ((r & 2) != 0)) continue;  // the other wave's entry
             const int t = 8 * (r >> 2) + 4 * h + (r & 3);
             const bool on = valid && t < c;
-            const float hv = on ? silu_mul(acc[r], x[r * 64 + lane]) : 0.0f;
+            const float own = acc[r], other = x[r * 64 + lane];
+            const float hv = on ? silu_mul(mat == 0 ? own : other, mat == 0 ? other : own) : 0.0f;
             const float v = fabsf(hv);
             const float a = half_max(v > 0.0f ? v : 0.0f);
             const float d = a / 127.0f;
