@@ -173,6 +173,27 @@ def test_routed_stack_sub_ranges(O, tglib):
         a.close()
 
 
+def test_deep_whole_unit_stack(O, tglib):
+    """H=4096 with I=768: units of eight loads per thread but fewer units
+    (192) than blocks (256), so the routed launch keeps whole units (the
+    deep variant without half units: down scales and residual rows staged in
+    LDS, down loads after the unit); two layers against the oracle's stack."""
+    gpu_note("one-token stack H=4096 I=768 L=2 (whole units, deep loads)")
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k, L = 4096, 768, 128, 8, 2
+    a, layers, routers = make_arena(O, L, H, I, E, k, seed=98)
+    try:
+        x0 = O.synth_normal(98, O.stream_id(0, 5, 4), 1.0, H).reshape(1, H)
+        ref, trace = O.moe_stack(layers, routers, H, I, E, k, x0)
+        xd = dev(x0)
+        idx, w = MoEBlock(a).step_trace(xd)
+        assert np.array_equal(host(idx), trace[:, 0, :])
+        assert np.array_equal(bits(host(xd)), bits(ref))
+        a.status()
+    finally:
+        a.close()
+
+
 def test_235b_shape_stack(O, tglib):
     """Qwen3-235B-A22B shape through two layers on the default one-token path
     (the routed launch: 16-row chunks, two per router group, two gate/up
