@@ -354,9 +354,9 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
 // = 16 round(S * dw) and acc = fma(u16, dx / 16, acc) = fma(round(S * dw),
 // dx, acc) bit for bit (powers of two scale exactly), blocks in ascending
 // order: the row-dot definition.  Gate/up: waves 2i / 2i+1
-// take gate / up of tile 2x + i, meet in LDS, and the gate wave applies
-// SwiGLU and Q8_0 to each entry's 32 rows (one per lane of a half-wave:
-// maximum and sum by row rotations and a swap of the rows).
+// take gate / up of tile 2x + i, meet in LDS, and each applies SwiGLU and
+// Q8_0 to half of the entries, each entry's 32 rows (one per lane of a
+// half-wave: maximum and sum by row rotations and a swap of the rows).
 // Weights: per chunk of MF_KC = 8 blocks, lane (n, h) loads row n's blocks
 // 4h .. 4h+3 (64 contiguous bytes; the two lanes of a row cover its whole
 // 128-byte line) and, with nb % 8 == 0, the row's 8 scales in one 16-byte
@@ -662,9 +662,10 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 //   acc = fma(u, dx, acc)
 // Each lane needs 4 row scales per row tile (its rows 4g .. 4g+3) and one
 // activation scale per column tile (entry c).  Gate/up: waves 2i / 2i + 1
-// take gate / up of the same 32 rows; the up wave hands its sums over in
-// LDS and the gate wave applies SwiGLU and Q8_0 (an entry's 32 rows sit in
-// lanes c, c + 16, c + 32, c + 48, 8 values each).  Down writes fp32 rows.
+// take gate / up of the same 32 rows; the two hand each other half of their
+// sums in LDS and each applies SwiGLU and Q8_0 to half of the column tiles
+// (an entry's 32 rows sit in lanes c, c + 16, c + 32, c + 48, 8 values
+// each).  Down writes fp32 rows.
 constexpr int XT_NW = 4;     // waves per block
 constexpr int XT_KC = 4;     // Q4_0 blocks per chunk
 constexpr int XT_CT = 10;    // 16-entry column tiles per item (160 entries)

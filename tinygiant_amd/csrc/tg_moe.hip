@@ -1392,10 +1392,10 @@ TG_DEV void ld_hu_map(const Shape &s, int m, int side, int ubase, int lnbh, int 
     }
 }
 
-// Wave 0: the chains of U rows 0..63 (half unit huA in rows 0..31, huB, if
-// >= 0, in rows 32..63), SwiGLU of each half's 16 rows, and the 16 h values
-// of each half published as tagged words (lanes 0..15: huA, 32..47: huB).
-// Readers form the Q8_0 block of a unit from its two halves.
+// The block's last wave: the chains of U rows 0..63 (half unit huA in rows
+// 0..31, huB, if >= 0, in rows 32..63), SwiGLU of each half's 16 rows, and
+// the 16 h values of each half published as tagged words (lanes 0..15: huA,
+// 32..47: huB).  Readers form the Q8_0 block of a unit from its two halves.
 TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
     const float *xd = reinterpret_cast<const float *>(smem + H);
