@@ -7,7 +7,7 @@ renormalised softmax, decode batch 1.  One step = one token through all 48
 layers (x <- x + MoE_l(rms_norm(x))).  Weights are synthetic N(0, 0.02)
 quantized to Q4_0 (16.3 GB resident in HBM) with fp32 N(0, 0.02) routers;
 every step copies a fresh N(0, 1) token into the stack's hidden-state
-buffer and replays the stack's HIP graph.  The timed region starts with all
+buffer and runs the stack (one launch per layer).  The timed region starts with all
 inputs in HBM.  The same line carries a "prefill" object: 2048 tokens through
 the same 48-layer stack on the grouped int8-MFMA path (BASELINE's second
 half: int8 TOPS against the MFMA peak), with its own roofline and CPU
@@ -244,8 +244,8 @@ def run_decode_stack(args, torch, call):
     torch.cuda.synchronize()
     blk = MoEBlock(arena)
 
-    # every step copies its token into the same buffer, so the stack call
-    # replays the one HIP graph captured in the warmup
+    # every step copies its token into the same buffer (with graphs on, the
+    # stack call replays the one HIP graph captured in the warmup)
     log(f"warmup {W} tokens")
     for i in range(W):
         xt.copy_(X[i:i + 1])

@@ -271,6 +271,14 @@ int tg_arena_set_decode_path(tg_arena *a, int path);
 #define TG_BATCH_PER_TOKEN 2
 #define TG_BATCH_GROUPED_DOT 3
 int tg_arena_set_batch_path(tg_arena *a, int path);
+/* Stack calls (tg_moe_stack_q40*) launched layer by layer (on = 0, the
+ * default; TG_GRAPH=1 in the environment makes 1 the default of new
+ * arenas) or replayed as a HIP graph captured on the first call with the
+ * same x, token count, layer range and eps (on = 1).  No counterpart in the
+ * reference (it has no device graphs); on MI355X the direct launches of the
+ * one-token and batched stacks measured 0.3-2.3% faster than the replay.
+ * Both give the same bytes. */
+int tg_arena_set_graphs(tg_arena *a, int on);
 /* Waits for the device and reports a device-side failure of an earlier
  * asynchronous call on this arena (a hand-off poll of the ROUTED or FUSED
  * launch that ran out of tries). */

@@ -112,10 +112,11 @@ def test_config4_prefill_layer_30b(O, tglib):
 
 @pytest.mark.parametrize("with_norm", [False, True])
 def test_config2_stack_48_layers(O, tglib, with_norm):
-    """One token through the 48-layer 30B stack on the default (routed,
-    graph-replayed) path against the oracle's layer-by-layer stack: bit for
-    bit, and within the 1e-3 tolerance allowed after the full stack.  The
-    second case loads N(1, 0.1) FFN norm weights into every layer."""
+    """One token through the 48-layer 30B stack on the default (routed)
+    path, launched layer by layer, against the oracle's layer-by-layer
+    stack: bit for bit, and within the 1e-3 tolerance allowed after the full
+    stack.  The second case loads N(1, 0.1) FFN norm weights into every
+    layer."""
     gpu_note(f"config 2: 48 layers H=2048, one token, norm={with_norm}")
     from tinygiant_amd.arena import HBMExpertArena
     from tinygiant_amd.moe import MoEBlock

@@ -67,18 +67,22 @@ def test_one_token_layer_matches_oracle(O, tglib, path, H, I, E, k):
         a.close()
 
 
+@pytest.mark.parametrize("graphs", [False, True])
 @pytest.mark.parametrize("path", ["routed", "fused", "per_layer"])
 @pytest.mark.parametrize("H,I,E,k,L", [(256, 64, 16, 4, 5), (2048, 768, 128, 8, 4)])
-def test_one_token_stack_matches_oracle(O, tglib, path, H, I, E, k, L):
-    gpu_note(f"one-token stack path={path} H={H} L={L}")
+def test_one_token_stack_matches_oracle(O, tglib, path, H, I, E, k, L, graphs):
+    gpu_note(f"one-token stack path={path} H={H} L={L} graphs={graphs}")
     from tinygiant_amd.moe import MoEBlock
     a, layers, routers = make_arena(O, L, H, I, E, k, seed=92)
     try:
         a.set_decode_path(PATHS[path])
+        a.set_graphs(graphs)
         x0 = O.synth_normal(92, O.stream_id(0, 1, 4), 1.0, H).reshape(1, H)
         ref, _ = O.moe_stack(layers, routers, H, I, E, k, x0)
-        for rep in range(2):  # second run replays the captured graph
-            xd = dev(x0)
+        src = dev(x0)
+        xd = dev(x0)
+        for rep in range(3):  # with graphs on, calls after the first replay the graph it captured
+            xd.copy_(src)
             MoEBlock(a).step(xd)
             got = host(xd)
             assert np.array_equal(bits(got), bits(ref)), f"rep {rep}: max |diff| {np.max(np.abs(got - ref)):.3e}"

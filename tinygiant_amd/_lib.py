@@ -77,6 +77,7 @@ NEW_SYMBOLS = [
     ("tg_moe_stack_q40_trace_dev", CI, [VP, VP, CI, CI, CF, VP, VP, VP]),
     ("tg_arena_set_decode_path", CI, [VP, CI]),
     ("tg_arena_set_batch_path", CI, [VP, CI]),
+    ("tg_arena_set_graphs", CI, [VP, CI]),
     ("tg_arena_status", CI, [VP]),
     ("tg_q40_quantize_q8_0_dev", CI, [VP, VP, CI, VP]),
     ("tg_q40_to_planar_dev", CI, [VP, VP, CI, CI, VP]),

@@ -78,6 +78,12 @@ class HBMExpertArena:
         resident at once: run nothing else on the device beside them."""
         call("tg_arena_set_decode_path", self.handle, int(path))
 
+    def set_graphs(self, on: bool) -> None:
+        """Stack calls launched layer by layer (False, the default) or
+        replayed as a HIP graph captured on the first call with the same x,
+        token count, layer range and eps (True).  Same bytes either way."""
+        call("tg_arena_set_graphs", self.handle, int(bool(on)))
+
     BATCH_AUTO, BATCH_GROUPED, BATCH_PER_TOKEN, BATCH_GROUPED_DOT = 0, 1, 2, 3
 
     def set_batch_path(self, path: int) -> None:

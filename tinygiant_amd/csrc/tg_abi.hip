@@ -286,9 +286,12 @@ struct tg_arena {
     };
     std::vector<Graph> graphs;
     hipStream_t capture = nullptr;
+    bool use_graphs = false;  // stack calls replayed as graphs (tg_arena_set_graphs)
     int decode_path = TG_DECODE_AUTO;
     int n_cu = 0;
 };
+
+static bool graphs_default();
 
 static void drop_graphs(tg_arena *a) {
     for (auto &g : a->graphs) {
@@ -343,6 +346,7 @@ extern "C" tg_arena *tg_arena_create(int n_layers, int n_experts, int embed_dim,
     tg_arena *a = new tg_arena();
     a->s = shape;
     a->L = n_layers;
+    a->use_graphs = graphs_default();
     {
         int dev = 0, v = 0;
         (void)hipGetDevice(&dev);
@@ -624,20 +628,20 @@ static int stack_launch(tg_arena *a, const Scratch &c, float *x, int T, int l0, 
     return TG_OK;
 }
 
-static bool graphs_enabled() {
-    static int on = -1;
-    if (on < 0) {
-        const char *e = getenv("TG_NO_GRAPH");
-        on = (e && e[0] == '1') ? 0 : 1;
-    }
-    return on == 1 && !g_prof_on;
+// the default of new arenas: direct launches unless TG_GRAPH=1
+static bool graphs_default() {
+    static const bool on = [] {
+        const char *e = getenv("TG_GRAPH");
+        return e && e[0] == '1';
+    }();
+    return on;
 }
 
-// A stack call is replayed as a HIP graph captured on first use for this
-// (x, T, layer range, eps), or launched layer by layer while kernel timing
-// is on.
+// A stack call is launched layer by layer (the default, and always while
+// kernel timing is on), or, with graphs on, replayed as a HIP graph captured
+// on first use for this (x, T, layer range, eps).
 static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hipStream_t st) {
-    if (!graphs_enabled()) return stack_launch(a, a->sc, x, T, l0, n, eps, st);
+    if (!a->use_graphs || g_prof_on) return stack_launch(a, a->sc, x, T, l0, n, eps, st);
     for (auto &g : a->graphs)
         if (g.x == x && g.T == T && g.layer0 == l0 && g.n == n && g.eps == eps) {
             HIP_TRY(hipGraphLaunch(g.exec, st));
@@ -729,6 +733,13 @@ extern "C" int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0, int
         HIP_TRY(hipMemcpyAsync(topk_idx + l * k, a->sc.idx, sizeof(int32_t) * k, hipMemcpyDeviceToDevice, st));
         HIP_TRY(hipMemcpyAsync(topk_w + l * k, a->sc.w, sizeof(float) * k, hipMemcpyDeviceToDevice, st));
     }
+    return TG_OK;
+}
+
+extern "C" int tg_arena_set_graphs(tg_arena *a, int on) {
+    if (!a) return set_err(TG_E_INVALID, "arena is NULL");
+    drop_graphs(a);
+    a->use_graphs = on != 0;
     return TG_OK;
 }
 
