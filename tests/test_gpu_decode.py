@@ -177,14 +177,17 @@ def test_routed_stack_sub_ranges(O, tglib):
         a.close()
 
 
-def test_deep_whole_unit_stack(O, tglib):
-    """H=4096 with I=768: units of eight loads per thread but fewer units
-    (192) than blocks (256), so the routed launch keeps whole units (the
-    deep variant without half units: down scales and residual rows staged in
-    LDS, down loads after the unit); two layers against the oracle's stack."""
-    gpu_note("one-token stack H=4096 I=768 L=2 (whole units, deep loads)")
+@pytest.mark.parametrize("H,I", [(4096, 768), (2048, 1536)])
+def test_deep_unit_variants_stack(O, tglib, H, I):
+    """The routed launch's deep variants off the 235B shape, two layers
+    against the oracle's stack.  H=4096, I=768: units of eight loads per
+    thread but fewer units (192) than blocks (256), so whole units (down
+    scales and residual rows staged in LDS, down loads after the unit).
+    H=2048, I=1536: more units (384) than blocks (256, eight rows each), so
+    half units of two loads per thread (nbH = 64), three per block."""
+    gpu_note(f"one-token stack H={H} I={I} L=2 (deep unit variants)")
     from tinygiant_amd.moe import MoEBlock
-    H, I, E, k, L = 4096, 768, 128, 8, 2
+    E, k, L = 128, 8, 2
     a, layers, routers = make_arena(O, L, H, I, E, k, seed=98)
     try:
         x0 = O.synth_normal(98, O.stream_id(0, 5, 4), 1.0, H).reshape(1, H)
