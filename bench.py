@@ -797,10 +797,17 @@ def run_legacy_moe(args, torch, call):
     for i in range(8):
         step(i)
     call("tg_prof_enable", 0)
-    kern = kernel_times(call, ("lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc"))
+    kern = kernel_times(call, ("lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc", "lg_moe_gateup",
+                               "lg_moe_silu", "lg_moe_down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    n_q, ms_q = kern["lg_q4k"]
-    q_bytes = gb + (H // 256) * 264  # one gate (or up) matrix and its Q8 activations
+    if "lg_moe_gateup" in kern:  # every expert's gate and up rows in one launch
+        n_q, ms_q = kern["lg_moe_gateup"]
+        q_bytes = K_TOP * 2 * gb + (H // 256) * 264
+        roof_name, roof_traffic = "k_moe_gateup_q4k", profiled_traffic("k_moe_gateup_q4k")
+    else:
+        n_q, ms_q = kern["lg_q4k"]
+        q_bytes = gb + (H // 256) * 264  # one gate (or up) matrix and its Q8 activations
+        roof_name, roof_traffic = "k_matmul_q4k (gate/up)", profiled_traffic("k_matmul_q4k/gate_up")
     achieved = q_bytes / (ms_q / n_q * 1e-3)
 
     cpu = None
@@ -831,9 +838,9 @@ def run_legacy_moe(args, torch, call):
                    "note": f"after tg_mlock of every expert: {mb.value / 1e6:.1f} MB in {mr.value} HBM copies, "
                            f"{mh.value} operand reads from them, {mm.value} copied"},
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": "k_matmul_q4k (gate/up)", "bytes_per_launch": q_bytes,
+        "roofline": {"bound": "hbm", "kernel": roof_name, "bytes_per_launch": q_bytes,
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic("k_matmul_q4k/gate_up")},
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": roof_traffic},
         "cpu_baseline": cpu,
     }
 

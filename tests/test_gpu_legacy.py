@@ -183,15 +183,20 @@ def test_expert_forward_contiguous(O, L):
     assert_exact(out, ref, "expert contiguous")
 
 
-def test_moe_forward(O, L):
-    """tg_moe_forward: output zeroed, then the weighted experts in order; the
-    reference's own combine weights {.15, .14, .13, ...}
-    (tools/nws_q8dot_bench.c:369)."""
-    gpu_note("tg_moe_forward 8 experts 2048x768")
-    rng = np.random.default_rng(91)
-    embed, inter, n = 2048, 768, 8
+@pytest.mark.parametrize("n", [8, 1, 3, 17])
+def test_moe_forward(O, L, n):
+    """tg_moe_forward: output zeroed, then the weighted experts in order; for
+    8 experts the reference's own combine weights {.15, .14, .13, ...}
+    (tools/nws_q8dot_bench.c:369).  Up to 16 experts run in three launches
+    over all of them, 17 expert by expert."""
+    gpu_note(f"tg_moe_forward {n} experts 2048x768")
+    rng = np.random.default_rng(91 + n)
+    embed, inter = 2048, 768
     experts = [np.concatenate(expert_operands(rng, embed, inter, 0)) for _ in range(n)]
-    w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
+    if n == 8:
+        w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
+    else:
+        w = rng.uniform(0.02, 0.3, n).astype(np.float32)
     x = rng.normal(0.0, 1.0, embed).astype(np.float32)
     out = np.full(embed, 7.0, np.float32)  # overwritten, not accumulated
     ptrs = (ctypes.c_void_p * n)(*[e.ctypes.data for e in experts])

@@ -1314,25 +1314,80 @@ extern "C" void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *u
     }
 }
 
+// tg_moe_forward with every expert staged first, then the whole block in
+// three launches after the Q8 of x (gate / up of every expert, SiLU and Q8 of
+// every h, the down rows summed over the experts in order): the same bytes as
+// the expert-by-expert chain (TG_LEGACY_MOE_ALL=0 keeps that chain).
+static bool lg_moe_all_enabled() {
+    static const bool on = [] {
+        const char *v = getenv("TG_LEGACY_MOE_ALL");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+// after the chain's buffers: every expert's staging (for experts not held in
+// HBM), the gate / up rows of all experts and their Q8 h blocks
+struct LgMoeAllBufs {
+    uint8_t *stage;
+    float *gu;
+    void *hq;
+};
+static LgMoeAllBufs lg_moe_all_carve(LgCarve &c, int n_exp, int embed, int inter, size_t eb) {
+    LgMoeAllBufs m;
+    m.stage = c.take<uint8_t>((size_t)n_exp * eb);
+    m.gu = c.take<float>(4 * (size_t)n_exp * 2 * inter);
+    m.hq = c.take<uint8_t>((size_t)n_exp * (inter / tg::LG_QK) * tg::LG_Q8K_BYTES);
+    (void)embed;
+    return m;
+}
+
+static int lg_moe_all(const uint8_t **expert_ptrs, const float *weights, int n_experts, const float *dx, float *dout,
+                      float *output, int embed, int inter, size_t gb, size_t eb, const LgExpertBufs &b, LgCarve &c) {
+    const LgMoeAllBufs m = lg_moe_all_carve(c, n_experts, embed, inter, eb);
+    tg::LgMoeOps P{};
+    for (int e = 0; e < n_experts; e++) {
+        const uint8_t *src = expert_ptrs[e];
+        uint8_t *de = m.stage + (size_t)e * eb;
+        int rc;
+        if ((rc = lg_in(src, gb, de, &P.gate[e])) || (rc = lg_in(src + gb, gb, de + gb, &P.up[e])) ||
+            (rc = lg_in(src + 2 * gb, eb - 2 * gb, de + 2 * gb, &P.down[e])))
+            return rc;
+        P.w[e] = weights[e];
+    }
+    hipStream_t st = g_lg_st;
+    PROFILED("lg_quant", st, tg::launch_quantize_q8k(dx, b.xq, embed / tg::LG_QK, st));
+    PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n_experts, b.xq, m.gu, embed, inter, st));
+    PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(m.gu, m.hq, n_experts, inter, st));
+    PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n_experts, m.hq, dout, embed, inter, st));
+    return lg_finish(output, dout, 4 * (size_t)embed);
+}
+
 extern "C" void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights, int n_experts, const float *input,
                                float *output, int embed_dim, int inter_dim) {
     if (embed_dim <= 0 || inter_dim <= 0) return;
     std::lock_guard<std::mutex> lk(g_lg_mu);
     const size_t gb = (size_t)inter_dim * (embed_dim / tg::LG_QK) * tg::LG_Q4K_BYTES;
     const size_t eb = 2 * gb + down_bytes(0, embed_dim, inter_dim);
+    const bool moe_all = n_experts <= tg::LG_MOE_MAX && lg_moe_all_enabled();
     auto run = [&]() -> int {
         for (int pass = 0; pass < 2; pass++) {
             LgCarve c{pass ? g_lg_buf : nullptr};
-            uint8_t *de = c.take<uint8_t>(eb);
+            uint8_t *de = c.take<uint8_t>(moe_all ? 0 : eb);
             float *dx = c.take<float>(4 * (size_t)embed_dim), *dout = c.take<float>(4 * (size_t)embed_dim);
             const LgExpertBufs b = lg_expert_bufs(c, embed_dim, inter_dim);
             if (!pass) {
+                if (moe_all) lg_moe_all_carve(c, n_experts, embed_dim, inter_dim, eb);
                 int rc = lg_reserve(c.off);
                 if (rc) return rc;
                 continue;
             }
             int rc = lg_h2d(dx, input, 4 * (size_t)embed_dim);
             if (rc) return rc;
+            if (moe_all) {  // every expert in three launches; the down launch writes every output row
+                return lg_moe_all(expert_ptrs, weights, n_experts, dx, dout, output, embed_dim, inter_dim, gb, eb,
+                                  b, c);
+            }
             HIP_TRY(hipMemsetAsync(dout, 0, 4 * (size_t)embed_dim, g_lg_st));  // the reference's memset
             for (int e = 0; e < n_experts; e++) {
                 // one expert's bytes at a time: a copy waits for the previous expert's kernels

@@ -136,6 +136,21 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *out, int dim, 
 hipError_t launch_matmul_q4k_scalar(const uint8_t *W, const float *x, float *y, int nrows, int bpr, hipStream_t st);
 hipError_t launch_silu_mul_vec(const float *g, const float *u, float *h, int n, hipStream_t st);
 hipError_t launch_acc_scaled(float *out, const float *v, float w, int n, hipStream_t st);
+// tg_moe_forward's experts in three launches (after the Q8 of x): device
+// pointers of each expert's gate, up and down (Q4_K) and its weight
+constexpr int LG_MOE_MAX = 16;
+struct LgMoeOps {
+    const uint8_t *gate[LG_MOE_MAX], *up[LG_MOE_MAX], *down[LG_MOE_MAX];
+    float w[LG_MOE_MAX];
+};
+// gu: n_exp * 2 * inter floats (every expert's gate then up rows), hq:
+// n_exp * inter / 256 Q8 blocks of SiLU(gate) * up; out: embed floats,
+// written (not added to)
+hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, float *gu, int embed, int inter,
+                                 hipStream_t st);
+hipError_t launch_moe_silu_q8k(const float *gu, void *hq, int n_exp, int inter, hipStream_t st);
+hipError_t launch_moe_down_acc_q4k(const LgMoeOps &P, int n_exp, const void *hq, float *out, int embed, int inter,
+                                   hipStream_t st);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
                                 hipStream_t st);
 hipError_t launch_rope(float *x, int n_heads, int hd, const float *c, const float *sn, hipStream_t st);

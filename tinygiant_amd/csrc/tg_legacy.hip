@@ -43,11 +43,8 @@ TG_DEV void scale_min_k4(int j, const uint8_t *s, int &sc, int &m) {
 // quantize_q8, libtinygiant.c:61-89: amax over the block, scale = amax/127,
 // q = RNE(x * (127/amax)), the int32 sum of q.  One wave per block, lane l
 // taking values 4l .. 4l+3.
-__global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ x, Q8K *__restrict__ out, int nblocks) {
-    const int lane = threadIdx.x & 63, b = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= nblocks) return;  // uniform over the wave
-    const float4 v4 = reinterpret_cast<const float4 *>(x + (size_t)b * LG_QK)[lane];
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+// one 256-value block by one wave, lane l holding values 4 l .. 4 l + 3
+TG_DEV void q8k_block(const float (&v)[4], int lane, Q8K *__restrict__ ob) {
     float a = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -70,11 +67,19 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ 
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, WAVE);
-    reinterpret_cast<uint32_t *>(out[b].qs)[lane] = packed;
+    reinterpret_cast<uint32_t *>(ob->qs)[lane] = packed;
     if (lane == 0) {
-        out[b].scale = a / 127.0f;
-        out[b].sum = s;
+        ob->scale = a / 127.0f;
+        ob->sum = s;
     }
+}
+
+__global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ x, Q8K *__restrict__ out, int nblocks) {
+    const int lane = threadIdx.x & 63, b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblocks) return;  // uniform over the wave
+    const float4 v4 = reinterpret_cast<const float4 *>(x + (size_t)b * LG_QK)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    q8k_block(v, lane, out + b);
 }
 
 // --------------------------------------------------------------- Q4_K dot
@@ -85,12 +90,9 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ 
 // differences added in group order, blocks added in order as scale * sum.
 // One wave per row; per pass four blocks, 16 lanes each (lane: group s / 4,
 // bytes 8 (s % 4) .. +8 of its 32).
-__global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
-                                                    float *__restrict__ y, int nrows, int bpr) {
-    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= nrows) return;  // uniform over the wave
+// (one wave: the row at wr, every lane returns the row's value)
+TG_DEV float q4k_row_dot(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
     const int bq = lane >> 4, s = lane & 15, g = s >> 2, part = s & 3;
-    const uint8_t *wr = W + (size_t)row * bpr * LG_Q4K_BYTES;
     float total = 0.0f;
     for (int b0 = 0; b0 < bpr; b0 += 4) {
         const int b = b0 + bq;
@@ -144,7 +146,55 @@ __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ 
             if (b0 + q < bpr) total = total + xq[b0 + q].scale * bsq;
         }
     }
+    return total;
+}
+
+__global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
+                                                    float *__restrict__ y, int nrows, int bpr) {
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= nrows) return;  // uniform over the wave
+    const float total = q4k_row_dot(W + (size_t)row * bpr * LG_Q4K_BYTES, xq, bpr, lane);
     if (lane == 0) y[row] = total;
+}
+
+// ------------------------------------------------ moe_forward, all experts
+// The k experts of tg_moe_forward (libtinygiant.c:647-655) in three launches
+// after the one Q8 of x: every expert's gate and up rows, every expert's
+// SiLU(gate) * up quantized to Q8 blocks, and every output row's down dots
+// added over the experts in their order (the reference zeroes the output,
+// then adds weight * down expert by expert: the same additions, in the same
+// order, from the same zero).  One wave per row or block.
+__global__ __launch_bounds__(256) void k_moe_gateup_q4k(const LgMoeOps P, const Q8K *__restrict__ xq,
+                                                        float *__restrict__ gu, int n_exp, int inter, int bpr) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= n_exp * 2 * inter) return;  // uniform over the wave
+    const int e = r / (2 * inter), rem = r - e * 2 * inter, m = rem >= inter ? 1 : 0, i = rem - m * inter;
+    const uint8_t *W = m ? P.up[e] : P.gate[e];
+    const float total = q4k_row_dot(W + (size_t)i * bpr * LG_Q4K_BYTES, xq, bpr, lane);
+    if (lane == 0) gu[r] = total;  // gu[e][gate 0 / up 1][i]
+}
+
+__global__ __launch_bounds__(256) void k_moe_silu_q8k(const float *__restrict__ gu, Q8K *__restrict__ hq, int n_exp,
+                                                      int inter) {
+    const int lane = threadIdx.x & 63, b = blockIdx.x * 4 + (threadIdx.x >> 6), nbh = inter / LG_QK;
+    if (b >= n_exp * nbh) return;  // uniform over the wave
+    const int e = b / nbh, j = b - e * nbh;
+    const float *g = gu + (size_t)e * 2 * inter + (size_t)j * LG_QK + 4 * lane, *u = g + inter;
+    const float4 g4 = *reinterpret_cast<const float4 *>(g), u4 = *reinterpret_cast<const float4 *>(u);
+    const float v[4] = {silu_mul(g4.x, u4.x), silu_mul(g4.y, u4.y), silu_mul(g4.z, u4.z), silu_mul(g4.w, u4.w)};
+    q8k_block(v, lane, hq + b);  // hq[e][j]
+}
+
+__global__ __launch_bounds__(256) void k_moe_down_acc_q4k(const LgMoeOps P, const Q8K *__restrict__ hq,
+                                                          float *__restrict__ out, int n_exp, int embed, int dbpr) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= embed) return;  // uniform over the wave
+    float acc = 0.0f;
+    for (int e = 0; e < n_exp; e++) {
+        const float d = q4k_row_dot(P.down[e] + (size_t)r * dbpr * LG_Q4K_BYTES, hq + (size_t)e * dbpr, dbpr, lane);
+        acc = acc + P.w[e] * d;
+    }
+    if (lane == 0) out[r] = acc;
 }
 
 // --------------------------------------------------------------- Q6_K dot
@@ -931,6 +981,33 @@ hipError_t launch_argmax(const float *x, int n, float *pv, int *pi, int *out, hi
 hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     TG_LAUNCH(k_add_vec, dim3(lg_cdiv(n, 256)), dim3(256), 0, st, x, a, n);
+    return hipGetLastError();
+}
+
+static bool moe_q4k_ok(int n_exp, int embed, int inter) {
+    return n_exp > 0 && n_exp <= LG_MOE_MAX && embed % LG_QK == 0 && inter % LG_QK == 0;
+}
+
+hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, float *gu, int embed, int inter,
+                                 hipStream_t st) {
+    if (!moe_q4k_ok(n_exp, embed, inter)) return hipErrorInvalidValue;
+    TG_LAUNCH(k_moe_gateup_q4k, dim3(lg_cdiv(n_exp * 2 * inter, 4)), dim3(256), 0, st, P,
+              static_cast<const Q8K *>(xq), gu, n_exp, inter, embed / LG_QK);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_silu_q8k(const float *gu, void *hq, int n_exp, int inter, hipStream_t st) {
+    if (!moe_q4k_ok(n_exp, LG_QK, inter)) return hipErrorInvalidValue;
+    TG_LAUNCH(k_moe_silu_q8k, dim3(lg_cdiv(n_exp * (inter / LG_QK), 4)), dim3(256), 0, st, gu,
+              static_cast<Q8K *>(hq), n_exp, inter);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_down_acc_q4k(const LgMoeOps &P, int n_exp, const void *hq, float *out, int embed, int inter,
+                                   hipStream_t st) {
+    if (!moe_q4k_ok(n_exp, embed, inter)) return hipErrorInvalidValue;
+    TG_LAUNCH(k_moe_down_acc_q4k, dim3(lg_cdiv(embed, 4)), dim3(256), 0, st, P, static_cast<const Q8K *>(hq), out,
+              n_exp, embed, inter / LG_QK);
     return hipGetLastError();
 }
 
