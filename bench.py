@@ -894,7 +894,8 @@ def run_legacy_layer(args, torch, call):
         step()
     call("tg_prof_enable", 0)
     kern = kernel_times(call, ("lg_f32", "lg_rms", "lg_rope", "lg_kv", "lg_attn_sc", "lg_attn_sm", "lg_attn", "lg_add",
-                               "lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc"))
+                               "lg_quant", "lg_q4k", "lg_silu", "lg_q4k_down", "lg_acc", "lg_moe_gateup",
+                               "lg_moe_silu", "lg_moe_down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     # dominant kernel: the f32 q / k / v / o projections (k_matvec_two_acc),
     # bytes per launch = weights + input averaged over the four launches

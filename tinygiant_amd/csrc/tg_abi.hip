@@ -1342,24 +1342,48 @@ static LgMoeAllBufs lg_moe_all_carve(LgCarve &c, int n_exp, int embed, int inter
     return m;
 }
 
+// each expert's gate, up and down (Q4_K) from its HBM copy or staged
+static int lg_moe_ops(int n, const uint8_t *const *gp, const uint8_t *const *up, const void *const *dp,
+                      const float *w, size_t gb, size_t db, uint8_t *stage, tg::LgMoeOps &P) {
+    P = tg::LgMoeOps{};
+    for (int e = 0; e < n; e++) {
+        uint8_t *de = stage + (size_t)e * (2 * gb + db);
+        int rc;
+        if ((rc = lg_in(gp[e], gb, de, &P.gate[e])) || (rc = lg_in(up[e], gb, de + gb, &P.up[e])) ||
+            (rc = lg_in(static_cast<const uint8_t *>(dp[e]), db, de + 2 * gb, &P.down[e])))
+            return rc;
+        P.w[e] = w[e];
+    }
+    return TG_OK;
+}
+
+// out = sum over the experts in order of weight * down(SiLU(gate x) * up x),
+// x the device input (Q8 once, then the three launches)
+static int lg_moe_run(const tg::LgMoeOps &P, int n, const float *x, float *out, int embed, int inter,
+                      const LgExpertBufs &b, const LgMoeAllBufs &m) {
+    hipStream_t st = g_lg_st;
+    PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, embed / tg::LG_QK, st));
+    PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n, b.xq, m.gu, embed, inter, st));
+    PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(m.gu, m.hq, n, inter, st));
+    PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n, m.hq, out, embed, inter, st));
+    return TG_OK;
+}
+
 static int lg_moe_all(const uint8_t **expert_ptrs, const float *weights, int n_experts, const float *dx, float *dout,
                       float *output, int embed, int inter, size_t gb, size_t eb, const LgExpertBufs &b, LgCarve &c) {
     const LgMoeAllBufs m = lg_moe_all_carve(c, n_experts, embed, inter, eb);
-    tg::LgMoeOps P{};
-    for (int e = 0; e < n_experts; e++) {
-        const uint8_t *src = expert_ptrs[e];
-        uint8_t *de = m.stage + (size_t)e * eb;
-        int rc;
-        if ((rc = lg_in(src, gb, de, &P.gate[e])) || (rc = lg_in(src + gb, gb, de + gb, &P.up[e])) ||
-            (rc = lg_in(src + 2 * gb, eb - 2 * gb, de + 2 * gb, &P.down[e])))
-            return rc;
-        P.w[e] = weights[e];
+    const uint8_t *gp[tg::LG_MOE_MAX], *up[tg::LG_MOE_MAX];
+    const void *dp[tg::LG_MOE_MAX];
+    for (int e = 0; e < n_experts; e++) {  // gate, up and down one after another in each expert's bytes
+        gp[e] = expert_ptrs[e];
+        up[e] = expert_ptrs[e] + gb;
+        dp[e] = expert_ptrs[e] + 2 * gb;
     }
-    hipStream_t st = g_lg_st;
-    PROFILED("lg_quant", st, tg::launch_quantize_q8k(dx, b.xq, embed / tg::LG_QK, st));
-    PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n_experts, b.xq, m.gu, embed, inter, st));
-    PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(m.gu, m.hq, n_experts, inter, st));
-    PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n_experts, m.hq, dout, embed, inter, st));
+    tg::LgMoeOps P;
+    int rc;
+    if ((rc = lg_moe_ops(n_experts, gp, up, dp, weights, gb, eb - 2 * gb, m.stage, P)) ||
+        (rc = lg_moe_run(P, n_experts, dx, dout, embed, inter, b, m)))
+        return rc;
     return lg_finish(output, dout, 4 * (size_t)embed);
 }
 
@@ -1732,7 +1756,13 @@ static int lg_transformer_layer(const float *wq, const float *wk, const float *w
     const int embed = g.embed;
     const size_t gb = (size_t)inter * (embed / tg::LG_QK) * tg::LG_Q4K_BYTES;
     size_t dbmax = 0;
-    for (int e = 0; e < n_active; e++) dbmax = std::max(dbmax, down_bytes(down_is_f16[e], embed, inter));
+    bool all_q4k = n_active > 0 && n_active <= tg::LG_MOE_MAX;
+    for (int e = 0; e < n_active; e++) {
+        dbmax = std::max(dbmax, down_bytes(down_is_f16[e], embed, inter));
+        all_q4k = all_q4k && down_is_f16[e] == 0;
+    }
+    // every expert Q4_K: the experts in three launches (as tg_moe_forward)
+    const bool moe_all = all_q4k && lg_moe_all_enabled();
     const size_t nb = 4 * (size_t)g.hd, ev = 4 * (size_t)embed;
     for (int pass = 0; pass < 2; pass++) {
         LgCarve c{pass ? g_lg_buf : nullptr};
@@ -1740,9 +1770,13 @@ static int lg_transformer_layer(const float *wq, const float *wk, const float *w
         uint8_t *dwo = c.take<uint8_t>(bo);
         float *dqn = c.take<float>(nb), *dkn = c.take<float>(nb), *dan = c.take<float>(ev), *dfn = c.take<float>(ev);
         float *dx = c.take<float>(ev), *dmo = c.take<float>(ev);
-        uint8_t *dg = c.take<uint8_t>(gb), *du = c.take<uint8_t>(gb), *dd = c.take<uint8_t>(dbmax);
+        // one expert's staging (the per-expert loop)
+        uint8_t *dg = c.take<uint8_t>(moe_all ? 0 : gb), *du = c.take<uint8_t>(moe_all ? 0 : gb);
+        uint8_t *dd = c.take<uint8_t>(moe_all ? 0 : dbmax);
         const LgAttnBufs b = lg_attn_bufs(c, g);
         const LgExpertBufs eb = lg_expert_bufs(c, embed, inter);
+        LgMoeAllBufs mb{};
+        if (moe_all) mb = lg_moe_all_carve(c, n_active, embed, inter, 2 * gb + down_bytes(0, embed, inter));
         if (!pass) {
             int rc = lg_reserve(c.off);
             if (rc) return rc;
@@ -1762,15 +1796,23 @@ static int lg_transformer_layer(const float *wq, const float *wk, const float *w
         if ((rc = lg_attn_core(false, pq, pk, pv, po, pqn, pkn, g, b))) return rc;
         PROFILED("lg_add", st, tg::launch_add_vec(dx, b.out, embed, st));
         PROFILED("lg_rms", st, tg::launch_rms_norm(dx, pfn, b.x, embed, 1e-6f, st));
-        HIP_TRY(hipMemsetAsync(dmo, 0, ev, st));  // moe_out starts at zero
-        for (int e = 0; e < n_active; e++) {
-            // one expert's operands at a time (a copy waits for the previous expert's kernels)
-            const int fmt = down_is_f16[e];
-            const uint8_t *pg, *pu, *pd;
-            if ((rc = lg_in(gate_ptrs[e], gb, dg, &pg)) || (rc = lg_in(up_ptrs[e], gb, du, &pu)) ||
-                (rc = lg_in(down_ptrs[e], down_bytes(fmt, embed, inter), dd, &pd)) ||
-                (rc = lg_expert(pg, pu, pd, fmt, b.x, dmo, expert_weights[e], embed, inter, eb)))
+        if (moe_all) {
+            tg::LgMoeOps P;
+            if ((rc = lg_moe_ops(n_active, gate_ptrs, up_ptrs, down_ptrs, expert_weights, gb, down_bytes(0, embed, inter),
+                                 mb.stage, P)) ||
+                (rc = lg_moe_run(P, n_active, b.x, dmo, embed, inter, eb, mb)))
                 return rc;
+        } else {
+            HIP_TRY(hipMemsetAsync(dmo, 0, ev, st));  // moe_out starts at zero
+            for (int e = 0; e < n_active; e++) {
+                // one expert's operands at a time (a copy waits for the previous expert's kernels)
+                const int fmt = down_is_f16[e];
+                const uint8_t *pg, *pu, *pd;
+                if ((rc = lg_in(gate_ptrs[e], gb, dg, &pg)) || (rc = lg_in(up_ptrs[e], gb, du, &pu)) ||
+                    (rc = lg_in(down_ptrs[e], down_bytes(fmt, embed, inter), dd, &pd)) ||
+                    (rc = lg_expert(pg, pu, pd, fmt, b.x, dmo, expert_weights[e], embed, inter, eb)))
+                    return rc;
+            }
         }
         PROFILED("lg_add", st, tg::launch_add_vec(dx, dmo, embed, st));
         if ((rc = lg_attn_out(g, b, kv_k, kv_v))) return rc;
