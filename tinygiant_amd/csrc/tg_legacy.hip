@@ -89,64 +89,114 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ 
 // (d sc_l) dl - (dmin m_l) su_l and (d sc_h) dh - (dmin m_h) su_h; the eight
 // differences added in group order, blocks added in order as scale * sum.
 // One wave per row; per pass four blocks, 16 lanes each (lane: group s / 4,
-// bytes 8 (s % 4) .. +8 of its 32).
-// (one wave: the row at wr, every lane returns the row's value)
-TG_DEV float q4k_row_dot(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
-    const int bq = lane >> 4, s = lane & 15, g = s >> 2, part = s & 3;
+// bytes 8 (s % 4) .. +8 of its 32).  A lane's operands for a pass are loaded
+// as whole words (d and dmin, the 12 scale bytes, 8 weight bytes, 16
+// activation bytes and the activation scale), every pass of a row before the
+// first pass's arithmetic, so a row costs one round trip to memory.
+struct Q4kLane {
+    uint32_t dm, s0, s1, s2;  // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
+    uint2 qv, xl, xh;
+    float xs;
+};
+
+TG_DEV void q4k_lane_load(const uint8_t *__restrict__ bl, const Q8K *__restrict__ xb, int g, int part, Q4kLane &L) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(bl);
+    L.dm = w[0];
+    L.s0 = w[1];
+    L.s1 = w[2];
+    L.s2 = w[3];
+    L.qv = *reinterpret_cast<const uint2 *>(bl + 16 + g * 32 + part * 8);
+    L.xl = *reinterpret_cast<const uint2 *>(xb->qs + g * 64 + part * 8);
+    L.xh = *reinterpret_cast<const uint2 *>(xb->qs + g * 64 + 32 + part * 8);
+    L.xs = xb->scale;
+}
+
+TG_DEV int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
+
+// scale_min_k4 on the scale field held as three words
+TG_DEV void scale_min_k4w(int j, const Q4kLane &L, int &sc, int &m) {
+    if (j < 4) {
+        sc = ubyte(L.s0, j) & 63;
+        m = ubyte(L.s1, j) & 63;
+    } else {
+        sc = (ubyte(L.s2, j - 4) & 0xF) | ((ubyte(L.s0, j - 4) >> 6) << 4);
+        m = (ubyte(L.s2, j - 4) >> 4) | ((ubyte(L.s1, j - 4) >> 6) << 4);
+    }
+}
+
+// block bq's sum over its groups in order (valid at lane 16 bq)
+TG_DEV float q4k_pass_sums(const Q4kLane &L, int bq, int g) {
+    int dl = 0, dh = 0, sul = 0, suh = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t v = ((i < 4 ? L.qv.x : L.qv.y) >> (8 * (i & 3))) & 0xFF;
+        const int lo = byte_s8(i < 4 ? L.xl.x : L.xl.y, i & 3), hi = byte_s8(i < 4 ? L.xh.x : L.xh.y, i & 3);
+        dl += (int)(v & 15) * lo;
+        dh += (int)(v >> 4) * hi;
+        sul += lo;
+        suh += hi;
+    }
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {
+        dl += __shfl_xor(dl, o, WAVE);
+        dh += __shfl_xor(dh, o, WAVE);
+        sul += __shfl_xor(sul, o, WAVE);
+        suh += __shfl_xor(suh, o, WAVE);
+    }
+    const float d = h2f((uint16_t)(L.dm & 0xFFFF)), dmin = h2f((uint16_t)(L.dm >> 16));
+    int sl, ml, sh, mh;
+    scale_min_k4w(2 * g, L, sl, ml);
+    scale_min_k4w(2 * g + 1, L, sh, mh);
+    const float tl = (d * (float)sl) * (float)dl, ul = (dmin * (float)ml) * (float)sul;
+    const float th = (d * (float)sh) * (float)dh, uh = (dmin * (float)mh) * (float)suh;
+    const float difl = tl - ul, difh = th - uh;
+    float bs = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+        const float a = __shfl(difl, bq * 16 + 4 * gg, WAVE), c = __shfl(difh, bq * 16 + 4 * gg, WAVE);
+        bs = bs + a;
+        bs = bs + c;
+    }
+    return bs;
+}
+
+// the pass's blocks b0 .. b0+3 (those below bpr) added in order
+TG_DEV float q4k_pass_add(float total, float bs, float xs, int b0, int bpr) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float bsq = __shfl(bs, 16 * q, WAVE), xsq = __shfl(xs, 16 * q, WAVE);
+        if (b0 + q < bpr) total = total + xsq * bsq;
+    }
+    return total;
+}
+
+// NP passes' loads at a time (block indices clamped to the row's last block;
+// the clamped lanes' sums are never added)
+template <int NP>
+TG_DEV float q4k_row_dot_np(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
+    const int bq = lane >> 4, g = (lane >> 2) & 3, part = lane & 3;
     float total = 0.0f;
-    for (int b0 = 0; b0 < bpr; b0 += 4) {
-        const int b = b0 + bq;
-        const bool on = b < bpr;
-        const uint8_t *bl = wr + (size_t)(on ? b : 0) * LG_Q4K_BYTES;
-        int dl = 0, dh = 0, sul = 0, suh = 0;
-        if (on) {
-            const uint2 qv = *reinterpret_cast<const uint2 *>(bl + 16 + g * 32 + part * 8);
-            const uint2 xl = *reinterpret_cast<const uint2 *>(xq[b].qs + g * 64 + part * 8);
-            const uint2 xh = *reinterpret_cast<const uint2 *>(xq[b].qs + g * 64 + 32 + part * 8);
+    for (int c = 0; c < bpr; c += 4 * NP) {
+        Q4kLane L[NP];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t v = ((i < 4 ? qv.x : qv.y) >> (8 * (i & 3))) & 0xFF;
-                const int lo = byte_s8(i < 4 ? xl.x : xl.y, i & 3), hi = byte_s8(i < 4 ? xh.x : xh.y, i & 3);
-                dl += (int)(v & 15) * lo;
-                dh += (int)(v >> 4) * hi;
-                sul += lo;
-                suh += hi;
-            }
+        for (int p = 0; p < NP; p++) {
+            const int b = min(c + 4 * p + bq, bpr - 1);
+            q4k_lane_load(wr + (size_t)b * LG_Q4K_BYTES, xq + b, g, part, L[p]);
         }
 #pragma unroll
-        for (int o = 1; o < 4; o <<= 1) {
-            dl += __shfl_xor(dl, o, WAVE);
-            dh += __shfl_xor(dh, o, WAVE);
-            sul += __shfl_xor(sul, o, WAVE);
-            suh += __shfl_xor(suh, o, WAVE);
-        }
-        float difl = 0.0f, difh = 0.0f;
-        if (on) {
-            const float d = h2f(ld16(bl)), dmin = h2f(ld16(bl + 2));
-            int sl, ml, sh, mh;
-            scale_min_k4(2 * g, bl + 4, sl, ml);
-            scale_min_k4(2 * g + 1, bl + 4, sh, mh);
-            const float tl = (d * (float)sl) * (float)dl, ul = (dmin * (float)ml) * (float)sul;
-            const float th = (d * (float)sh) * (float)dh, uh = (dmin * (float)mh) * (float)suh;
-            difl = tl - ul;
-            difh = th - uh;
-        }
-        // block sum of block bq over its groups in order (lanes 16 bq + 4 g)
-        float bs = 0.0f;
-#pragma unroll
-        for (int gg = 0; gg < 4; gg++) {
-            const float a = __shfl(difl, bq * 16 + 4 * gg, WAVE), c = __shfl(difh, bq * 16 + 4 * gg, WAVE);
-            bs = bs + a;
-            bs = bs + c;
-        }
-        // the pass's blocks in order
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float bsq = __shfl(bs, 16 * q, WAVE);
-            if (b0 + q < bpr) total = total + xq[b0 + q].scale * bsq;
+        for (int p = 0; p < NP; p++) {
+            const int b0 = c + 4 * p;
+            if (b0 < bpr) total = q4k_pass_add(total, q4k_pass_sums(L[p], bq, g), L[p].xs, b0, bpr);
         }
     }
     return total;
+}
+
+// (one wave: the row at wr, every lane returns the row's value)
+TG_DEV float q4k_row_dot(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
+    if (bpr <= 4) return q4k_row_dot_np<1>(wr, xq, bpr, lane);
+    if (bpr <= 8) return q4k_row_dot_np<2>(wr, xq, bpr, lane);
+    return q4k_row_dot_np<4>(wr, xq, bpr, lane);
 }
 
 __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
@@ -190,9 +240,32 @@ __global__ __launch_bounds__(256) void k_moe_down_acc_q4k(const LgMoeOps P, cons
     const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= embed) return;  // uniform over the wave
     float acc = 0.0f;
-    for (int e = 0; e < n_exp; e++) {
-        const float d = q4k_row_dot(P.down[e] + (size_t)r * dbpr * LG_Q4K_BYTES, hq + (size_t)e * dbpr, dbpr, lane);
-        acc = acc + P.w[e] * d;
+    if (dbpr <= 4) {
+        // one pass per expert: eight experts' loads at a time (expert index
+        // clamped to the last; the clamped experts are never added)
+        constexpr int NE = 8;
+        const int bq = lane >> 4, g = (lane >> 2) & 3, part = lane & 3, b = min(bq, dbpr - 1);
+        for (int e0 = 0; e0 < n_exp; e0 += NE) {
+            Q4kLane L[NE];
+#pragma unroll
+            for (int k = 0; k < NE; k++) {
+                const int e = min(e0 + k, n_exp - 1);
+                q4k_lane_load(P.down[e] + ((size_t)r * dbpr + b) * LG_Q4K_BYTES, hq + (size_t)e * dbpr + b, g, part,
+                              L[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < NE; k++) {
+                if (e0 + k >= n_exp) break;  // uniform
+                const float d = q4k_pass_add(0.0f, q4k_pass_sums(L[k], bq, g), L[k].xs, 0, dbpr);
+                acc = acc + P.w[e0 + k] * d;
+            }
+        }
+    } else {
+        for (int e = 0; e < n_exp; e++) {
+            const float d =
+                q4k_row_dot(P.down[e] + (size_t)r * dbpr * LG_Q4K_BYTES, hq + (size_t)e * dbpr, dbpr, lane);
+            acc = acc + P.w[e] * d;
+        }
     }
     if (lane == 0) out[r] = acc;
 }
