@@ -88,123 +88,157 @@ __global__ __launch_bounds__(256) void k_quantize_q8k(const float *__restrict__ 
 // activations and the activations' sums, turned into
 // (d sc_l) dl - (dmin m_l) su_l and (d sc_h) dh - (dmin m_h) su_h; the eight
 // differences added in group order, blocks added in order as scale * sum.
-// One wave per row; per pass four blocks, 16 lanes each (lane: group s / 4,
-// bytes 8 (s % 4) .. +8 of its 32).  A lane's operands for a pass are loaded
-// as whole words (d and dmin, the 12 scale bytes, 8 weight bytes, 16
-// activation bytes and the activation scale), every pass of a row before the
-// first pass's arithmetic, so a row costs one round trip to memory.
-struct Q4kLane {
+// A wave walks a sequence of blocks (the blocks of consecutive rows, or one
+// row's blocks over several experts) 16 at a time, one lane per (block,
+// group): lane l takes block 16 p + l / 4 of pass p and its group g = l % 4,
+// i.e. the 32 weight bytes 32 g .. +31 (low nibbles against activations
+// 64 g .. +31, high nibbles against 64 g + 32 .. +63) and the block's d, dmin
+// and scale bytes.  The integer dots are four-byte dot products; a block's
+// eight group differences are added in order by broadcasts within its quad of
+// lanes, and the blocks' scale * sum terms are added in order from the
+// lanes that hold them (the row values are wave-uniform).  Loads are plain
+// 16-byte loads at any alignment.
+struct Q4kGrp {
     uint32_t dm, s0, s1, s2;  // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
-    uint2 qv, xl, xh;
+    uint4 q0, q1;             // weight bytes 32 g .. +31
+};
+struct Q8kGrp {
+    uint4 l0, l1, h0, h1;  // activations 64 g .. +31 and 64 g + 32 .. +63
     float xs;
 };
 
-TG_DEV void q4k_lane_load(const uint8_t *__restrict__ bl, const Q8K *__restrict__ xb, int g, int part, Q4kLane &L) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(bl);
-    L.dm = w[0];
-    L.s0 = w[1];
-    L.s1 = w[2];
-    L.s2 = w[3];
-    L.qv = *reinterpret_cast<const uint2 *>(bl + 16 + g * 32 + part * 8);
-    L.xl = *reinterpret_cast<const uint2 *>(xb->qs + g * 64 + part * 8);
-    L.xh = *reinterpret_cast<const uint2 *>(xb->qs + g * 64 + 32 + part * 8);
-    L.xs = xb->scale;
+TG_DEV uint4 ldu4(const void *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
+TG_DEV void q4k_grp_load(const uint8_t *__restrict__ bl, int g, Q4kGrp &W) {
+    const uint4 h = ldu4(bl);
+    W.dm = h.x;
+    W.s0 = h.y;
+    W.s1 = h.z;
+    W.s2 = h.w;
+    W.q0 = ldu4(bl + 16 + 32 * g);
+    W.q1 = ldu4(bl + 32 + 32 * g);
+}
+
+TG_DEV void q8k_grp_load(const Q8K *__restrict__ xb, int g, Q8kGrp &X) {
+    const int8_t *q = xb->qs + 64 * g;
+    X.l0 = ldu4(q);
+    X.l1 = ldu4(q + 16);
+    X.h0 = ldu4(q + 32);
+    X.h1 = ldu4(q + 48);
+    X.xs = xb->scale;
 }
 
 TG_DEV int ubyte(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFF); }
 
-// scale_min_k4 on the scale field held as three words
-TG_DEV void scale_min_k4w(int j, const Q4kLane &L, int &sc, int &m) {
+// get_scale_min_k4 on the scale field held as three words
+TG_DEV void scale_min_k4w(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m) {
     if (j < 4) {
-        sc = ubyte(L.s0, j) & 63;
-        m = ubyte(L.s1, j) & 63;
+        sc = ubyte(s0, j) & 63;
+        m = ubyte(s1, j) & 63;
     } else {
-        sc = (ubyte(L.s2, j - 4) & 0xF) | ((ubyte(L.s0, j - 4) >> 6) << 4);
-        m = (ubyte(L.s2, j - 4) >> 4) | ((ubyte(L.s1, j - 4) >> 6) << 4);
+        sc = (ubyte(s2, j - 4) & 0xF) | ((ubyte(s0, j - 4) >> 6) << 4);
+        m = (ubyte(s2, j - 4) >> 4) | ((ubyte(s1, j - 4) >> 6) << 4);
     }
 }
 
-// block bq's sum over its groups in order (valid at lane 16 bq)
-TG_DEV float q4k_pass_sums(const Q4kLane &L, int bq, int g) {
+// lane g of the lane's quad, by DPP (quad_perm [g, g, g, g])
+template <int G>
+TG_DEV float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), G * 0x55, 0xF, 0xF, false));
+}
+
+TG_DEV float lane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// scale * (block sum over its groups in order), in every lane of the quad
+TG_DEV float q4k_grp_term(const Q4kGrp &W, const Q8kGrp &X, int g) {
+    const uint32_t q[8] = {W.q0.x, W.q0.y, W.q0.z, W.q0.w, W.q1.x, W.q1.y, W.q1.z, W.q1.w};
+    const uint32_t xl[8] = {X.l0.x, X.l0.y, X.l0.z, X.l0.w, X.l1.x, X.l1.y, X.l1.z, X.l1.w};
+    const uint32_t xh[8] = {X.h0.x, X.h0.y, X.h0.z, X.h0.w, X.h1.x, X.h1.y, X.h1.z, X.h1.w};
     int dl = 0, dh = 0, sul = 0, suh = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const uint32_t v = ((i < 4 ? L.qv.x : L.qv.y) >> (8 * (i & 3))) & 0xFF;
-        const int lo = byte_s8(i < 4 ? L.xl.x : L.xl.y, i & 3), hi = byte_s8(i < 4 ? L.xh.x : L.xh.y, i & 3);
-        dl += (int)(v & 15) * lo;
-        dh += (int)(v >> 4) * hi;
-        sul += lo;
-        suh += hi;
+        dl = __builtin_amdgcn_sdot4((int)(q[i] & 0x0F0F0F0Fu), (int)xl[i], dl, false);
+        dh = __builtin_amdgcn_sdot4((int)((q[i] >> 4) & 0x0F0F0F0Fu), (int)xh[i], dh, false);
+        sul = __builtin_amdgcn_sdot4(0x01010101, (int)xl[i], sul, false);
+        suh = __builtin_amdgcn_sdot4(0x01010101, (int)xh[i], suh, false);
     }
-#pragma unroll
-    for (int o = 1; o < 4; o <<= 1) {
-        dl += __shfl_xor(dl, o, WAVE);
-        dh += __shfl_xor(dh, o, WAVE);
-        sul += __shfl_xor(sul, o, WAVE);
-        suh += __shfl_xor(suh, o, WAVE);
-    }
-    const float d = h2f((uint16_t)(L.dm & 0xFFFF)), dmin = h2f((uint16_t)(L.dm >> 16));
+    const float d = h2f((uint16_t)(W.dm & 0xFFFF)), dmin = h2f((uint16_t)(W.dm >> 16));
     int sl, ml, sh, mh;
-    scale_min_k4w(2 * g, L, sl, ml);
-    scale_min_k4w(2 * g + 1, L, sh, mh);
+    scale_min_k4w(2 * g, W.s0, W.s1, W.s2, sl, ml);
+    scale_min_k4w(2 * g + 1, W.s0, W.s1, W.s2, sh, mh);
     const float tl = (d * (float)sl) * (float)dl, ul = (dmin * (float)ml) * (float)sul;
     const float th = (d * (float)sh) * (float)dh, uh = (dmin * (float)mh) * (float)suh;
     const float difl = tl - ul, difh = th - uh;
     float bs = 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < 4; gg++) {
-        const float a = __shfl(difl, bq * 16 + 4 * gg, WAVE), c = __shfl(difh, bq * 16 + 4 * gg, WAVE);
-        bs = bs + a;
-        bs = bs + c;
-    }
-    return bs;
+    bs = bs + quad_lane<0>(difl);
+    bs = bs + quad_lane<0>(difh);
+    bs = bs + quad_lane<1>(difl);
+    bs = bs + quad_lane<1>(difh);
+    bs = bs + quad_lane<2>(difl);
+    bs = bs + quad_lane<2>(difh);
+    bs = bs + quad_lane<3>(difl);
+    bs = bs + quad_lane<3>(difh);
+    return X.xs * bs;
 }
 
-// the pass's blocks b0 .. b0+3 (those below bpr) added in order
-TG_DEV float q4k_pass_add(float total, float bs, float xs, int b0, int bpr) {
+// The values of rows of bpr blocks each: nblk consecutive blocks from wb
+// (starting at a row's first block) against xq; lane 0 stores the k-th row's
+// value at out[k].  Two passes' loads at a time (block indices clamped to the
+// last block; the clamped lanes' terms are never added).
+TG_DEV void q4k_rows_seq(const uint8_t *__restrict__ wb, int nblk, const Q8K *__restrict__ xq, int bpr, int lane,
+                         float *__restrict__ out) {
+    const int j4 = lane >> 2, g = lane & 3;
+    float cur = 0.0f;
+    int b = 0, k = 0;  // wave-uniform: the block within its row, the row
+    for (int p0 = 0; p0 < nblk; p0 += 32) {
+        Q4kGrp W[2];
+        Q8kGrp X[2];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float bsq = __shfl(bs, 16 * q, WAVE), xsq = __shfl(xs, 16 * q, WAVE);
-        if (b0 + q < bpr) total = total + xsq * bsq;
-    }
-    return total;
-}
-
-// NP passes' loads at a time (block indices clamped to the row's last block;
-// the clamped lanes' sums are never added)
-template <int NP>
-TG_DEV float q4k_row_dot_np(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
-    const int bq = lane >> 4, g = (lane >> 2) & 3, part = lane & 3;
-    float total = 0.0f;
-    for (int c = 0; c < bpr; c += 4 * NP) {
-        Q4kLane L[NP];
-#pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int b = min(c + 4 * p + bq, bpr - 1);
-            q4k_lane_load(wr + (size_t)b * LG_Q4K_BYTES, xq + b, g, part, L[p]);
+        for (int pp = 0; pp < 2; pp++) {
+            const int f = min(p0 + 16 * pp + j4, nblk - 1);
+            q4k_grp_load(wb + (size_t)f * LG_Q4K_BYTES, g, W[pp]);
+            q8k_grp_load(xq + f % bpr, g, X[pp]);
         }
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int b0 = c + 4 * p;
-            if (b0 < bpr) total = q4k_pass_add(total, q4k_pass_sums(L[p], bq, g), L[p].xs, b0, bpr);
+        for (int pp = 0; pp < 2; pp++) {
+            const float t = q4k_grp_term(W[pp], X[pp], g);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (p0 + 16 * pp + j >= nblk) break;  // uniform
+                cur = cur + lane_f(t, 4 * j);
+                if (++b == bpr) {
+                    if (lane == 0) out[k] = cur;
+                    k++;
+                    b = 0;
+                    cur = 0.0f;
+                }
+            }
         }
     }
-    return total;
 }
 
-// (one wave: the row at wr, every lane returns the row's value)
-TG_DEV float q4k_row_dot(const uint8_t *__restrict__ wr, const Q8K *__restrict__ xq, int bpr, int lane) {
-    if (bpr <= 4) return q4k_row_dot_np<1>(wr, xq, bpr, lane);
-    if (bpr <= 8) return q4k_row_dot_np<2>(wr, xq, bpr, lane);
-    return q4k_row_dot_np<4>(wr, xq, bpr, lane);
+// rows per wave: a power of two up to 16, with at most 32 blocks per wave
+// when a row has at most 16 (rows of no blocks: 16)
+__host__ __device__ inline int q4k_rows_per_wave(int bpr) {
+    int r = 1;
+    while (r < 16 && 2 * r * bpr <= 32) r *= 2;
+    return r;
 }
 
 __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
                                                     float *__restrict__ y, int nrows, int bpr) {
-    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= nrows) return;  // uniform over the wave
-    const float total = q4k_row_dot(W + (size_t)row * bpr * LG_Q4K_BYTES, xq, bpr, lane);
-    if (lane == 0) y[row] = total;
+    const int lane = threadIdx.x & 63, R = q4k_rows_per_wave(bpr);
+    const int r0 = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (r0 >= nrows) return;  // uniform over the wave
+    if (bpr == 0) {  // rows of no blocks: the empty sum
+        if (lane < min(R, nrows - r0)) y[r0 + lane] = 0.0f;
+        return;
+    }
+    q4k_rows_seq(W + (size_t)r0 * bpr * LG_Q4K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
 }
 
 // ------------------------------------------------ moe_forward, all experts
@@ -216,12 +250,14 @@ __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ 
 // order, from the same zero).  One wave per row or block.
 __global__ __launch_bounds__(256) void k_moe_gateup_q4k(const LgMoeOps P, const Q8K *__restrict__ xq,
                                                         float *__restrict__ gu, int n_exp, int inter, int bpr) {
-    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // R rows per wave, all of one matrix (R is a power of two at most 16 and
+    // inter a multiple of 256)
+    const int lane = threadIdx.x & 63, R = q4k_rows_per_wave(bpr);
+    const int r = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (r >= n_exp * 2 * inter) return;  // uniform over the wave
     const int e = r / (2 * inter), rem = r - e * 2 * inter, m = rem >= inter ? 1 : 0, i = rem - m * inter;
     const uint8_t *W = m ? P.up[e] : P.gate[e];
-    const float total = q4k_row_dot(W + (size_t)i * bpr * LG_Q4K_BYTES, xq, bpr, lane);
-    if (lane == 0) gu[r] = total;  // gu[e][gate 0 / up 1][i]
+    q4k_rows_seq(W + (size_t)i * bpr * LG_Q4K_BYTES, R * bpr, xq, bpr, lane, gu + r);  // gu[e][gate / up][i]
 }
 
 __global__ __launch_bounds__(256) void k_moe_silu_q8k(const float *__restrict__ gu, Q8K *__restrict__ hq, int n_exp,
@@ -235,36 +271,48 @@ __global__ __launch_bounds__(256) void k_moe_silu_q8k(const float *__restrict__ 
     q8k_block(v, lane, hq + b);  // hq[e][j]
 }
 
+// the expert of lane-varying index e (< n) from the wave-uniform table
+TG_DEV const uint8_t *pick_expert(const uint8_t *const (&t)[LG_MOE_MAX], int n, int e) {
+    const uint8_t *p = t[0];
+#pragma unroll
+    for (int k = 1; k < LG_MOE_MAX; k++)
+        if (k < n && e == k) p = t[k];
+    return p;
+}
+
+// one output row per wave: the sequence of its n_exp * dbpr blocks (expert
+// by expert), each expert's row value added as acc + w * value when its last
+// block is in
 __global__ __launch_bounds__(256) void k_moe_down_acc_q4k(const LgMoeOps P, const Q8K *__restrict__ hq,
                                                           float *__restrict__ out, int n_exp, int embed, int dbpr) {
-    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (r >= embed) return;  // uniform over the wave
-    float acc = 0.0f;
-    if (dbpr <= 4) {
-        // one pass per expert: eight experts' loads at a time (expert index
-        // clamped to the last; the clamped experts are never added)
-        constexpr int NE = 8;
-        const int bq = lane >> 4, g = (lane >> 2) & 3, part = lane & 3, b = min(bq, dbpr - 1);
-        for (int e0 = 0; e0 < n_exp; e0 += NE) {
-            Q4kLane L[NE];
+    const int j4 = lane >> 2, g = lane & 3, nblk = n_exp * dbpr;
+    float acc = 0.0f, cur = 0.0f;
+    int b = 0, e = 0;  // wave-uniform: the block within the expert's row, the expert
+    for (int p0 = 0; p0 < nblk; p0 += 32) {
+        Q4kGrp W[2];
+        Q8kGrp X[2];
 #pragma unroll
-            for (int k = 0; k < NE; k++) {
-                const int e = min(e0 + k, n_exp - 1);
-                q4k_lane_load(P.down[e] + ((size_t)r * dbpr + b) * LG_Q4K_BYTES, hq + (size_t)e * dbpr + b, g, part,
-                              L[k]);
-            }
-#pragma unroll
-            for (int k = 0; k < NE; k++) {
-                if (e0 + k >= n_exp) break;  // uniform
-                const float d = q4k_pass_add(0.0f, q4k_pass_sums(L[k], bq, g), L[k].xs, 0, dbpr);
-                acc = acc + P.w[e0 + k] * d;
-            }
+        for (int pp = 0; pp < 2; pp++) {
+            const int f = min(p0 + 16 * pp + j4, nblk - 1), fe = f / dbpr, fb = f - fe * dbpr;
+            q4k_grp_load(pick_expert(P.down, n_exp, fe) + ((size_t)r * dbpr + fb) * LG_Q4K_BYTES, g, W[pp]);
+            q8k_grp_load(hq + f, g, X[pp]);  // hq[e][fb]
         }
-    } else {
-        for (int e = 0; e < n_exp; e++) {
-            const float d =
-                q4k_row_dot(P.down[e] + (size_t)r * dbpr * LG_Q4K_BYTES, hq + (size_t)e * dbpr, dbpr, lane);
-            acc = acc + P.w[e] * d;
+#pragma unroll
+        for (int pp = 0; pp < 2; pp++) {
+            const float t = q4k_grp_term(W[pp], X[pp], g);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (p0 + 16 * pp + j >= nblk) break;  // uniform
+                cur = cur + lane_f(t, 4 * j);
+                if (++b == dbpr) {
+                    acc = acc + P.w[e] * cur;
+                    e++;
+                    b = 0;
+                    cur = 0.0f;
+                }
+            }
         }
     }
     if (lane == 0) out[r] = acc;
@@ -948,8 +996,8 @@ hipError_t launch_quantize_q8k(const float *x, void *xq, int nblocks, hipStream_
 
 hipError_t launch_matmul_q4k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    TG_LAUNCH(k_matmul_q4k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
-                       nrows, bpr);
+    TG_LAUNCH(k_matmul_q4k, dim3(lg_cdiv(nrows, 4 * q4k_rows_per_wave(bpr))), dim3(256), 0, st, W,
+              static_cast<const Q8K *>(xq), y, nrows, bpr);
     return hipGetLastError();
 }
 
@@ -1064,7 +1112,7 @@ static bool moe_q4k_ok(int n_exp, int embed, int inter) {
 hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, float *gu, int embed, int inter,
                                  hipStream_t st) {
     if (!moe_q4k_ok(n_exp, embed, inter)) return hipErrorInvalidValue;
-    TG_LAUNCH(k_moe_gateup_q4k, dim3(lg_cdiv(n_exp * 2 * inter, 4)), dim3(256), 0, st, P,
+    TG_LAUNCH(k_moe_gateup_q4k, dim3(lg_cdiv(n_exp * 2 * inter, 4 * q4k_rows_per_wave(embed / LG_QK))), dim3(256), 0, st, P,
               static_cast<const Q8K *>(xq), gu, n_exp, inter, embed / LG_QK);
     return hipGetLastError();
 }
