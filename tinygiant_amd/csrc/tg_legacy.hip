@@ -185,27 +185,39 @@ TG_DEV float q4k_grp_term(const Q4kGrp &W, const Q8kGrp &X, int g) {
     return X.xs * bs;
 }
 
+// The Q4_K form of one lane's share of a block (sub = the lane's group)
+struct Q4kFmt {
+    static constexpr int BYTES = LG_Q4K_BYTES;
+    using G = Q4kGrp;
+    using X = Q8kGrp;
+    TG_DEV static void load(const uint8_t *bl, const Q8K *xb, int sub, G &w, X &x) {
+        q4k_grp_load(bl, sub, w);
+        q8k_grp_load(xb, sub, x);
+    }
+    TG_DEV static float term(const G &w, const X &x, int sub) { return q4k_grp_term(w, x, sub); }
+};
+
 // The values of rows of bpr blocks each: nblk consecutive blocks from wb
 // (starting at a row's first block) against xq; lane 0 stores the k-th row's
 // value at out[k].  Two passes' loads at a time (block indices clamped to the
 // last block; the clamped lanes' terms are never added).
-TG_DEV void q4k_rows_seq(const uint8_t *__restrict__ wb, int nblk, const Q8K *__restrict__ xq, int bpr, int lane,
-                         float *__restrict__ out) {
-    const int j4 = lane >> 2, g = lane & 3;
+template <class F>
+TG_DEV void rows_seq(const uint8_t *__restrict__ wb, int nblk, const Q8K *__restrict__ xq, int bpr, int lane,
+                     float *__restrict__ out) {
+    const int j4 = lane >> 2, sub = lane & 3;
     float cur = 0.0f;
     int b = 0, k = 0;  // wave-uniform: the block within its row, the row
     for (int p0 = 0; p0 < nblk; p0 += 32) {
-        Q4kGrp W[2];
-        Q8kGrp X[2];
+        typename F::G W[2];
+        typename F::X X[2];
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const int f = min(p0 + 16 * pp + j4, nblk - 1);
-            q4k_grp_load(wb + (size_t)f * LG_Q4K_BYTES, g, W[pp]);
-            q8k_grp_load(xq + f % bpr, g, X[pp]);
+            F::load(wb + (size_t)f * F::BYTES, xq + f % bpr, sub, W[pp], X[pp]);
         }
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
-            const float t = q4k_grp_term(W[pp], X[pp], g);
+            const float t = F::term(W[pp], X[pp], sub);
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 if (p0 + 16 * pp + j >= nblk) break;  // uniform
@@ -229,16 +241,17 @@ __host__ __device__ inline int q4k_rows_per_wave(int bpr) {
     return r;
 }
 
+// R rows per wave (a power of two, from the launcher)
 __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
-                                                    float *__restrict__ y, int nrows, int bpr) {
-    const int lane = threadIdx.x & 63, R = q4k_rows_per_wave(bpr);
+                                                    float *__restrict__ y, int nrows, int bpr, int R) {
+    const int lane = threadIdx.x & 63;
     const int r0 = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (r0 >= nrows) return;  // uniform over the wave
     if (bpr == 0) {  // rows of no blocks: the empty sum
         if (lane < min(R, nrows - r0)) y[r0 + lane] = 0.0f;
         return;
     }
-    q4k_rows_seq(W + (size_t)r0 * bpr * LG_Q4K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
+    rows_seq<Q4kFmt>(W + (size_t)r0 * bpr * LG_Q4K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
 }
 
 // ------------------------------------------------ moe_forward, all experts
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup_q4k(const LgMoeOps P, const 
     if (r >= n_exp * 2 * inter) return;  // uniform over the wave
     const int e = r / (2 * inter), rem = r - e * 2 * inter, m = rem >= inter ? 1 : 0, i = rem - m * inter;
     const uint8_t *W = m ? P.up[e] : P.gate[e];
-    q4k_rows_seq(W + (size_t)i * bpr * LG_Q4K_BYTES, R * bpr, xq, bpr, lane, gu + r);  // gu[e][gate / up][i]
+    rows_seq<Q4kFmt>(W + (size_t)i * bpr * LG_Q4K_BYTES, R * bpr, xq, bpr, lane, gu + r);  // gu[e][gate / up][i]
 }
 
 __global__ __launch_bounds__(256) void k_moe_silu_q8k(const float *__restrict__ gu, Q8K *__restrict__ hq, int n_exp,
@@ -323,68 +336,101 @@ __global__ __launch_bounds__(256) void k_moe_down_acc_q4k(const LgMoeOps P, cons
 // half and each 16-element step `is` four integer dots d1..d4 of 6-bit
 // values (low nibble | 2 high bits, minus 32) with activations 0, 32, 64 and
 // 96 ahead; the sixteen products sc * d added in (half, is, 1..4) order;
-// blocks added in order as (d * scale) * sum.  One wave per row; per pass
-// four blocks, 16 lanes each (lane: half s / 8, step (s / 4) % 2, four of
-// the step's 16 elements).
-__global__ __launch_bounds__(256) void k_matmul_q6k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
-                                                    float *__restrict__ y, int nrows, int bpr) {
-    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= nrows) return;  // uniform over the wave
-    const int bq = lane >> 4, s = lane & 15, half = s >> 3, is = (s >> 2) & 1, part = s & 3;
-    const uint8_t *wr = W + (size_t)row * bpr * LG_Q6K_BYTES;
-    float total = 0.0f;
-    for (int b0 = 0; b0 < bpr; b0 += 4) {
-        const int b = b0 + bq;
-        const bool on = b < bpr;
-        const uint8_t *bl = wr + (size_t)(on ? b : 0) * LG_Q6K_BYTES;
-        int d1 = 0, d2 = 0, d3 = 0, d4 = 0;
-        if (on) {
-            const uint8_t *ql = bl + half * 64, *qh = bl + 128 + half * 32;
-            const int8_t *xh = xq[b].qs + half * 128;
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const int j = is * 16 + part * 4 + kk;
-                const int hb = qh[j], l0 = ql[j], l1 = ql[j + 32];
-                d1 += (((l0 & 0xF) | ((hb & 3) << 4)) - 32) * xh[j];
-                d2 += (((l1 & 0xF) | (((hb >> 2) & 3) << 4)) - 32) * xh[j + 32];
-                d3 += (((l0 >> 4) | (((hb >> 4) & 3) << 4)) - 32) * xh[j + 64];
-                d4 += (((l1 >> 4) | (((hb >> 6) & 3) << 4)) - 32) * xh[j + 96];
-            }
-        }
-#pragma unroll
-        for (int o = 1; o < 4; o <<= 1) {
-            d1 += __shfl_xor(d1, o, WAVE);
-            d2 += __shfl_xor(d2, o, WAVE);
-            d3 += __shfl_xor(d3, o, WAVE);
-            d4 += __shfl_xor(d4, o, WAVE);
-        }
-        float t1 = 0.0f, t2 = 0.0f, t3 = 0.0f, t4 = 0.0f;
-        if (on) {
-            const int8_t *sc = reinterpret_cast<const int8_t *>(bl + 192) + half * 8;
-            t1 = (float)sc[is] * (float)d1;
-            t2 = (float)sc[is + 2] * (float)d2;
-            t3 = (float)sc[is + 4] * (float)d3;
-            t4 = (float)sc[is + 6] * (float)d4;
-        }
-        float bs = 0.0f;
-#pragma unroll
-        for (int st = 0; st < 4; st++) {  // (half, is) = (0,0), (0,1), (1,0), (1,1): lanes 16 bq + 4 st
-            const int src = bq * 16 + 4 * st;
-            bs = bs + __shfl(t1, src, WAVE);
-            bs = bs + __shfl(t2, src, WAVE);
-            bs = bs + __shfl(t3, src, WAVE);
-            bs = bs + __shfl(t4, src, WAVE);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float bsq = __shfl(bs, 16 * q, WAVE);
-            if (b0 + q < bpr) {
-                const float d = h2f(ld16(wr + (size_t)(b0 + q) * LG_Q6K_BYTES + 208));
-                total = total + (d * xq[b0 + q].scale) * bsq;
-            }
-        }
+// blocks added in order as (d * scale) * sum.  One lane per (block, step):
+// lane l takes block l / 4 of its pass and (half, is) = (s / 2, s % 2) for
+// s = l % 4, i.e. the step's 16 elements of each of the four dots; a value
+// minus 32 times x is summed as the four-byte dot of the unsigned 6-bit
+// values with x, minus 32 times the sum of x (the same integer).
+struct Q6kGrp {
+    uint4 l0, l1, h;  // ql[64 half + 16 is ..], ql[.. + 32], qh[32 half + 16 is ..]
+    uint2 sc;         // scales 8 half .. +7
+    uint32_t d;
+};
+struct Q8kStep {
+    uint4 x1, x2, x3, x4;  // activations 128 half + 16 is + 0, 32, 64, 96 .. +15
+    float xs;
+};
+
+struct Q6kFmt {
+    static constexpr int BYTES = LG_Q6K_BYTES;
+    using G = Q6kGrp;
+    using X = Q8kStep;
+    TG_DEV static void load(const uint8_t *bl, const Q8K *xb, int sub, G &w, X &x) {
+        const int half = sub >> 1, is = sub & 1;
+        w.l0 = ldu4(bl + half * 64 + is * 16);
+        w.l1 = ldu4(bl + half * 64 + 32 + is * 16);
+        w.h = ldu4(bl + 128 + half * 32 + is * 16);
+        __builtin_memcpy(&w.sc, bl + 192 + half * 8, 8);
+        w.d = ld16(bl + 208);
+        const int8_t *q = xb->qs + half * 128 + is * 16;
+        x.x1 = ldu4(q);
+        x.x2 = ldu4(q + 32);
+        x.x3 = ldu4(q + 64);
+        x.x4 = ldu4(q + 96);
+        x.xs = xb->scale;
     }
-    if (lane == 0) y[row] = total;
+    // (d * x scale) * (the block's sixteen sc * dot products in order), in
+    // every lane of the quad
+    TG_DEV static float term(const G &w, const X &x, int sub) {
+        const int is = sub & 1;
+        const uint32_t L0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w}, L1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+        const uint32_t H[4] = {w.h.x, w.h.y, w.h.z, w.h.w};
+        const uint32_t X1[4] = {x.x1.x, x.x1.y, x.x1.z, x.x1.w}, X2[4] = {x.x2.x, x.x2.y, x.x2.z, x.x2.w};
+        const uint32_t X3[4] = {x.x3.x, x.x3.y, x.x3.z, x.x3.w}, X4[4] = {x.x4.x, x.x4.y, x.x4.z, x.x4.w};
+        constexpr uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x03030303u;
+        constexpr int ONES = 0x01010101;
+        int a1 = 0, a2 = 0, a3 = 0, a4 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q1 = (L0[i] & M4) | ((H[i] & M2) << 4);
+            const uint32_t q2 = (L1[i] & M4) | (((H[i] >> 2) & M2) << 4);
+            const uint32_t q3 = ((L0[i] >> 4) & M4) | (((H[i] >> 4) & M2) << 4);
+            const uint32_t q4 = ((L1[i] >> 4) & M4) | (((H[i] >> 6) & M2) << 4);
+            a1 = __builtin_amdgcn_sdot4((int)q1, (int)X1[i], a1, false);
+            a2 = __builtin_amdgcn_sdot4((int)q2, (int)X2[i], a2, false);
+            a3 = __builtin_amdgcn_sdot4((int)q3, (int)X3[i], a3, false);
+            a4 = __builtin_amdgcn_sdot4((int)q4, (int)X4[i], a4, false);
+            s1 = __builtin_amdgcn_sdot4(ONES, (int)X1[i], s1, false);
+            s2 = __builtin_amdgcn_sdot4(ONES, (int)X2[i], s2, false);
+            s3 = __builtin_amdgcn_sdot4(ONES, (int)X3[i], s3, false);
+            s4 = __builtin_amdgcn_sdot4(ONES, (int)X4[i], s4, false);
+        }
+        const float t1 = (float)byte_s8(w.sc.x, is) * (float)(a1 - 32 * s1);
+        const float t2 = (float)byte_s8(w.sc.x, is + 2) * (float)(a2 - 32 * s2);
+        const float t3 = (float)byte_s8(w.sc.y, is) * (float)(a3 - 32 * s3);
+        const float t4 = (float)byte_s8(w.sc.y, is + 2) * (float)(a4 - 32 * s4);
+        float bs = 0.0f;
+        bs = bs + quad_lane<0>(t1);
+        bs = bs + quad_lane<0>(t2);
+        bs = bs + quad_lane<0>(t3);
+        bs = bs + quad_lane<0>(t4);
+        bs = bs + quad_lane<1>(t1);
+        bs = bs + quad_lane<1>(t2);
+        bs = bs + quad_lane<1>(t3);
+        bs = bs + quad_lane<1>(t4);
+        bs = bs + quad_lane<2>(t1);
+        bs = bs + quad_lane<2>(t2);
+        bs = bs + quad_lane<2>(t3);
+        bs = bs + quad_lane<2>(t4);
+        bs = bs + quad_lane<3>(t1);
+        bs = bs + quad_lane<3>(t2);
+        bs = bs + quad_lane<3>(t3);
+        bs = bs + quad_lane<3>(t4);
+        return (h2f((uint16_t)(w.d & 0xFFFF)) * x.xs) * bs;
+    }
+};
+
+// R rows per wave (a power of two, from the launcher)
+__global__ __launch_bounds__(256) void k_matmul_q6k(const uint8_t *__restrict__ W, const Q8K *__restrict__ xq,
+                                                    float *__restrict__ y, int nrows, int bpr, int R) {
+    const int lane = threadIdx.x & 63;
+    const int r0 = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (r0 >= nrows) return;  // uniform over the wave
+    if (bpr == 0) {  // rows of no blocks: the empty sum
+        if (lane < min(R, nrows - r0)) y[r0 + lane] = 0.0f;
+        return;
+    }
+    rows_seq<Q6kFmt>(W + (size_t)r0 * bpr * LG_Q6K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
 }
 
 // ------------------------------------------------------ f16 / f32 matvec
@@ -996,15 +1042,20 @@ hipError_t launch_quantize_q8k(const float *x, void *xq, int nblocks, hipStream_
 
 hipError_t launch_matmul_q4k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    TG_LAUNCH(k_matmul_q4k, dim3(lg_cdiv(nrows, 4 * q4k_rows_per_wave(bpr))), dim3(256), 0, st, W,
-              static_cast<const Q8K *>(xq), y, nrows, bpr);
+    // fewer rows per wave where that keeps about 1024 waves in the launch
+    int R = q4k_rows_per_wave(bpr);
+    while (R > 1 && nrows / R < 1024) R /= 2;
+    TG_LAUNCH(k_matmul_q4k, dim3(lg_cdiv(nrows, 4 * R)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y, nrows,
+              bpr, R);
     return hipGetLastError();
 }
 
 hipError_t launch_matmul_q6k(const uint8_t *W, const void *xq, float *y, int nrows, int bpr, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    TG_LAUNCH(k_matmul_q6k, dim3(lg_cdiv(nrows, 4)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y,
-                       nrows, bpr);
+    int R = q4k_rows_per_wave(bpr);  // the same rows per wave as Q4_K
+    while (R > 1 && nrows / R < 1024) R /= 2;
+    TG_LAUNCH(k_matmul_q6k, dim3(lg_cdiv(nrows, 4 * R)), dim3(256), 0, st, W, static_cast<const Q8K *>(xq), y, nrows,
+              bpr, R);
     return hipGetLastError();
 }
 
