@@ -364,7 +364,7 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
 // computes.  Block bl's 16 bytes reach both lanes of the row through one
 // lane-half swap.
 constexpr int MS_NW = 4;    // waves per block
-constexpr int MS_PF = 2;    // weight chunks in flight per wave
+constexpr int MS_PF = 2;    // weight chunks in flight per wave (down; gate/up one more)
 
 __host__ __device__ inline size_t ms_lds_bytes() { return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4; }
 
@@ -504,16 +504,20 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
 
-    // weights run MS_PF chunks ahead in MS_PF + 1 register sets, each with a
+    // weights run PF chunks ahead in PF + 1 register sets, each with a
     // fixed role per unrolled step (a copy between sets would wait for the
     // loads in flight); the activations one chunk ahead, issued before the
     // newer weight loads so the wait before their commit leaves those in
     // flight
-    static_assert(MS_PF == 2, "three register sets");
-    uint4 wa[4], sa, wb[4], sbv, wcx[4], scx;
+    // (gate / up with 16-byte scale loads: three chunks ahead in four sets,
+    // still two waves per SIMD; otherwise two ahead in three)
+    constexpr int PF = PAIR && SCV ? MS_PF + 1 : MS_PF;
+    static_assert(MS_PF == 2, "three or four register sets");
+    uint4 wa[4], sa, wb[4], sbv, wcx[4], scx, wdx[4], sdx;
     wload(0, wa, sa);
     stage(0);
     wload(1, wb, sbv);
+    if constexpr (PF == 3) wload(2, wcx, scx);
     commit(0, 0);
     const v16i czero = {};  // the accumulator operand: an inline 0, no registers
     const int nsh = h ? 0 : 4;  // this half's nibble to the high half of each byte
@@ -522,12 +526,12 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     // register groups holding entries of the item (8 entries per group)
     auto run = [&](auto ngc) {
         constexpr int NG = decltype(ngc)::value;
-        // chunk ch from set w (scales sc); chunk ch + MS_PF loads into set wl
+        // chunk ch from set w (scales sc); chunk ch + PF loads into set wl
         auto step = [&](int ch, uint4 (&w)[4], const uint4 &sc, uint4 (&wl)[4], uint4 &sl) {
             const int q = ch & 1;
             stage(ch + 1);
             __builtin_amdgcn_sched_barrier(0);  // activations issued before the weights
-            wload(ch + MS_PF, wl, sl);
+            wload(ch + PF, wl, sl);
             if (ch < nch) {  // uniform
                 const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
                 const float *xq = dxl + q * MF_KC * M + 4 * h;
@@ -580,10 +584,19 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
             commit(q ^ 1, ch + 1);
             __syncthreads();
         };
-        for (int ch = 0; ch < nch; ch += 3) {
-            step(ch, wa, sa, wcx, scx);
-            step(ch + 1, wb, sbv, wa, sa);
-            step(ch + 2, wcx, scx, wb, sbv);
+        if constexpr (PF == 3) {
+            for (int ch = 0; ch < nch; ch += 4) {
+                step(ch, wa, sa, wdx, sdx);
+                step(ch + 1, wb, sbv, wa, sa);
+                step(ch + 2, wcx, scx, wb, sbv);
+                step(ch + 3, wdx, sdx, wcx, scx);
+            }
+        } else {
+            for (int ch = 0; ch < nch; ch += 3) {
+                step(ch, wa, sa, wcx, scx);
+                step(ch + 1, wb, sbv, wa, sa);
+                step(ch + 2, wcx, scx, wb, sbv);
+            }
         }
     };
     const int ng = (c + 7) >> 3;
