@@ -1090,14 +1090,45 @@ static int lg_reserve(size_t bytes) {
     return TG_OK;
 }
 
+// Copies of up to LG_PIN_MAX bytes go through a pinned bounce buffer (one
+// DMA from pinned memory instead of the runtime's staging of pageable
+// memory).  A call's bounce slots are handed out in order and reused only
+// after the call's closing synchronisation; a call that fails before it
+// leaves them taken until the next call that finishes, and copies that do
+// not fit go straight from pageable memory.  Kept until process exit.
+static uint8_t *g_lg_pin = nullptr;
+static size_t g_lg_pin_off = 0;
+constexpr size_t LG_PIN_BYTES = (size_t)1 << 20, LG_PIN_MAX = (size_t)256 << 10;
+
+static void *lg_pin_take(size_t n) {
+    if (n > LG_PIN_MAX) return nullptr;
+    if (!g_lg_pin && hipHostMalloc(reinterpret_cast<void **>(&g_lg_pin), LG_PIN_BYTES, hipHostMallocDefault) !=
+                         hipSuccess) {
+        g_lg_pin = nullptr;
+        return nullptr;
+    }
+    const size_t o = (g_lg_pin_off + 255) & ~(size_t)255;
+    if (o + n > LG_PIN_BYTES) return nullptr;
+    g_lg_pin_off = o + n;
+    return g_lg_pin + o;
+}
+
 static int lg_h2d(void *dst, const void *src, size_t n) {
-    if (n) HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_lg_st));
+    if (!n) return TG_OK;
+    if (void *p = lg_pin_take(n)) {
+        memcpy(p, src, n);
+        src = p;
+    }
+    HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_lg_st));
     return TG_OK;
 }
 
 static int lg_finish(void *host_dst, const void *dev_src, size_t n) {
-    if (n) HIP_TRY(hipMemcpyAsync(host_dst, dev_src, n, hipMemcpyDeviceToHost, g_lg_st));
+    void *p = n ? lg_pin_take(n) : nullptr;
+    if (n) HIP_TRY(hipMemcpyAsync(p ? p : host_dst, dev_src, n, hipMemcpyDeviceToHost, g_lg_st));
     HIP_TRY(hipStreamSynchronize(g_lg_st));
+    if (p) memcpy(host_dst, p, n);
+    g_lg_pin_off = 0;  // every copy of the call has completed
     return TG_OK;
 }
 
