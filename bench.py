@@ -26,6 +26,8 @@ Other workloads (--workload):
   legacy-moe   the reference's own legacy call, tg_moe_forward: 8 Q4_K experts
                of the 30B shape on caller-owned host buffers (operands copied
                in per call, as the reference's ABI hands them over).
+  legacy-expert the reference engine's own MoE loop on the same buffers: one
+               tg_expert_forward_mixed call per expert into a zeroed output.
   legacy-layer the reference's tg_transformer_layer on the same buffers: f32
                attention (32 heads / 4 kv heads of 128, 1024 cached positions)
                and 8 Q4_K experts, one token.
@@ -845,6 +847,95 @@ def run_legacy_moe(args, torch, call):
     }
 
 
+def run_legacy_expert(args, torch, call):
+    """The reference engine's own MoE loop (engine.py:240-257): moe_out
+    zeroed, then one tg_expert_forward_mixed call per selected expert
+    (libtinygiant.c:599-643; 8 Q4_K experts of the 30B shape, down format 0)
+    adding weight * expert(x) into it; rotates over 16 sets of experts, first
+    with the operands copied per call, then ("pinned") after tg_mlock of every
+    expert, as the reference's cache locks its pinned experts."""
+    from tinygiant_amd._lib import require_lib
+    lib = require_lib()
+    rng = np.random.default_rng(args.seed)
+    gb = I * (H // 256) * 144
+    eb = 2 * gb + H * (I // 256) * 144
+    NSET = 16
+    sets = [[q4k_blocks(rng, eb // 144) for _ in range(K_TOP)] for _ in range(NSET)]
+    w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
+    x = rng.normal(0.0, 1.0, H).astype(np.float32)
+    out = np.zeros(H, np.float32)
+    K, W = args.steps or 64, 4 if args.warmup is None else args.warmup
+
+    def step(i):
+        out[:] = 0.0
+        for j, e in enumerate(sets[i % NSET]):
+            base = e.ctypes.data
+            lib.tg_expert_forward_mixed(ctypes.c_void_p(base), ctypes.c_void_p(base + gb),
+                                        ctypes.c_void_p(base + 2 * gb), 0, x.ctypes.data, out.ctypes.data,
+                                        ctypes.c_float(float(w[j])), H, I)
+
+    def timed():
+        for i in range(W):
+            step(i)
+        t0 = time.perf_counter()
+        for i in range(K):
+            step(i)
+        return time.perf_counter() - t0
+
+    log(f"timing {K} layers (8 calls each), operands copied per call")
+    wall = timed()
+    for st in sets:
+        for e in st:
+            lib.tg_mlock(ctypes.c_void_p(e.ctypes.data), ctypes.c_size_t(e.nbytes))
+    log(f"timing {K} layers after tg_mlock")
+    wall_pin = timed()
+    call("tg_prof_enable", 1)
+    for i in range(4):
+        step(i)
+    call("tg_prof_enable", 0)
+    kern = kernel_times(call, ("lg_quant", "lg_moe_gateup", "lg_moe_silu", "lg_moe_down", "lg_q4k", "lg_silu",
+                               "lg_q4k_down", "lg_acc"))
+    kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    if "lg_moe_gateup" in kern:  # one expert's gate and up rows in one launch
+        n_q, ms_q = kern["lg_moe_gateup"]
+        q_bytes, roof_name = 2 * gb + (H // 256) * 264, "k_moe_gateup_q4k (one expert)"
+    else:  # the per-expert chain (TG_LEGACY_MOE_ALL=0)
+        n_q, ms_q = kern["lg_q4k"]
+        q_bytes, roof_name = gb + (H // 256) * 264, "k_matmul_q4k (gate/up)"
+    achieved = q_bytes / (ms_q / n_q * 1e-3)
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        from oracle import oracle as O  # the checker, timed as the CPU baseline
+        step(0)
+        ref = O.moe_forward_q4k(sets[0], w, x, H, I)  # zero, then out += w * expert(x) expert by expert
+        assert np.array_equal(ref.view(np.uint32), out.view(np.uint32)), "GPU expert loop differs from the oracle"
+        n, t1 = 0, time.perf_counter()
+        while time.perf_counter() - t1 < min(args.cpu_seconds, 10.0):
+            O.moe_forward_q4k(sets[n % NSET], w, x, H, I)
+            n += 1
+        cpu_s = (time.perf_counter() - t1) / n
+        cpu = {"value": round(1.0 / cpu_s, 2), "unit": "layer/s", "cores": 1, "kind": "port",
+               "sample": f"{n} layers of 8 Q4_K experts (2048x768) through the C oracle, one thread; the GPU loop "
+                         "bit-identical to it on the first set"}
+    return {
+        "metric": "legacy engine MoE loop layers/s (8 tg_expert_forward_mixed calls, 30B shape, host pointers)",
+        "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k x q8 (int dot, fp32 accumulate)",
+        "data": "synthetic (random Q4_K blocks, N(0,1) input)",
+        "config": {"workload": "legacy-engine-expert-loop", "hidden": H, "moe_intermediate": I, "experts": K_TOP,
+                   "expert_bytes": eb},
+        "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4)},
+        "kernel_avg_us": kern_us,
+        "roofline": {"bound": "hbm", "kernel": roof_name, "bytes_per_launch": q_bytes,
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_legacy_layer(args, torch, call):
     """The legacy entry point tg_transformer_layer (libtinygiant.c:662-702)
     with host buffers, as the reference's engine calls it: a 30B-shaped layer
@@ -1141,6 +1232,7 @@ WORKLOADS = {"decode-stack": run_decode_stack, "batched": run_batched, "prefill"
              "decode-235b": lambda a, t, c: run_235b(a, t, c, 1),
              "batched-235b": lambda a, t, c: run_235b(a, t, c, 32),
              "hbm-ceiling": run_hbm_ceiling, "legacy-moe": run_legacy_moe, "legacy-layer": run_legacy_layer,
+             "legacy-expert": run_legacy_expert,
              "output-head": run_output_head, "sample": run_sample}
 
 

@@ -1263,11 +1263,24 @@ static LgExpertBufs lg_expert_bufs(LgCarve &c, int embed, int inter) {
     LgExpertBufs b;
     b.xq = c.take<uint8_t>((size_t)(embed / tg::LG_QK) * tg::LG_Q8K_BYTES);
     b.hq = c.take<uint8_t>((size_t)(inter / tg::LG_QK) * tg::LG_Q8K_BYTES);
-    b.g = c.take<float>(4 * (size_t)inter);
-    b.u = c.take<float>(4 * (size_t)inter);
+    b.g = c.take<float>(8 * (size_t)inter);  // gate rows, then the up rows (one expert's gate | up)
+    b.u = b.g + inter;
     b.h = c.take<float>(4 * (size_t)inter);
     b.dn = c.take<float>(4 * (size_t)embed);
     return b;
+}
+
+// tg_moe_forward with every expert staged first, then the whole block in
+// three launches after the Q8 of x (gate / up of every expert, SiLU and Q8 of
+// every h, the down rows summed over the experts in order): the same bytes as
+// the expert-by-expert chain (TG_LEGACY_MOE_ALL=0 keeps that chain, here
+// and for a single expert with a Q4_K down matrix).
+static bool lg_moe_all_enabled() {
+    static const bool on = [] {
+        const char *v = getenv("TG_LEGACY_MOE_ALL");
+        return !(v && v[0] == '0');
+    }();
+    return on;
 }
 
 // expert_forward_mixed on device operands (libtinygiant.c:599-643):
@@ -1277,6 +1290,20 @@ static int lg_expert(const uint8_t *gate, const uint8_t *up, const void *down, i
                      float weight, int embed, int inter, const LgExpertBufs &b) {
     const int gbpr = embed / tg::LG_QK, dbpr = inter / tg::LG_QK;
     hipStream_t st = g_lg_st;
+    if (fmt == 0 && embed % tg::LG_QK == 0 && inter % tg::LG_QK == 0 && lg_moe_all_enabled()) {
+        // Q4_K down: the fused launches for one expert (gate | up, SiLU + Q8,
+        // down added to out as out + weight * down)
+        tg::LgMoeOps P{};
+        P.gate[0] = gate;
+        P.up[0] = up;
+        P.down[0] = static_cast<const uint8_t *>(down);
+        P.w[0] = weight;
+        PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, gbpr, st));
+        PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, 1, b.xq, b.g, embed, inter, st));
+        PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(b.g, b.hq, 1, inter, st));
+        PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, 1, b.hq, out, embed, inter, true, st));
+        return TG_OK;
+    }
     PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, gbpr, st));
     PROFILED("lg_q4k", st, tg::launch_matmul_q4k(gate, b.xq, b.g, inter, gbpr, st));
     PROFILED("lg_q4k", st, tg::launch_matmul_q4k(up, b.xq, b.u, inter, gbpr, st));
@@ -1345,17 +1372,6 @@ extern "C" void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *u
     }
 }
 
-// tg_moe_forward with every expert staged first, then the whole block in
-// three launches after the Q8 of x (gate / up of every expert, SiLU and Q8 of
-// every h, the down rows summed over the experts in order): the same bytes as
-// the expert-by-expert chain (TG_LEGACY_MOE_ALL=0 keeps that chain).
-static bool lg_moe_all_enabled() {
-    static const bool on = [] {
-        const char *v = getenv("TG_LEGACY_MOE_ALL");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
 
 // after the chain's buffers: every expert's staging (for experts not held in
 // HBM), the gate / up rows of all experts and their Q8 h blocks
@@ -1396,7 +1412,7 @@ static int lg_moe_run(const tg::LgMoeOps &P, int n, const float *x, float *out, 
     PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, embed / tg::LG_QK, st));
     PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n, b.xq, m.gu, embed, inter, st));
     PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(m.gu, m.hq, n, inter, st));
-    PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n, m.hq, out, embed, inter, st));
+    PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n, m.hq, out, embed, inter, false, st));
     return TG_OK;
 }
 

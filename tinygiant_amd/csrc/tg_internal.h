@@ -150,6 +150,7 @@ hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, f
                                  hipStream_t st);
 hipError_t launch_moe_silu_q8k(const float *gu, void *hq, int n_exp, int inter, hipStream_t st);
 hipError_t launch_moe_down_acc_q4k(const LgMoeOps &P, int n_exp, const void *hq, float *out, int embed, int inter,
+                                   bool add_to_out,
                                    hipStream_t st);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int dim, int rows, float eps,
                                 hipStream_t st);

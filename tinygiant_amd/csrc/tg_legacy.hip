@@ -296,12 +296,14 @@ TG_DEV const uint8_t *pick_expert(const uint8_t *const (&t)[LG_MOE_MAX], int n, 
 // one output row per wave: the sequence of its n_exp * dbpr blocks (expert
 // by expert), each expert's row value added as acc + w * value when its last
 // block is in
+// (acc starts at out[r] when add_to_out: expert_forward's out += w * down)
 __global__ __launch_bounds__(256) void k_moe_down_acc_q4k(const LgMoeOps P, const Q8K *__restrict__ hq,
-                                                          float *__restrict__ out, int n_exp, int embed, int dbpr) {
+                                                          float *__restrict__ out, int n_exp, int embed, int dbpr,
+                                                          int add_to_out) {
     const int lane = threadIdx.x & 63, r = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (r >= embed) return;  // uniform over the wave
     const int j4 = lane >> 2, g = lane & 3, nblk = n_exp * dbpr;
-    float acc = 0.0f, cur = 0.0f;
+    float acc = add_to_out ? out[r] : 0.0f, cur = 0.0f;
     int b = 0, e = 0;  // wave-uniform: the block within the expert's row, the expert
     for (int p0 = 0; p0 < nblk; p0 += 32) {
         Q4kGrp W[2];
@@ -1176,10 +1178,10 @@ hipError_t launch_moe_silu_q8k(const float *gu, void *hq, int n_exp, int inter, 
 }
 
 hipError_t launch_moe_down_acc_q4k(const LgMoeOps &P, int n_exp, const void *hq, float *out, int embed, int inter,
-                                   hipStream_t st) {
+                                   bool add_to_out, hipStream_t st) {
     if (!moe_q4k_ok(n_exp, embed, inter)) return hipErrorInvalidValue;
     TG_LAUNCH(k_moe_down_acc_q4k, dim3(lg_cdiv(embed, 4)), dim3(256), 0, st, P, static_cast<const Q8K *>(hq), out,
-              n_exp, embed, inter / LG_QK);
+              n_exp, embed, inter / LG_QK, add_to_out ? 1 : 0);
     return hipGetLastError();
 }
 
