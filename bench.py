@@ -980,6 +980,18 @@ def run_legacy_layer(args, torch, call):
     for _ in range(K):
         step()
     wall = time.perf_counter() - t0
+    # the same calls after tg_mlock of every weight, as the reference's engine locks its attention weights
+    # (engine.py:134-139) and its cache the pinned experts (cache.py:59-67): the weights are then read from
+    # HBM copies; the KV rows, x and the rope rows are still copied per call
+    for a in (*w, an, fn_, qn, kn, *experts):
+        lib.tg_mlock(ctypes.c_void_p(a.ctypes.data), ctypes.c_size_t(a.nbytes))
+    for _ in range(W):
+        step()
+    log(f"timing {K} calls after tg_mlock")
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    wall_pin = time.perf_counter() - t0
     call("tg_prof_enable", 1)
     for _ in range(4):
         step()
@@ -1026,6 +1038,8 @@ def run_legacy_layer(args, torch, call):
         "dtype": "f32 attention, q4_k x q8 experts", "data": "synthetic",
         "config": {"workload": "legacy-transformer-layer", "hidden": H, "heads": Hh, "kv_heads": KV, "head_dim": hd,
                    "kv_len": kv_len, "experts": K_TOP, "moe_intermediate": I},
+        "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4),
+                   "note": "after tg_mlock of every weight (attention, norms, experts); the KV rows still copied"},
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": "k_matvec_two_acc (f32 projections)",
                      "bytes_per_launch": round(proj_bytes), "achieved": round(achieved / 1e9, 1),
