@@ -1271,7 +1271,7 @@ static LgExpertBufs lg_expert_bufs(LgCarve &c, int embed, int inter) {
 }
 
 // tg_moe_forward with every expert staged first, then the whole block in
-// three launches after the Q8 of x (gate / up of every expert, SiLU and Q8 of
+// three launches (the Q8 of x and gate / up of every expert, SiLU and Q8 of
 // every h, the down rows summed over the experts in order): the same bytes as
 // the expert-by-expert chain (TG_LEGACY_MOE_ALL=0 keeps that chain, here
 // and for a single expert with a Q4_K down matrix).
@@ -1290,16 +1290,15 @@ static int lg_expert(const uint8_t *gate, const uint8_t *up, const void *down, i
                      float weight, int embed, int inter, const LgExpertBufs &b) {
     const int gbpr = embed / tg::LG_QK, dbpr = inter / tg::LG_QK;
     hipStream_t st = g_lg_st;
-    if (fmt == 0 && embed % tg::LG_QK == 0 && inter % tg::LG_QK == 0 && lg_moe_all_enabled()) {
-        // Q4_K down: the fused launches for one expert (gate | up, SiLU + Q8,
-        // down added to out as out + weight * down)
+    if (fmt == 0 && tg::moe_q4k_ok(1, embed, inter) && lg_moe_all_enabled()) {
+        // Q4_K down: the fused launches for one expert (Q8 of x and gate | up,
+        // SiLU + Q8, down added to out as out + weight * down)
         tg::LgMoeOps P{};
         P.gate[0] = gate;
         P.up[0] = up;
         P.down[0] = static_cast<const uint8_t *>(down);
         P.w[0] = weight;
-        PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, gbpr, st));
-        PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, 1, b.xq, b.g, embed, inter, st));
+        PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, 1, x, b.g, embed, inter, st));
         PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(b.g, b.hq, 1, inter, st));
         PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, 1, b.hq, out, embed, inter, true, st));
         return TG_OK;
@@ -1405,12 +1404,11 @@ static int lg_moe_ops(int n, const uint8_t *const *gp, const uint8_t *const *up,
 }
 
 // out = sum over the experts in order of weight * down(SiLU(gate x) * up x),
-// x the device input (Q8 once, then the three launches)
+// x the device input (its Q8 blocks formed inside the gate / up launch)
 static int lg_moe_run(const tg::LgMoeOps &P, int n, const float *x, float *out, int embed, int inter,
                       const LgExpertBufs &b, const LgMoeAllBufs &m) {
     hipStream_t st = g_lg_st;
-    PROFILED("lg_quant", st, tg::launch_quantize_q8k(x, b.xq, embed / tg::LG_QK, st));
-    PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n, b.xq, m.gu, embed, inter, st));
+    PROFILED("lg_moe_gateup", st, tg::launch_moe_gateup_q4k(P, n, x, m.gu, embed, inter, st));
     PROFILED("lg_moe_silu", st, tg::launch_moe_silu_q8k(m.gu, m.hq, n, inter, st));
     PROFILED("lg_moe_down", st, tg::launch_moe_down_acc_q4k(P, n, m.hq, out, embed, inter, false, st));
     return TG_OK;
@@ -1440,7 +1438,7 @@ extern "C" void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights
     std::lock_guard<std::mutex> lk(g_lg_mu);
     const size_t gb = (size_t)inter_dim * (embed_dim / tg::LG_QK) * tg::LG_Q4K_BYTES;
     const size_t eb = 2 * gb + down_bytes(0, embed_dim, inter_dim);
-    const bool moe_all = n_experts <= tg::LG_MOE_MAX && lg_moe_all_enabled();
+    const bool moe_all = tg::moe_q4k_ok(n_experts, embed_dim, inter_dim) && lg_moe_all_enabled();
     auto run = [&]() -> int {
         for (int pass = 0; pass < 2; pass++) {
             LgCarve c{pass ? g_lg_buf : nullptr};
@@ -1803,7 +1801,7 @@ static int lg_transformer_layer(const float *wq, const float *wk, const float *w
     const int embed = g.embed;
     const size_t gb = (size_t)inter * (embed / tg::LG_QK) * tg::LG_Q4K_BYTES;
     size_t dbmax = 0;
-    bool all_q4k = n_active > 0 && n_active <= tg::LG_MOE_MAX;
+    bool all_q4k = tg::moe_q4k_ok(n_active, embed, inter);
     for (int e = 0; e < n_active; e++) {
         dbmax = std::max(dbmax, down_bytes(down_is_f16[e], embed, inter));
         all_q4k = all_q4k && down_is_f16[e] == 0;

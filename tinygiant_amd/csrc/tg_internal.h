@@ -146,7 +146,11 @@ struct LgMoeOps {
 // gu: n_exp * 2 * inter floats (every expert's gate then up rows), hq:
 // n_exp * inter / 256 Q8 blocks of SiLU(gate) * up; out: embed floats,
 // written (not added to)
-hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, float *gu, int embed, int inter,
+// shapes the fused launches take: 1 .. LG_MOE_MAX experts, embed and inter
+// multiples of 256, embed at most 32768
+bool moe_q4k_ok(int n_exp, int embed, int inter);
+// (x: the fp32 input; each block forms its Q8 blocks in LDS)
+hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const float *x, float *gu, int embed, int inter,
                                  hipStream_t st);
 hipError_t launch_moe_silu_q8k(const float *gu, void *hq, int n_exp, int inter, hipStream_t st);
 hipError_t launch_moe_down_acc_q4k(const LgMoeOps &P, int n_exp, const void *hq, float *out, int embed, int inter,

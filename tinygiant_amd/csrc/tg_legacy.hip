@@ -198,11 +198,12 @@ struct Q4kFmt {
 };
 
 // The values of rows of bpr blocks each: nblk consecutive blocks from wb
-// (starting at a row's first block) against xq; lane 0 stores the k-th row's
+// (starting at a row's first block) against the Q8 blocks of x at xb, xs
+// bytes apart (global memory, or a padded copy in LDS); lane 0 stores the k-th row's
 // value at out[k].  Two passes' loads at a time (block indices clamped to the
 // last block; the clamped lanes' terms are never added).
 template <class F>
-TG_DEV void rows_seq(const uint8_t *__restrict__ wb, int nblk, const Q8K *__restrict__ xq, int bpr, int lane,
+TG_DEV void rows_seq(const uint8_t *__restrict__ wb, int nblk, const uint8_t *xb, int xs, int bpr, int lane,
                      float *__restrict__ out) {
     const int j4 = lane >> 2, sub = lane & 3;
     float cur = 0.0f;
@@ -213,7 +214,8 @@ TG_DEV void rows_seq(const uint8_t *__restrict__ wb, int nblk, const Q8K *__rest
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const int f = min(p0 + 16 * pp + j4, nblk - 1);
-            F::load(wb + (size_t)f * F::BYTES, xq + f % bpr, sub, W[pp], X[pp]);
+            F::load(wb + (size_t)f * F::BYTES, reinterpret_cast<const Q8K *>(xb + (size_t)(f % bpr) * xs), sub, W[pp],
+                    X[pp]);
         }
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
@@ -251,26 +253,40 @@ __global__ __launch_bounds__(256) void k_matmul_q4k(const uint8_t *__restrict__ 
         if (lane < min(R, nrows - r0)) y[r0 + lane] = 0.0f;
         return;
     }
-    rows_seq<Q4kFmt>(W + (size_t)r0 * bpr * LG_Q4K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
+    rows_seq<Q4kFmt>(W + (size_t)r0 * bpr * LG_Q4K_BYTES, min(R, nrows - r0) * bpr,
+                     reinterpret_cast<const uint8_t *>(xq), (int)sizeof(Q8K), bpr, lane, y + r0);
 }
 
 // ------------------------------------------------ moe_forward, all experts
-// The k experts of tg_moe_forward (libtinygiant.c:647-655) in three launches
-// after the one Q8 of x: every expert's gate and up rows, every expert's
+// The k experts of tg_moe_forward (libtinygiant.c:647-655) in three launches:
+// the Q8 of x and every expert's gate and up rows, every expert's
 // SiLU(gate) * up quantized to Q8 blocks, and every output row's down dots
 // added over the experts in their order (the reference zeroes the output,
 // then adds weight * down expert by expert: the same additions, in the same
 // order, from the same zero).  One wave per row or block.
-__global__ __launch_bounds__(256) void k_moe_gateup_q4k(const LgMoeOps P, const Q8K *__restrict__ xq,
+// The block first forms the Q8 blocks of x itself, in LDS at a stride of
+// LG_XQ_LDS bytes from byte 8 (so that every qs array is 16-byte aligned);
+// each wave quantizes every fourth block.
+constexpr int LG_XQ_LDS = 272;
+__global__ __launch_bounds__(256) void k_moe_gateup_q4k(const LgMoeOps P, const float *__restrict__ x,
                                                         float *__restrict__ gu, int n_exp, int inter, int bpr) {
+    extern __shared__ __align__(16) uint8_t lsm[];
+    uint8_t *xl = lsm + 8;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int b = wv; b < bpr; b += 4) {
+        const float4 v4 = reinterpret_cast<const float4 *>(x + (size_t)b * LG_QK)[lane];
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        q8k_block(v, lane, reinterpret_cast<Q8K *>(xl + b * LG_XQ_LDS));
+    }
+    __syncthreads();
     // R rows per wave, all of one matrix (R is a power of two at most 16 and
     // inter a multiple of 256)
-    const int lane = threadIdx.x & 63, R = q4k_rows_per_wave(bpr);
-    const int r = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int R = q4k_rows_per_wave(bpr);
+    const int r = R * __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + wv);
     if (r >= n_exp * 2 * inter) return;  // uniform over the wave
     const int e = r / (2 * inter), rem = r - e * 2 * inter, m = rem >= inter ? 1 : 0, i = rem - m * inter;
     const uint8_t *W = m ? P.up[e] : P.gate[e];
-    rows_seq<Q4kFmt>(W + (size_t)i * bpr * LG_Q4K_BYTES, R * bpr, xq, bpr, lane, gu + r);  // gu[e][gate / up][i]
+    rows_seq<Q4kFmt>(W + (size_t)i * bpr * LG_Q4K_BYTES, R * bpr, xl, LG_XQ_LDS, bpr, lane, gu + r);  // gu[e][m][i]
 }
 
 __global__ __launch_bounds__(256) void k_moe_silu_q8k(const float *__restrict__ gu, Q8K *__restrict__ hq, int n_exp,
@@ -432,7 +448,8 @@ __global__ __launch_bounds__(256) void k_matmul_q6k(const uint8_t *__restrict__ 
         if (lane < min(R, nrows - r0)) y[r0 + lane] = 0.0f;
         return;
     }
-    rows_seq<Q6kFmt>(W + (size_t)r0 * bpr * LG_Q6K_BYTES, min(R, nrows - r0) * bpr, xq, bpr, lane, y + r0);
+    rows_seq<Q6kFmt>(W + (size_t)r0 * bpr * LG_Q6K_BYTES, min(R, nrows - r0) * bpr,
+                     reinterpret_cast<const uint8_t *>(xq), (int)sizeof(Q8K), bpr, lane, y + r0);
 }
 
 // ------------------------------------------------------ f16 / f32 matvec
@@ -1158,15 +1175,18 @@ hipError_t launch_add_vec(float *x, const float *a, int n, hipStream_t st) {
     return hipGetLastError();
 }
 
-static bool moe_q4k_ok(int n_exp, int embed, int inter) {
-    return n_exp > 0 && n_exp <= LG_MOE_MAX && embed % LG_QK == 0 && inter % LG_QK == 0;
+// the fused launches' shapes (x's Q8 blocks in at most 34.8 KB of LDS)
+bool moe_q4k_ok(int n_exp, int embed, int inter) {
+    return n_exp > 0 && n_exp <= LG_MOE_MAX && embed > 0 && inter > 0 && embed % LG_QK == 0 &&
+           inter % LG_QK == 0 && embed / LG_QK <= 128;
 }
 
-hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const void *xq, float *gu, int embed, int inter,
+hipError_t launch_moe_gateup_q4k(const LgMoeOps &P, int n_exp, const float *x, float *gu, int embed, int inter,
                                  hipStream_t st) {
     if (!moe_q4k_ok(n_exp, embed, inter)) return hipErrorInvalidValue;
-    TG_LAUNCH(k_moe_gateup_q4k, dim3(lg_cdiv(n_exp * 2 * inter, 4 * q4k_rows_per_wave(embed / LG_QK))), dim3(256), 0, st, P,
-              static_cast<const Q8K *>(xq), gu, n_exp, inter, embed / LG_QK);
+    const int bpr = embed / LG_QK;
+    TG_LAUNCH(k_moe_gateup_q4k, dim3(lg_cdiv(n_exp * 2 * inter, 4 * q4k_rows_per_wave(bpr))), dim3(256),
+              8 + (size_t)bpr * LG_XQ_LDS, st, P, x, gu, n_exp, inter, bpr);
     return hipGetLastError();
 }
 
