@@ -7,11 +7,20 @@ renormalised softmax, decode batch 1.  One step = one token through all 48
 layers (x <- x + MoE_l(rms_norm(x))).  Weights are synthetic N(0, 0.02)
 quantized to Q4_0 (16.3 GB resident in HBM) with fp32 N(0, 0.02) routers;
 every step copies a fresh N(0, 1) token into the stack's hidden-state
-buffer and runs the stack (one launch per layer).  The timed region starts with all
-inputs in HBM.  The same line carries a "prefill" object: 2048 tokens through
-the same 48-layer stack on the grouped int8-MFMA path (BASELINE's second
-half: int8 TOPS against the MFMA peak), with its own roofline and CPU
-baseline.  Step times are also reported as the median of the timed steps.
+buffer and runs the stack (one launch per layer).  The timed region starts
+with all inputs in HBM.  Step times are also reported as the median of the
+timed steps.  The same line carries one object per other configuration,
+each with its own roofline and CPU baseline:
+  prefill       2048 tokens through the same 48-layer stack on the grouped
+                int8-MFMA path: int8 TOPS against the MFMA peak, nominal and
+                at the shader clock measured under MFMA load.
+  batched       64 tokens per step through one layer, steps rotating over 16
+                of the stack's layers, routers skewed to Zipf(1.1).
+  decode_235b   the Qwen3-235B-A22B-shaped stack (H=4096, I=1536, 94 layers,
+                127.7 GB resident; built after the 30B arena is released),
+                one token per step.
+  batched_235b  the same stack, 32 tokens per step, routers skewed to
+                Zipf(1.1).
 
 Other workloads (--workload):
   batched      one layer per step, 64 tokens per step, router skewed so that
@@ -284,12 +293,14 @@ def run_decode_stack(args, torch, call):
     arena.status()
     kern = kernel_times(call, ("dec_part", "layer", "route", "experts", "gateup", "down"))
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
+    router_bytes = None
     if "layer" in kern:
-        # one launch = routing, gate/up and down of one layer (expert weights
-        # plus the next layer's router columns)
+        # one launch = routing, gate/up and down of one layer: the expert
+        # weights (the roofline's bytes) and the next layer's router columns
+        # (reported apart)
         n_x, ms_x = kern["layer"]
         avg = ms_x / max(n_x, 1) * 1e-3
-        roof_kernel, roof_bytes = "k_layer_dec", K_TOP * EXPERT_Q4_BYTES + ROUTER_BYTES
+        roof_kernel, roof_bytes, router_bytes = "k_layer_dec", K_TOP * EXPERT_Q4_BYTES, ROUTER_BYTES
         path = "routed"
     elif "experts" in kern:
         # one launch = gate/up and down of the token's k experts in one layer
@@ -319,6 +330,32 @@ def run_decode_stack(args, torch, call):
     if not args.no_prefill:
         log("prefill leg: 2048 tokens through the same stack")
         prefill = prefill_leg(args, torch, call, arena, L, K=20, W=2)
+        clk = measure_clock(call)
+        prefill["clock"] = clk
+        prefill["roofline"]["peak_at_measured_clock"] = clk["int8_peak_tops"]
+        prefill["roofline"]["frac_at_measured_clock"] = round(prefill["roofline"]["achieved"] / clk["int8_peak_tops"], 4)
+        prefill["mfma_frac_at_measured_clock"] = round(prefill["value"] / clk["int8_peak_tops"], 4)
+
+    batched = None
+    if not args.no_batched and L >= 16:
+        log("batched leg: 64 tokens per step over 16 of the stack's layers, Zipf(1.1) routers")
+        batched = batched_leg(args, torch, call, arena, 16, K=256, W=16)
+    arena.close()
+
+    d235 = b235 = None
+    if not args.no_235b:
+        log("235B legs: the 30B arena closed, the 94-layer 235B-shaped arena filled")
+        a5 = synth_235b_arena(args, L5)
+        d235 = leg_235b(args, torch, call, a5, 1, K=64, W=8)
+        b235 = leg_235b(args, torch, call, a5, 32, K=16, W=2)
+        a5.close()
+
+    roofline = {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
+                "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(roof_kernel)}
+    if router_bytes:
+        roofline.update({"router_bytes_per_launch": router_bytes,
+                         "frac_with_router": round((roof_bytes + router_bytes) / avg / HBM_PEAK, 4)})
 
     out = {
         "metric": "MoE-layer decode tok/s (48-layer Q4_0 stack, batch 1)",
@@ -341,55 +378,86 @@ def run_decode_stack(args, torch, call):
         "step_ms": steps_ms,
         "kernel_avg_us": kern_us,
         "decode_path": path,
-        "roofline": {"bound": "hbm", "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
-                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(roof_kernel)},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "batched": batched,
+        "decode_235b": d235,
+        "batched_235b": b235,
     }
-    arena.close()
     return out
 
 
-def run_batched(args, torch, call):
-    """Config 3: 64 tokens per step through one layer, Zipf(1.1) expert skew."""
-    from tinygiant_amd.arena import HBMExpertArena
+ZIPF_TARGET = 1.1
+ZIPF_BETA0 = 0.54 / 0.905  # bias scale (per unit of logit noise) that gave ~1.1 at the 30B shape
+
+
+def calibrate_zipf(build, measure, beta=ZIPF_BETA0, iters=4, tol=0.02):
+    """Scales the per-expert router bias until the fitted rank-frequency
+    exponent of the routing is within tol of 1.1: build(beta) loads the
+    routers, measure() routes sample tokens and fits the exponent.  The
+    exponent grows about in proportion to the bias, so each step multiplies
+    beta by 1.1 / fit.  Returns (beta, fit) of the routers left loaded."""
+    fit = float("nan")
+    for it in range(iters):
+        build(beta)
+        fit = measure()
+        log(f"zipf calibration {it}: bias scale {beta:.4f} -> fitted exponent {fit:.3f}")
+        if abs(fit - ZIPF_TARGET) <= tol or it == iters - 1:
+            break
+        beta *= ZIPF_TARGET / fit
+    return beta, fit
+
+
+def batched_leg(args, torch, call, arena, LR=16, K=256, W=16, T=64):
+    """Config 3 on the first LR layers of a 30B-shaped arena: T tokens per
+    step through one layer, steps rotating over the LR layers (LR * 340 MB,
+    more than the 256 MB MALL), the router of each layer skewed so that
+    expert popularity follows Zipf(1.1): a per-expert bias along a direction
+    u that every token shares (tokens N(0, 1) + c u), scaled until the fitted
+    exponent of the routing is 1.1.  Returns the batched object of the bench
+    line."""
     from tinygiant_amd.moe import MoEBlock
     from tinygiant_amd.synth import fit_zipf_exponent, stream_id, zipf_router_bias
 
-    T, LR = 64, 16
-    K, W = args.steps or 256, 16 if args.warmup is None else args.warmup
-    log(f"arena: {LR} layers x {E} experts ({LR * E * EXPERT_Q4_BYTES / 1e9:.2f} GB Q4_0)")
-    arena = HBMExpertArena(LR, E, H, I, K_TOP)
+    H_, E_ = arena.embed_dim, arena.n_experts
     rng = np.random.default_rng(args.seed)
-    u = rng.standard_normal(H)
+    u = rng.standard_normal(H_)
     u /= np.linalg.norm(u)
-    c = 0.5 * np.sqrt(H)                       # token component along u
-    rms = np.sqrt(1.0 + c * c / H)
-    noise_std = 0.02 * np.sqrt(H) / rms         # std of the unskewed logits
-    bias = zipf_router_bias(E, 0.54 * noise_std / 0.905)
+    c = 0.5 * np.sqrt(H_)                       # token component along u
+    rms = np.sqrt(1.0 + c * c / H_)
+    noise_std = 0.02 * np.sqrt(H_) / rms         # std of the unskewed logits
     routers = []
-    for l in range(LR):
-        arena.synth_layer(l, args.seed)
-        Wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
-        Wr += (bias[:, None] * (rms / c) * u[None, :]).astype(np.float32)
-        arena.load_router(l, Wr)
-        routers.append(Wr)
+
+    def build(beta):
+        r2 = np.random.default_rng(args.seed + 17)
+        bias = zipf_router_bias(E_, beta * noise_std)
+        routers.clear()
+        for l in range(LR):
+            Wr = (r2.standard_normal((E_, H_)) * 0.02).astype(np.float32)
+            Wr += (bias[:, None] * (rms / c) * u[None, :]).astype(np.float32)
+            arena.load_router(l, Wr)
+            routers.append(Wr)
+
     arena.set_batch_path(arena.BATCH_GROUPED)
     stream = torch.cuda.current_stream().cuda_stream
-    X = torch.empty((W + K, T, H), dtype=torch.float32, device="cuda")
+    X = torch.empty((W + K, T, H_), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
     X += torch.from_numpy((c * u).astype(np.float32)).cuda()
     torch.cuda.synchronize()
     blk = MoEBlock(arena)
-    outs = torch.empty((T, H), dtype=torch.float32, device="cuda")
 
-    log(f"warmup {W} steps")
+    def measure():
+        idx = [blk.forward(i % LR, X[i], return_routing=True)[1].cpu().numpy() for i in range(LR)]
+        return fit_zipf_exponent(np.concatenate(idx), E_)
+
+    beta, _ = calibrate_zipf(build, measure)
+
+    log(f"batched: warmup {W} steps")
     for i in range(W):
         blk.forward(i % LR, X[i])
     torch.cuda.synchronize()
-    log(f"timing {K} steps of {T} tokens")
-    torch.cuda.synchronize()
+    log(f"batched: timing {K} steps of {T} tokens over {LR} layers")
     t0 = time.perf_counter()
     for i in range(W, W + K):
         blk.forward(i % LR, X[i])
@@ -406,11 +474,11 @@ def run_batched(args, torch, call):
         uniq.append(len(np.unique(ih)))
         all_idx.append(ih)
     n_uniq = float(np.mean(uniq))
-    zipf_s = fit_zipf_exponent(np.concatenate(all_idx), E)
+    zipf_s = fit_zipf_exponent(np.concatenate(all_idx), E_)
     bytes_step = n_uniq * EXPERT_Q4_BYTES
     gbps = bytes_step / (ms_step * 1e-3) / 1e9
 
-    log("kernel timing pass")
+    log("batched: kernel timing pass")
     call("tg_prof_enable", 1)
     for i in range(W, W + K):
         blk.forward(i % LR, X[i])
@@ -428,29 +496,23 @@ def run_batched(args, torch, call):
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (oracle)")
+        log("batched: cpu baseline (oracle)")
         l0 = W % LR
         lb = arena.read_layer(l0)
         Xh = [X[W + j].cpu().numpy() for j in range(0, K, LR)][:4]
         out = blk.forward(l0, X[W])
         cpu = cpu_baseline_layer(lb, routers[l0], Xh, args.cpu_seconds, (X[W].cpu().numpy(), out.cpu().numpy()))
-
-    res = {
+    arena.set_batch_path(arena.BATCH_AUTO)
+    del X
+    return {
         "metric": "MoE-layer batched decode tok/s (64 tokens/step, Zipf(1.1) routing)",
-        "value": round(tok_s, 1),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "value": round(tok_s, 1), "unit": "tok/s", "steps": K, "warmup": W, "ms_per_step": round(ms_step, 4),
         "dtype": "q4_0 x q8_0 (int8 MFMA, fp32 accumulate)",
-        "data": "synthetic (N(0,0.02) Q4_0 experts, skewed fp32 routers, N(0,1) tokens + shared direction)",
-        "config": {"workload": "qwen3-30b-a3b-moe-layer-batched-decode", "hidden": H, "experts": E,
-                   "moe_intermediate": I, "top_k": K_TOP, "tokens_per_step": T, "layers_rotated": LR,
-                   "zipf_fit": round(zipf_s, 3), "unique_experts_per_step": round(n_uniq, 2)},
+        "data": "synthetic (N(0,0.02) Q4_0 experts, Zipf-skewed fp32 routers, N(0,1) tokens + shared direction)",
+        "config": {"workload": "qwen3-30b-a3b-moe-layer-batched-decode", "hidden": H_, "experts": E_,
+                   "moe_intermediate": arena.inter_dim, "top_k": K_TOP, "tokens_per_step": T, "layers_rotated": LR,
+                   "zipf_target": ZIPF_TARGET, "zipf_fit": round(zipf_s, 3), "zipf_bias_scale": round(beta, 4),
+                   "unique_experts_per_step": round(n_uniq, 2)},
         "hbm_gbps_expert_weights": round(gbps, 1),
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "kernel_avg_us": kern_us,
@@ -460,29 +522,53 @@ def run_batched(args, torch, call):
                      "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(gu_kernel + "/gate_up")},
         "cpu_baseline": cpu,
     }
-    del outs
+
+
+def run_batched(args, torch, call):
+    """Config 3 alone: a 16-layer 30B-shaped arena, 64 tokens per step."""
+    from tinygiant_amd.arena import HBMExpertArena
+
+    LR = 16
+    log(f"arena: {LR} layers x {E} experts ({LR * E * EXPERT_Q4_BYTES / 1e9:.2f} GB Q4_0)")
+    arena = HBMExpertArena(LR, E, H, I, K_TOP)
+    for l in range(LR):
+        arena.synth_layer(l, args.seed)
+    b = batched_leg(args, torch, call, arena, LR, K=args.steps or 256, W=16 if args.warmup is None else args.warmup)
     arena.close()
-    return res
+    return headline(b)
+
+
+def headline(leg):
+    """A leg's object as a bench line of its own."""
+    out = {"metric": leg.pop("metric"), "value": leg.pop("value"), "unit": leg.pop("unit"), "n_gpus": 1,
+           "steps": leg.pop("steps"), "warmup": leg.pop("warmup"), "ms_per_step": leg.pop("ms_per_step"),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": leg.pop("dtype"),
+           "data": leg.pop("data"), "config": leg.pop("config")}
+    out.update(leg)
+    return out
 
 
 # Qwen3-235B-A22B MoE shape (config 5)
 H5, I5, E5, K5, L5 = 4096, 1536, 128, 8, 94
 EXPERT5_BYTES = 3 * I5 * (H5 // 32) * 18          # 10,616,832
 GATEUP5_BYTES = 2 * I5 * (H5 // 32) * 18          # 7,077,888
+ROUTER5_BYTES = E5 * H5 * 4                        # 2,097,152
 
 
-def skewed_stack_routers(arena, blk, x0, u, c, shape, rng, torch):
-    """Routers of a stack whose expert popularity follows Zipf(1.1) at every
-    depth: a per-expert component along the direction u that tokens share.
-    Layer l's component is scaled by rms(x_l) / (u . x_l) measured on the
-    hidden states that reach it (x0 pushed through the layers before it), so
-    the logit bias stays the same although the residual stream grows."""
+def skewed_stack_routers(arena, blk, x0, u, c, beta, seed, torch):
+    """Routers of a stack whose expert popularity follows a power law at
+    every depth: a per-expert component along the direction u that tokens
+    share.  Layer l's component is scaled by rms(x_l) / (u . x_l) measured on
+    the hidden states that reach it (x0 pushed through the layers before
+    it), so the logit bias stays the same although the residual stream
+    grows.  beta: the bias per unit of logit noise."""
     from tinygiant_amd.synth import zipf_router_bias
-    Hs, _, Es, _ = shape
+    Hs, Es = arena.embed_dim, arena.n_experts
     rms0 = np.sqrt(1.0 + c * c / Hs)
     noise_std = 0.02 * np.sqrt(Hs) / rms0
-    bias = zipf_router_bias(Es, 0.54 * noise_std / 0.905)
+    bias = zipf_router_bias(Es, beta * noise_std)
     ut = torch.from_numpy(u.astype(np.float32)).cuda()
+    rng = np.random.default_rng(seed + 29)
     x = x0.clone()
     routers = []
     for l in range(arena.n_layers):
@@ -497,44 +583,65 @@ def skewed_stack_routers(arena, blk, x0, u, c, shape, rng, torch):
     return routers
 
 
-def run_235b(args, torch, call, T):
-    """Config 5: the Qwen3-235B-A22B-shaped MoE stack (H=4096, I=1536, 128
-    experts, top-8, 94 layers, 127.7 GB of Q4_0 resident in HBM); one step =
-    T tokens through all 94 layers.  T = 1: synthetic N(0, 0.02) routers,
-    one-token decode path.  T = 32: Zipf(1.1)-skewed routers, grouped path."""
+def synth_235b_arena(args, L):
     from tinygiant_amd.arena import HBMExpertArena
-    from tinygiant_amd.moe import MoEBlock
-    from tinygiant_amd.synth import fit_zipf_exponent, stream_id
-
-    shape = (H5, I5, E5, K5)
-    L = args.layers if args.layers != 48 else L5
-    K = args.steps or (64 if T == 1 else 16)
-    W = (8 if T == 1 else 2) if args.warmup is None else args.warmup
     log(f"arena: {L} layers x {E5} experts ({L * E5 * EXPERT5_BYTES / 1e9:.1f} GB Q4_0)")
+    t0 = time.perf_counter()
     arena = HBMExpertArena(L, E5, H5, I5, K5)
     for l in range(L):
         arena.synth_layer(l, args.seed)
+    arena.status()
+    log(f"arena filled in {time.perf_counter() - t0:.1f} s")
+    return arena
+
+
+def leg_235b(args, torch, call, arena, T, K, W):
+    """Config 5 on a 235B-shaped arena (H=4096, I=1536, 128 experts, top-8;
+    94 layers, 127.7 GB of Q4_0 resident in HBM); one step = T tokens
+    through every layer.  T = 1: the synthetic N(0, 0.02) routers, one-token
+    decode path.  T = 32: routers skewed to a fitted Zipf exponent of 1.1,
+    grouped path.  Returns the leg's object of the bench line."""
+    from tinygiant_amd.moe import MoEBlock
+    from tinygiant_amd.synth import fit_zipf_exponent, stream_id
+
+    L = arena.n_layers
     rng = np.random.default_rng(args.seed)
     stream = torch.cuda.current_stream().cuda_stream
     X = torch.empty((W + K, T, H5), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
     blk = MoEBlock(arena)
-    routers = None
+    routers, beta = None, None
     if T > 1:
         u = rng.standard_normal(H5)
         u /= np.linalg.norm(u)
         c = 0.5 * np.sqrt(H5)
         X += torch.from_numpy((c * u).astype(np.float32)).cuda()
-        log("router calibration through the stack")
-        routers = skewed_stack_routers(arena, blk, X[0], u, c, shape, rng, torch)
+        holder = []
+
+        def build(b):
+            holder[:] = [skewed_stack_routers(arena, blk, X[0], u, c, b, args.seed, torch)]
+
+        def measure():
+            idx = []
+            for i in (1, 2):
+                x = X[i].clone()
+                for l in range(L):
+                    out, ix, _ = blk.forward(l, x, return_routing=True)
+                    idx.append(ix.cpu().numpy())
+                    x += out
+            return fit_zipf_exponent(np.concatenate(idx), E5)
+
+        log("235B batched: router calibration through the stack")
+        beta, _ = calibrate_zipf(build, measure)
+        routers = holder[0]
     X0 = X.clone()
     torch.cuda.synchronize()
 
-    log(f"warmup {W} steps")
+    log(f"235B: warmup {W} steps")
     for i in range(W):
         blk.step(X[i])
     torch.cuda.synchronize()
-    log(f"timing {K} steps of {T} token(s) x {L} layers")
+    log(f"235B: timing {K} steps of {T} token(s) x {L} layers")
     t0 = time.perf_counter()
     for i in range(W, W + K):
         blk.step(X[i])
@@ -561,7 +668,7 @@ def run_235b(args, torch, call, T):
     bytes_step = L * n_uniq * EXPERT5_BYTES
     gbps = bytes_step / (ms_step * 1e-3) / 1e9
 
-    log("kernel timing pass")
+    log("235B: kernel timing pass")
     X.copy_(X0)
     torch.cuda.synchronize()
     call("tg_prof_enable", 1)
@@ -573,9 +680,9 @@ def run_235b(args, torch, call, T):
              "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    if "layer" in kern:
-        rk, rb = "layer", K5 * EXPERT5_BYTES + E5 * H5 * 4
-        roof = "k_layer_dec"
+    router_bytes = None
+    if "layer" in kern:  # expert bytes only; the next layer's router columns it also reads are reported apart
+        rk, rb, roof, router_bytes = "layer", K5 * EXPERT5_BYTES, "k_layer_dec", ROUTER5_BYTES
     elif "experts" in kern:
         rk, rb = "experts", K5 * EXPERT5_BYTES
         roof = "k_experts"
@@ -587,22 +694,30 @@ def run_235b(args, torch, call, T):
         # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries
         roof = "k_mfma_small/gate_up" if T * K5 <= 16 * E5 else "k_mfma_grouped/gate_up"
     n_r, ms_r = kern[rk]
-    achieved = rb / (ms_r / n_r * 1e-3)
+    avg_s = ms_r / n_r * 1e-3
+    achieved = rb / avg_s
+    roofline = {"bound": "hbm", "kernel": roof, "bytes_per_launch": rb, "achieved": round(achieved / 1e9, 1),
+                "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                "traffic": profiled_traffic(roof + "@235b")}  # this shape's own counter run
+    if router_bytes:
+        roofline.update({"router_bytes_per_launch": router_bytes,
+                         "frac_with_router": round((rb + router_bytes) / avg_s / HBM_PEAK, 4)})
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (oracle)")
+        log("235B: cpu baseline (oracle)")
         if T == 1:
             xt = X0[W, :1].cpu().numpy()
             xg = X0[W, :1].clone()
             blk.step(xg, 0, 2)
             torch.cuda.synchronize()
-            cpu = cpu_baseline_stack(arena, args.seed, L, args.cpu_seconds, (xt, xg.cpu().numpy()), shape, 2)
+            cpu = cpu_baseline_stack(arena, args.seed, L, args.cpu_seconds, (xt, xg.cpu().numpy()),
+                                     (H5, I5, E5, K5), 2)
         else:
             lb = arena.read_layer(0)
             out = blk.forward(0, X0[W])
             cpu = cpu_baseline_layer(lb, routers[0], [X0[W].cpu().numpy()], args.cpu_seconds,
-                                     (X0[W].cpu().numpy(), out.cpu().numpy()), shape)
+                                     (X0[W].cpu().numpy(), out.cpu().numpy()), (H5, I5, E5, K5))
             cpu["sample"] += f"; the stack rate is this over {L} layers"
             cpu["value"] = round(cpu["value"] / L, 3)
             cpu["single_thread"]["value"] = round(cpu["single_thread"]["value"] / L, 3)
@@ -610,11 +725,12 @@ def run_235b(args, torch, call, T):
     cfg = {"workload": f"qwen3-235b-a22b-moe-stack-{'decode' if T == 1 else 'batched-decode'}", "layers": L,
            "hidden": H5, "experts": E5, "moe_intermediate": I5, "top_k": K5, "tokens_per_step": T}
     if zipf_s is not None:
-        cfg.update({"zipf_fit": round(zipf_s, 3), "unique_experts_per_layer_step": round(n_uniq, 2)})
-    res = {
+        cfg.update({"zipf_target": ZIPF_TARGET, "zipf_fit": round(zipf_s, 3), "zipf_bias_scale": round(beta, 4),
+                    "unique_experts_per_layer_step": round(n_uniq, 2)})
+    del X, X0
+    return {
         "metric": f"MoE stack decode tok/s (94-layer 235B-shaped Q4_0 stack, {T} token(s)/step)",
-        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
-        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": round(tok_s, 2), "unit": "tok/s", "steps": K, "warmup": W, "ms_per_step": round(ms_step, 4),
         "dtype": "q4_0 x q8_0 (int8 dot / int8 MFMA, fp32 accumulate)",
         "data": "synthetic (N(0,0.02) Q4_0 experts, fp32 routers" + (", Zipf-skewed" if T > 1 else "") +
                 ", N(0,1) tokens)",
@@ -622,16 +738,41 @@ def run_235b(args, torch, call, T):
         "hbm_gbps_expert_weights": round(gbps, 1),
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": roof, "bytes_per_launch": rb, "achieved": round(achieved / 1e9, 1),
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                     "traffic": profiled_traffic(roof + "@235b")},  # this shape's own counter run
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
+
+
+def run_235b(args, torch, call, T):
+    """Config 5 alone, at batch T."""
+    L = args.layers if args.layers != 48 else L5
+    arena = synth_235b_arena(args, L)
+    K = args.steps or (64 if T == 1 else 16)
+    W = (8 if T == 1 else 2) if args.warmup is None else args.warmup
+    leg = leg_235b(args, torch, call, arena, T, K, W)
     arena.close()
-    return res
+    return headline(leg)
 
 
-MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA, ops/s
+MFMA_INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA, ops/s (256 CUs x 8192 ops/clk x 2.4 GHz)
+MFMA_INT8_OPS_PER_CLK_CU = 8192
+
+
+def measure_clock(call):
+    """The shader clock while every CU runs int8 MFMA chains (the library's
+    clock probe: shader-cycle and 100 MHz real-time counters of each block),
+    and the int8 MFMA peak at that clock beside the nominal 2.4 GHz one."""
+    import torch
+    md, mn, mx = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    call("tg_clock_mfma_mhz", 20000, ctypes.byref(md), ctypes.byref(mn), ctypes.byref(mx))  # warm
+    call("tg_clock_mfma_mhz", 200000, ctypes.byref(md), ctypes.byref(mn), ctypes.byref(mx))
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    peak = n_cu * MFMA_INT8_OPS_PER_CLK_CU * md.value * 1e6
+    return {"mhz_median": round(md.value, 1), "mhz_min": round(mn.value, 1), "mhz_max": round(mx.value, 1),
+            "cus": n_cu, "int8_peak_tops": round(peak / 1e12, 1),
+            "nominal": {"mhz": 2400.0, "int8_peak_tops": MFMA_INT8_PEAK / 1e12},
+            "method": "s_memtime / s_memrealtime around 200k rounds of four v_mfma_i32_16x16x32_i8 chains per wave, "
+                      "4 blocks of 256 threads per CU, median over blocks; HBM peak is not clock-scaled"}
 
 
 def prefill_leg(args, torch, call, arena, L, K=20, W=2):
@@ -731,13 +872,12 @@ def run_prefill(args, torch, call):
         arena.synth_layer(l, args.seed)
     p = prefill_leg(args, torch, call, arena, L, K=K, W=W)
     arena.close()
-    out = {"metric": p.pop("metric"), "value": p.pop("value"), "unit": p.pop("unit"), "n_gpus": 1,
-           "steps": p.pop("steps"), "warmup": p.pop("warmup"), "ms_per_step": p.pop("ms_per_step"),
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": p.pop("dtype"),
-           "data": "synthetic (N(0,0.02) Q4_0 experts and fp32 routers, N(0,1) tokens)",
-           "config": p.pop("config")}
-    out.update(p)
-    return out
+    clk = measure_clock(call)
+    p["clock"] = clk
+    p["roofline"]["peak_at_measured_clock"] = clk["int8_peak_tops"]
+    p["roofline"]["frac_at_measured_clock"] = round(p["roofline"]["achieved"] / clk["int8_peak_tops"], 4)
+    p["data"] = "synthetic (N(0,0.02) Q4_0 experts and fp32 routers, N(0,1) tokens)"
+    return headline(p)
 
 
 def q4k_blocks(rng, n):
@@ -747,6 +887,26 @@ def q4k_blocks(rng, n):
     b[:, 0:2] = rng.uniform(0.0005, 0.004, n).astype(np.float16).view(np.uint8).reshape(n, 2)
     b[:, 2:4] = rng.uniform(0.0, 0.004, n).astype(np.float16).view(np.uint8).reshape(n, 2)
     return b.reshape(-1)
+
+
+def readonly_views(arrays):
+    """The arrays written to one temporary file and mapped back read-only,
+    one uint8 view per array: the form in which the reference's cache holds
+    its experts (np.frombuffer over an ACCESS_READ mmap of the layer file,
+    cache.py:31-55).  Returns the views and the mapping (kept open by the
+    caller while the views are in use)."""
+    import mmap
+    import tempfile
+    with tempfile.TemporaryFile() as f:
+        for a in arrays:
+            f.write(a.tobytes())
+        f.flush()
+        mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+    views, off = [], 0
+    for a in arrays:
+        views.append(np.frombuffer(mm, np.uint8, count=a.nbytes, offset=off))
+        off += a.nbytes
+    return views, mm
 
 
 def run_legacy_moe(args, torch, call):
@@ -764,7 +924,8 @@ def run_legacy_moe(args, torch, call):
     gb = I * (H // 256) * 144
     eb = 2 * gb + H * (I // 256) * 144
     NSET = 16
-    sets = [[q4k_blocks(rng, eb // 144) for _ in range(K_TOP)] for _ in range(NSET)]
+    flat, mm = readonly_views([q4k_blocks(rng, eb // 144) for _ in range(K_TOP * NSET)])
+    sets = [flat[i * K_TOP:(i + 1) * K_TOP] for i in range(NSET)]
     ptrs = [(ctypes.c_void_p * K_TOP)(*[e.ctypes.data for e in st]) for st in sets]
     w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)  # tools/nws_q8dot_bench.c:369
     x = rng.normal(0.0, 1.0, H).astype(np.float32)
@@ -783,7 +944,8 @@ def run_legacy_moe(args, torch, call):
         step(i)
     wall = time.perf_counter() - t0
     # the same calls with every expert locked, as the reference's cache locks its pinned experts
-    # (cache.py:59-67): tg_mlock keeps an HBM copy and the calls read the experts from it
+    # (cache.py:59-67): the views are read-only mappings, so tg_mlock keeps an HBM copy by default
+    # and the calls read the experts from it
     for st in sets:
         for e in st:
             lib.tg_mlock(ctypes.c_void_p(e.ctypes.data), ctypes.c_size_t(e.nbytes))
@@ -828,6 +990,7 @@ def run_legacy_moe(args, torch, call):
                "sample": f"{n} tg_moe_forward calls (8 Q4_K experts, 2048x768) through the C oracle, one thread; "
                          "bit-identical to the GPU call on the first set"}
 
+    lib.tg_mirror_drop(None, 0)  # before the mapping goes with the views
     return {
         "metric": "legacy tg_moe_forward calls/s (8 Q4_K experts, 30B shape, host pointers)",
         "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -835,7 +998,8 @@ def run_legacy_moe(args, torch, call):
         "dtype": "q4_k x q8 (int dot, fp32 accumulate)",
         "data": "synthetic (random Q4_K blocks, N(0,1) input)",
         "config": {"workload": "legacy-q4k-moe-forward", "hidden": H, "moe_intermediate": I, "experts": K_TOP,
-                   "expert_bytes": eb, "note": "each call copies 21.2 MB of host operands to the device"},
+                   "expert_bytes": eb, "note": "experts in read-only mmap views of one file, as the reference's "
+                                               "cache maps them; each call copies 21.2 MB of them to the device"},
         "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4),
                    "note": f"after tg_mlock of every expert: {mb.value / 1e6:.1f} MB in {mr.value} HBM copies, "
                            f"{mh.value} operand reads from them, {mm.value} copied"},
@@ -860,7 +1024,8 @@ def run_legacy_expert(args, torch, call):
     gb = I * (H // 256) * 144
     eb = 2 * gb + H * (I // 256) * 144
     NSET = 16
-    sets = [[q4k_blocks(rng, eb // 144) for _ in range(K_TOP)] for _ in range(NSET)]
+    flat, mm = readonly_views([q4k_blocks(rng, eb // 144) for _ in range(K_TOP * NSET)])
+    sets = [flat[i * K_TOP:(i + 1) * K_TOP] for i in range(NSET)]
     w = np.array([0.15, 0.14, 0.13, 0.13, 0.12, 0.11, 0.11, 0.11], np.float32)
     x = rng.normal(0.0, 1.0, H).astype(np.float32)
     out = np.zeros(H, np.float32)
@@ -919,6 +1084,7 @@ def run_legacy_expert(args, torch, call):
         cpu = {"value": round(1.0 / cpu_s, 2), "unit": "layer/s", "cores": 1, "kind": "port",
                "sample": f"{n} layers of 8 Q4_K experts (2048x768) through the C oracle, one thread; the GPU loop "
                          "bit-identical to it on the first set"}
+    lib.tg_mirror_drop(None, 0)  # before the mapping goes with the views
     return {
         "metric": "legacy engine MoE loop layers/s (8 tg_expert_forward_mixed calls, 30B shape, host pointers)",
         "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -926,7 +1092,8 @@ def run_legacy_expert(args, torch, call):
         "dtype": "q4_k x q8 (int dot, fp32 accumulate)",
         "data": "synthetic (random Q4_K blocks, N(0,1) input)",
         "config": {"workload": "legacy-engine-expert-loop", "hidden": H, "moe_intermediate": I, "experts": K_TOP,
-                   "expert_bytes": eb},
+                   "expert_bytes": eb, "note": "experts in read-only mmap views of one file, as the reference's "
+                                               "cache maps them"},
         "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4)},
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": roof_name, "bytes_per_launch": q_bytes,
@@ -955,7 +1122,7 @@ def run_legacy_layer(args, torch, call):
     kv_k = rng.normal(0, 1, (KV, kv_max, hd)).astype(np.float32)
     kv_v = rng.normal(0, 1, (KV, kv_max, hd)).astype(np.float32)
     gb = I * (H // 256) * 144
-    experts = [q4k_blocks(rng, (2 * gb + H * (I // 256) * 144) // 144) for _ in range(K_TOP)]
+    experts, mm = readonly_views([q4k_blocks(rng, (2 * gb + H * (I // 256) * 144) // 144) for _ in range(K_TOP)])
     gp = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data for e in experts])
     up = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data + gb for e in experts])
     dp = (ctypes.c_void_p * K_TOP)(*[e.ctypes.data + 2 * gb for e in experts])
@@ -982,7 +1149,9 @@ def run_legacy_layer(args, torch, call):
     wall = time.perf_counter() - t0
     # the same calls after tg_mlock of every weight, as the reference's engine locks its attention weights
     # (engine.py:134-139) and its cache the pinned experts (cache.py:59-67): the weights are then read from
-    # HBM copies; the KV rows, x and the rope rows are still copied per call
+    # HBM copies; the KV rows, x and the rope rows are still copied per call.  The attention weights are
+    # writable numpy arrays, copied only in TG_MIRROR_ALL (they are never written after the lock)
+    lib.tg_mirror_mode(2)
     for a in (*w, an, fn_, qn, kn, *experts):
         lib.tg_mlock(ctypes.c_void_p(a.ctypes.data), ctypes.c_size_t(a.nbytes))
     for _ in range(W):
@@ -1031,6 +1200,8 @@ def run_legacy_layer(args, torch, call):
                "sample": f"{n} tg_transformer_layer calls through the C oracle, one thread; bit-identical to the "
                          "GPU call"}
 
+    lib.tg_mirror_drop(None, 0)  # before the mapping goes with the views
+    lib.tg_mirror_mode(1)
     return {
         "metric": "legacy tg_transformer_layer calls/s (30B-shaped layer, 1024 cached positions, host pointers)",
         "value": round(K / wall, 2), "unit": "layer/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -1039,7 +1210,8 @@ def run_legacy_layer(args, torch, call):
         "config": {"workload": "legacy-transformer-layer", "hidden": H, "heads": Hh, "kv_heads": KV, "head_dim": hd,
                    "kv_len": kv_len, "experts": K_TOP, "moe_intermediate": I},
         "pinned": {"value": round(K / wall_pin, 2), "unit": "layer/s", "ms_per_step": round(wall_pin * 1e3 / K, 4),
-                   "note": "after tg_mlock of every weight (attention, norms, experts); the KV rows still copied"},
+                   "note": "after tg_mlock of every weight (attention, norms, experts; tg_mirror_mode "
+                           "TG_MIRROR_ALL, since the attention weights are writable arrays); the KV rows still copied"},
         "kernel_avg_us": kern_us,
         "roofline": {"bound": "hbm", "kernel": "k_matvec_two_acc (f32 projections)",
                      "bytes_per_launch": round(proj_bytes), "achieved": round(achieved / 1e9, 1),
@@ -1261,6 +1433,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="default workload: skip the prefill leg")
+    ap.add_argument("--no-batched", action="store_true", help="default workload: skip the batched leg")
+    ap.add_argument("--no-235b", action="store_true", help="default workload: skip the two 235B-shaped legs")
     ap.add_argument("--path", choices=list(DECODE_PATHS), default="auto",
                     help="decode path of one-token stack calls")
     args = ap.parse_args()

@@ -115,12 +115,16 @@ void tg_prefetch(const void *addr, size_t len);
 /* csrc/libtinygiant.c:752 */
 void tg_prefetch_batch(const void **addrs, const size_t *lens, int count);
 /* csrc/libtinygiant.c:761.  Returns mlock()'s result on the 16 KiB-aligned
- * range, as the reference.  The range is also copied to HBM once (the
- * reference locks pinned experts' mmap views, cache.py:59-67, and the
- * attention weights, engine.py:134-139, all read-only from then on); the
- * legacy entry points then read any weight operand lying inside it from HBM
- * instead of copying it per call.  A range whose first or last 64 bytes
- * change is copied again per call; TG_MLOCK_MIRROR=0 disables the copies. */
+ * range, as the reference.  The range may also be copied to HBM once
+ * (tg_mirror_mode): by default when it lies wholly in mappings without write
+ * permission, as the reference cache's mmap views of the relayout files
+ * (cache.py:31-67); writable memory (the engine's attention weights,
+ * engine.py:134-139) only in TG_MIRROR_ALL.  The legacy entry points then
+ * read any weight operand lying inside a copied range from HBM instead of
+ * copying it per call.  Each use first compares the range's first and last
+ * 64 bytes and 16 words spread over it with what it held when locked (only
+ * the parts inside the caller's operand are read); a mismatch drops the copy
+ * and the call reads host memory. */
 int tg_mlock(const void *addr, size_t len);
 /* Release the HBM copies of every tg_mlock range overlapping
  * [addr, addr + len) (all of them for NULL), e.g. before unmapping or
@@ -131,6 +135,18 @@ void tg_mirror_drop(const void *addr, size_t len);
  * weight operands were read from them (hits) or copied (misses).  Any
  * pointer may be NULL.  No counterpart in the reference. */
 void tg_mirror_stats(size_t *bytes, int *ranges, uint64_t *hits, uint64_t *misses);
+/* Which tg_mlock ranges are copied to HBM from now on: TG_MIRROR_OFF (none:
+ * every legacy call reads host memory, as the reference), TG_MIRROR_READONLY
+ * (the default: ranges wholly in read-only mappings), TG_MIRROR_ALL (also
+ * writable memory; the caller promises that a locked range keeps its bytes
+ * until tg_mirror_drop).  The environment variable TG_MLOCK_MIRROR (0, all)
+ * sets the initial mode.  A negative mode only queries.  Returns the mode in
+ * force, or TG_E_INVALID.  Copies already made are kept.  No counterpart in
+ * the reference. */
+#define TG_MIRROR_OFF 0
+#define TG_MIRROR_READONLY 1
+#define TG_MIRROR_ALL 2
+int tg_mirror_mode(int mode);
 /* csrc/libtinygiant.c:662 */
 void tg_transformer_layer(
     const float *wq, const float *wk, const float *wv, const float *wo,
@@ -192,6 +208,11 @@ int tg_arena_load_norm(tg_arena *a, int layer, const float *host_norm,
 /* Read one layer back in the relayout layout (host memory). */
 int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes,
                         size_t nbytes);
+/* Read one expert of one layer back (gate | up | down, relayout layout,
+ * tg_arena_expert_bytes bytes).  Role: tinygiant/cache.py:154-160
+ * (ExpertCache.get: one expert's views). */
+int tg_arena_read_expert(tg_arena *a, int layer, int expert, void *host_bytes,
+                         size_t nbytes);
 /* Fill one layer (experts and router) with the synthetic workload on the
  * device: weights N(0, sigma) quantized to Q4_0, router N(0, sigma) fp32,
  * from SplitMix64 counters keyed by (seed, layer, expert, tensor). */
@@ -208,6 +229,9 @@ int tg_arena_synth_layer(tg_arena *a, int layer, uint64_t seed, float sigma);
 int tg_moe_layer_q40_dev(tg_arena *a, int layer, const float *x,
                          float *moe_out, int n_tokens, int32_t *topk_idx,
                          float *topk_w, float eps, void *stream);
+/* The same on host buffers (x, moe_out, topk_idx, topk_w), synchronous.
+ * Also returns TG_E_HIP when a device-side poll of its launch ran out of
+ * tries (those rows are NaN), as tg_arena_status would. */
 int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out,
                      int n_tokens, int32_t *topk_idx, float *topk_w,
                      float eps);
@@ -220,9 +244,12 @@ int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *moe_out,
  * fail with TG_E_INVALID (the message gives the largest n_tokens at the
  * arena's shape).  tg_gpu_init must have
  * run.  Every call on a GPU shares that GPU's array: calls that overlap on
- * one GPU (other streams, other threads) race.  A call whose shape or
- * n_tokens differs from the previous call's on that GPU first clears the
- * array's exchange words with a kernel on `stream`. */
+ * one GPU (other streams, other threads) race.  Every call of one shape
+ * uses the layout of the largest n_tokens that fits; each call first runs a
+ * one-block kernel on `stream` that clears the array's exchange words when
+ * the array last served another shape (the array's header records which, on
+ * the device, so replays of a captured call decide the same way).  A poll
+ * failure of these calls is reported by tg_arena_status on any arena. */
 int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float *x,
                                  float *moe_out, int n_tokens,
                                  int32_t *topk_idx, float *topk_w, float eps,
@@ -231,6 +258,7 @@ int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float *x,
  * decode path of one-token calls is chosen by tg_arena_set_decode_path. */
 int tg_moe_stack_q40_dev(tg_arena *a, float *x, int n_tokens, int layer0,
                          int n_layers, float eps, void *stream);
+/* (host buffer x, synchronous; returns what tg_arena_status then reports) */
 int tg_moe_stack_q40(tg_arena *a, float *x, int n_tokens, int layer0,
                      int n_layers, float eps);
 /* One token through layers layer0.. with the routing of every layer
@@ -280,9 +308,27 @@ int tg_arena_set_batch_path(tg_arena *a, int path);
  * Both give the same bytes. */
 int tg_arena_set_graphs(tg_arena *a, int on);
 /* Waits for the device and reports a device-side failure of an earlier
- * asynchronous call on this arena (a hand-off poll of the ROUTED or FUSED
- * launch that ran out of tries). */
+ * asynchronous call on this arena, or of a no-alloc call on this device (a
+ * hand-off poll of the ROUTED or FUSED launch that ran out of tries):
+ * TG_E_HIP.  The failure is reported once: reading it clears it, and the
+ * next calls run as before. */
 int tg_arena_status(tg_arena *a);
+/* Measurement, no counterpart in the reference: the shader clock (MHz)
+ * while every CU runs int8 MFMA chains (four 256-thread blocks per CU,
+ * `iters` rounds of four v_mfma_i32_16x16x32_i8 per wave), from each
+ * block's shader-cycle and 100 MHz real-time counters: median, min, max
+ * over the blocks (min / max may be NULL).  For the int8 peak at the clock
+ * the MFMA kernels actually run at. */
+int tg_clock_mfma_mhz(int iters, double *mhz_median, double *mhz_min,
+                      double *mhz_max);
+/* Test hook of the failure channel, no counterpart in the reference: the
+ * poll bound of the ROUTED and FUSED launches (spin_limit tries; 0 restores
+ * the normal bound) and one h line those launches leave unpublished
+ * (drop_line: a gate/up unit, or half unit on shapes that split units; -1
+ * none).  Every reader of that line then gives up after spin_limit tries,
+ * each kernel exits normally, the rows come back NaN and the failure is
+ * reported.  Not for production use. */
+int tg_debug_fault_inject(uint32_t spin_limit, int drop_line);
 
 /* ------------------------------------------------------------------ */
 /* building blocks (device pointers; used by the parity tests)          */

@@ -7,8 +7,16 @@
             (grouped int8-MFMA path)
   config 4  2048 tokens through one 30B layer (prefill: multi-tile work items
             of ~128 entries per expert)
+  config 4  the full prefill: 2048 tokens through all 48 layers on the grouped
+            path, compared with the oracle after every layer on every 8th
+            token (tokens do not interact in the MoE block, so the oracle's
+            stack over a subset of the tokens is the reference for them),
+            bit for bit and within 1e-3 at the end
   config 5  32 tokens through one Qwen3-235B-A22B layer (H=4096, I=1536) with
-            Zipf(1.1)-skewed routing (grouped path)
+            Zipf(1.1)-skewed routing (grouped path); and one token through
+            all 94 layers of the 235B stack with Zipf-skewed routers on the
+            default (routed) path, every layer's routing and the final x
+            against the oracle's stack, bit for bit and within 1e-3
 
 The experts are generated on the device (the generator is bit-identical to
 the host's) and read back for the oracle, which checks every token's routing
@@ -144,6 +152,106 @@ def test_config2_stack_48_layers(O, tglib, with_norm):
                                norms=[norms[l]] if with_norm else None)
         err = rel_err(got, x)
         gpu_note(f"  stack rel err {err:.2e}")
+        assert err <= 1e-3
+        assert np.array_equal(bits(got), bits(x)), f"max |diff| {np.max(np.abs(got - x)):.3e}"
+    finally:
+        a.close()
+
+
+def test_config4_prefill_stack_48_layers(O, tglib):
+    """2048 tokens through the 48-layer 30B stack (grouped int8-MFMA path,
+    one stack call per layer), checked after every layer against the
+    oracle's stack on every 8th token, bit for bit; 1e-3 at the end."""
+    gpu_note("config 4: 2048 tokens x 48 layers H=2048, grouped MFMA, oracle on every 8th token per layer")
+    from tinygiant_amd.arena import HBMExpertArena
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k, L, T = 2048, 768, 128, 8, 48, 2048
+    seed = 402
+    a = HBMExpertArena(L, E, H, I, k)
+    try:
+        for l in range(L):
+            a.synth_layer(l, seed)
+        a.set_batch_path(a.BATCH_GROUPED)
+        x0 = O.synth_normal(seed, O.stream_id(0, 0, 4), 1.0, T * H).reshape(T, H)
+        sample = np.arange(0, T, 8)
+        xs = x0[sample].copy()
+        xd = dev(x0)
+        blk = MoEBlock(a)
+        for l in range(L):
+            blk.step(xd, l, 1)
+            got = host(xd)[sample]
+            a.status()
+            router = O.synth_normal(seed, O.stream_id(l, 0, 3), 0.02, E * H).reshape(E, H)
+            xs, _ = O.moe_stack([a.read_layer(l)], [router], H, I, E, k, xs)
+            assert np.array_equal(bits(got), bits(xs)), \
+                f"layer {l}: {int(np.sum(bits(got) != bits(xs)))} values differ, max |diff| {np.max(np.abs(got - xs)):.3e}"
+            if l % 8 == 7:
+                gpu_note(f"  layer {l} bit-exact")
+        err = rel_err(got, xs)
+        gpu_note(f"  48 layers bit-exact on {sample.size} tokens, rel err {err:.2e}")
+        assert err <= 1e-3
+    finally:
+        a.close()
+
+
+def zipf_stack_routers(rng, L, E, H, beta=0.6):
+    """Per-layer routers N(0, 0.02) plus a per-expert bias along one shared
+    direction u (the construction of synth.zipf_skew, one u for the whole
+    stack), and the token shift c u."""
+    from tinygiant_amd.synth import zipf_router_bias
+    u = rng.standard_normal(H)
+    u /= np.linalg.norm(u)
+    c = 0.5 * np.sqrt(H)
+    rms = np.sqrt(1.0 + c * c / H)
+    bias = zipf_router_bias(E, beta * 0.02 * np.sqrt(H) / rms)
+    routers = []
+    for _ in range(L):
+        r = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        r += (bias[:, None] * (rms / c) * u[None, :]).astype(np.float32)
+        routers.append(r)
+    return routers, (c * u).astype(np.float32)
+
+
+def test_config5_decode_stack_94_layers_zipf(O, tglib):
+    """One token through all 94 layers of the 235B-shaped stack (127.7 GB of
+    experts generated on the device) with Zipf-skewed routers, on the default
+    routed path with the routing of every layer recorded.  The oracle runs
+    the same stack layer by layer on the experts the GPU selected, read back
+    one by one (an expert the oracle selects but the GPU did not would be
+    zero bytes and change its output)."""
+    gpu_note("config 5: one token x 94 layers H=4096 I=1536, Zipf routers, routed path")
+    from tinygiant_amd.arena import HBMExpertArena
+    from tinygiant_amd.moe import MoEBlock
+    from tinygiant_amd.synth import fit_zipf_exponent
+    H, I, E, k, L = 4096, 1536, 128, 8, 94
+    seed = 502
+    rng = np.random.default_rng(seed)
+    routers, shift = zipf_stack_routers(rng, L, E, H)
+    a = HBMExpertArena(L, E, H, I, k)
+    try:
+        for l in range(L):
+            a.synth_layer(l, seed)
+            a.load_router(l, routers[l])
+        x0 = (O.synth_normal(seed, O.stream_id(0, 0, 4), 1.0, H).reshape(1, H) + shift).astype(np.float32)
+        xd = dev(x0)
+        idx, w = MoEBlock(a).step_trace(xd)
+        got, gidx, gw = host(xd), host(idx).reshape(L, k), host(w).reshape(L, k)
+        a.status()
+        gpu_note(f"  routing over the stack: {len(np.unique(gidx))} distinct experts, "
+                 f"fitted exponent {fit_zipf_exponent(gidx, E):.2f}")
+        layer = np.zeros(a.layer_bytes, np.uint8)
+        eb = a.expert_bytes
+        x = x0.copy()
+        for l in range(L):
+            layer[:] = 0
+            for e in gidx[l]:
+                layer[e * eb:(e + 1) * eb] = a.read_expert(l, int(e))
+            x, tr = O.moe_stack([layer], [routers[l]], H, I, E, k, x)
+            assert np.array_equal(tr[0, 0], gidx[l]), f"layer {l}: routing {tr[0, 0]} vs {gidx[l]}"
+            if l % 16 == 15:
+                gpu_note(f"  oracle through layer {l}")
+        err = rel_err(got, x)
+        gpu_note(f"  94 layers: stack rel err {err:.2e}")
         assert err <= 1e-3
         assert np.array_equal(bits(got), bits(x)), f"max |diff| {np.max(np.abs(got - x)):.3e}"
     finally:

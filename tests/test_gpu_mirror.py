@@ -1,13 +1,16 @@
 """HBM residency of tg_mlock ranges for the reference's legacy entry points.
 
 The reference pins hot experts by calling tg_mlock on the mmap views of
-their gate / up / down tensors (tinygiant/cache.py:59-67) and pins the
+their gate / up / down tensors (tinygiant/cache.py:31-67) and pins the
 attention weights the same way (engine.py:134-139).  tg_mlock keeps that
-contract and also copies each range to HBM once; the legacy calls then read
-those operands from HBM.  Checked here: outputs stay bit-identical to the
-oracle, the operands are read from the copies (hit counters, no copy per
-call), a range rewritten after the lock is copied again per call, and
-copies of read-only mmap views of a layer file serve tg_moe_forward.
+contract and may also copy a range to HBM once; the legacy calls then read
+those operands from HBM.  By default only ranges in read-only mappings are
+copied (the reference's expert views); writable memory only in
+TG_MIRROR_ALL.  Checked here: outputs stay bit-identical to the oracle, the
+operands are read from the copies (hit counters, no copy per call), a range
+rewritten after the lock (its first bytes, or in bulk inside) is read from
+host memory again, writable memory is not copied by default, and copies of
+read-only mmap views of a layer file serve tg_moe_forward.
 """
 import ctypes
 import mmap
@@ -31,10 +34,17 @@ def lock(L, a):
     L.tg_mlock(ctypes.c_void_p(a.ctypes.data), ctypes.c_size_t(a.nbytes))  # mlock may be refused by RLIMIT_MEMLOCK
 
 
+MIRROR_OFF, MIRROR_READONLY, MIRROR_ALL = 0, 1, 2
+
+
 @pytest.fixture
 def L(tglib):
+    """The library with no copies held, in TG_MIRROR_ALL (the operands below
+    are writable numpy arrays); the default mode again afterwards."""
     tglib.tg_mirror_drop(None, 0)
+    assert tglib.tg_mirror_mode(MIRROR_ALL) == MIRROR_ALL
     yield tglib
+    tglib.tg_mirror_mode(MIRROR_READONLY)
     tglib.tg_mirror_drop(None, 0)
     assert stats(tglib)[:2] == (0, 0)
 
@@ -78,6 +88,75 @@ def test_rewritten_range_is_copied_again(O, L):
     assert (h1 - h0, m1 - m0, r1) == (2, 1, 2)  # the stale copy is dropped
 
 
+def test_interior_rewrite_is_seen(O, L):
+    """A locked buffer reloaded in place (its middle half rewritten): the
+    spread samples differ, the copy is dropped, the call reads host memory."""
+    gpu_note("tg_mlock, middle of a range rewritten, tg_expert_forward_mixed")
+    embed, inter = 512, 256
+    rng = np.random.default_rng(8)
+    gate, up, down = expert_operands(rng, embed, inter, 0)
+    for a in (gate, up, down):
+        lock(L, a)
+    n = up.nbytes
+    up[n // 4: 3 * n // 4] = expert_operands(rng, embed, inter, 0)[1][n // 4: 3 * n // 4]
+    _, _, h0, m0 = stats(L)
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out = np.zeros(embed, np.float32)
+    L.tg_expert_forward_mixed(ptr(gate), ptr(up), ptr(down), 0, ptr(x), ptr(out), ctypes.c_float(0.5), embed, inter)
+    assert_exact(out, O.expert_forward_mixed(gate, up, down, 0, x, np.zeros(embed, np.float32), 0.5, embed, inter),
+                 "expert after an interior rewrite")
+    _, r1, h1, m1 = stats(L)
+    assert (h1 - h0, m1 - m0, r1) == (2, 1, 2)
+
+
+def test_unsampled_rewrite_keeps_copy_in_mirror_all(O, L):
+    """The documented limit of TG_MIRROR_ALL: one byte rewritten away from the
+    hashed ends and the sampled words is not seen; the call reads the copy,
+    i.e. the bytes as locked."""
+    gpu_note("tg_mlock (TG_MIRROR_ALL), one unsampled byte rewritten")
+    embed, inter = 512, 256
+    rng = np.random.default_rng(9)
+    gate, up, down = expert_operands(rng, embed, inter, 0)
+    for a in (gate, up, down):
+        lock(L, a)
+    locked = up.copy()
+    n = up.nbytes
+    step = (n - 8) // 15
+    pos = step // 2 + 100  # between the first and second sampled words, past the hashed head
+    assert 64 <= pos and pos + 8 < step
+    up[pos] ^= 0x5A
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out = np.zeros(embed, np.float32)
+    _, _, h0, m0 = stats(L)
+    L.tg_expert_forward_mixed(ptr(gate), ptr(up), ptr(down), 0, ptr(x), ptr(out), ctypes.c_float(0.5), embed, inter)
+    assert_exact(out, O.expert_forward_mixed(gate, locked, down, 0, x, np.zeros(embed, np.float32), 0.5, embed,
+                                             inter), "expert from the copy")
+    _, _, h1, m1 = stats(L)
+    assert (h1 - h0, m1 - m0) == (3, 0)
+
+
+def test_writable_range_not_copied_by_default(O, L):
+    """Default mode: tg_mlock of writable memory copies nothing, so every
+    call reads host memory as the reference's does."""
+    gpu_note("tg_mlock of writable memory in the default mode")
+    assert L.tg_mirror_mode(MIRROR_READONLY) == MIRROR_READONLY
+    embed, inter = 512, 256
+    rng = np.random.default_rng(10)
+    gate, up, down = expert_operands(rng, embed, inter, 0)
+    for a in (gate, up, down):
+        lock(L, a)
+    assert stats(L)[:2] == (0, 0)
+    up[len(up) // 2] ^= 0x11  # read from host memory: seen
+    x = rng.normal(0.0, 1.0, embed).astype(np.float32)
+    out = np.zeros(embed, np.float32)
+    _, _, h0, m0 = stats(L)
+    L.tg_expert_forward_mixed(ptr(gate), ptr(up), ptr(down), 0, ptr(x), ptr(out), ctypes.c_float(0.5), embed, inter)
+    assert_exact(out, O.expert_forward_mixed(gate, up, down, 0, x, np.zeros(embed, np.float32), 0.5, embed, inter),
+                 "expert from host memory")
+    _, _, h1, m1 = stats(L)
+    assert (h1 - h0, m1 - m0) == (0, 3)
+
+
 def _moe_on_views(O, L, mm, parts, gb, eb, rng):
     embed, inter, n = 2048, 768, len(parts)
     views = [[np.frombuffer(mm, np.uint8, count=sz, offset=e * eb + off)
@@ -108,6 +187,7 @@ def test_moe_forward_on_mmap_views(O, L, tmp_path):
     f = tmp_path / "layer_000.q4.bin"
     np.concatenate([np.concatenate(p) for p in parts]).tofile(f)
     gb, eb = parts[0][0].nbytes, sum(a.nbytes for a in parts[0])
+    assert L.tg_mirror_mode(MIRROR_READONLY) == MIRROR_READONLY  # the default copies read-only views
     with open(f, "rb") as fd:
         mm = mmap.mmap(fd.fileno(), 0, access=mmap.ACCESS_READ)
         _moe_on_views(O, L, mm, parts, gb, eb, rng)

@@ -68,6 +68,7 @@ NEW_SYMBOLS = [
     ("tg_arena_load_router", CI, [VP, CI, VP, SZ]),
     ("tg_arena_load_norm", CI, [VP, CI, VP, SZ]),
     ("tg_arena_read_layer", CI, [VP, CI, VP, SZ]),
+    ("tg_arena_read_expert", CI, [VP, CI, CI, VP, SZ]),
     ("tg_arena_synth_layer", CI, [VP, CI, U64, CF]),
     ("tg_moe_layer_q40_dev", CI, [VP, CI, VP, VP, CI, VP, VP, CF, VP]),
     ("tg_moe_layer_q40", CI, [VP, CI, VP, VP, CI, VP, VP, CF]),
@@ -97,6 +98,9 @@ NEW_SYMBOLS = [
     ("tg_head_sample", CI, [VP, VP, CF, CF, CD, CD, VP, VP]),
     ("tg_mirror_drop", None, [VP, SZ]),
     ("tg_mirror_stats", None, [VP, VP, VP, VP]),
+    ("tg_mirror_mode", CI, [CI]),
+    ("tg_debug_fault_inject", CI, [ctypes.c_uint32, CI]),
+    ("tg_clock_mfma_mhz", CI, [CI, VP, VP, VP]),
 ]
 
 ALL_SYMBOLS = LEGACY_SYMBOLS + UNREGISTERED_SYMBOLS + NEW_SYMBOLS

@@ -120,6 +120,12 @@ class HBMExpertArena:
         call("tg_arena_read_layer", self.handle, layer, out.ctypes.data, out.size)
         return out
 
+    def read_expert(self, layer: int, expert: int) -> np.ndarray:
+        """One expert's gate | up | down bytes in the relayout layout."""
+        out = np.empty(self.expert_bytes, dtype=np.uint8)
+        call("tg_arena_read_expert", self.handle, layer, expert, out.ctypes.data, out.size)
+        return out
+
     def synth_layer(self, layer: int, seed: int, sigma: float = 0.02) -> None:
         """Fill a layer with the synthetic N(0, sigma) Q4_0 workload on the GPU."""
         call("tg_arena_synth_layer", self.handle, layer, int(seed), float(sigma))

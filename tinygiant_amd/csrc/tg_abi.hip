@@ -10,6 +10,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -426,6 +428,24 @@ extern "C" int tg_arena_read_layer(tg_arena *a, int layer, void *host_bytes, siz
     return TG_OK;
 }
 
+extern "C" int tg_arena_read_expert(tg_arena *a, int layer, int expert, void *host_bytes, size_t nbytes) {
+    int rc = arena_layer_check(a, layer);
+    if (rc) return rc;
+    const Shape &s = a->s;
+    if (expert < 0 || expert >= s.E) return set_err(TG_E_INVALID, "expert %d out of range 0..%d", expert, s.E - 1);
+    if (!host_bytes) return set_err(TG_E_INVALID, "host_bytes is NULL");
+    if (nbytes != s.EB) return set_err(TG_E_INVALID, "buffer has %zu bytes, expected %zu", nbytes, s.EB);
+    if ((rc = arena_staging(a))) return rc;
+    // gate, up and down are planar each: three tensors back to the relayout blocks
+    const uint8_t *src = a->experts + (size_t)layer * s.LB + (size_t)expert * s.EB;
+    const size_t gblk = (size_t)s.I * s.nbH, dblk = (size_t)s.H * s.nbI;
+    HIP_TRY(tg::launch_repack_tensor(src, a->staging, gblk, false, nullptr));
+    HIP_TRY(tg::launch_repack_tensor(src + s.GB, a->staging + s.GB, gblk, false, nullptr));
+    HIP_TRY(tg::launch_repack_tensor(src + 2 * s.GB, a->staging + 2 * s.GB, dblk, false, nullptr));
+    HIP_TRY(hipMemcpy(host_bytes, a->staging, nbytes, hipMemcpyDeviceToHost));
+    return TG_OK;
+}
+
 static const float *norm_of(const tg_arena *a, int layer) { return a->norms + (size_t)layer * a->s.H; }
 
 // The kernels use router * g (per column), recomputed from the router as
@@ -669,6 +689,8 @@ static int stack_run(tg_arena *a, float *x, int T, int l0, int n, float eps, hip
     return TG_OK;
 }
 
+extern "C" int tg_arena_status(tg_arena *a);
+
 static int check_tokens(int T) {
     if (T <= 0 || T > 65535) return set_err(TG_E_INVALID, "n_tokens must be in 1..65535 (got %d)", T);
     return TG_OK;
@@ -699,7 +721,7 @@ extern "C" int tg_moe_layer_q40(tg_arena *a, int layer, const float *x, float *m
     HIP_TRY(hipMemcpy(moe_out, a->obuf, nx * sizeof(float), hipMemcpyDeviceToHost));
     if (topk_idx) HIP_TRY(hipMemcpy(topk_idx, a->sc.idx, sizeof(int32_t) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
     if (topk_w) HIP_TRY(hipMemcpy(topk_w, a->sc.w, sizeof(float) * (size_t)n_tokens * s.k, hipMemcpyDeviceToHost));
-    return TG_OK;
+    return tg_arena_status(a);  // a poll that ran out of tries (its rows are NaN)
 }
 
 static int stack_check(tg_arena *a, int layer0, int n_layers, int T, const float *x) {
@@ -775,19 +797,27 @@ extern "C" int tg_arena_set_decode_path(tg_arena *a, int path) {
 // copy until the process ends), so the call allocates nothing.  In host code
 // the array's name is not a device address: each device's address comes
 // from hipGetSymbolAddress at set-up (tg_gpu_init, with that device
-// current) and only that address is used.  The array keeps the last call's
-// contents; the tagged exchange words and generations must start at zero
-// for a layout (shape, token count), so a call whose layout differs from the
-// previous call's on that device clears them first with a fill kernel on
-// its stream.  Calls that overlap on one device race.
+// current) and only that address is used.
+//
+// The array keeps the last call's contents.  It starts with a 256-byte
+// header: the layout key of the words behind it (8 bytes) and the error word
+// of the one-token launches (4 bytes).  Behind it every call of one shape
+// uses the same layout, the scratch of the largest token count that fits, so
+// calls with different token counts share their tagged exchange words and
+// generations.  Those must start at zero for a layout: each call first runs
+// a one-block kernel that compares the header's key with the call's shape
+// and, when they differ, clears the exchange words and stores the key.  The
+// decision is taken on the device, so it holds for calls replayed from a
+// captured graph as well as for direct ones.  Calls that overlap on one
+// device race.
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+constexpr size_t NOALLOC_HEADER = 256;
 constexpr int NOALLOC_MAX_DEV = 64;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 
 struct NoAllocDev {
     uint8_t *ptr = nullptr;  // this device's copy of `scratch`
-    uint64_t key = 0;        // layout of the last call (0: none since set-up)
-    size_t err_off = 0;      // its error word
+    bool used = false;       // a call has run on it since set-up
 };
 static std::mutex g_na_mu;
 static NoAllocDev g_na[NOALLOC_MAX_DEV];
@@ -802,14 +832,28 @@ static int noalloc_setup(int device) {
     if (e != hipSuccess || !p)
         return set_err(TG_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
     g_na[device].ptr = static_cast<uint8_t *>(p);
-    g_na[device].key = 0;
     return TG_OK;
 }
 
-static uint64_t noalloc_key(const Shape &s, int T) {
-    return (1ull << 63) | ((uint64_t)s.H << 46) | ((uint64_t)s.I << 32) | ((uint64_t)s.E << 24) |
-           ((uint64_t)s.k << 16) | (uint64_t)T;
+static uint64_t noalloc_key(const Shape &s) {
+    return (1ull << 63) | ((uint64_t)s.H << 40) | ((uint64_t)s.I << 20) | ((uint64_t)s.E << 8) | (uint64_t)s.k;
 }
+
+// The largest token count whose scratch fits behind the header (0: none).
+static int noalloc_tmax(const Shape &s) {
+    const size_t room = NOALLOC_SCRATCH_BYTES - NOALLOC_HEADER;
+    int lo = 0, hi = 65535;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (scratch_layout(s, mid, nullptr, nullptr) <= room)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+static uint32_t *noalloc_err(uint8_t *base) { return reinterpret_cast<uint32_t *>(base + 8); }
 
 extern "C" int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float *x, float *moe_out, int n_tokens,
                                             int32_t *topk_idx, float *topk_w, float eps, void *stream) {
@@ -826,27 +870,35 @@ extern "C" int tg_moe_layer_q40_noalloc_dev(tg_arena *a, int layer, const float 
     HIP_TRY(hipGetDevice(&cur));
     if (cur != dev) HIP_TRY(hipSetDevice(dev));
     if (!g_na[dev].ptr && (rc = noalloc_setup(dev))) return rc;
-    const size_t need = scratch_layout(a->s, n_tokens, nullptr, nullptr);
-    if (need > NOALLOC_SCRATCH_BYTES) {
-        int tmax = 0;
-        while (tmax < 65535 && scratch_layout(a->s, tmax + 1, nullptr, nullptr) <= NOALLOC_SCRATCH_BYTES) tmax++;
+    const int tmax = noalloc_tmax(a->s);
+    if (n_tokens > tmax)
         return set_err(TG_E_INVALID,
                        "no-alloc layer call: %d tokens need %zu bytes of scratch, above its %zu (at most %d tokens at "
                        "this shape)",
-                       n_tokens, need, NOALLOC_SCRATCH_BYTES, tmax);
-    }
+                       n_tokens, scratch_layout(a->s, n_tokens, nullptr, nullptr),
+                       NOALLOC_SCRATCH_BYTES - NOALLOC_HEADER, tmax);
     std::lock_guard<std::mutex> lk(g_na_mu);
     NoAllocDev &d = g_na[dev];
     Scratch c;
-    scratch_layout(a->s, n_tokens, d.ptr, &c);
+    scratch_layout(a->s, tmax, d.ptr + NOALLOC_HEADER, &c);
+    c.dec_err = noalloc_err(d.ptr);  // one error word per device, whatever the layout
     hipStream_t st = as_stream(stream);
-    const uint64_t key = noalloc_key(a->s, n_tokens);
-    if (d.key != key) {  // exchange words of another layout: back to zero (a kernel, not a memset node)
-        HIP_TRY(tg::launch_fill(reinterpret_cast<float *>(d.ptr), 0.0f, c.dec_bytes / 4, st));
-        d.key = key;
-        d.err_off = (size_t)(reinterpret_cast<uint8_t *>(c.dec_err) - d.ptr);
-    }
+    // exchange words of another shape: back to zero (a kernel, not a memset node)
+    HIP_TRY(tg::launch_keyed_clear(reinterpret_cast<uint64_t *>(d.ptr), noalloc_key(a->s),
+                                   reinterpret_cast<uint32_t *>(c.dec), c.dec_bytes / 4, st));
+    d.used = true;
     return moe_layer_launch(a, c, layer, x, moe_out, nullptr, n_tokens, topk_idx, topk_w, eps, st);
+}
+
+// Reads and clears one device-side error word (the first poll failure since
+// it was last read).
+static int take_err_word(uint32_t *word, uint32_t *v) {
+    HIP_TRY(hipMemcpy(v, word, sizeof *v, hipMemcpyDeviceToHost));
+    if (*v) {
+        const uint32_t zero = 0u;
+        HIP_TRY(hipMemcpy(word, &zero, sizeof zero, hipMemcpyHostToDevice));
+    }
+    return TG_OK;
 }
 
 extern "C" int tg_arena_status(tg_arena *a) {
@@ -854,16 +906,49 @@ extern "C" int tg_arena_status(tg_arena *a) {
     int rc = ensure_device();
     if (rc) return rc;
     HIP_TRY(hipDeviceSynchronize());
-    if (a->sc.dec_err) {
-        uint32_t v = 0;
-        HIP_TRY(hipMemcpy(&v, a->sc.dec_err, sizeof v, hipMemcpyDeviceToHost));
-        if (v != 0u) return set_err(TG_E_HIP, "decode routing: a device-side poll ran out of tries");
+    uint32_t v = 0, vn = 0;
+    if (a->sc.dec_err && (rc = take_err_word(a->sc.dec_err, &v))) return rc;
+    if (g_dev >= 0 && g_dev < NOALLOC_MAX_DEV && g_na[g_dev].used &&  // the no-alloc call's error word
+        (rc = take_err_word(noalloc_err(g_na[g_dev].ptr), &vn)))
+        return rc;
+    if (v) return set_err(TG_E_HIP, "decode launch: a device-side poll ran out of tries (code %u)", v);
+    if (vn) return set_err(TG_E_HIP, "no-alloc layer call: a device-side poll ran out of tries (code %u)", vn);
+    return TG_OK;
+}
+
+extern "C" int tg_clock_mfma_mhz(int iters, double *mhz_median, double *mhz_min, double *mhz_max) {
+    if (iters <= 0 || !mhz_median) return set_err(TG_E_INVALID, "tg_clock_mfma_mhz: iters %d, null output", iters);
+    int rc = ensure_device();
+    if (rc) return rc;
+    int dev = 0, n_cu = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    HIP_TRY(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    const int blocks = 4 * n_cu;
+    unsigned long long *d = nullptr;
+    if (hipMalloc(&d, sizeof(unsigned long long) * 4 * (size_t)blocks) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(TG_E_NOMEM, "tg_clock_mfma_mhz: stamps");
     }
-    if (g_dev >= 0 && g_dev < NOALLOC_MAX_DEV && g_na[g_dev].key) {  // the no-alloc call's error word
-        uint32_t v = 0;
-        HIP_TRY(hipMemcpy(&v, g_na[g_dev].ptr + g_na[g_dev].err_off, sizeof v, hipMemcpyDeviceToHost));
-        if (v != 0u) return set_err(TG_E_HIP, "no-alloc layer call: a device-side poll ran out of tries");
+    std::vector<unsigned long long> h(4 * (size_t)blocks);
+    hipError_t e = tg::launch_clock_mfma(d, blocks, iters, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(h.data(), d, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return set_err(TG_E_HIP, "tg_clock_mfma_mhz: %s", hipGetErrorString(e));
+    std::vector<double> mhz;
+    for (int b = 0; b < blocks; b++) {
+        const double cyc = (double)(h[4 * b + 2] - h[4 * b]), ticks = (double)(h[4 * b + 3] - h[4 * b + 1]);
+        if (ticks > 0) mhz.push_back(cyc / (ticks / 100.0));  // 100 MHz real-time counter
     }
+    if (mhz.empty()) return set_err(TG_E_HIP, "tg_clock_mfma_mhz: no elapsed real time");
+    std::sort(mhz.begin(), mhz.end());
+    *mhz_median = mhz[mhz.size() / 2];
+    if (mhz_min) *mhz_min = mhz.front();
+    if (mhz_max) *mhz_max = mhz.back();
+    return TG_OK;
+}
+
+extern "C" int tg_debug_fault_inject(uint32_t spin_limit, int drop_line) {
+    tg::set_fault_injection(spin_limit, drop_line);
     return TG_OK;
 }
 
@@ -1061,6 +1146,9 @@ struct LgCarve {
     }
 };
 
+static size_t g_lg_pin_off = 0;  // bounce bytes handed out since the last wait (pinned buffer below)
+static int lg_sync();
+
 static int lg_reserve(size_t bytes) {
     int rc = ensure_device();
     if (rc) return rc;
@@ -1075,6 +1163,10 @@ static int lg_reserve(size_t bytes) {
     }
     g_lg_dev = dev;
     if (!g_lg_st) HIP_TRY(hipStreamCreateWithFlags(&g_lg_st, hipStreamNonBlocking));
+    if (g_lg_pin_off) {  // a call that failed before its closing wait left bounce slots taken
+        int rc2 = lg_sync();
+        if (rc2) return rc2;
+    }
     if (bytes > g_lg_cap) {
         if (g_lg_buf) HIP_TRY(hipFree(g_lg_buf));
         g_lg_buf = nullptr;
@@ -1097,7 +1189,6 @@ static int lg_reserve(size_t bytes) {
 // leaves them taken until the next call that finishes, and copies that do
 // not fit go straight from pageable memory.  Kept until process exit.
 static uint8_t *g_lg_pin = nullptr;
-static size_t g_lg_pin_off = 0;
 constexpr size_t LG_PIN_BYTES = (size_t)1 << 20, LG_PIN_MAX = (size_t)256 << 10;
 
 static void *lg_pin_take(size_t n) {
@@ -1123,53 +1214,107 @@ static int lg_h2d(void *dst, const void *src, size_t n) {
     return TG_OK;
 }
 
+// Waits for the legacy stream; every bounce slot handed out before is free
+// again afterwards.
+static int lg_sync() {
+    HIP_TRY(hipStreamSynchronize(g_lg_st));
+    g_lg_pin_off = 0;  // every copy issued so far has completed
+    return TG_OK;
+}
+
 static int lg_finish(void *host_dst, const void *dev_src, size_t n) {
     void *p = n ? lg_pin_take(n) : nullptr;
     if (n) HIP_TRY(hipMemcpyAsync(p ? p : host_dst, dev_src, n, hipMemcpyDeviceToHost, g_lg_st));
-    HIP_TRY(hipStreamSynchronize(g_lg_st));
+    int rc = lg_sync();
+    if (rc) return rc;
     if (p) memcpy(host_dst, p, n);
-    g_lg_pin_off = 0;  // every copy of the call has completed
     return TG_OK;
 }
 
 // ------------------------------------------------------------- residency
 // The reference keeps its hot experts resident by locking their pages: the
-// cache calls tg_mlock on each pinned expert's gate / up / down views
-// (cache.py:59-67) and the engine on every attention weight
-// (engine.py:134-139).  Those ranges are read-only from then on (mmap views
-// of the relayout files, weights loaded once).  Here tg_mlock also copies
-// the range to HBM once, and every legacy entry point reads a weight operand
-// that lies inside such a range from that copy instead of sending it over
-// PCIe per call.  A copy is used only on the device it was made on, and only
-// while the range still starts and ends with the bytes it had when locked
-// (64 bytes at each end, hashed: an address reused for other data drops the
-// copy).  tg_mirror_drop releases copies; TG_MLOCK_MIRROR=0 turns the mirror
-// off.  All of it under g_lg_mu.
+// cache calls tg_mlock on each pinned expert's gate / up / down views, which
+// are read-only mmap views of the relayout files (cache.py:31-67), and the
+// engine locks every attention weight (engine.py:134-139).  Here tg_mlock
+// also copies a range to HBM once, and every legacy entry point reads a
+// weight operand that lies inside such a range from that copy instead of
+// sending it over PCIe per call.
+//
+// Which ranges are copied (tg_mirror_mode): by default only ranges that lie
+// wholly in mappings without write permission, such as the reference's
+// expert views.  Their bytes cannot be changed through this process's
+// mapping, so reading the copy gives what the reference's call reads.
+// Writable memory (the engine's attention weights: numpy arrays) is copied
+// only in mode TG_MIRROR_ALL, in which the caller promises that a locked
+// range keeps its bytes until tg_mirror_drop.
+//
+// Every use of a copy first compares the range with what it held when
+// locked: its first and last 64 bytes (hashed) and MIRROR_SAMPLES words
+// spread evenly over it, each read only where it lies inside the operand the
+// caller passed, so nothing outside [host, host + n) is read.  A mismatch
+// (an address reused for other data, a buffer reloaded in place) drops the
+// copy and the call reads host memory.  A rewrite that changes none of the
+// sampled bytes is not seen: that is the promise of TG_MIRROR_ALL.  A copy is
+// used only on the device it was made on.  All of it under g_lg_mu.
+constexpr int MIRROR_SAMPLES = 16;
 struct Mirror {
     size_t len;
     void *dev;
     int device;
-    uint64_t fp;
+    uint64_t head, tail;             // FNV-1a of the first / last min(64, len) bytes
+    uint64_t word[MIRROR_SAMPLES];   // 8 bytes at mirror_sample_at(len, i)
 };
 static std::map<uintptr_t, Mirror> g_mirror;
 static size_t g_mirror_bytes = 0;
 static uint64_t g_mirror_hits = 0, g_mirror_misses = 0;
+static int g_mirror_mode = -1;  // TG_MIRROR_*; -1: from TG_MLOCK_MIRROR at first use
 
-static uint64_t range_fp(const void *p, size_t n) {
-    const uint8_t *b = static_cast<const uint8_t *>(p);
-    uint64_t h = 1469598103934665603ull ^ n;  // FNV-1a over both ends
-    const size_t e = n < 64 ? n : 64;
-    for (size_t i = 0; i < e; i++) h = (h ^ b[i]) * 1099511628211ull;
-    for (size_t i = n - e; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
+static uint64_t fnv(const uint8_t *b, size_t n) {
+    uint64_t h = 1469598103934665603ull ^ n;
+    for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 1099511628211ull;
     return h;
 }
 
-static bool mirror_enabled() {
-    static const int on = [] {
+static size_t mirror_sample_at(size_t len, int i) {
+    return len < 8 ? 0 : (len - 8) / (MIRROR_SAMPLES - 1) * (size_t)i;
+}
+
+static uint64_t load8(const uint8_t *p) {
+    uint64_t v;
+    memcpy(&v, p, 8);
+    return v;
+}
+
+static int mirror_mode() {
+    if (g_mirror_mode < 0) {
         const char *e = getenv("TG_MLOCK_MIRROR");
-        return !(e && e[0] == '0');
-    }();
-    return on;
+        g_mirror_mode = !e ? TG_MIRROR_READONLY
+                        : e[0] == '0' ? TG_MIRROR_OFF
+                        : strcmp(e, "all") == 0 ? TG_MIRROR_ALL
+                                                : TG_MIRROR_READONLY;
+    }
+    return g_mirror_mode;
+}
+
+// Whether every page of [addr, addr + len) lies in a mapping of this process
+// without write permission (/proc/self/maps).
+static bool range_readonly(const void *addr, size_t len) {
+    FILE *f = fopen("/proc/self/maps", "r");
+    if (!f) return false;
+    uintptr_t cur = (uintptr_t)addr;
+    const uintptr_t end = cur + len;
+    char line[512];
+    while (cur < end && fgets(line, sizeof line, f)) {
+        unsigned long lo = 0, hi = 0;
+        char perm[8] = {0};
+        if (sscanf(line, "%lx-%lx %7s", &lo, &hi, perm) != 3) continue;
+        if (cur >= lo && cur < hi) {
+            if (perm[1] == 'w') break;
+            cur = hi;
+        }
+    }
+    fclose(f);
+    return cur >= end;
 }
 
 static void mirror_erase(std::map<uintptr_t, Mirror>::iterator it) {
@@ -1178,33 +1323,59 @@ static void mirror_erase(std::map<uintptr_t, Mirror>::iterator it) {
     g_mirror.erase(it);
 }
 
+// Whether the locked range starting at a still holds its bytes, judged from
+// the parts of it that lie in the caller's window [w0, w1).
+static bool mirror_intact(uintptr_t a, const Mirror &m, uintptr_t w0, uintptr_t w1) {
+    const size_t e = m.len < 64 ? m.len : 64;
+    if (w0 == a && w1 - w0 >= e && fnv(reinterpret_cast<const uint8_t *>(a), e) != m.head) return false;
+    if (w1 == a + m.len && w1 - w0 >= e && fnv(reinterpret_cast<const uint8_t *>(w1 - e), e) != m.tail) return false;
+    if (m.len < 8) return true;
+    for (int i = 0; i < MIRROR_SAMPLES; i++) {
+        const uintptr_t p = a + mirror_sample_at(m.len, i);
+        if (p >= w0 && p + 8 <= w1 && load8(reinterpret_cast<const uint8_t *>(p)) != m.word[i]) return false;
+    }
+    return true;
+}
+
 // The device copy of [host, host + n), or NULL.
 static const void *mirror_find(const void *host, size_t n) {
     if (g_mirror.empty() || !host) return nullptr;
     auto it = g_mirror.upper_bound((uintptr_t)host);
     if (it == g_mirror.begin()) return nullptr;
     --it;
-    const uintptr_t a = it->first;
+    const uintptr_t a = it->first, w0 = (uintptr_t)host, w1 = w0 + n;
     const Mirror &m = it->second;
-    if ((uintptr_t)host + n > a + m.len || m.device != g_lg_dev) return nullptr;
-    if (range_fp((const void *)a, m.len) != m.fp) {  // the range holds other data now
+    if (w1 > a + m.len || m.device != g_lg_dev) return nullptr;
+    if (!mirror_intact(a, m, w0, w1)) {  // the range holds other bytes now
         mirror_erase(it);
         return nullptr;
     }
-    return static_cast<const uint8_t *>(m.dev) + ((uintptr_t)host - a);
+    return static_cast<const uint8_t *>(m.dev) + (w0 - a);
 }
 
 static void mirror_add(const void *addr, size_t len) {
-    if (!addr || !len || !mirror_enabled()) return;
+    if (!addr || !len) return;
     std::lock_guard<std::mutex> lk(g_lg_mu);
+    const int mode = mirror_mode();
+    if (mode == TG_MIRROR_OFF || (mode == TG_MIRROR_READONLY && !range_readonly(addr, len))) return;
     const std::string err = g_err;  // best effort: the caller sees mlock's result only
-    if (lg_reserve(0) == TG_OK && !mirror_find(addr, len)) {
+    if (lg_reserve(0) == TG_OK) {
+        auto it = g_mirror.find((uintptr_t)addr);
+        if (it != g_mirror.end() && it->second.len >= len && it->second.device == g_lg_dev &&
+            mirror_intact(it->first, it->second, (uintptr_t)addr, (uintptr_t)addr + it->second.len)) {
+            g_err = err;
+            return;  // already copied
+        }
         void *d = nullptr;
         if (hipMalloc(&d, len) == hipSuccess) {
             if (hipMemcpy(d, addr, len, hipMemcpyHostToDevice) == hipSuccess) {
-                auto it = g_mirror.find((uintptr_t)addr);
-                if (it != g_mirror.end()) mirror_erase(it);  // a shorter copy of the same start
-                g_mirror[(uintptr_t)addr] = Mirror{len, d, g_lg_dev, range_fp(addr, len)};
+                if (it != g_mirror.end()) mirror_erase(it);  // an older copy of the same start
+                const uint8_t *b = static_cast<const uint8_t *>(addr);
+                const size_t e = len < 64 ? len : 64;
+                Mirror m{len, d, g_lg_dev, fnv(b, e), fnv(b + len - e, e), {}};
+                if (len >= 8)
+                    for (int i = 0; i < MIRROR_SAMPLES; i++) m.word[i] = load8(b + mirror_sample_at(len, i));
+                g_mirror[(uintptr_t)addr] = m;
                 g_mirror_bytes += len;
             } else {
                 (void)hipFree(d);
@@ -1213,6 +1384,15 @@ static void mirror_add(const void *addr, size_t len) {
         (void)hipGetLastError();
     }
     g_err = err;
+}
+
+extern "C" int tg_mirror_mode(int mode) {
+    std::lock_guard<std::mutex> lk(g_lg_mu);
+    if (mode < 0) return mirror_mode();
+    if (mode != TG_MIRROR_OFF && mode != TG_MIRROR_READONLY && mode != TG_MIRROR_ALL)
+        return set_err(TG_E_INVALID, "tg_mirror_mode: unknown mode %d", mode);
+    g_mirror_mode = mode;
+    return mode;
 }
 
 extern "C" void tg_mirror_drop(const void *addr, size_t len) {
@@ -2045,14 +2225,15 @@ static int sampler_run(tg_sampler *s, const float *dl, float temperature, double
     PROFILED("sample", st, tg::launch_sample_main(s->b, dl, s->vocab, temperature, top_p, u, st));
     HIP_TRY(hipMemcpyAsync(s->hctl, s->b.ctl, sizeof(tg::SmpCtl), hipMemcpyDeviceToHost, st));
     if (probs) HIP_TRY(hipMemcpyAsync(probs, s->b.q, sizeof(float) * (size_t)s->vocab, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    int rc = lg_sync();
+    if (rc) return rc;
     tg::SmpCtl c = *s->hctl;
     if (c.bad || c.status == tg::SMP_ST_INPUT)
         return set_err(TG_E_INVALID, "sample: the logits hold NaN or +inf, or every logit is -inf");
     if (c.large) {
         PROFILED("sample_large", st, tg::launch_sample_large(s->b, s->vocab, (int)c.C, top_p, u, st));
         HIP_TRY(hipMemcpyAsync(s->hctl, s->b.ctl, sizeof(tg::SmpCtl), hipMemcpyDeviceToHost, st));
-        HIP_TRY(hipStreamSynchronize(st));
+        if ((rc = lg_sync())) return rc;
         c = *s->hctl;
     }
     if (c.status != tg::SMP_ST_OK || c.token < 0 || c.token >= s->vocab)

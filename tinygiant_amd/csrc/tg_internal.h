@@ -86,6 +86,8 @@ constexpr int MAX_NB = 256;      // blocks per row (H, I <= 8192)
 hipError_t launch_scale_router(const float *raw, const float *g, float *router, int E, int H, hipStream_t st);
 // every one of the n floats at p set to v
 hipError_t launch_fill(float *p, float v, size_t n, hipStream_t st);
+// one block: if *keyp != key, the n words at p are set to zero, then *keyp = key
+hipError_t launch_keyed_clear(uint64_t *keyp, uint64_t key, uint32_t *p, size_t n, hipStream_t st);
 hipError_t launch_synth_layer(uint8_t *layer_pl, float *router, const Shape &s, int layer,
                               uint64_t seed, float sigma, hipStream_t st);
 hipError_t launch_synth_q40(uint8_t *pl, uint64_t key, float sigma, int rows, int nb, hipStream_t st);
@@ -244,6 +246,14 @@ hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_c
 hipError_t launch_down(const uint8_t *layer_pl, const Shape &s, int T, const int32_t *idx, const float *w,
                        const int8_t *hq, const float *hd, const int *hs, const float *resid, float *out,
                        hipStream_t st);
+
+// Failure-channel test hook: poll bound of the one-token expert launches
+// (0: the normal bound) and one h line they leave unpublished (-1: none).
+void set_fault_injection(uint32_t spin_limit, int drop_line);
+
+// shader clock under int8 MFMA load: out[4 * block] = s_memtime, s_memrealtime
+// (100 MHz) before, and both after, `iters` rounds of four MFMA chains
+hipError_t launch_clock_mfma(unsigned long long *out, int blocks, int iters, hipStream_t st);
 
 hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *sink, hipStream_t st);
 

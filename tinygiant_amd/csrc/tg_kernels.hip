@@ -124,6 +124,18 @@ __global__ __launch_bounds__(256) void k_fill(float *__restrict__ p, float v, si
     if (i < n) p[i] = v;
 }
 
+// One block: when *keyp differs from key, n words at p are cleared and then
+// *keyp = key.  Every thread reads the key before the barrier that precedes
+// its only store, so the block decides as one.
+__global__ __launch_bounds__(1024) void k_keyed_clear(uint64_t *keyp, uint64_t key, uint32_t *__restrict__ p,
+                                                      size_t n) {
+    const uint64_t cur = __hip_atomic_load(keyp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cur == key) return;
+    for (size_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(keyp, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ================================================================= repack
 // relayout 18-byte blocks <-> tensor-planar, one thread per block.
 TG_DEV void aos_to_planar_block(const uint8_t *src, uint8_t *qs_dst, uint16_t *d_dst) {
@@ -382,6 +394,11 @@ hipError_t launch_scale_router(const float *raw, const float *g, float *router, 
 hipError_t launch_fill(float *p, float v, size_t n, hipStream_t st) {
     if (n == 0) return hipSuccess;
     TG_LAUNCH(k_fill, dim3(cdiv(n, 256)), dim3(256), 0, st, p, v, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_keyed_clear(uint64_t *keyp, uint64_t key, uint32_t *p, size_t n, hipStream_t st) {
+    TG_LAUNCH(k_keyed_clear, dim3(1), dim3(1024), 0, st, keyp, key, p, n);
     return hipGetLastError();
 }
 

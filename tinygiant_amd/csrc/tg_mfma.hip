@@ -1030,6 +1030,43 @@ static bool x16_ok(const Shape &s, bool pair);
 
 // entries per work item of the MFMA path at mt M-tiles: the 16 x 16 kernels
 // take up to XT_CT * 16 (both of them must fit the shape)
+// Shader clock under int8 MFMA load: every wave of the grid runs `iters`
+// rounds of four independent v_mfma_i32_16x16x32_i8 chains and records
+// s_memtime (shader clock cycles) and s_memrealtime (a 100 MHz counter)
+// before and after them; lane 0 of each block's first wave stores the four
+// stamps at out[4 * block].
+__global__ __launch_bounds__(256) void k_clock_mfma(unsigned long long *out, int iters) {
+    const int tid = threadIdx.x;
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+    // operands depend on the stamp, so no MFMA can be placed before it
+    const long a = (long)(0x0102030405060708ull ^ (t0 >> 62)) + tid, b = (long)0x0807060504030201ll - tid;
+    v4i c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+    for (int i = 0; i < iters; i++) {
+        c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, a, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, a, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, b, c3, 0, 0, 0);
+    }
+    const int sink = c0.x + c1.y + c2.z + c3.w;
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid == 0) {
+        unsigned long long *o = out + 4 * (size_t)blockIdx.x;
+        o[0] = t0;
+        o[1] = r0;
+        o[2] = t1 + (sink == 0x7FFFFFFF ? 1u : 0u);  // keeps the chains
+        o[3] = r1;
+    }
+}
+
+hipError_t launch_clock_mfma(unsigned long long *out, int blocks, int iters, hipStream_t st) {
+    TG_LAUNCH(k_clock_mfma, dim3(blocks), dim3(256), 0, st, out, iters);
+    return hipGetLastError();
+}
+
 int mfma_item_entries(const Shape &s, int mt) {
     return mt == 4 && x16_ok(s, true) && x16_ok(s, false) ? XT_CT * 16 : 32 * mt;
 }

@@ -533,6 +533,20 @@ __host__ __device__ inline int round4(int n) { return (n + 3) & ~3; }
 constexpr uint32_t RD_SPIN_LIMIT = 1u << 20;
 constexpr int RD_THREADS = 1024;  // several threads per expert in the ranking
 
+// Failure-channel test hook (set_fault_injection): the poll bound of the
+// one-token expert launches (k_experts, k_layer_dec) and one h line whose
+// publication they leave out, so that every reader's bounded wait runs out
+// while each kernel still exits normally.  0 / -1 in normal use.
+static uint32_t g_fault_spin = 0;
+static int g_fault_drop = -1;
+
+static uint32_t fault_spin_limit() { return g_fault_spin ? g_fault_spin : RD_SPIN_LIMIT; }
+
+void set_fault_injection(uint32_t spin_limit, int drop_line) {
+    g_fault_spin = spin_limit;
+    g_fault_drop = drop_line < 0 ? -1 : drop_line;
+}
+
 TG_DEV uint32_t next_gen(uint32_t g) { return g >= 0x7FFFFFFFu ? 1u : g + 1u; }
 
 // Top-k of E ranked keys (LDS) by a block of RD_THREADS threads: rank =
@@ -905,6 +919,8 @@ struct FxArgs {
     const float *resid;
     float *out;
     int rd;               // down rows per block (grid = H / rd)
+    uint32_t spin;        // poll bound (fault_spin_limit())
+    int drop;             // h line left unpublished (-1 in normal use)
 };
 
 __host__ __device__ inline size_t fx_down_lds_bytes(int k, int I, int nbI, int rd) {
@@ -997,7 +1013,7 @@ TG_DEV void fx_gu_dots(const int8_t *gxq, const float *gxd, const int *gxs, cons
 // tagged words.  Wave 0 alone does this part (lane r chains row r: gate
 // rows in lanes 0..31, up rows in 32..63) and needs no block barrier, so it
 // never waits for the down loads the block has in flight.
-TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
+TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, const uint8_t *smem, int drop) {
     constexpr int RT = GU_ROWS;
     static_assert(2 * RT == 64, "one wave holds the gate and up rows of a unit");
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
@@ -1017,7 +1033,7 @@ TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, 
                               ((uint32_t)(__shfl(q, l4 + 3, WAVE) & 255) << 24);
         // lanes 0..7 the packed bytes, 8 the scale, 9 the sum: one store
         const uint32_t pay = tid < 8 ? word : (tid == 8 ? __float_as_uint(dq) : (uint32_t)qsum);
-        if (tid < FX_QW) ll_put(hw + (size_t)unit * FX_QS + tid, pay, tag);
+        if (tid < FX_QW && unit != drop) ll_put(hw + (size_t)unit * FX_QS + tid, pay, tag);
     }
 }
 
@@ -1027,7 +1043,7 @@ TG_DEV void fx_gu_publish(const Shape &s, int unit, uint32_t tag, uint64_t *hw, 
 // word that still carries an old tag.  Bounded (tries counts on); false
 // when a poll ran out of tries.
 template <int NW>
-TG_DEV bool fx_read_rest(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW], uint32_t &tries) {
+TG_DEV bool fx_read_rest(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW], uint32_t &tries, uint32_t lim) {
     constexpr int LAST = NW - 1;
     __asm__ volatile("" ::: "memory");  // the plain loads stay after the poll
     uint32_t pend = 0;
@@ -1052,7 +1068,7 @@ TG_DEV bool fx_read_rest(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW],
                 pend &= ~(1u << i);
             }
         if (!pend) break;
-        if (++tries >= RD_SPIN_LIMIT) return false;
+        if (++tries >= lim) return false;
         __builtin_amdgcn_s_sleep(2);
     }
     return true;
@@ -1062,26 +1078,26 @@ TG_DEV bool fx_read_rest(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW],
 // word with coherent loads until it carries `tag`, then the rest as above.
 // Bounded; false when a poll ran out of tries.
 template <int NW>
-TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW]) {
+TG_DEV bool fx_read_words(const uint64_t *src, uint32_t tag, uint32_t (&pay)[NW], uint32_t lim) {
     constexpr int LAST = NW - 1;
     uint32_t tries = 0;
 #pragma unroll
     for (int i = 0; i < NW; i++) pay[i] = 0u;
     uint64_t v = ll_get(src + LAST);
     while ((uint32_t)(v >> 32) != tag) {
-        if (++tries >= RD_SPIN_LIMIT) return false;
+        if (++tries >= lim) return false;
         __builtin_amdgcn_s_sleep(2);
         v = ll_get(src + LAST);
     }
     pay[LAST] = (uint32_t)v;
-    return fx_read_rest<NW>(src, tag, pay, tries);
+    return fx_read_rest<NW>(src, tag, pay, tries, lim);
 }
 
 // The two half-unit lines of one unit: both last words are polled in the
 // same rounds (one poll latency for the two lines), then each line's rest.
 template <int NW>
 TG_DEV bool fx_read_pair(const uint64_t *sa, const uint64_t *sb, uint32_t tag, uint32_t (&pa)[NW],
-                         uint32_t (&pb)[NW]) {
+                         uint32_t (&pb)[NW], uint32_t lim) {
     constexpr int LAST = NW - 1;
     uint32_t tries = 0;
 #pragma unroll
@@ -1091,19 +1107,19 @@ TG_DEV bool fx_read_pair(const uint64_t *sa, const uint64_t *sb, uint32_t tag, u
     }
     uint64_t va = ll_get(sa + LAST), vb = ll_get(sb + LAST);
     while ((uint32_t)(va >> 32) != tag || (uint32_t)(vb >> 32) != tag) {
-        if (++tries >= RD_SPIN_LIMIT) return false;
+        if (++tries >= lim) return false;
         __builtin_amdgcn_s_sleep(2);
         if ((uint32_t)(va >> 32) != tag) va = ll_get(sa + LAST);
         if ((uint32_t)(vb >> 32) != tag) vb = ll_get(sb + LAST);
     }
     pa[LAST] = (uint32_t)va;
     pb[LAST] = (uint32_t)vb;
-    return fx_read_rest<NW>(sa, tag, pa, tries) && fx_read_rest<NW>(sb, tag, pb, tries);
+    return fx_read_rest<NW>(sa, tag, pa, tries, lim) && fx_read_rest<NW>(sb, tag, pb, tries, lim);
 }
 
 
-TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW]) {
-    return fx_read_words<FX_QW>(src, tag, pay);
+TG_DEV bool fx_read_unit(const uint64_t *src, uint32_t tag, uint32_t (&pay)[FX_QW], uint32_t lim) {
+    return fx_read_words<FX_QW>(src, tag, pay, lim);
 }
 
 template <int UG, int UD>
@@ -1138,7 +1154,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     if (u0 < ng) {
         fx_gu_load<UG>(A.layer_pl, s, u0, sidx, g);
         fx_gu_dots<UG>(A.xq, A.xd, A.xs, s, g, smem);
-        fx_gu_publish(s, u0, tag, hw, smem);
+        fx_gu_publish(s, u0, tag, hw, smem, A.drop);
     }
     // 2. this block's down weights (waves 3.., item p on down thread
     //    p % FX_DT), then further gate/up units
@@ -1165,7 +1181,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
         fx_gu_load<UG>(A.layer_pl, s, unit, sidx, g);
         __syncthreads();  // wave 0 has read the previous unit's LDS
         fx_gu_dots<UG>(A.xq, A.xd, A.xs, s, g, smem);
-        fx_gu_publish(s, unit, tag, hw, smem);
+        fx_gu_publish(s, unit, tag, hw, smem, A.drop);
     }
 
     // 3. waves 0..2 read h of every unit into LDS; then the down rows
@@ -1177,7 +1193,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_experts(FxArgs A, Shape s) {
     if (tid < FX_PT) {
         for (int unit = tid; unit < ng; unit += FX_PT) {
             uint32_t pay[FX_QW];
-            const bool ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
+            const bool ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay, A.spin);
             const int jj = unit / nb, b = unit - jj * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
 #pragma unroll
@@ -1259,6 +1275,8 @@ struct LdArgs {
     float *w;
     float eps;
     int rd;                 // output rows per block (grid = H / rd)
+    uint32_t spin;          // poll bound (fault_spin_limit())
+    int drop;               // h line (unit, or half unit) left unpublished (-1 in normal use)
 };
 
 // generation `back` steps before g in next_gen's cycle 1 .. 2^31 - 1
@@ -1396,7 +1414,8 @@ TG_DEV void ld_hu_map(const Shape &s, int m, int side, int ubase, int lnbh, int 
 // 0..31, huB, if >= 0, in rows 32..63), SwiGLU of each half's 16 rows, and
 // the 16 h values of each half published as tagged words (lanes 0..15: huA,
 // 32..47: huB).  Readers form the Q8_0 block of a unit from its two halves.
-TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64_t *hw, const uint8_t *smem) {
+TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64_t *hw, const uint8_t *smem,
+                          int drop) {
     const int nb = s.nbH, ust = round4(nb) + 4, H = s.H, tid = threadIdx.x;
     const float *xd = reinterpret_cast<const float *>(smem + H);
     const float *U = xd + 2 * round4(nb);
@@ -1406,7 +1425,8 @@ TG_DEV void fx_hu_publish(const Shape &s, int huA, int huB, uint32_t tag, uint64
         const float gv = __shfl(a, ln, WAVE), uv = __shfl(a, (ln + HU_ROWS) & (WAVE - 1), WAVE);
         const int l = ln & 31, half = ln >> 5;
         const int hu = half ? huB : huA;
-        if (l < HU_ROWS && hu >= 0) ll_put(hw + (size_t)hu * HU_QS + l, __float_as_uint(silu_mul(gv, uv)), tag);
+        if (l < HU_ROWS && hu >= 0 && hu != drop)
+            ll_put(hw + (size_t)hu * HU_QS + l, __float_as_uint(silu_mul(gv, uv)), tag);
     }
 }
 
@@ -1679,7 +1699,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
                 ld_gu_dots<UH>(s, hmb, hgb, smem, HU_ROWS);
                 fx_consume<UH>(hgb);
             }
-            fx_hu_publish(s, u0, hu1 < nu ? hu1 : -1, tag, hw, smem);
+            fx_hu_publish(s, u0, hu1 < nu ? hu1 : -1, tag, hw, smem, A.drop);
         }
         // 2. further half units, one at a time
         for (int hu = u0 + 2 * NB; hu < nu; hu += NB) {
@@ -1689,12 +1709,12 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hm2, hga);
             ld_gu_dots<UH>(s, hm2, hga, smem, HU_ROWS);
             fx_consume<UH>(hga);
-            fx_hu_publish(s, hu, -1, tag, hw, smem);
+            fx_hu_publish(s, hu, -1, tag, hw, smem, A.drop);
         }
     } else {
         if (u0 < ng) {
             ld_gu_dots<UG>(s, gm, g, smem);
-            fx_gu_publish(s, u0, tag, hw, smem);
+            fx_gu_publish(s, u0, tag, hw, smem, A.drop);
         }
         if (DOWN_FIRST) down_loads();
         // 2. further gate/up units
@@ -1703,7 +1723,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             ld_gu_map<UG>(s, unit % mI, lnbh, usth, gm2);
             ld_gu_load<UG>(A.layer_pl + (size_t)sidx[unit / mI] * s.EB, gm2, g);
             ld_gu_dots<UG>(s, gm2, g, smem);
-            fx_gu_publish(s, unit, tag, hw, smem);
+            fx_gu_publish(s, unit, tag, hw, smem, A.drop);
         }
     }
     if (!DOWN_FIRST) {
@@ -1729,7 +1749,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             if constexpr (HU) {  // the unit's two halves, then its Q8_0 block here
                 uint32_t pa[HU_QS], pb[HU_QS];
                 ok = fx_read_pair<HU_QS>(hw + (size_t)(2 * unit) * HU_QS, hw + (size_t)(2 * unit + 1) * HU_QS, tag,
-                                         pa, pb);
+                                         pa, pb, A.spin);
                 float v[2 * HU_QS];
 #pragma unroll
                 for (int i = 0; i < HU_QS; i++) {
@@ -1745,7 +1765,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
                 pay[8] = __float_as_uint(dsc);
                 pay[9] = (uint32_t)qs;
             } else {
-                ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay);
+                ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay, A.spin);
             }
             const int jj = unit / nb, b = unit - jj * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
@@ -1779,7 +1799,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             const int unit = (int)__umul24((uint32_t)jj, (uint32_t)nb) + b;
             uint32_t tries = 0;
             while (__hip_atomic_load(uflag + unit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
-                if (++tries >= RD_SPIN_LIMIT) {
+                if (++tries >= A.spin) {
                     bad = 1;
                     break;
                 }
@@ -1853,7 +1873,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         uint64_t v = ll_get(src);
         uint32_t tries = 0;
         while ((uint32_t)(v >> 32) != tag) {
-            if (++tries >= RD_SPIN_LIMIT) {
+            if (++tries >= A.spin) {
                 bad = 1;
                 break;
             }
@@ -2557,7 +2577,8 @@ hipError_t launch_experts_fused(const uint8_t *layer_pl, const Shape &s, int n_c
                                 const int8_t *xq, const float *xd, const int *xs, uint64_t *hw, const uint32_t *ctl,
                                 uint32_t *err, const float *resid, float *out, hipStream_t st) {
     if (!experts_fused_ok(s, n_cu)) return hipErrorInvalidValue;
-    const FxArgs A{layer_pl, idx, w, xq, xd, xs, hw, ctl, err, resid, out, fx_rows(s, n_cu)};
+    const FxArgs A{layer_pl, idx, w, xq, xd, xs, hw, ctl, err, resid, out, fx_rows(s, n_cu), fault_spin_limit(),
+                   g_fault_drop};
     const int ug = (int)cdiv((size_t)2 * GU_ROWS * s.nbH, FX_THREADS);
     if (ug <= 1) return experts_ud<1, 6>(A, s, st);
     if (ug <= 2) return experts_ud<2, 6>(A, s, st);
@@ -2628,7 +2649,8 @@ hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, c
                             int32_t *idx, float *w, float eps, hipStream_t st) {
     if (!layer_dec_ok(s, n_cu)) return hipErrorInvalidValue;
     const int rd = ld_rows(s, n_cu);
-    const LdArgs A{layer_pl, x, gn, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd};
+    const LdArgs A{layer_pl, x, gn, part_in, wr_next, part_out, hw, ow, ctl, back, err, resid, out, idx, w, eps, rd,
+                   fault_spin_limit(), g_fault_drop};
     if (ld_shallow(s, rd)) return ld_go<4, 2, false>(A, s, st);
     // more units than blocks: half units, so every block carries the same
     // number (each half unit's items fit four loads per thread)
