@@ -1458,7 +1458,7 @@ TG_DEV void q8_block32(const float (&v)[32], uint32_t (&wq)[8], float &dscale, i
     qsum = sum;
 }
 
-template <int UG, int UD, bool HU>
+template <int UG, int UD, bool HU, bool XS>
 __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restrict__ part_in, int pe, int pg, LdArgs A,
                                                           Shape s) {
     float4 pv0[LD_PC];
@@ -1482,12 +1482,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     const int ng = (I / GU_ROWS) * k, NB = gridDim.x, mI = I / GU_ROWS;
     const int nu = HU ? 2 * ng : ng;  // work units: units, or half units
     const LdRole role = ld_role(blockIdx.x, NB, GQ);
-    const int r0 = role.chunk * RD;
+    // expert-sliced down (XS): block b dots slot jx = b % k over the rows
+    // [r0, r0 + k RD) (so it reads the h of one expert only) and publishes
+    // them; each group's owner combines the k slots of its RG rows.
+    // Otherwise block b takes its RD rows of every slot.
+    const int jx = XS ? (int)blockIdx.x % k : 0;
+    const int r0 = XS ? ((int)blockIdx.x / k) * (k * RD) : role.chunk * RD;
+    const int g0 = role.group * RG;
     const uint32_t tag =
         gen_back(__hip_atomic_load(const_cast<uint32_t *>(A.ctl) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                  A.back);
     uint64_t *hw = A.hw + (size_t)(tag & 1u) * ng * (HU ? 2 * HU_QS : FX_QS);
-    uint64_t *ow = A.ow + (size_t)(tag & 1u) * H;
+    uint64_t *ow = A.ow + (size_t)(tag & 1u) * (XS ? (size_t)k * H : (size_t)H);
     const bool nx = role.owner && A.wr_next;
 
     // 0. loads that depend on nothing: x and the norm weight (the threads
@@ -1513,11 +1519,15 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     const int dsl_off = (int)ld_lds_bytes(s, RD);
     const uint32_t *dsl = reinterpret_cast<const uint32_t *>(smem + dsl_off);
     float rv = 0.0f;
+    // the residual rows this block combines: its RD rows, or (XS) its group's
+    // RG rows when it owns the group
+    const int rrow = XS ? g0 : r0, rn = XS ? RG : RD;
+    const bool rown = !XS || role.owner;
     if constexpr (DOWN_FIRST) {
-        if (A.resid && tid < RD) rv = A.resid[r0 + tid];
+        if (A.resid && rown && tid < rn) rv = A.resid[rrow + tid];
     } else {
-        if (A.resid && tid < WAVE)  // wave 0; the wait before the unit loads retires it
-            lds_dma4(A.resid + r0 + min(tid, RD - 1), lds_addr(smem, dsl_off + 4 * UD * FX_THREADS));
+        if (A.resid && rown && tid < WAVE)  // wave 0; the wait before the unit loads retires it
+            lds_dma4(A.resid + rrow + min(tid, rn - 1), lds_addr(smem, dsl_off + 4 * UD * FX_THREADS));
     }
     float4 wn = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nx && tid < E * (RG / 4))
@@ -1564,7 +1574,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         for (int u = 0; u < UD; u++) {
             const int p = min(u * dthr + max(dt, 0), items - 1);
             const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int row = r0 + (rdi & (RD - 1));
+            const int row = XS ? r0 + rdi : r0 + (rdi & (RD - 1));
             doff[u] = (uint32_t)(2 * s.GB) + 16u * (uint32_t)(row * nb + b);
             dpk[u] = ((uint32_t)rdi << 16) | (uint32_t)b;
         }
@@ -1628,7 +1638,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             if constexpr (DOWN_FIRST) {
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
                     wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
                     const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
                     dv[u] = reinterpret_cast<const uint16_t *>(ex + 2 * s.GB + ntb * 16)[bi];
@@ -1639,14 +1649,14 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
                 // nibbles: a wait for any nibble load covers every scale
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
                     const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
                     lds_dma4(ex + 2 * s.GB + ntb * 16 + (size_t)(bi & ~1u) * 2,
                              lds_addr(smem, dsl_off + 4 * (u * FX_THREADS + (tid & ~(WAVE - 1)))));
                 }
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[(dpk[u] >> 16) >> lrd] * s.EB;
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
                     wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
                 }
             }
@@ -1743,7 +1753,9 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     // (half units: a unit's two lines are polled together; more polling
     // waves were slower, the coherent poll traffic grows with them)
     if (tid < FX_PT) {
-        for (int unit = tid; unit < ng; unit += FX_PT) {
+        const int nun = XS ? nb : ng;  // the units to read: slot jx's, or every unit
+        for (int uu = tid; uu < nun; uu += FX_PT) {
+            const int unit = XS ? jx * nb + uu : uu;
             uint32_t pay[FX_QW];
             bool ok;
             if constexpr (HU) {  // the unit's two halves, then its Q8_0 block here
@@ -1767,7 +1779,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             } else {
                 ok = fx_read_unit(hw + (size_t)unit * FX_QS, tag, pay, A.spin);
             }
-            const int jj = unit / nb, b = unit - jj * nb;
+            const int jj = XS ? 0 : unit / nb, b = unit - (XS ? jx : jj) * nb;
             uint32_t *dq = reinterpret_cast<uint32_t *>(hq + (size_t)jj * I + b * QK);
 #pragma unroll
             for (int wd = 0; wd < 8; wd++) dq[wd] = pay[wd];
@@ -1775,7 +1787,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             hs[jj * nbp + b] = (int)pay[9];
             if (!ok) bad = 1;
             // release: the copies above are in LDS before the flag is
-            __hip_atomic_store(uflag + unit, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(uflag + uu, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     }
     if (nx && tid < E * (RG / 4)) {
@@ -1795,7 +1807,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
 #pragma unroll
     for (int u = 0; u < UD; u++) {
         if (dt >= 0 && u * dthr + dt < items) {
-            const int rdi = (int)(dpk[u] >> 16), b = (int)(dpk[u] & 0xFFFFu), jj = rdi >> lrd;
+            const int rdi = (int)(dpk[u] >> 16), b = (int)(dpk[u] & 0xFFFFu), jj = XS ? 0 : rdi >> lrd;
             const int unit = (int)__umul24((uint32_t)jj, (uint32_t)nb) + b;
             uint32_t tries = 0;
             while (__hip_atomic_load(uflag + unit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
@@ -1818,10 +1830,56 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         }
     }
     lds_barrier();
+    if constexpr (XS) {
+        // the chains of the slice's k RD rows of slot jx, published for the
+        // owners of their groups
+        if (tid < k * RD) {
+            float dvl = chain4(U + tid * ust, hd, nb);
+            if (bad) dvl = __builtin_nanf("");
+            ll_put(ow + (size_t)jx * H + r0 + tid, __float_as_uint(dvl), tag);
+        }
+        if (!role.owner) {  // uniform
+            if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        // (owners) the k slots of the group's RG rows (over the unused
+        // slots of hq), combined in the reference's order, plus the
+        // residual
+        float *dsum = reinterpret_cast<float *>(hq + ((I + 15) & ~15));
+        if (tid < k * RG) {
+            const int jj = tid / RG, r = tid - jj * RG;
+            const uint64_t *src = ow + (size_t)jj * H + g0 + r;
+            uint64_t v = ll_get(src);
+            uint32_t tries = 0;
+            while ((uint32_t)(v >> 32) != tag) {
+                if (++tries >= A.spin) {
+                    bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                v = ll_get(src);
+            }
+            dsum[tid] = __uint_as_float((uint32_t)v);
+        }
+        __syncthreads();
+        if (tid < RG) {
+            const float acc = combine_slots(sw, dsum, RG, k, tid);
+            if constexpr (!DOWN_FIRST) rv = __uint_as_float(dsl[UD * FX_THREADS + tid]);
+            float o = A.resid ? rv + acc : acc;
+            if (bad) o = __builtin_nanf("");
+            A.out[g0 + tid] = o;
+            xo[tid] = o;
+        }
+        if (!nx) {  // uniform
+            if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
     // chains and combine: with k * RD <= 64 one wave holds every (slot, row)
     // chain and gathers a row's k slots by lane shuffles
     float o = 0.0f;
-    if (k * RD <= WAVE) {
+    if (XS) {
+    } else if (k * RD <= WAVE) {
         if (tid < WAVE) {
             const int t = tid < k * RD ? tid : 0;
             const float dvl = chain4(U + t * ust, hd + (t >> lrd) * nbp, nb);
@@ -1851,7 +1909,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
         }
     }
     // a non-owner publishes its rows to the group's owner
-    if (tid < RD) {
+    if (!XS && tid < RD) {
         if (bad) o = __builtin_nanf("");
         A.out[r0 + tid] = o;
         if (A.wr_next) {
@@ -1861,14 +1919,14 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
                 ll_put(ow + r0 + tid, __float_as_uint(o), tag);
         }
     }
-    if (!nx) {  // uniform
+    if (!XS && !nx) {  // uniform
         if (tid == 0 && bad) __hip_atomic_store(A.err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     // 4. (owners) the group's other rows, then the next layer's partials of
     //    the group from its RG rows
     const int gr0 = role.group * RG;
-    if (tid < RG - RD) {
+    if (!XS && tid < RG - RD) {
         const uint64_t *src = ow + gr0 + tid;
         uint64_t v = ll_get(src);
         uint32_t tries = 0;
@@ -2633,14 +2691,39 @@ hipError_t launch_dec_part(const float *Wr, const float *x, const Shape &s, floa
     return hipGetLastError();
 }
 
+template <int UG, int UD, bool HU, bool XS>
+static hipError_t ld_go_xs(const LdArgs &A, const Shape &s, hipStream_t st) {
+    const size_t lds = ld_launch_lds<UG, UD>(s, A.rd);
+    hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD, HU, XS>, lds);
+    if (e != hipSuccess) return e;
+    TG_LAUNCH((k_layer_dec<UG, UD, HU, XS>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG,
+              A, s);
+    return hipGetLastError();
+}
+
+// TG_LD_XS=0 keeps the down rows of every slot in each block (each block
+// then reads the h of every expert)
+static bool ld_xs_enabled() {
+    static const bool on = [] {
+        const char *v = getenv("TG_LD_XS");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+// The expert-sliced down: the grid splits into k slots of whole row slices
+// (k RD rows each), the slice's chains fit the block, an owner's k RG slot
+// values fit behind slot 0 of hq, every slot's units are polled in one pass.
+static bool ld_xs_ok(const Shape &s, int rd) {
+    const int nblk = s.H / rd;
+    return ld_xs_enabled() && nblk % s.k == 0 && s.k * rd <= FX_THREADS && s.k * RG <= FX_THREADS &&
+           (size_t)((s.I + 15) & ~15) + 4 * (size_t)s.k * RG <= (size_t)s.k * s.I && s.nbI <= FX_PT;
+}
+
 template <int UG, int UD, bool HU>
 static hipError_t ld_go(const LdArgs &A, const Shape &s, hipStream_t st) {
-    const size_t lds = ld_launch_lds<UG, UD>(s, A.rd);
-    hipError_t e = allow_lds((const void *)k_layer_dec<UG, UD, HU>, lds);
-    if (e != hipSuccess) return e;
-    TG_LAUNCH((k_layer_dec<UG, UD, HU>), dim3(s.H / A.rd), dim3(FX_THREADS), lds, st, A.part_in, s.E, s.H / RG, A,
-              s);
-    return hipGetLastError();
+    if (ld_xs_ok(s, A.rd)) return ld_go_xs<UG, UD, HU, true>(A, s, st);
+    return ld_go_xs<UG, UD, HU, false>(A, s, st);
 }
 
 hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, const float *x, const float *gn,
@@ -2660,7 +2743,7 @@ hipError_t launch_layer_dec(const uint8_t *layer_pl, const Shape &s, int n_cu, c
 }
 
 size_t dec_part_floats(const Shape &s) { return 2 * (size_t)(s.H / RG) * (s.E + 1); }
-size_t dec_ow_words(const Shape &s) { return 2 * (size_t)s.H; }
+size_t dec_ow_words(const Shape &s) { return 2 * (size_t)s.k * s.H; }  // [2][k][H] (expert-sliced down)
 
 bool grouped_shape_ok(const Shape &s) {
     return decode_shape_ok(s) && 64 * s.nbH <= 16 * 512 && 32 * s.nbI <= 16 * RO_THREADS &&
