@@ -367,6 +367,11 @@ constexpr int MS_NW = 4;    // waves per block
 constexpr int MS_PF = 2;    // weight chunks in flight per wave (down; gate/up one more)
 
 __host__ __device__ inline size_t ms_lds_bytes() { return 2 * 32 * (size_t)MF_TS + 2 * MF_KC * 32 * 4; }
+// Items whose K spans at most MS_FC chunks stage all of their activations
+// once, before the weight loop: [chunk][entry][256 bytes, 16-byte pieces
+// rotated by the entry] then [chunk][block][entry] activation scales.
+constexpr int MS_FC = 8;
+__host__ __device__ inline size_t ms_full_lds_bytes() { return (size_t)MS_FC * (32 * 256 + MF_KC * 32 * 4); }
 
 // one lane-half swap: lo takes half 0's value of v on every lane, hi half 1's
 // (lane i and lane i ^ 32 end with the same pair)
@@ -406,7 +411,7 @@ TG_DEV int half_sum(int v) {
     return v;
 }
 
-template <bool PAIR, bool SCV>
+template <bool PAIR, bool SCV, bool FULL>
 __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__restrict__ layer_pl, Shape s,
                                                            const int32_t *__restrict__ work,
                                                            const int32_t *__restrict__ work_n,
@@ -452,6 +457,43 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     const size_t ntb = (size_t)rows * nb;
     const uint4 *q0 = reinterpret_cast<const uint4 *>(tb) + (size_t)R * nb;
     const uint16_t *s0 = reinterpret_cast<const uint16_t *>(tb + ntb * 16) + (size_t)R * nb;
+
+    // (FULL) every chunk's activations and activation scales straight into
+    // LDS, issued before any weight load: the waits of the weight loop then
+    // count weight loads only.  Entries past the item stage the item's last
+    // entry's bytes (their sums are never stored).
+    constexpr int FA = M * 256, FD = MF_KC * M;  // bytes of one chunk's rows, scales of one chunk
+    if constexpr (FULL) {
+        constexpr int JA = M * 256 / (NT * 16), JD = FD / NT;  // DMA rounds per chunk: rows, scales
+        static_assert(JA * NT * 16 == M * 256 && JD * NT == FD, "staging map");
+        // this lane's entries (looked up once): its row slots' and its scale slots'
+        const int8_t *asrc[JA];
+        const float *dsrc[JD];
+#pragma unroll
+        for (int j = 0; j < JA; j++) {
+            const int L = (j * NW + wave) * 64 + lane;  // 16-byte slot of a chunk's rows
+            const int t = L >> 4, pc = ((L & 15) - t) & 15;
+            const int et = entries[o + min(t, c - 1)];
+            asrc[j] = aq + (size_t)(PAIR ? et / k : et) * K + pc * 16;
+        }
+#pragma unroll
+        for (int j = 0; j < JD; j++) {
+            const int L = (j * NW + wave) * 64 + lane;  // scale slot: block L / M, entry L % M
+            const int et = entries[o + min(L % M, c - 1)];
+            dsrc[j] = ad + (size_t)(PAIR ? et / k : et) * nb + L / M;
+        }
+#pragma unroll
+        for (int ch = 0; ch < MS_FC; ch++) {
+            if (ch < nch) {  // uniform
+#pragma unroll
+                for (int j = 0; j < JA; j++)
+                    lds_dma16(asrc[j] + ch * MF_KC * 32, lds_addr(smem, ch * FA + (j * NW + wave) * 1024));
+#pragma unroll
+                for (int j = 0; j < JD; j++)
+                    lds_dma4(dsrc[j] + ch * MF_KC, lds_addr(smem, MS_FC * FA + (ch * FD + (j * NW + wave) * 64) * 4));
+            }
+        }
+    }
 
     // activation staging: unconditional loads from clamped, in-bounds
     // addresses (entries past the item and blocks past K select zero when
@@ -516,10 +558,16 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     static_assert(MS_PF == 2, "three or four register sets");
     uint4 wa[4], sa, wb[4], sbv, wcx[4], scx, wdx[4], sdx;
     wload(0, wa, sa);
-    stage(0);
+    if constexpr (!FULL) stage(0);
     wload(1, wb, sbv);
     if constexpr (PF == 3) wload(2, wcx, scx);
-    commit(0, 0);
+    if constexpr (FULL) {
+        // this wave's staging landed (it was issued before the 5 PF weight
+        // loads in flight); the barrier below makes every wave's visible
+        __builtin_amdgcn_s_waitcnt(VMCNT0 | (5 * PF));
+    } else {
+        commit(0, 0);
+    }
     const v16i czero = {};  // the accumulator operand: an inline 0, no registers
     const int nsh = h ? 0 : 4;  // this half's nibble to the high half of each byte
     __syncthreads();
@@ -530,12 +578,16 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         // chunk ch from set w (scales sc); chunk ch + PF loads into set wl
         auto step = [&](int ch, uint4 (&w)[4], const uint4 &sc, uint4 (&wl)[4], uint4 &sl) {
             const int q = ch & 1;
-            stage(ch + 1);
-            __builtin_amdgcn_sched_barrier(0);  // activations issued before the weights
+            if constexpr (!FULL) {
+                stage(ch + 1);
+                __builtin_amdgcn_sched_barrier(0);  // activations issued before the weights
+            }
             wload(ch + PF, wl, sl);
             if (ch < nch) {  // uniform
-                const uint8_t *tq = tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
-                const float *xq = dxl + q * MF_KC * M + 4 * h;
+                const uint8_t *tq = FULL ? smem + ch * FA + n * 256
+                                         : tokl + (size_t)q * M * MF_TS + (size_t)n * MF_TS + 16 * h;
+                const float *xq = FULL ? reinterpret_cast<const float *>(smem + MS_FC * FA) + ch * FD + 4 * h
+                                       : dxl + q * MF_KC * M + 4 * h;
                 const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
                 for (int bl = 0; bl < MF_KC; bl++) {
@@ -559,8 +611,12 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                         wq.y = (int)(((blk.y << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
                         wq.z = (int)(((blk.z << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
                         wq.w = (int)(((blk.w << nsh) & 0xF0F0F0F0u) ^ 0x80808080u);
-                        const v4i ta = *reinterpret_cast<const v4i *>(tq + bl * 32);
-                        const float dw = h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1))));
+                        const v4i ta = FULL ? *reinterpret_cast<const v4i *>(tq + (((2 * bl + h + n) & 15) << 4))
+                                            : *reinterpret_cast<const v4i *>(tq + bl * 32);
+                        // (FULL: the staged scales are dx itself, so the 1/16 goes with dw;
+                        // both are exact: powers of two)
+                        const float dw = FULL ? h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1)))) * 0.0625f
+                                              : h2f((uint16_t)(scw[bl >> 1] >> (16 * (bl & 1))));
                         float4 dx[NG];
 #pragma unroll
                         for (int g = 0; g < NG; g++) dx[g] = *reinterpret_cast<const float4 *>(xq + bl * M + 8 * g);
@@ -582,8 +638,10 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
             }
             // unconditional (zeros past the last chunk), so the activation
             // loads stay ahead of the weight loads
-            commit(q ^ 1, ch + 1);
-            __syncthreads();
+            if constexpr (!FULL) {
+                commit(q ^ 1, ch + 1);
+                __syncthreads();
+            }
         };
         if constexpr (PF == 3) {
             for (int ch = 0; ch < nch; ch += 4) {
@@ -613,6 +671,7 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         // its sums of the other half.  Register groups past the item's
         // entries are skipped (uniform).
         float *x = reinterpret_cast<float *>(smem) + (size_t)(wave >> 1) * 16 * 64;
+        if constexpr (FULL) __syncthreads();  // every wave is done with the staged activations
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const bool give = r < 4 * ng && (mat == 0) == ((r & 2) != 0);  // uniform
@@ -1105,14 +1164,32 @@ static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
                         const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
                         float *D, hipStream_t st) {
     const int rows = PAIR ? s.I : s.H, nb = (PAIR ? s.H : s.I) / QK;
-    const size_t lds = ms_lds_bytes();
     const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (MS_NW / 2)) : mf_cdiv((size_t)rows, 32 * MS_NW);
+    // whole chunks, at most MS_FC of them: the activations staged once (TG_MS_FULL=0: per chunk)
+    static const bool full_on = [] {
+        const char *v = getenv("TG_MS_FULL");
+        return !(v && v[0] == '0');
+    }();
+    if (full_on && nb % MF_KC == 0 && nb <= MS_FC * MF_KC) {
+        const size_t lds = ms_full_lds_bytes();
+        static bool attr = false;
+        if (!attr) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_small<PAIR, true, true>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+        TG_LAUNCH((k_mfma_small<PAIR, true, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+                  work_n, entries, aq, ad, oq, od, os, D);
+        return hipGetLastError();
+    }
+    const size_t lds = ms_lds_bytes();
     // 16-byte scale loads need every row's scales 16-byte aligned (nb % 8 == 0)
     if (nb % MF_KC == 0)
-        TG_LAUNCH((k_mfma_small<PAIR, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+        TG_LAUNCH((k_mfma_small<PAIR, true, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
                            work_n, entries, aq, ad, oq, od, os, D);
     else
-        TG_LAUNCH((k_mfma_small<PAIR, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
+        TG_LAUNCH((k_mfma_small<PAIR, false, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
                            work_n, entries, aq, ad, oq, od, os, D);
     return hipGetLastError();
 }

@@ -1568,18 +1568,18 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     // in flight (measured faster than keeping the polling waves free).
     const int items = k * RD * nb;
     const int dthr = FX_THREADS, dt = tid;  // every thread; the polls wait for these loads, which thins them
-    uint32_t doff[UD], dpk[UD];
-    auto down_map = [&]() {
-#pragma unroll
-        for (int u = 0; u < UD; u++) {
-            const int p = min(u * dthr + max(dt, 0), items - 1);
-            const int rdi = (int)fdiv((uint32_t)p, s.divI), b = p - rdi * nb;
-            const int row = XS ? r0 + rdi : r0 + (rdi & (RD - 1));
-            doff[u] = (uint32_t)(2 * s.GB) + 16u * (uint32_t)(row * nb + b);
-            dpk[u] = ((uint32_t)rdi << 16) | (uint32_t)b;
-        }
+    // item u of this thread: (slot * RD + row) or (XS) the slice row, and the
+    // block; derived where used, so no register holds the map while the
+    // loads are in flight
+    auto dpos = [&](int u, int &rdi, int &b) {
+        const int p = min(u * dthr + max(dt, 0), items - 1);
+        rdi = (int)fdiv((uint32_t)p, s.divI);
+        b = p - rdi * nb;
     };
-    if (DOWN_FIRST) down_map();
+    auto doff_of = [&](int rdi, int b) -> uint32_t {
+        const int row = XS ? r0 + rdi : r0 + (rdi & (RD - 1));
+        return (uint32_t)(2 * s.GB) + 16u * (uint32_t)(row * nb + b);
+    };
     __syncthreads();
     const float sc = ssc;
     // keys (the experts beyond E rank below every logit)
@@ -1638,9 +1638,12 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             if constexpr (DOWN_FIRST) {
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
-                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
-                    const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
+                    int rdi, b;
+                    dpos(u, rdi, b);
+                    const uint32_t doff = doff_of(rdi, b);
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : rdi >> lrd] * s.EB;
+                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff);
+                    const uint32_t bi = (doff - (uint32_t)(2 * s.GB)) >> 4;
                     dv[u] = reinterpret_cast<const uint16_t *>(ex + 2 * s.GB + ntb * 16)[bi];
                 }
             } else {
@@ -1649,15 +1652,19 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
                 // nibbles: a wait for any nibble load covers every scale
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
-                    const uint32_t bi = (doff[u] - (uint32_t)(2 * s.GB)) >> 4;
+                    int rdi, b;
+                    dpos(u, rdi, b);
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : rdi >> lrd] * s.EB;
+                    const uint32_t bi = (doff_of(rdi, b) - (uint32_t)(2 * s.GB)) >> 4;
                     lds_dma4(ex + 2 * s.GB + ntb * 16 + (size_t)(bi & ~1u) * 2,
                              lds_addr(smem, dsl_off + 4 * (u * FX_THREADS + (tid & ~(WAVE - 1)))));
                 }
 #pragma unroll
                 for (int u = 0; u < UD; u++) {
-                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : (int)(dpk[u] >> 16) >> lrd] * s.EB;
-                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff[u]);
+                    int rdi, b;
+                    dpos(u, rdi, b);
+                    const uint8_t *ex = A.layer_pl + (size_t)sidx[XS ? jx : rdi >> lrd] * s.EB;
+                    wv[u] = *reinterpret_cast<const uint4 *>(ex + doff_of(rdi, b));
                 }
             }
         }
@@ -1736,10 +1743,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             fx_gu_publish(s, unit, tag, hw, smem, A.drop);
         }
     }
-    if (!DOWN_FIRST) {
-        down_map();
-        down_loads();
-    }
+    if (!DOWN_FIRST) down_loads();
 
     // 3. waves 0..2 read h of every unit into LDS (after the gate/up part,
     //    which wave 0 may still be reading); then the down rows
@@ -1807,7 +1811,9 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
 #pragma unroll
     for (int u = 0; u < UD; u++) {
         if (dt >= 0 && u * dthr + dt < items) {
-            const int rdi = (int)(dpk[u] >> 16), b = (int)(dpk[u] & 0xFFFFu), jj = XS ? 0 : rdi >> lrd;
+            int rdi, b;
+            dpos(u, rdi, b);
+            const int jj = XS ? 0 : rdi >> lrd;
             const int unit = (int)__umul24((uint32_t)jj, (uint32_t)nb) + b;
             uint32_t tries = 0;
             while (__hip_atomic_load(uflag + unit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0) {
