@@ -205,3 +205,38 @@ def test_mfma16_every_item_size(O, tglib):
         assert np.array_equal(bits(got), bits(ref)), f"max |diff| {np.max(np.abs(got - ref)):.3e}"
     finally:
         a.close()
+
+
+def test_fused_combine_counts_across_calls(O, tglib):
+    """With TG_FUSE_COMBINE=1 the one-tile and 16 x 16 down launches also
+    combine (off by default: measured slower than k_combine): each block counts
+    its entries in at (token, 128-row tile) in the arena's scratch, and the
+    block that brings a count to k folds that token's k rows over its tile
+    and sets the count back to zero.  Calls of different sizes on one arena
+    (one-tile items, two-tile items whose combine is a launch of its own,
+    16 x 16 items), each made twice, must equal the oracle bit for bit every
+    time: no call leaves a count behind for the next."""
+    import os
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k = 512, 256, 32, 8
+    a, layers, routers = make_arena(O, 1, H, I, E, k, seed=37)
+    old = os.environ.get("TG_FUSE_COMBINE")
+    os.environ["TG_FUSE_COMBINE"] = "1"  # the library reads it per call
+    try:
+        a.set_batch_path(a.BATCH_GROUPED)
+        blk = MoEBlock(a)
+        # entries per expert 10 (one tile), 250 (16 x 16), 24 (two tiles)
+        for i, T in enumerate((40, 1000, 96, 40, 1000)):
+            x = O.synth_normal(37, O.stream_id(0, i, 4), 1.0, T * H).reshape(T, H)
+            ref, _, _, _ = O.moe_layer(layers[0], routers[0], H, I, E, k, x)
+            xd = dev(x)
+            for rep in range(2):
+                gpu_note(f"fused combine H={H} T={T} call {i} rep {rep}")
+                got = host(blk.forward(0, xd))
+                assert np.array_equal(bits(got), bits(ref)), f"T={T} rep {rep}: max |diff| {np.max(np.abs(got - ref)):.3e}"
+    finally:
+        if old is None:
+            os.environ.pop("TG_FUSE_COMBINE", None)
+        else:
+            os.environ["TG_FUSE_COMBINE"] = old
+        a.close()

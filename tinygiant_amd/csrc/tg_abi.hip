@@ -199,6 +199,7 @@ struct Scratch {
     uint32_t *dec_err = nullptr;
     float *dec_part = nullptr;
     uint64_t *dec_ow = nullptr;
+    uint32_t *fc_cnt = nullptr;   // arrival counts of the combine in the down launch (zero between calls)
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
     // grouped (batched) path
@@ -236,6 +237,7 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     uint8_t *dec0 = take(dec_words_bytes(s, T));
     c.dec_part = reinterpret_cast<float *>(take(4 * tg::dec_part_floats(s)));
     c.dec_ow = reinterpret_cast<uint64_t *>(take(8 * tg::dec_ow_words(s)));
+    c.fc_cnt = reinterpret_cast<uint32_t *>(take(4 * tg::fuse_count_words(s, T)));
     c.dec = dec0;
     c.dec_bytes = off;
     c.dec_lw = reinterpret_cast<uint64_t *>(dec0);
@@ -555,10 +557,19 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
         PROFILED("gateup_mfma", st,
                  tg::launch_gateup_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.xq, c.xd, c.xs, c.hq,
                                         c.hd, c.hs, st));
+        // the combine inside the down launch where its kernel takes it
+        tg::FuseArgs F;
+        const bool fuse = tg::down_fuses(s, mt, T);
+        if (fuse) {
+            F.w = c.w;
+            F.resid = resid;
+            F.out = out;
+            F.cnt = c.fc_cnt;
+        }
         PROFILED("down_mfma", st,
-                 tg::launch_down_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.hq, c.hd, c.hs, c.D,
+                 tg::launch_down_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.hq, c.hd, c.hs, c.D, F,
                                       st));
-        PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
+        if (!fuse) PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
         return TG_OK;
     }
     PROFILED("group", st,

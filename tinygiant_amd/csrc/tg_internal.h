@@ -280,9 +280,23 @@ int mfma_item_entries(const Shape &s, int mt);
 hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                               const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
                               const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st);
+// The combine folded into the down launch: w [T][k] routing weights, resid
+// (may be null) and out [T][H], and cnt, one arrival count per (token, tile of
+// FC_ROWS output rows), zero between calls (the down launch leaves them zero).
+constexpr int FC_ROWS = 128;
+struct FuseArgs {
+    const float *w = nullptr;
+    const float *resid = nullptr;
+    float *out = nullptr;
+    uint32_t *cnt = nullptr;  // null: no combine in the down launch
+};
+inline size_t fuse_count_words(const Shape &s, int T) { return (size_t)T * (size_t)(s.H / FC_ROWS); }
+// The down launch at mt M-tiles combines too (FuseArgs honoured): its kernel
+// takes whole FC_ROWS-row tiles (H % FC_ROWS == 0) and TG_FUSE_COMBINE is 1.
+bool down_fuses(const Shape &s, int mt, int T);
 hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                             const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
-                            const int *hs, float *D, hipStream_t st);
+                            const int *hs, float *D, const FuseArgs &F, hipStream_t st);
 hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st);
 hipError_t launch_gateup_grouped(const uint8_t *layer_pl, const Shape &s, int n, const int32_t *work,

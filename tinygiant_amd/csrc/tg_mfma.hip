@@ -341,6 +341,89 @@ __global__ __launch_bounds__(NW * 64) void k_mfma_grouped(const uint8_t *__restr
     }
 }
 
+// ================================================================ combine in the down launch
+// The weighted combine of the grouped path (engine.py:240-258: out = x +
+// sum_j w_j down_j; the slots in order k-1 .. 0 from zero, then the
+// residual, as k_combine) inside the down launch.  A block stores its D rows
+// with device-coherent stores, waits until every one of them is
+// acknowledged, and then counts each of its entries in at (token, tile of
+// FC_ROWS rows).  The block whose count reaches k holds the last of that
+// token's k slots over its tile: it folds the k rows there (coherent loads)
+// and writes the output rows, and sets the count back to zero for the next
+// call.  No block waits for another, so the launch completes in any
+// dispatch order.
+TG_DEV void st_coh(float *p, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+TG_DEV void st_coh2(float *p, float a, float b) {  // p 8-byte aligned
+    const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+TG_DEV float ld_coh(const float *p) {
+    return __uint_as_float(__hip_atomic_load(const_cast<uint32_t *>(reinterpret_cast<const uint32_t *>(p)),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Every thread of the block calls it after its last D store; smem: at least
+// 4 (c + 1) bytes, free.  Tokens per pass: NT / FC_ROWS * FC_TOK.
+constexpr int FC_TOK = 4;   // tokens per thread per pass (k loads each in flight)
+template <int NT>
+TG_DEV void fused_combine(const FuseArgs &F, const Shape &s, const int32_t *__restrict__ entries, int o, int c,
+                          int tile, const float *D, uint8_t *smem) {
+    static_assert(NT % FC_ROWS == 0, "whole rows of tokens per pass");
+    constexpr int TP = NT / FC_ROWS;
+    int *ln = reinterpret_cast<int *>(smem), *ltok = ln + 1;
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // this thread's D stores acknowledged
+    __syncthreads();                     // ... every thread's; the LDS is free
+    const int tid = threadIdx.x, k = s.k, H = s.H, ntile = H / FC_ROWS;
+    if (tid == 0) *ln = 0;
+    __syncthreads();
+    for (int t = tid; t < c; t += NT) {
+        const int tok = entries[o + t] / k;
+        uint32_t *p = F.cnt + (size_t)tok * ntile + tile;
+        if (__hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(k - 1)) {
+            __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ltok[atomicAdd(ln, 1)] = tok;
+        }
+    }
+    __syncthreads();
+    const int nl = *ln, r = tid % FC_ROWS, q = tid / FC_ROWS, row = tile * FC_ROWS + r;
+    for (int b0 = 0; b0 < nl; b0 += TP * FC_TOK) {
+        int tok[FC_TOK];
+#pragma unroll
+        for (int i = 0; i < FC_TOK; i++) {
+            const int b = b0 + q + TP * i;
+            tok[i] = ltok[b < nl ? b : nl - 1];  // past the list: the last token again, not stored
+        }
+        float acc[FC_TOK];
+#pragma unroll
+        for (int i = 0; i < FC_TOK; i++) acc[i] = 0.0f;
+        for (int j0 = k - 1; j0 >= 0; j0 -= 8) {  // slots j0 .. j0 - 7, loads of every token in flight
+            float v[FC_TOK][8];
+#pragma unroll
+            for (int i = 0; i < FC_TOK; i++)
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int j = j0 - u >= 0 ? j0 - u : 0;
+                    v[i][u] = ld_coh(D + ((size_t)tok[i] * k + j) * H + row);
+                }
+#pragma unroll
+            for (int i = 0; i < FC_TOK; i++)
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (j0 - u >= 0) acc[i] = __builtin_fmaf(F.w[(size_t)tok[i] * k + j0 - u], v[i][u], acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < FC_TOK; i++) {
+            if (b0 + q + TP * i < nl) {
+                const size_t oi = (size_t)tok[i] * H + row;
+                F.out[oi] = F.resid ? F.resid[oi] + acc[i] : acc[i];
+            }
+        }
+    }
+}
+
 // ================================================================ one M-tile
 // Work items of at most 32 entries (batched decode, a few entries per expert):
 // the operands swap roles, A = the item's Q8_0 activations (lane h*32+m:
@@ -418,7 +501,7 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                                                            const int32_t *__restrict__ entries,
                                                            const int8_t *__restrict__ aq, const float *__restrict__ ad,
                                                            int8_t *__restrict__ oq, float *__restrict__ od,
-                                                           int *__restrict__ os, float *__restrict__ D) {
+                                                           int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
     constexpr int M = 32, NW = MS_NW, NT = NW * 64, TP = 2 * MF_KC;
     constexpr int NTP = M * TP / NT, NDX = M * MF_KC / NT;
     static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC == 8 && NTP >= 1 && NDX >= 1, "staging map");
@@ -701,12 +784,23 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                 }
             }
         }
-    } else if (valid) {
+    } else {
+        if (valid) {
+            const bool coh = F.cnt != nullptr;  // uniform
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int t = 8 * (r >> 2) + 4 * h + (r & 3);
-            if (t < c) D[(size_t)entries[o + t] * s.H + nt * 32 + n] = acc[r];
+            for (int r = 0; r < 16; r++) {
+                const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+                if (t < c) {
+                    float *dst = D + (size_t)entries[o + t] * s.H + nt * 32 + n;
+                    if (coh)
+                        st_coh(dst, acc[r]);
+                    else
+                        *dst = acc[r];
+                }
+            }
         }
+        // NW * 32 == FC_ROWS: block x covers output tile x
+        if (F.cnt) fused_combine<NT>(F, s, entries, o, c, (int)blockIdx.x, D, smem);
     }
 }
 
@@ -783,7 +877,7 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
                                                        const int32_t *__restrict__ entries,
                                                        const int8_t *__restrict__ aq, const float *__restrict__ ad,
                                                        int8_t *__restrict__ oq, float *__restrict__ od,
-                                                       int *__restrict__ os, float *__restrict__ D) {
+                                                       int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
     constexpr int NW = XT_NW, ROWS = XtLds::ROWS;
     constexpr int NACT = ROWS * XT_NP / 64;          // activation load instructions per chunk (full item)
     constexpr int NAXS = XT_KC * 16 * XT_CS / 64;    // activation-scale load instructions per chunk
@@ -1068,17 +1162,26 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
             }
         }
     } else {
+        const bool coh = F.cnt != nullptr;  // uniform
 #pragma unroll
         for (int ct = 0; ct < XT_CT; ct++) {
             const int t = ct * 16 + cl;
             if (t < c) {
                 float *dst = D + (size_t)entries[o + t] * s.H + rb + 4 * g;
 #pragma unroll
-                for (int rt = 0; rt < 2; rt++)
-                    *reinterpret_cast<float4 *>(dst + 16 * rt) =
-                        make_float4(acc[rt][ct][0], acc[rt][ct][1], acc[rt][ct][2], acc[rt][ct][3]);
+                for (int rt = 0; rt < 2; rt++) {
+                    if (coh) {
+                        st_coh2(dst + 16 * rt, acc[rt][ct][0], acc[rt][ct][1]);
+                        st_coh2(dst + 16 * rt + 2, acc[rt][ct][2], acc[rt][ct][3]);
+                    } else {
+                        *reinterpret_cast<float4 *>(dst + 16 * rt) =
+                            make_float4(acc[rt][ct][0], acc[rt][ct][1], acc[rt][ct][2], acc[rt][ct][3]);
+                    }
+                }
             }
         }
+        // NW * 32 == FC_ROWS: the block's rows are output tile bx
+        if (F.cnt) fused_combine<XT_NW * 64>(F, s, entries, o, c, bx, D, smem);
     }
 }
 
@@ -1162,7 +1265,8 @@ static hipError_t mf_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
 template <bool PAIR>
 static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work, const int32_t *work_n,
                         const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq, float *od, int *os,
-                        float *D, hipStream_t st) {
+                        float *D, const FuseArgs &F, hipStream_t st) {
+    static_assert(MS_NW * 32 == FC_ROWS && XT_NW * 32 == FC_ROWS, "one down block per output tile");
     const int rows = PAIR ? s.I : s.H, nb = (PAIR ? s.H : s.I) / QK;
     const unsigned gx = PAIR ? mf_cdiv((size_t)rows, 32 * (MS_NW / 2)) : mf_cdiv((size_t)rows, 32 * MS_NW);
     // whole chunks, at most MS_FC of them: the activations staged once (TG_MS_FULL=0: per chunk)
@@ -1180,17 +1284,17 @@ static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
             attr = true;
         }
         TG_LAUNCH((k_mfma_small<PAIR, true, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
-                  work_n, entries, aq, ad, oq, od, os, D);
+                  work_n, entries, aq, ad, oq, od, os, D, F);
         return hipGetLastError();
     }
     const size_t lds = ms_lds_bytes();
     // 16-byte scale loads need every row's scales 16-byte aligned (nb % 8 == 0)
     if (nb % MF_KC == 0)
         TG_LAUNCH((k_mfma_small<PAIR, true, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
-                           work_n, entries, aq, ad, oq, od, os, D);
+                           work_n, entries, aq, ad, oq, od, os, D, F);
     else
         TG_LAUNCH((k_mfma_small<PAIR, false, false>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
-                           work_n, entries, aq, ad, oq, od, os, D);
+                           work_n, entries, aq, ad, oq, od, os, D, F);
     return hipGetLastError();
 }
 
@@ -1207,7 +1311,7 @@ static bool x16_ok(const Shape &s, bool pair) {
 template <bool PAIR>
 static hipError_t x16_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
                          const int32_t *work_n, const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq,
-                         float *od, int *os, float *D, hipStream_t st) {
+                         float *od, int *os, float *D, const FuseArgs &F, hipStream_t st) {
     const unsigned gx = PAIR ? (unsigned)(s.I / (32 * (XT_NW / 2))) : (unsigned)(s.H / (32 * XT_NW));
     static bool attr = false;
     if (!attr && XtLds::BYTES > 65536) {
@@ -1219,7 +1323,7 @@ static hipError_t x16_go(const uint8_t *layer_pl, const Shape &s, int wmax, cons
     // one dimension: gx blocks for each of wmax items, wmax rounded up to 8
     const unsigned wm8 = (unsigned)((wmax + 7) / 8 * 8);
     TG_LAUNCH((k_mfma16<PAIR>), dim3(gx * wm8), dim3(XT_NW * 64), XtLds::BYTES, st, layer_pl, s, work, work_n,
-              entries, aq, ad, oq, od, os, D);
+              entries, aq, ad, oq, od, os, D, F);
     return hipGetLastError();
 }
 
@@ -1228,24 +1332,39 @@ hipError_t launch_gateup_mfma(const uint8_t *layer_pl, const Shape &s, int mt, i
                               const int *xs, int8_t *hq, float *hd, int *hs, hipStream_t st) {
     if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
     (void)xs;
-    if (mt == 1) return ms_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+    const FuseArgs none;
+    if (mt == 1) return ms_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, none, st);
     if (mt == 2) return mf_go<2, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
     if (mfma_item_entries(s, mt) > 128)
-        return x16_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+        return x16_go<true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, none, st);
     return mf_go<4, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, st);
+}
+
+// The kernels that can fold the combine in: the one-tile and the 16 x 16
+// down kernels (blocks of FC_ROWS output rows).  Off unless TG_FUSE_COMBINE
+// is 1 (read per call): the fold is bit-exact but measured slower than the
+// separate k_combine launch, since each down block then waits for its
+// stores, its arrival counts and its coherent loads in turn.
+bool down_fuses(const Shape &s, int mt, int T) {
+    const char *v = getenv("TG_FUSE_COMBINE");
+    const bool on = v && v[0] == '1';
+    const bool kern = mt == 1 || (mt == 4 && mfma_item_entries(s, mt) > 128);
+    return on && kern && s.H % FC_ROWS == 0 && (size_t)T * s.k * s.H < ((size_t)1 << 31);
 }
 
 hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                             const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
-                            const int *hs, float *D, hipStream_t st) {
+                            const int *hs, float *D, const FuseArgs &F, hipStream_t st) {
     if (!mfma_shape_ok(s)) return hipErrorInvalidValue;
     (void)hs;
     if (mt == 1) return ms_go<false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
-                                     D, st);
+                                     D, F, st);
+    if (mt == 4 && mfma_item_entries(s, mt) > 128)
+        return x16_go<false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, F,
+                             st);
+    if (F.cnt) return hipErrorInvalidValue;  // the kernels below leave the combine to k_combine
     if (mt == 2) return mf_go<2, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
                                         D, st);
-    if (mfma_item_entries(s, mt) > 128)
-        return x16_go<false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
     return mf_go<4, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
 }
 

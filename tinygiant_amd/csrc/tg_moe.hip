@@ -136,50 +136,54 @@ __global__ __launch_bounds__(1024) void k_route_small(const float *__restrict__ 
 }
 
 // Few tokens, first half of the routing: block (g, tile) forms, for the
-// RC_T tokens of its tile and every expert, the fma chain of group g (its 32
+// RCT tokens of its tile and every expert, the fma chain of group g (its 32
 // elements in order, from 0) and writes it to chains[g][t][e]; k_route_q8
 // adds a token's chains in ascending group order, so the logits are k_route's
-// bit for bit.  Every router and x element is read once (group g's columns
-// staged in LDS).  Thread (ti, ej): tokens 4 ti .. 4 ti + 3, experts
-// ej + 32 b (b < 4; E <= 128), so a wave's router reads are 32 consecutive
-// rows (conflict-free at the 9-float4 row stride) and its stores coalesce.
-constexpr int RC_T = 32;
+// bit for bit.  Every router and x element of a tile is read once (group g's
+// columns staged in LDS).  Thread (ti, ej): tokens RCT/8 ti .. + RCT/8 - 1,
+// experts ej + 32 b (b < 4; E <= 128), so a wave's router reads are 32
+// consecutive rows (conflict-free at the 9-float4 row stride) and its stores
+// coalesce.  Tiles of 16 tokens up to 64 tokens (256 blocks at H = 2048), of
+// 32 above.
 constexpr int RC_THREADS = 256;
 
 __host__ __device__ inline bool route_chains_ok(int E, int H) { return E <= 128 && E % 32 == 0 && H % RG == 0; }
 
+template <int RCT>
 __global__ __launch_bounds__(RC_THREADS) void k_route_chains(const float *__restrict__ Wr, const float *__restrict__ x,
                                                              int T, int E, int H, float *__restrict__ chains) {
     constexpr int Q = RG / 4, QS = Q + 1;  // float4 per group row, padded stride
-    __shared__ float4 xs[RC_T * QS];
+    constexpr int TPT = RCT / 8;           // tokens per thread
+    static_assert(RCT % 8 == 0 && RC_THREADS == 8 * 32, "thread map");
+    __shared__ float4 xs[RCT * QS];
     __shared__ float4 ws[128 * QS];
-    const int g = blockIdx.x, t0 = blockIdx.y * RC_T, tid = threadIdx.x;
-    {
-        const int r = tid / Q, q = tid % Q, t = t0 + r;  // RC_T * Q == RC_THREADS
+    const int g = blockIdx.x, t0 = blockIdx.y * RCT, tid = threadIdx.x;
+    for (int i = tid; i < RCT * Q; i += RC_THREADS) {
+        const int r = i / Q, q = i % Q, t = t0 + r;
         xs[r * QS + q] = t < T ? reinterpret_cast<const float4 *>(x + (size_t)t * H + (size_t)g * RG)[q]
                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int e = r + RC_T * v;
-            if (e < E) ws[e * QS + q] = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + (size_t)g * RG)[q];
-        }
+    for (int v = 0; v < 128 * Q / RC_THREADS; v++) {
+        const int i = v * RC_THREADS + tid, e = i / Q, q = i % Q;
+        if (e < E) ws[e * QS + q] = reinterpret_cast<const float4 *>(Wr + (size_t)e * H + (size_t)g * RG)[q];
     }
     __syncthreads();
     const int ti = tid >> 5, ej = tid & 31;
-    float acc[4][4];
+    float acc[TPT][4];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < TPT; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
 #pragma unroll
     for (int q = 0; q < Q; q++) {
-        float4 xv[4], wv[4];
+        float4 xv[TPT], wv[4];
 #pragma unroll
-        for (int a = 0; a < 4; a++) xv[a] = xs[(4 * ti + a) * QS + q];
+        for (int a = 0; a < TPT; a++) xv[a] = xs[(TPT * ti + a) * QS + q];
 #pragma unroll
         for (int b = 0; b < 4; b++) wv[b] = ws[min(ej + 32 * b, E - 1) * QS + q];
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < TPT; a++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 acc[a][b] = __builtin_fmaf(wv[b].x, xv[a].x, acc[a][b]);
@@ -189,8 +193,8 @@ __global__ __launch_bounds__(RC_THREADS) void k_route_chains(const float *__rest
             }
     }
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const int t = t0 + 4 * ti + a;
+    for (int a = 0; a < TPT; a++) {
+        const int t = t0 + TPT * ti + a;
         if (t < T)
 #pragma unroll
             for (int b = 0; b < 4; b++)
@@ -317,26 +321,41 @@ TG_DEV uint64_t rank_key(float l, int e) {
 constexpr int RO_THREADS = 256;
 constexpr int RO_MAXPASS = 4;  // H <= 4 * 8 * 256
 
-TG_DEV void route_token(const float *__restrict__ xt, const float *__restrict__ rawt, int E, int H, int k,
-                        float eps, float (&xv)[RO_MAXPASS][8], float *xf, float *gss, float *slog, uint64_t *keys,
-                        int *sidx, float *sred) {
-    const int tid = threadIdx.x, G = H / RG;
+// Token t's x into registers: thread tid holds elements ps * 2048 + 8 tid ..
+// + 7 of pass ps (zeros past H).
+TG_DEV void route_x_load(const float *__restrict__ xt, int H, float (&xv)[RO_MAXPASS][8]) {
+    const int tid = threadIdx.x;
 #pragma unroll
     for (int ps = 0; ps < RO_MAXPASS; ps++) {
-        int i0 = ps * RO_THREADS * 8 + tid * 8;
+        const int i0 = ps * RO_THREADS * 8 + tid * 8;
         if (i0 < H) {
-            float4 a = *reinterpret_cast<const float4 *>(xt + i0);
-            float4 b = *reinterpret_cast<const float4 *>(xt + i0 + 4);
+            const float4 a = *reinterpret_cast<const float4 *>(xt + i0);
+            const float4 b = *reinterpret_cast<const float4 *>(xt + i0 + 4);
             xv[ps][0] = a.x; xv[ps][1] = a.y; xv[ps][2] = a.z; xv[ps][3] = a.w;
             xv[ps][4] = b.x; xv[ps][5] = b.y; xv[ps][6] = b.z; xv[ps][7] = b.w;
-            *reinterpret_cast<float4 *>(xf + i0) = a;
-            *reinterpret_cast<float4 *>(xf + i0 + 4) = b;
         } else {
 #pragma unroll
             for (int c = 0; c < 8; c++) xv[ps][c] = 0.0f;
         }
     }
-    float r = tid < E ? rawt[tid] : 0.0f;
+}
+
+// xt null: x already in xv (route_x_load); rawt null: this thread's raw dot
+// already in r_in (thread e < E: expert e)
+TG_DEV void route_token(const float *__restrict__ xt, const float *__restrict__ rawt, int E, int H, int k,
+                        float eps, float (&xv)[RO_MAXPASS][8], float *xf, float *gss, float *slog, uint64_t *keys,
+                        int *sidx, float *sred, float r_in = 0.0f) {
+    const int tid = threadIdx.x, G = H / RG;
+    if (xt) route_x_load(xt, H, xv);
+#pragma unroll
+    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+        const int i0 = ps * RO_THREADS * 8 + tid * 8;
+        if (i0 < H) {
+            *reinterpret_cast<float4 *>(xf + i0) = make_float4(xv[ps][0], xv[ps][1], xv[ps][2], xv[ps][3]);
+            *reinterpret_cast<float4 *>(xf + i0 + 4) = make_float4(xv[ps][4], xv[ps][5], xv[ps][6], xv[ps][7]);
+        }
+    }
+    float r = rawt ? (tid < E ? rawt[tid] : 0.0f) : r_in;
     if (tid < k) sidx[tid] = 0;
     __syncthreads();
     if (tid < G) {
@@ -1677,12 +1696,17 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     LdGu<UH> hma, hmb;
     FxGu<UH> hga, hgb;
     const int hu1 = u0 + NB;
+    // (half units) odd blocks stream one half unit first and then two, even
+    // blocks two and then one: the loads of one set run while the other
+    // dots, so the fabric is not left idle while every block dots at once
+    // (with one order for all blocks the 235B launch took 1.5 us longer)
+    const bool one_first = HU && (blockIdx.x & 1) && u0 + 2 * NB < nu;
     if constexpr (HU) {
         if (u0 < nu) {  // nested like the dots below, so no path leaves a load unconsumed
             const int un = u0 >> 1;
             ld_hu_map<UH>(s, un % mI, u0 & 1, 0, lnbh, usth, hma);
             ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un / mI] * s.EB, hma, hga);
-            if (hu1 < nu) {
+            if (hu1 < nu && !one_first) {
                 const int un1 = hu1 >> 1;
                 ld_hu_map<UH>(s, un1 % mI, hu1 & 1, GU_ROWS, lnbh, usth, hmb);
                 ld_gu_load<UH>(A.layer_pl + (size_t)sidx[un1 / mI] * s.EB, hmb, hgb);
@@ -1709,7 +1733,22 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
     if (qon) q8_group8(xsv, true, qt * 8, xq, xd, xs);
 
     if constexpr (HU) {
-        if (u0 < nu) {  // uniform
+        if (one_first) {  // uniform: u0, then u0 + NB and u0 + 2 NB together
+            ld_gu_dots<UH>(s, hma, hga, smem, HU_ROWS);
+            fx_consume<UH>(hga);
+            fx_hu_publish(s, u0, -1, tag, hw, smem, A.drop);
+            const int hb = u0 + NB, hc = u0 + 2 * NB;
+            const int ub = hb >> 1, uc = hc >> 1;
+            ld_hu_map<UH>(s, ub % mI, hb & 1, 0, lnbh, usth, hma);
+            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[ub / mI] * s.EB, hma, hga);
+            ld_hu_map<UH>(s, uc % mI, hc & 1, GU_ROWS, lnbh, usth, hmb);
+            ld_gu_load<UH>(A.layer_pl + (size_t)sidx[uc / mI] * s.EB, hmb, hgb);
+            ld_gu_dots<UH>(s, hma, hga, smem, HU_ROWS);
+            fx_consume<UH>(hga);
+            ld_gu_dots<UH>(s, hmb, hgb, smem, HU_ROWS);
+            fx_consume<UH>(hgb);
+            fx_hu_publish(s, hb, hc, tag, hw, smem, A.drop);
+        } else if (u0 < nu) {  // uniform
             ld_gu_dots<UH>(s, hma, hga, smem, HU_ROWS);
             fx_consume<UH>(hga);
             if (hu1 < nu) {
@@ -1719,7 +1758,7 @@ __global__ __launch_bounds__(FX_THREADS) void k_layer_dec(const float *__restric
             fx_hu_publish(s, u0, hu1 < nu ? hu1 : -1, tag, hw, smem, A.drop);
         }
         // 2. further half units, one at a time
-        for (int hu = u0 + 2 * NB; hu < nu; hu += NB) {
+        for (int hu = u0 + (one_first ? 3 : 2) * NB; hu < nu; hu += NB) {
             LdGu<UH> hm2;
             const int un = hu >> 1;
             ld_hu_map<UH>(s, un % mI, hu & 1, 0, lnbh, usth, hm2);
@@ -2032,6 +2071,7 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 // raw: the router dots [T][E], or (chains != null) the group chains of
 // k_route_chains [G][T][E], which thread e adds in ascending group order
 // first (the same sums as k_route's).
+template <bool CHAINS>
 __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ chains,
                                                          int T, const float *__restrict__ x,
                                                          const float *__restrict__ gn, int E, int H, int k, float eps,
@@ -2043,18 +2083,22 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
     RouteLds L = route_lds(smem, H);
     const int t = blockIdx.x, tid = threadIdx.x, nbH = H / QK;
     const float *rawt = raw + (size_t)t * E;
-    if (chains) {  // uniform
+    float r0 = 0.0f;
+    if (!CHAINS && tid < E) r0 = rawt[tid];  // in flight with x
+    float xv[RO_MAXPASS][8];
+    route_x_load(x + (size_t)t * H, H, xv);  // in flight with the chain loads
+    if constexpr (CHAINS) {
         if (tid < E) {
             const int G = H / RG;
             const float *cp = chains + (size_t)t * E + tid;
             const size_t gs = (size_t)T * E;
             float tot = 0.0f;
-            for (int g0 = 0; g0 < G; g0 += 32) {  // 32 loads in flight, then the adds in order
-                float cv[32];
+            for (int g0 = 0; g0 < G; g0 += 64) {  // 64 loads in flight, then the adds in order
+                float cv[64];
 #pragma unroll
-                for (int u = 0; u < 32; u++) cv[u] = cp[(size_t)min(g0 + u, G - 1) * gs];
+                for (int u = 0; u < 64; u++) cv[u] = cp[(size_t)min(g0 + u, G - 1) * gs];
 #pragma unroll
-                for (int u = 0; u < 32; u++)
+                for (int u = 0; u < 64; u++)
                     if (g0 + u < G) tot = tot + cv[u];
             }
             rsum[tid] = tot;
@@ -2062,8 +2106,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
         __syncthreads();
         rawt = rsum;
     }
-    float xv[RO_MAXPASS][8];
-    route_token(x + (size_t)t * H, rawt, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred);
+    route_token(nullptr, CHAINS ? rawt : nullptr, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred, r0);
     if (tid == 0) {
         topk_softmax(L.slog, L.sidx, k, L.sw, L.sex);
         for (int i = 0; i < k; i++) {
@@ -2145,13 +2188,16 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
     }
     __syncthreads();
     // GR_PER entries per thread per pass, loaded together before the atomics
-    // (one load latency per pass rather than one per entry)
+    // (one load latency per pass rather than one per entry); the first
+    // pass's ids stay in registers for the entry lists below
+    int ev0[GR_PER];
     for (int base = 0; base < n; base += GR_THREADS * GR_PER) {
         int ev[GR_PER];
 #pragma unroll
         for (int u = 0; u < GR_PER; u++) {
             const int i = base + u * GR_THREADS + tid;
             ev[u] = i < n ? idx[i] : -1;
+            if (base == 0) ev0[u] = ev[u];
         }
 #pragma unroll
         for (int u = 0; u < GR_PER; u++) {
@@ -2254,7 +2300,7 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
 #pragma unroll
         for (int u = 0; u < GR_PER; u++) {
             const int i = base + u * GR_THREADS + tid;
-            ev[u] = i < n ? idx[i] : -1;
+            ev[u] = base == 0 ? ev0[u] : (i < n ? idx[i] : -1);
         }
 #pragma unroll
         for (int u = 0; u < GR_PER; u++) {
@@ -2760,10 +2806,14 @@ hipError_t launch_route_q8(const float *raw, const float *chains, const float *x
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
                            hipStream_t st) {
     const size_t lds = route_lds_bytes(H);
-    hipError_t e = allow_lds((const void *)k_route_q8, lds);
+    hipError_t e = chains ? allow_lds((const void *)k_route_q8<true>, lds) : allow_lds((const void *)k_route_q8<false>, lds);
     if (e != hipSuccess) return e;
-    TG_LAUNCH(k_route_q8, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd,
-              xs);
+    if (chains)
+        TG_LAUNCH(k_route_q8<true>, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w,
+                  xq, xd, xs);
+    else
+        TG_LAUNCH(k_route_q8<false>, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w,
+                  xq, xd, xs);
     return hipGetLastError();
 }
 
@@ -2771,7 +2821,12 @@ bool route_chains_usable(int T, int E, int H) { return T < 128 && route_chains_o
 
 hipError_t launch_route_chains(const float *Wr, const float *x, int T, int E, int H, float *chains, hipStream_t st) {
     if (!route_chains_usable(T, E, H)) return hipErrorInvalidValue;
-    TG_LAUNCH(k_route_chains, dim3(H / RG, cdiv((size_t)T, RC_T)), dim3(RC_THREADS), 0, st, Wr, x, T, E, H, chains);
+    if (T <= 64)
+        TG_LAUNCH(k_route_chains<16>, dim3(H / RG, cdiv((size_t)T, 16)), dim3(RC_THREADS), 0, st, Wr, x, T, E, H,
+                  chains);
+    else
+        TG_LAUNCH(k_route_chains<32>, dim3(H / RG, cdiv((size_t)T, 32)), dim3(RC_THREADS), 0, st, Wr, x, T, E, H,
+                  chains);
     return hipGetLastError();
 }
 
