@@ -40,8 +40,9 @@ def make_arena(O, n_layers, H, I, E, k, seed, routers=None):
     return a, layers, rs
 
 
+# router chains: 16-token tiles (T 17, 64), 32-token tiles with a partial last tile (T 100)
 @pytest.mark.parametrize("H,I,E,k,T", [(256, 64, 16, 4, 5), (256, 64, 16, 4, 33), (512, 96, 32, 8, 17),
-                                       (256, 352, 16, 4, 40), (2048, 768, 128, 8, 64)])
+                                       (256, 352, 16, 4, 40), (2048, 768, 128, 8, 64), (512, 96, 32, 8, 100)])
 def test_grouped_layer_matches_oracle(O, tglib, H, I, E, k, T):
     gpu_note(f"grouped layer H={H} I={I} E={E} k={k} T={T}")
     from tinygiant_amd.moe import MoEBlock

@@ -675,7 +675,12 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
 #pragma unroll
                 for (int bl = 0; bl < MF_KC; bl++) {
                     const int b = ch * MF_KC + bl;
-                    if (b < nb) {
+                    // SCV: nb % MF_KC == 0, so every block of a chunk below nch
+                    // exists; without the test the chunk is one basic block and
+                    // the scheduler overlaps one block's epilogue with the next
+                    // block's swaps and MFMA (the guard cost 16 register moves
+                    // per chunk and 2-3 us of gate/up)
+                    if (SCV || b < nb) {
                         // block bl sits in w[bl % 4] of the half bl / 4 lane: the swap
                         // at bl < 4 yields block bl and keeps block bl + 4 in w[bl]
                         uint4 blk;
