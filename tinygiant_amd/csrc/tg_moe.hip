@@ -1389,12 +1389,21 @@ TG_DEV void ld_gu_dots(const Shape &s, const LdGu<UG> &M, const FxGu<UG> &g, uin
     const int *xs = reinterpret_cast<const int *>(xq + H + 4 * round4(nbh));
     float *U = reinterpret_cast<float *>(smem + H + 8 * round4(nbh));
     lds_barrier();  // Q8_0 x in LDS; the previous unit's U read
+    if (items >= UG * FX_THREADS) {  // uniform: every item exists, so no branch per item (30B: +0.8%)
 #pragma unroll
-    for (int u = 0; u < UG; u++) {
-        if (u * FX_THREADS + tid < items) {
+        for (int u = 0; u < UG; u++) {
             const int cb = (int)(M.pk[u] & 255u), ui = (int)(M.pk[u] >> 8);
             const int S = dot_q4_q8(g.wv[u], reinterpret_cast<const int *>(xq + cb * QK)) - 8 * xs[cb];
             U[ui] = (float)S * h2f((uint16_t)at_use(g.dv[u]));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < UG; u++) {
+            if (u * FX_THREADS + tid < items) {
+                const int cb = (int)(M.pk[u] & 255u), ui = (int)(M.pk[u] >> 8);
+                const int S = dot_q4_q8(g.wv[u], reinterpret_cast<const int *>(xq + cb * QK)) - 8 * xs[cb];
+                U[ui] = (float)S * h2f((uint16_t)at_use(g.dv[u]));
+            }
         }
     }
     lds_barrier();
