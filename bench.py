@@ -441,7 +441,8 @@ def batched_leg(args, torch, call, arena, LR=16, K=256, W=16, T=64):
 
     arena.set_batch_path(arena.BATCH_GROUPED)
     stream = torch.cuda.current_stream().cuda_stream
-    X = torch.empty((W + K, T, H_), dtype=torch.float32, device="cuda")
+    # at least one input per layer: the calibration routes one step through every layer
+    X = torch.empty((max(W + K, LR), T, H_), dtype=torch.float32, device="cuda")
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
     X += torch.from_numpy((c * u).astype(np.float32)).cuda()
     torch.cuda.synchronize()
@@ -607,7 +608,7 @@ def leg_235b(args, torch, call, arena, T, K, W):
     L = arena.n_layers
     rng = np.random.default_rng(args.seed)
     stream = torch.cuda.current_stream().cuda_stream
-    X = torch.empty((W + K, T, H5), dtype=torch.float32, device="cuda")
+    X = torch.empty((max(W + K, 3), T, H5), dtype=torch.float32, device="cuda")  # the calibration routes X[1], X[2]
     call("tg_synth_normal_dev", args.seed, stream_id(0, 0, 4), 1.0, X.numel(), X.data_ptr(), stream)
     blk = MoEBlock(arena)
     routers, beta = None, None
