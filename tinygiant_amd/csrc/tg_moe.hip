@@ -372,9 +372,27 @@ TG_DEV void route_token(const float *__restrict__ xt, const float *__restrict__ 
         gss[tid] = a;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // in ascending group order; the values read 32 at a time, ahead of their adds
         float tot = 0.0f;
-        for (int g = 0; g < G; g++) tot = tot + gss[g];
+        if ((G & 3) == 0) {
+            const float4 *g4 = reinterpret_cast<const float4 *>(gss);
+            for (int q0 = 0; q0 < G / 4; q0 += 8) {
+                float4 v[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) v[q] = g4[min(q0 + q, G / 4 - 1)];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    if (q0 + q < G / 4) {
+                        tot = tot + v[q].x;
+                        tot = tot + v[q].y;
+                        tot = tot + v[q].z;
+                        tot = tot + v[q].w;
+                    }
+                }
+            }
+        } else {
+            for (int g = 0; g < G; g++) tot = tot + gss[g];
+        }
         sred[0] = rms_scale(tot, H, eps);
     }
     __syncthreads();
@@ -2116,11 +2134,12 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
         rawt = rsum;
     }
     route_token(nullptr, CHAINS ? rawt : nullptr, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred, r0);
-    if (tid == 0) {
-        topk_softmax(L.slog, L.sidx, k, L.sw, L.sex);
-        for (int i = 0; i < k; i++) {
-            idx[(size_t)t * k + i] = L.sidx[i];
-            w[(size_t)t * k + i] = L.sw[i];
+    if (tid < WAVE) {  // wave 0: lane i the weight of slot k - 1 - i (one exp and one division per lane)
+        const float wj = topk_softmax_lane(L.slog, L.sidx, k);
+        if (tid < k) {
+            const int j = k - 1 - tid;
+            idx[(size_t)t * k + j] = L.sidx[j];
+            w[(size_t)t * k + j] = wj;
         }
     }
     const float sc = L.sred[0];
