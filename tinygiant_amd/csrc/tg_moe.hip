@@ -323,10 +323,11 @@ constexpr int RO_MAXPASS = 4;  // H <= 4 * 8 * 256
 
 // Token t's x into registers: thread tid holds elements ps * 2048 + 8 tid ..
 // + 7 of pass ps (zeros past H).
-TG_DEV void route_x_load(const float *__restrict__ xt, int H, float (&xv)[RO_MAXPASS][8]) {
+template <int NP = RO_MAXPASS>
+TG_DEV void route_x_load(const float *__restrict__ xt, int H, float (&xv)[NP][8]) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+    for (int ps = 0; ps < NP; ps++) {
         const int i0 = ps * RO_THREADS * 8 + tid * 8;
         if (i0 < H) {
             const float4 a = *reinterpret_cast<const float4 *>(xt + i0);
@@ -342,13 +343,14 @@ TG_DEV void route_x_load(const float *__restrict__ xt, int H, float (&xv)[RO_MAX
 
 // xt null: x already in xv (route_x_load); rawt null: this thread's raw dot
 // already in r_in (thread e < E: expert e)
+template <int NP = RO_MAXPASS>
 TG_DEV void route_token(const float *__restrict__ xt, const float *__restrict__ rawt, int E, int H, int k,
-                        float eps, float (&xv)[RO_MAXPASS][8], float *xf, float *gss, float *slog, uint64_t *keys,
+                        float eps, float (&xv)[NP][8], float *xf, float *gss, float *slog, uint64_t *keys,
                         int *sidx, float *sred, float r_in = 0.0f) {
     const int tid = threadIdx.x, G = H / RG;
-    if (xt) route_x_load(xt, H, xv);
+    if (xt) route_x_load<NP>(xt, H, xv);
 #pragma unroll
-    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+    for (int ps = 0; ps < NP; ps++) {
         const int i0 = ps * RO_THREADS * 8 + tid * 8;
         if (i0 < H) {
             *reinterpret_cast<float4 *>(xf + i0) = make_float4(xv[ps][0], xv[ps][1], xv[ps][2], xv[ps][3]);
@@ -2098,7 +2100,7 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 // raw: the router dots [T][E], or (chains != null) the group chains of
 // k_route_chains [G][T][E], which thread e adds in ascending group order
 // first (the same sums as k_route's).
-template <bool CHAINS>
+template <bool CHAINS, int NP>
 __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict__ raw, const float *__restrict__ chains,
                                                          int T, const float *__restrict__ x,
                                                          const float *__restrict__ gn, int E, int H, int k, float eps,
@@ -2112,8 +2114,8 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
     const float *rawt = raw + (size_t)t * E;
     float r0 = 0.0f;
     if (!CHAINS && tid < E) r0 = rawt[tid];  // in flight with x
-    float xv[RO_MAXPASS][8];
-    route_x_load(x + (size_t)t * H, H, xv);  // in flight with the chain loads
+    float xv[NP][8];
+    route_x_load<NP>(x + (size_t)t * H, H, xv);  // in flight with the chain loads
     if constexpr (CHAINS) {
         if (tid < E) {
             const int G = H / RG;
@@ -2133,7 +2135,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
         __syncthreads();
         rawt = rsum;
     }
-    route_token(nullptr, CHAINS ? rawt : nullptr, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred, r0);
+    route_token<NP>(nullptr, CHAINS ? rawt : nullptr, E, H, k, eps, xv, L.xf, L.gss, L.slog, L.keys, L.sidx, L.sred, r0);
     if (tid < WAVE) {  // wave 0: lane i the weight of slot k - 1 - i (one exp and one division per lane)
         const float wj = topk_softmax_lane(L.slog, L.sidx, k);
         if (tid < k) {
@@ -2144,7 +2146,7 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
     }
     const float sc = L.sred[0];
 #pragma unroll
-    for (int ps = 0; ps < RO_MAXPASS; ps++) {
+    for (int ps = 0; ps < NP; ps++) {
         const int i0 = ps * RO_THREADS * 8 + tid * 8;
         if (ps * RO_THREADS * 8 < H) {
             float v[8];
@@ -2833,16 +2835,24 @@ bool grouped_shape_ok(const Shape &s) {
 hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
                            hipStream_t st) {
-    const size_t lds = route_lds_bytes(H);
-    hipError_t e = chains ? allow_lds((const void *)k_route_q8<true>, lds) : allow_lds((const void *)k_route_q8<false>, lds);
-    if (e != hipSuccess) return e;
-    if (chains)
-        TG_LAUNCH(k_route_q8<true>, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w,
-                  xq, xd, xs);
-    else
-        TG_LAUNCH(k_route_q8<false>, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w,
-                  xq, xd, xs);
-    return hipGetLastError();
+    // x in registers: NP passes of 8 x 256 elements.  The raw-dot form (many
+    // tokens, one block each) takes as few passes as H needs, so its blocks
+    // need fewer registers and more of them are resident (H 2048: 52 VGPRs,
+    // 8 waves per SIMD, 11.7 -> 10.8 us at 2048 tokens); the chains form keeps
+    // four (the two-pass build measured slower at H 4096, 9.4 -> 12.8 us)
+    const int np = (H + RO_THREADS * 8 - 1) / (RO_THREADS * 8);
+    if (np > RO_MAXPASS) return hipErrorInvalidValue;
+    auto go = [&](auto kern) -> hipError_t {
+        const size_t lds = route_lds_bytes(H);
+        hipError_t e = allow_lds((const void *)kern, lds);
+        if (e != hipSuccess) return e;
+        TG_LAUNCH(kern, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd, xs);
+        return hipGetLastError();
+    };
+    if (chains) return go(k_route_q8<true, RO_MAXPASS>);
+    if (np == 1) return go(k_route_q8<false, 1>);
+    if (np == 2) return go(k_route_q8<false, 2>);
+    return go(k_route_q8<false, RO_MAXPASS>);
 }
 
 bool route_chains_usable(int T, int E, int H) { return T < 128 && route_chains_ok(E, H); }
