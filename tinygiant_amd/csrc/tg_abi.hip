@@ -200,6 +200,8 @@ struct Scratch {
     float *dec_part = nullptr;
     uint64_t *dec_ow = nullptr;
     uint32_t *fc_cnt = nullptr;   // arrival counts of the combine in the down launch (zero between calls)
+    int32_t *ecnt = nullptr;      // E: entries placed per expert by route_q8 (zero between calls)
+    int32_t *ent_cap = nullptr;   // E * T: per-expert entry lists of capacity T (chains path: over raw, unused there)
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
     // grouped (batched) path
@@ -238,6 +240,7 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     c.dec_part = reinterpret_cast<float *>(take(4 * tg::dec_part_floats(s)));
     c.dec_ow = reinterpret_cast<uint64_t *>(take(8 * tg::dec_ow_words(s)));
     c.fc_cnt = reinterpret_cast<uint32_t *>(take(4 * tg::fuse_count_words(s, T)));
+    c.ecnt = reinterpret_cast<int32_t *>(take(4 * (size_t)s.E));
     c.dec = dec0;
     c.dec_bytes = off;
     c.dec_lw = reinterpret_cast<uint64_t *>(dec0);
@@ -253,6 +256,7 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     c.counts = reinterpret_cast<int32_t *>(take(4 * (size_t)s.E));
     c.offsets = reinterpret_cast<int32_t *>(take(4 * ((size_t)s.E + 1)));
     c.entries = reinterpret_cast<int32_t *>(take(4 * n));
+    c.ent_cap = reinterpret_cast<int32_t *>(c.raw);  // T * E words, like the router dots the chains path leaves unused
     c.hq = reinterpret_cast<int8_t *>(take(n * s.I));
     c.hd = reinterpret_cast<float *>(take(4 * n * s.nbI));
     c.hs = reinterpret_cast<int *>(take(4 * n * s.nbI));
@@ -545,18 +549,29 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
         PROFILED("route", st, tg::launch_route_chains(router_of(a, layer), x, T, s.E, s.H, c.D, st));
     else
         PROFILED("route", st, tg::launch_route(router_of(a, layer), x, T, s.E, s.H, c.raw, st));
+    // MFMA path with few tokens: route_q8 also places each entry in its
+    // expert's list (capacity T), so the grouping kernel only builds the work
+    // items (from 128 tokens the placement's global atomics, about 16 per
+    // expert per 128 tokens on one counter, cost more than the grouping kernel
+    // saves: 2048 tokens, route_q8 10.6 -> 32.4 us for group 12.6 -> 7.1 us)
+    const bool mfma = mfma_usable(a, T), placed = mfma && chains;
     PROFILED("route_q8", st,
              tg::launch_route_q8(c.raw, chains ? c.D : nullptr, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, c.idx,
-                                 c.w, c.xq, c.xd, c.xs, st));
+                                 c.w, c.xq, c.xd, c.xs, placed ? c.ecnt : nullptr, placed ? c.ent_cap : nullptr, st));
     const int n = T * s.k;
-    if (mfma_usable(a, T)) {
+    if (mfma) {
         const int mt = tg::mfma_tiles(s, T), ch = tg::mfma_item_entries(s, mt), wmax = tg::group_work_max(s, n, ch);
-        PROFILED("group", st,
-                 tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
-                                          st));
+        int32_t *ent = placed ? c.ent_cap : c.entries;
+        if (placed)
+            PROFILED("group", st,
+                     tg::launch_group_placed(s, n, ch, T, c.ecnt, c.counts, c.offsets, c.work, c.work_n, st));
+        else
+            PROFILED("group", st,
+                     tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
+                                              st));
         PROFILED("gateup_mfma", st,
-                 tg::launch_gateup_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.xq, c.xd, c.xs, c.hq,
-                                        c.hd, c.hs, st));
+                 tg::launch_gateup_mfma(lp, s, mt, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.xs, c.hq, c.hd, c.hs,
+                                        st));
         // the combine inside the down launch where its kernel takes it
         tg::FuseArgs F;
         const bool fuse = tg::down_fuses(s, mt, T);
@@ -567,8 +582,7 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
             F.cnt = c.fc_cnt;
         }
         PROFILED("down_mfma", st,
-                 tg::launch_down_mfma(lp, s, mt, wmax, c.work, c.work_n, c.entries, c.hq, c.hd, c.hs, c.D, F,
-                                      st));
+                 tg::launch_down_mfma(lp, s, mt, wmax, c.work, c.work_n, ent, c.hq, c.hd, c.hs, c.D, F, st));
         if (!fuse) PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
         return TG_OK;
     }

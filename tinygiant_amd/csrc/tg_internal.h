@@ -260,9 +260,11 @@ hipError_t launch_stream_read(const void *p, size_t bytes, int grid, uint32_t *s
 // grouped (batched decode / prefill) MoE layer pieces
 bool grouped_shape_ok(const Shape &s);
 // raw [T][E] router dots, or chains [H/32][T][E] (non-null: summed first)
+// ent_cap non-null: each token's k entries also go into per-expert lists
+// ent_cap[e * T + i] (i from the atomic count ecnt[e], zero before the call)
 hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                           hipStream_t st);
+                           int32_t *ecnt, int32_t *ent_cap, hipStream_t st);
 // Few tokens: the router's per-group fma chains [H/32][T][E], for
 // launch_route_q8 to add (T < 128, E <= 128 and a multiple of 32).
 bool route_chains_usable(int T, int E, int H);
@@ -272,6 +274,10 @@ int group_work_max(const Shape &s, int n);
 int group_work_max(const Shape &s, int n, int ch);
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
                                 int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st);
+// work items over entries placed by launch_route_q8 (lists of capacity cap);
+// clears ecnt for the next call
+hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *ecnt, int32_t *counts,
+                               int32_t *offsets, int32_t *work, int32_t *work_n, hipStream_t st);
 // int8-MFMA grouped gate/up and down (mt = M-tiles of 32 entries per item)
 bool mfma_shape_ok(const Shape &s);
 int mfma_tiles(const Shape &s, int T);

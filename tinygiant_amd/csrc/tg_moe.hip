@@ -2106,7 +2106,8 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
                                                          const float *__restrict__ gn, int E, int H, int k, float eps,
                                                          int32_t *__restrict__ idx,
                                                          float *__restrict__ w, int8_t *__restrict__ xq,
-                                                         float *__restrict__ xd, int *__restrict__ xs) {
+                                                         float *__restrict__ xd, int *__restrict__ xs,
+                                                         int32_t *__restrict__ ecnt, int32_t *__restrict__ ent_cap) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float rsum[RO_THREADS];
     RouteLds L = route_lds(smem, H);
@@ -2142,6 +2143,14 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
             const int j = k - 1 - tid;
             idx[(size_t)t * k + j] = L.sidx[j];
             w[(size_t)t * k + j] = wj;
+            if (ent_cap) {  // entry t k + j into its expert's list of capacity T, in arrival order
+                const int e = L.sidx[j];
+                const int pos = atomicAdd(ecnt + e, 1);
+                // at most T tokens pick an expert, so pos < T when the count
+                // started at zero (a call cut short could leave it nonzero:
+                // never write past the list)
+                if (pos < T) ent_cap[(size_t)e * T + pos] = t * k + j;
+            }
         }
     }
     const float sc = L.sred[0];
@@ -2205,16 +2214,29 @@ TG_DEV void scan_256_n(int (&v)[N], int n, int *tmp) {
 // remainders of more than half, more than a quarter, the rest), since blocks
 // are dispatched in item order and the short ones then fill the tail of the
 // grid; otherwise each expert's items follow one another in expert order.
-template <bool SORT>
+// PLACED: the entries are already in per-expert lists of capacity cap
+// (entries[e * cap + i], placed by k_route_q8) and ecnt[e] holds their
+// counts: only the work items are built (items of expert e start at e * cap)
+// and ecnt is cleared for the next layer.
+template <bool SORT, bool PLACED = false>
 __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict__ idx, int n, int E, int ch, int chd,
                                                       int wmax, int32_t *__restrict__ counts,
                                                       int32_t *__restrict__ offsets, int32_t *__restrict__ entries,
-                                                      int32_t *__restrict__ work, int32_t *__restrict__ work_n) {
+                                                      int32_t *__restrict__ work, int32_t *__restrict__ work_n,
+                                                      int32_t *__restrict__ ecnt, int cap) {
     __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E], tmp9[4 * 9], cls_tot[8];
     const int tid = threadIdx.x;
     for (int e = tid; e < E; e += GR_THREADS) {
         cnt[e] = 0;
         fill[e] = 0;
+    }
+    if constexpr (PLACED) {
+        if (tid < E) {
+            const int v = ecnt[tid];
+            cnt[tid] = v < cap ? v : cap;  // never past the list
+            ecnt[tid] = 0;
+        }
+        n = 0;  // no entry to count or list
     }
     __syncthreads();
     // GR_PER entries per thread per pass, loaded together before the atomics
@@ -2243,6 +2265,7 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         int sv[3] = {c, (c + ch - 1) / ch, (c + chd - 1) / chd};
         scan_256_n<3>(sv, E, tmp9);
         const int o = sv[0], bg = sv[1], bd = sv[2], ng = (c + ch - 1) / ch, nd = (c + chd - 1) / chd;
+        const int ob = PLACED ? tid * cap : o;  // the expert's first entry
         if (tid < E) {
             off[tid] = o;
             offsets[tid] = o;
@@ -2250,13 +2273,13 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
             for (int i = 0; i < ng && bg + i < wmax; i++) {
                 int32_t *it = work + 3 * (size_t)(bg + i);
                 it[0] = tid;
-                it[1] = o + i * ch;
+                it[1] = ob + i * ch;
                 it[2] = c - i * ch < ch ? c - i * ch : ch;
             }
             for (int i = 0; i < nd && bd + i < wmax; i++) {
                 int32_t *it = work + 3 * ((size_t)wmax + bd + i);
                 it[0] = tid;
-                it[1] = o + i * chd;
+                it[1] = ob + i * chd;
                 it[2] = c - i * chd < chd ? c - i * chd : chd;
             }
             if (tid == E - 1) {
@@ -2281,7 +2304,7 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
 #pragma unroll
     for (int j = 0; j < 9; j++) sc[j] = sv[j];
     scan_256_n<9>(sc, E, tmp9);
-    const int o = sc[0];
+    const int o = sc[0], ob = PLACED ? tid * cap : o;  // ob: the expert's first entry
     if (tid < E) {
         off[tid] = o;
         offsets[tid] = o;
@@ -2303,13 +2326,13 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
             for (int i = 0; i < nfull && bf + i < wmax; i++) {
                 int32_t *it = wl + 3 * (size_t)(bf + i);
                 it[0] = tid;
-                it[1] = o + i * chk;
+                it[1] = ob + i * chk;
                 it[2] = chk;
             }
             if (cls >= 0 && base_r < wmax) {
                 int32_t *it = wl + 3 * (size_t)base_r;
                 it[0] = tid;
-                it[1] = o + nfull * chk;
+                it[1] = ob + nfull * chk;
                 it[2] = r;
             }
         }
@@ -2834,7 +2857,7 @@ bool grouped_shape_ok(const Shape &s) {
 
 hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                           hipStream_t st) {
+                           int32_t *ecnt, int32_t *ent_cap, hipStream_t st) {
     // x in registers: NP passes of 8 x 256 elements.  The raw-dot form (many
     // tokens, one block each) takes as few passes as H needs, so its blocks
     // need fewer registers and more of them are resident (H 2048: 52 VGPRs,
@@ -2846,7 +2869,8 @@ hipError_t launch_route_q8(const float *raw, const float *chains, const float *x
         const size_t lds = route_lds_bytes(H);
         hipError_t e = allow_lds((const void *)kern, lds);
         if (e != hipSuccess) return e;
-        TG_LAUNCH(kern, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd, xs);
+        TG_LAUNCH(kern, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd, xs,
+                  ecnt, ent_cap);
         return hipGetLastError();
     };
     if (chains) return go(k_route_q8<true, RO_MAXPASS>);
@@ -2885,7 +2909,7 @@ static hipError_t group_go(const int32_t *idx, int n, int E, int ch, int chd, in
     hipError_t e = allow_lds((const void *)k_group<SORT>, lds);
     if (e != hipSuccess) return e;
     TG_LAUNCH(k_group<SORT>, dim3(1), dim3(GR_THREADS), lds, st, idx, n, E, ch, chd, wmax, counts, offsets, entries,
-              work, work_n);
+              work, work_n, nullptr, 0);
     return hipGetLastError();
 }
 
@@ -2893,6 +2917,18 @@ hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *coun
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
     return group_go<false>(idx, n, s.E, gu_chunk(s.nbH), dn_chunk(s.nbI, s.I), group_work_max(s, n), counts,
                            offsets, entries, work, work_n, st);
+}
+
+hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *ecnt, int32_t *counts,
+                               int32_t *offsets, int32_t *work, int32_t *work_n, hipStream_t st) {
+    const int wmax = group_work_max(s, n, ch);
+    if (ch > 32)  // items of several M-tiles: largest first
+        TG_LAUNCH((k_group<true, true>), dim3(1), dim3(GR_THREADS), 0, st, nullptr, n, s.E, ch, ch, wmax, counts,
+                  offsets, nullptr, work, work_n, ecnt, cap);
+    else
+        TG_LAUNCH((k_group<false, true>), dim3(1), dim3(GR_THREADS), 0, st, nullptr, n, s.E, ch, ch, wmax, counts,
+                  offsets, nullptr, work, work_n, ecnt, cap);
+    return hipGetLastError();
 }
 
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
