@@ -214,29 +214,37 @@ __global__ __launch_bounds__(RC_THREADS) void k_route_chains(const float *__rest
 // LDS and thread p adds them to the totals of pairs p and p + 256 in
 // ascending group order, exactly as k_route does.
 constexpr int RTT_T = 16, RTT_E = 32;
-constexpr int RT_CH = 4;                   // groups per staging step (a multiple of 4: waves take w, w + 4, ..)
-constexpr int RT_W = RT_CH * RG + 4;       // LDS row stride (floats)
-constexpr int RT_F4 = RT_CH * RG / 4;      // float4 per staged row and step
+constexpr int RT_CH = 4;                   // groups per staging step of the 4-wave form
 constexpr int RT_PAIRS = RTT_T * RTT_E;    // 512
 
-__global__ __launch_bounds__(256) void k_route_tiled(const float *__restrict__ Wr, const float *__restrict__ x,
-                                                     int T, int E, int H, float *__restrict__ raw) {
-    __shared__ __align__(16) float xs[RTT_T][RT_W];
-    __shared__ __align__(16) float ws[RTT_E][RT_W];
-    __shared__ float cs[RT_CH][RT_PAIRS];
+// NW waves per block, one group of each staging step per wave (NW = 8: 512
+// threads, 8 groups of 32 elements staged per step, 66 KB of LDS; two blocks
+// per CU keep four waves per SIMD where the 4-wave form kept two: 28.5 -> 25.0
+// us at 2048 tokens)
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_route_tiled(const float *__restrict__ Wr, const float *__restrict__ x,
+                                                         int T, int E, int H, float *__restrict__ raw) {
+    constexpr int NT = NW * 64, CH = NW;      // threads, groups per step
+    constexpr int RW = CH * RG + 4;           // LDS row stride (floats)
+    constexpr int F4 = CH * RG / 4;           // float4 per staged row and step
+    __shared__ __align__(16) float xs[RTT_T][RW];
+    __shared__ __align__(16) float ws[RTT_E][RW];
+    __shared__ float cs[CH][RT_PAIRS];
     const int tid = threadIdx.x, t0 = blockIdx.x * RTT_T, e0 = blockIdx.y * RTT_E;
     const int gw = tid >> 6, ti = (tid >> 3) & 7, ej = tid & 7;
-    // staging: thread loads rows r = tid / 32 + 8 v, float4 column c4
-    const int sr = tid / RT_F4, sc = (tid % RT_F4) * 4;
-    constexpr int RS = 256 / RT_F4;  // rows per staging pass (8)
-    constexpr int TA = RTT_T / 8, TP = RT_PAIRS / 256;  // tokens per lane, pairs per thread
-    float tot[TP];                    // pairs tid + 256 j: token p / 32, expert p % 32
+    // staging: thread loads rows r = tid / F4 + RS v, float4 column c4
+    const int sr = tid / F4, sc = (tid % F4) * 4;
+    constexpr int RS = NT / F4;  // rows per staging pass (8)
+    static_assert(RS == 8 && RTT_T % RS == 0 && RTT_E % RS == 0, "staging map");
+    constexpr int TA = RTT_T / 8, TP = RT_PAIRS / NT;  // tokens per lane, pairs per thread
+    static_assert(TP >= 1 && RT_PAIRS % NT == 0, "pairs per thread");
+    float tot[TP];                    // pairs tid + NT j: token p / 32, expert p % 32
 #pragma unroll
     for (int j = 0; j < TP; j++) tot[j] = 0.0f;
-    const int G = H / RG, nst = G / RT_CH;
+    const int G = H / RG, nst = G / CH;
     float4 xv[RTT_T / RS], wv[RTT_E / RS];
     auto fetch = [&](int st) {
-        const size_t col = (size_t)st * RT_CH * RG + sc;
+        const size_t col = (size_t)st * CH * RG + sc;
 #pragma unroll
         for (int v = 0; v < RTT_T / RS; v++) {
             const int t = t0 + sr + RS * v;
@@ -256,9 +264,7 @@ __global__ __launch_bounds__(256) void k_route_tiled(const float *__restrict__ W
         for (int v = 0; v < RTT_E / RS; v++) *reinterpret_cast<float4 *>(&ws[sr + RS * v][sc]) = wv[v];
         __syncthreads();  // staged rows in; the previous step's chains read
         if (st + 1 < nst) fetch(st + 1);
-#pragma unroll
-        for (int h = 0; h < RT_CH / 4; h++) {
-        const int gl = gw + 4 * h;
+        const int gl = gw;
         float a[TA][4];
 #pragma unroll
         for (int i = 0; i < TA; i++)
@@ -289,16 +295,15 @@ __global__ __launch_bounds__(256) void k_route_tiled(const float *__restrict__ W
         for (int i = 0; i < TA; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) cs[gl][(ti + 8 * i) * RTT_E + ej + 8 * j] = a[i][j];
-        }
         __syncthreads();  // the step's chains in
 #pragma unroll
         for (int j = 0; j < TP; j++)
 #pragma unroll
-            for (int g = 0; g < RT_CH; g++) tot[j] = tot[j] + cs[g][tid + 256 * j];
+            for (int g = 0; g < CH; g++) tot[j] = tot[j] + cs[g][tid + NT * j];
     }
 #pragma unroll
     for (int j = 0; j < TP; j++) {
-        const int p = tid + 256 * j, t = t0 + p / RTT_E, e = e0 + p % RTT_E;
+        const int p = tid + NT * j, t = t0 + p / RTT_E, e = e0 + p % RTT_E;
         if (t < T && e < E) raw[(size_t)t * E + e] = tot[j];
     }
 }
@@ -2619,8 +2624,11 @@ bool decode_shape_ok(const Shape &s) {
 }
 
 hipError_t launch_route(const float *Wr, const float *x, int T, int E, int H, float *raw, hipStream_t st) {
-    if (T >= 128 && (H / RG) % RT_CH == 0) {
-        TG_LAUNCH(k_route_tiled, dim3(cdiv((size_t)T, RTT_T), cdiv((size_t)E, RTT_E)), dim3(256), 0, st, Wr, x, T,
+    if (T >= 128 && (H / RG) % 8 == 0) {
+        TG_LAUNCH(k_route_tiled<8>, dim3(cdiv((size_t)T, RTT_T), cdiv((size_t)E, RTT_E)), dim3(512), 0, st, Wr, x, T,
+                  E, H, raw);
+    } else if (T >= 128 && (H / RG) % RT_CH == 0) {
+        TG_LAUNCH(k_route_tiled<4>, dim3(cdiv((size_t)T, RTT_T), cdiv((size_t)E, RTT_E)), dim3(256), 0, st, Wr, x, T,
                   E, H, raw);
     } else if (T >= RS_T && (H / RG) % (2 * RS_PARTS) == 0 && route_small_lds(H) <= 64 * 1024) {
         const size_t lds = route_small_lds(H);
