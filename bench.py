@@ -485,15 +485,21 @@ def batched_leg(args, torch, call, arena, LR=16, K=256, W=16, T=64):
         blk.forward(i % LR, X[i])
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
-    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "gateup_grouped", "down_grouped", "combine")
+    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "gateup_grouped",
+             "down_grouped", "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    gu_name = "gateup_mfma" if "gateup_mfma" in kern else "gateup_grouped"
-    # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries
-    gu_kernel = (("k_mfma_small" if T * K_TOP <= 16 * E else "k_mfma_grouped") if gu_name == "gateup_mfma"
-                 else "k_gateup_grouped")
+    if "gu_down_mfma" in kern:  # gate/up and down of the one-tile items in one launch
+        gu_name, gu_kernel, part = "gu_down_mfma", "k_mfma_small_gd", "gate/up + down"
+        roof_bytes = n_uniq * EXPERT_Q4_BYTES
+    else:
+        gu_name = "gateup_mfma" if "gateup_mfma" in kern else "gateup_grouped"
+        # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries
+        gu_kernel = (("k_mfma_small" if T * K_TOP <= 16 * E else "k_mfma_grouped") if gu_name == "gateup_mfma"
+                     else "k_gateup_grouped")
+        part, roof_bytes = "gate/up", n_uniq * GATEUP_BYTES_PER_EXPERT
     n_gu, ms_gu = kern[gu_name]
-    achieved = n_uniq * GATEUP_BYTES_PER_EXPERT / (ms_gu / n_gu * 1e-3)
+    achieved = roof_bytes / (ms_gu / n_gu * 1e-3)
 
     cpu = None
     if not args.no_cpu:
@@ -517,10 +523,11 @@ def batched_leg(args, torch, call, arena, LR=16, K=256, W=16, T=64):
         "hbm_gbps_expert_weights": round(gbps, 1),
         "hbm_frac_expert_weights": round(gbps * 1e9 / HBM_PEAK, 4),
         "kernel_avg_us": kern_us,
-        "roofline": {"bound": "hbm", "kernel": gu_kernel + " (gate/up)",
-                     "bytes_per_launch": round(n_uniq * GATEUP_BYTES_PER_EXPERT),
+        "roofline": {"bound": "hbm", "kernel": f"{gu_kernel} ({part})",
+                     "bytes_per_launch": round(roof_bytes),
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": profiled_traffic(gu_kernel + "/gate_up")},
+                     "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": profiled_traffic(gu_kernel + ("/gate_up" if part == "gate/up" else ""))},
         "cpu_baseline": cpu,
     }
 
@@ -678,7 +685,7 @@ def leg_235b(args, torch, call, arena, T, K, W):
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
     names = ("dec_part", "layer", "route", "experts", "gateup", "down", "route_q8", "group", "gateup_mfma", "down_mfma",
-             "combine")
+             "gu_down_mfma", "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     router_bytes = None
@@ -690,6 +697,8 @@ def leg_235b(args, torch, call, arena, T, K, W):
     elif "gateup" in kern:
         rk, rb = "gateup", K5 * GATEUP5_BYTES
         roof = "k_gateup"
+    elif "gu_down_mfma" in kern:  # gate/up and down of the one-tile items in one launch
+        rk, rb, roof = "gu_down_mfma", round(n_uniq * EXPERT5_BYTES), "k_mfma_small_gd"
     else:
         rk, rb = "gateup_mfma", round(n_uniq * GATEUP5_BYTES)
         # one M-tile per expert (k_mfma_small) while T*top_k/E averages <= 16 entries

@@ -309,7 +309,8 @@ int tg_arena_set_batch_path(tg_arena *a, int path);
 int tg_arena_set_graphs(tg_arena *a, int on);
 /* Waits for the device and reports a device-side failure of an earlier
  * asynchronous call on this arena, or of a no-alloc call on this device (a
- * hand-off poll of the ROUTED or FUSED launch that ran out of tries):
+ * hand-off poll of the ROUTED or FUSED launch, or a down block's wait in
+ * the batched path's gate/up + down launch, that ran out of tries):
  * TG_E_HIP.  The failure is reported once: reading it clears it, and the
  * next calls run as before. */
 int tg_arena_status(tg_arena *a);
@@ -322,9 +323,11 @@ int tg_arena_status(tg_arena *a);
 int tg_clock_mfma_mhz(int iters, double *mhz_median, double *mhz_min,
                       double *mhz_max);
 /* Test hook of the failure channel, no counterpart in the reference: the
- * poll bound of the ROUTED and FUSED launches (spin_limit tries; 0 restores
- * the normal bound) and one h line those launches leave unpublished
- * (drop_line: a gate/up unit, or half unit on shapes that split units; -1
+ * poll bound of the ROUTED and FUSED launches and of the batched path's
+ * gate/up + down launch (spin_limit tries; 0 restores the normal bound) and
+ * one h line those launches leave unpublished (drop_line: a gate/up unit,
+ * or half unit on shapes that split units, of the one-token launches; the
+ * work item whose gate/up blocks never count in, in the batched launch; -1
  * none).  Every reader of that line then gives up after spin_limit tries,
  * each kernel exits normally, the rows come back NaN and the failure is
  * reported.  Not for production use. */

@@ -146,3 +146,53 @@ def test_recovered_call_matches_oracle(O, tglib, inject):
         assert tglib.tg_arena_status(a.handle) == 0
     finally:
         a.close()
+
+
+def test_fused_gate_up_down_wait_failure(O, tglib, inject):
+    """The batched path's fused gate/up + down launch: the down blocks of a
+    work item wait (bounded) until the item's gate/up blocks have stored h.
+    With the hook, the gate/up blocks of item 0 (all entries of the lowest
+    expert any token selected, at 16 tokens) never count in: exactly the
+    tokens that selected that expert come back NaN, every other row is
+    bit-exact, the host call returns TG_E_HIP, and the next call on the same
+    arena equals the oracle again."""
+    import os
+    from tinygiant_amd.arena import HBMExpertArena
+    H, I, E, k, T = 2048, 768, 128, 8, 16
+    lb, r = O.synth_layer(91, 0, H, I, E)
+    a = HBMExpertArena(1, E, H, I, k)
+    old = os.environ.get("TG_FUSE_GD")
+    os.environ["TG_FUSE_GD"] = "1"
+    try:
+        a.load_layer(0, lb)
+        a.load_router(0, r)
+        x = O.synth_normal(91, O.stream_id(0, 5, 4), 1.0, T * H).reshape(T, H)
+        ref, ridx, _, _ = O.moe_layer(lb, r, H, I, E, k, x)
+        gpu_note("fused gate/up + down: clean call")
+        rc, out = host_layer(tglib, a, 0, x)
+        assert rc == 0 and np.array_equal(bits(out), bits(ref))
+
+        gpu_note("fused gate/up + down: item 0 never counted in, 4096 tries per wait")
+        inject(4096, 0)
+        rc, bad = host_layer(tglib, a, 0, x)
+        assert rc == TG_E_HIP
+        assert "ran out of tries" in tglib.tg_last_error().decode()
+        hit = (ridx == ridx.min()).any(axis=1)
+        nan_rows = np.isnan(bad).any(axis=1)
+        assert hit.any() and np.array_equal(nan_rows, hit), (np.nonzero(nan_rows)[0], np.nonzero(hit)[0])
+        assert np.isnan(bad[hit]).all()
+        assert np.array_equal(bits(bad[~hit]), bits(ref[~hit]))
+
+        gpu_note("fused gate/up + down: hook cleared")
+        tglib.tg_debug_fault_inject(0, -1)
+        for rep in range(2):
+            rc, out = host_layer(tglib, a, 0, x)
+            assert rc == 0 and np.array_equal(bits(out), bits(ref)), f"rep {rep}"
+        assert tglib.tg_arena_status(a.handle) == 0
+    finally:
+        tglib.tg_debug_fault_inject(0, -1)
+        if old is None:
+            os.environ.pop("TG_FUSE_GD", None)
+        else:
+            os.environ["TG_FUSE_GD"] = old
+        a.close()

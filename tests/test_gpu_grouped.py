@@ -241,3 +241,39 @@ def test_fused_combine_counts_across_calls(O, tglib):
         else:
             os.environ["TG_FUSE_COMBINE"] = old
         a.close()
+
+
+# (H, I, E, k, token counts): gate/up K of 8 chunks (activations staged once)
+# and of 16 (staged per chunk); the placed-entry grouping below 128 tokens and
+# the listing one from 128
+@pytest.mark.parametrize("H,I,E,k,Ts", [(512, 256, 32, 8, (40, 9, 64)), (2048, 768, 128, 8, (64, 200, 3)),
+                                        (4096, 1536, 128, 8, (32, 5))])
+def test_fused_gate_up_down_across_calls(O, tglib, H, I, E, k, Ts):
+    """One-tile work items run gate/up and down in one launch (down blocks
+    wait, bounded, for their item's gate/up blocks to store h; the grouping
+    kernel clears the per-item counts for every call).  Calls of different
+    sizes on one arena, each made with the fused launch and with the two
+    launches (TG_FUSE_GD=0, read per call), all equal the oracle bit for bit."""
+    import os
+    from tinygiant_amd.moe import MoEBlock
+    a, layers, routers = make_arena(O, 1, H, I, E, k, seed=41)
+    old = os.environ.get("TG_FUSE_GD")
+    try:
+        blk = MoEBlock(a)
+        for i, T in enumerate(Ts):
+            x = O.synth_normal(41, O.stream_id(0, i, 4), 1.0, T * H).reshape(T, H)
+            ref, _, _, _ = O.moe_layer(layers[0], routers[0], H, I, E, k, x)
+            xd = dev(x)
+            for mode in ("1", "0", "1"):
+                os.environ["TG_FUSE_GD"] = mode
+                gpu_note(f"fused gate/up + down H={H} T={T} TG_FUSE_GD={mode}")
+                got = host(blk.forward(0, xd))
+                assert np.array_equal(bits(got), bits(ref)), \
+                    f"T={T} mode {mode}: max |diff| {np.max(np.abs(got - ref)):.3e}"
+        assert tglib.tg_arena_status(a.handle) == 0
+    finally:
+        if old is None:
+            os.environ.pop("TG_FUSE_GD", None)
+        else:
+            os.environ["TG_FUSE_GD"] = old
+        a.close()

@@ -213,6 +213,7 @@ struct Scratch {
     int32_t *entries = nullptr;   // T * k
     int32_t *work = nullptr;      // 2 lists x 3 * group_work_max
     int32_t *work_n = nullptr;    // 2
+    int32_t *rdy = nullptr;       // group_work_max: per work item, gate/up blocks done (fused gate/up + down launch)
     int8_t *hq = nullptr;         // T * k * I  Q8_0 h per (token, slot)
     float *hd = nullptr;          // T * k * nbI
     int *hs = nullptr;            // T * k * nbI
@@ -263,6 +264,7 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     c.D = reinterpret_cast<float *>(take(4 * n * s.H));
     c.work = reinterpret_cast<int32_t *>(take(4 * 2 * 3 * wmax));
     c.work_n = reinterpret_cast<int32_t *>(take(4 * 2));
+    c.rdy = reinterpret_cast<int32_t *>(take(4 * wmax));
     if (sc) *sc = c;
     return (off + 255) & ~(size_t)255;
 }
@@ -562,13 +564,29 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
     if (mfma) {
         const int mt = tg::mfma_tiles(s, T), ch = tg::mfma_item_entries(s, mt), wmax = tg::group_work_max(s, n, ch);
         int32_t *ent = placed ? c.ent_cap : c.entries;
+        // gate/up and down in one launch where the one-tile kernels take it
+        // (the combine stays a launch of its own)
+        const bool gd = tg::gd_fuses(s, mt) && !tg::down_fuses(s, mt, T) && wmax <= tg::group_work_max(s, n);
+        int32_t *rdy = gd ? c.rdy : nullptr;
         if (placed)
             PROFILED("group", st,
-                     tg::launch_group_placed(s, n, ch, T, c.ecnt, c.counts, c.offsets, c.work, c.work_n, st));
+                     tg::launch_group_placed(s, n, ch, T, c.ecnt, c.counts, c.offsets, c.work, c.work_n, rdy, st));
         else
             PROFILED("group", st,
                      tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
-                                              st));
+                                              rdy, st));
+        if (gd) {
+            tg::GdArgs G;
+            G.rdy = c.rdy;
+            G.err = c.dec_err;
+            G.spin = tg::poll_spin_limit();
+            G.drop = tg::poll_drop();
+            PROFILED("gu_down_mfma", st,
+                     tg::launch_gu_down_ms(lp, s, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.hq, c.hd, c.hs, c.D, G,
+                                           st));
+            PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
+            return TG_OK;
+        }
         PROFILED("gateup_mfma", st,
                  tg::launch_gateup_mfma(lp, s, mt, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.xs, c.hq, c.hd, c.hs,
                                         st));
@@ -936,7 +954,7 @@ extern "C" int tg_arena_status(tg_arena *a) {
     if (g_dev >= 0 && g_dev < NOALLOC_MAX_DEV && g_na[g_dev].used &&  // the no-alloc call's error word
         (rc = take_err_word(noalloc_err(g_na[g_dev].ptr), &vn)))
         return rc;
-    if (v) return set_err(TG_E_HIP, "decode launch: a device-side poll ran out of tries (code %u)", v);
+    if (v) return set_err(TG_E_HIP, "MoE launch: a device-side wait ran out of tries (code %u)", v);
     if (vn) return set_err(TG_E_HIP, "no-alloc layer call: a device-side poll ran out of tries (code %u)", vn);
     return TG_OK;
 }

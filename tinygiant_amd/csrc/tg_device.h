@@ -197,6 +197,17 @@ TG_DEV void lds_dma4(const void *src, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src),
                  "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
 }
+// The same at agent scope (sc1): the bytes come from the device's point of
+// coherence, not from a copy an XCD's L2 may still hold, for data another
+// block of the same launch wrote with agent-scope stores.
+TG_DEV void lds_dma16_coh(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
+TG_DEV void lds_dma4_coh(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off sc1" ::"v"(src),
+                 "s"(__builtin_amdgcn_readfirstlane(m0)) : "memory", "m0");
+}
 
 // Tagged words: a 32-bit payload and a 32-bit tag in one 64-bit word,
 // stored and loaded with relaxed agent-scope atomics, so a reader that sees

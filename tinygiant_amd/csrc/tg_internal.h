@@ -272,12 +272,14 @@ hipError_t launch_route_chains(const float *Wr, const float *x, int T, int E, in
 // work list: at most group_work_max(s, n) items per list, two lists
 int group_work_max(const Shape &s, int n);
 int group_work_max(const Shape &s, int n, int ch);
+// rdy (may be null): one word per work item, zeroed for launch_gu_down_ms
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
-                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st);
+                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, int32_t *rdy,
+                                hipStream_t st);
 // work items over entries placed by launch_route_q8 (lists of capacity cap);
 // clears ecnt for the next call
 hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *ecnt, int32_t *counts,
-                               int32_t *offsets, int32_t *work, int32_t *work_n, hipStream_t st);
+                               int32_t *offsets, int32_t *work, int32_t *work_n, int32_t *rdy, hipStream_t st);
 // int8-MFMA grouped gate/up and down (mt = M-tiles of 32 entries per item)
 bool mfma_shape_ok(const Shape &s);
 int mfma_tiles(const Shape &s, int T);
@@ -300,6 +302,26 @@ inline size_t fuse_count_words(const Shape &s, int T) { return (size_t)T * (size
 // The down launch at mt M-tiles combines too (FuseArgs honoured): its kernel
 // takes whole FC_ROWS-row tiles (H % FC_ROWS == 0) and TG_FUSE_COMBINE is 1.
 bool down_fuses(const Shape &s, int mt, int T);
+// Gate/up and down of one-tile work items in one launch (k_mfma_small_gd):
+// rdy holds one word per work item, zero at the launch (the grouping kernel
+// clears them); a down block whose wait for its item's h runs out of tries
+// stores NaN rows and sets *err to 4.
+struct GdArgs {
+    int32_t *rdy = nullptr;
+    uint32_t *err = nullptr;
+    uint32_t spin = 0;  // poll bound
+    int drop = -1;      // failure-channel hook: the item whose gate/up blocks never count in
+    int need = 0;       // gate/up blocks per item (set by the launcher)
+};
+// the fused launch applies: one-tile items (mt == 1), the down K at most 8
+// chunks of 8 blocks, and TG_FUSE_GD not 0 (read per call)
+bool gd_fuses(const Shape &s, int mt);
+hipError_t launch_gu_down_ms(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                             const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                             int8_t *hq, float *hd, int *hs, float *D, const GdArgs &G, hipStream_t st);
+// the poll bound and the withheld line / item of the failure-channel hook
+uint32_t poll_spin_limit();
+int poll_drop();
 hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int wmax, const int32_t *work,
                             const int32_t *work_n, const int32_t *entries, const int8_t *hq, const float *hd,
                             const int *hs, float *D, const FuseArgs &F, hipStream_t st);

@@ -494,19 +494,24 @@ TG_DEV int half_sum(int v) {
     return v;
 }
 
-template <bool PAIR, bool SCV, bool FULL>
-__global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__restrict__ layer_pl, Shape s,
-                                                           const int32_t *__restrict__ work,
-                                                           const int32_t *__restrict__ work_n,
-                                                           const int32_t *__restrict__ entries,
-                                                           const int8_t *__restrict__ aq, const float *__restrict__ ad,
-                                                           int8_t *__restrict__ oq, float *__restrict__ od,
-                                                           int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
+// One block of the one-tile kernels: item wi, row tile bx.  GD: gate/up and
+// down blocks of the same launch (k_mfma_small_gd): a gate/up block stores
+// h with agent-scope stores and, once they are acknowledged, counts itself in
+// at rdy[wi]; a down block waits (bounded) until all `need` gate/up blocks of
+// its item have, then stages h at agent scope.
+template <bool PAIR, bool SCV, bool FULL, bool GD>
+TG_DEV __attribute__((always_inline)) void ms_item(const uint8_t *__restrict__ layer_pl, const Shape &s,
+                                                   const int32_t *__restrict__ work,
+                                                   const int32_t *__restrict__ work_n,
+                                                   const int32_t *__restrict__ entries,
+                                                   const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                   int8_t *__restrict__ oq, float *__restrict__ od,
+                                                   int *__restrict__ os, float *__restrict__ D, const FuseArgs &F,
+                                                   int wi, int bx, uint8_t *smem, const GdArgs &G) {
     constexpr int M = 32, NW = MS_NW, NT = NW * 64, TP = 2 * MF_KC;
     constexpr int NTP = M * TP / NT, NDX = M * MF_KC / NT;
     static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC == 8 && NTP >= 1 && NDX >= 1, "staging map");
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int wi = blockIdx.y;
+    static_assert(!GD || PAIR || FULL, "a waiting down block stages its activations once, at agent scope");
     if (wi >= work_n[0]) return;  // uniform over the block
     const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n = lane & 31, h = lane >> 5;
@@ -532,7 +537,7 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     }
 
     const int mat = PAIR ? (wave & 1) : 0;  // 0 gate / down, 1 up
-    const int nt = PAIR ? blockIdx.x * (NW / 2) + (wave >> 1) : blockIdx.x * NW + wave;
+    const int nt = PAIR ? bx * (NW / 2) + (wave >> 1) : bx * NW + wave;
     const bool valid = nt * 32 < rows;
     const int R = valid ? nt * 32 + n : n;
     const uint8_t *ex = layer_pl + (size_t)e * s.EB;
@@ -545,6 +550,28 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
     // LDS, issued before any weight load: the waits of the weight loop then
     // count weight loads only.  Entries past the item stage the item's last
     // entry's bytes (their sums are never stored).
+    // GD down block: every gate/up block of the item has counted in
+    // (bounded; when the wait runs out the rows are stored as NaN and *err set)
+    bool gd_bad = false;
+    if constexpr (GD && !PAIR) {
+        __shared__ int gd_flag;
+        if (tid == 0) {
+            uint32_t tries = 0;
+            int bad = 0;
+            while (__hip_atomic_load(G.rdy + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G.need) {
+                if (++tries >= G.spin) {
+                    bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            gd_flag = bad;
+            if (bad) __hip_atomic_store(G.err, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        gd_bad = gd_flag != 0;
+    }
+
     constexpr int FA = M * 256, FD = MF_KC * M;  // bytes of one chunk's rows, scales of one chunk
     if constexpr (FULL) {
         constexpr int JA = M * 256 / (NT * 16), JD = FD / NT;  // DMA rounds per chunk: rows, scales
@@ -569,11 +596,21 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
         for (int ch = 0; ch < MS_FC; ch++) {
             if (ch < nch) {  // uniform
 #pragma unroll
-                for (int j = 0; j < JA; j++)
-                    lds_dma16(asrc[j] + ch * MF_KC * 32, lds_addr(smem, ch * FA + (j * NW + wave) * 1024));
+                for (int j = 0; j < JA; j++) {
+                    const uint32_t m0 = lds_addr(smem, ch * FA + (j * NW + wave) * 1024);
+                    if constexpr (GD && !PAIR)
+                        lds_dma16_coh(asrc[j] + ch * MF_KC * 32, m0);
+                    else
+                        lds_dma16(asrc[j] + ch * MF_KC * 32, m0);
+                }
 #pragma unroll
-                for (int j = 0; j < JD; j++)
-                    lds_dma4(dsrc[j] + ch * MF_KC, lds_addr(smem, MS_FC * FA + (ch * FD + (j * NW + wave) * 64) * 4));
+                for (int j = 0; j < JD; j++) {
+                    const uint32_t m0 = lds_addr(smem, MS_FC * FA + (ch * FD + (j * NW + wave) * 64) * 4);
+                    if constexpr (GD && !PAIR)
+                        lds_dma4_coh(dsrc[j] + ch * MF_KC, m0);
+                    else
+                        lds_dma4(dsrc[j] + ch * MF_KC, m0);
+                }
             }
         }
     }
@@ -782,12 +819,28 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
             const int sum = half_sum(qv);
             if (on) {
                 const int ent = entries[o + t];
-                oq[(size_t)ent * s.I + nt * 32 + n] = (int8_t)qv;
-                if (n == 0) {
-                    od[(size_t)ent * s.nbI + nt] = h2f(f2h(d));
-                    os[(size_t)ent * s.nbI + nt] = sum;
+                int8_t *qp = oq + (size_t)ent * s.I + nt * 32 + n;
+                const size_t si = (size_t)ent * s.nbI + nt;
+                if constexpr (GD) {  // read by down blocks of this launch
+                    __hip_atomic_store(qp, (int8_t)qv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (n == 0) {
+                        st_coh(od + si, h2f(f2h(d)));
+                        __hip_atomic_store(os + si, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                } else {
+                    *qp = (int8_t)qv;
+                    if (n == 0) {
+                        od[si] = h2f(f2h(d));
+                        os[si] = sum;
+                    }
                 }
             }
+        }
+        if constexpr (GD) {
+            __builtin_amdgcn_s_waitcnt(VMCNT0);  // this thread's h stores acknowledged
+            __syncthreads();                     // ... every thread's
+            if (tid == 0 && wi != G.drop)
+                __hip_atomic_fetch_add(G.rdy + wi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     } else {
         if (valid) {
@@ -797,15 +850,57 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                 const int t = 8 * (r >> 2) + 4 * h + (r & 3);
                 if (t < c) {
                     float *dst = D + (size_t)entries[o + t] * s.H + nt * 32 + n;
+                    const float v = gd_bad ? __builtin_nanf("") : acc[r];
                     if (coh)
-                        st_coh(dst, acc[r]);
+                        st_coh(dst, v);
                     else
-                        *dst = acc[r];
+                        *dst = v;
                 }
             }
         }
         // NW * 32 == FC_ROWS: block x covers output tile x
-        if (F.cnt) fused_combine<NT>(F, s, entries, o, c, (int)blockIdx.x, D, smem);
+        if (F.cnt) fused_combine<NT>(F, s, entries, o, c, bx, D, smem);
+    }
+}
+
+template <bool PAIR, bool SCV, bool FULL>
+__global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                           const int32_t *__restrict__ work,
+                                                           const int32_t *__restrict__ work_n,
+                                                           const int32_t *__restrict__ entries,
+                                                           const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                           int8_t *__restrict__ oq, float *__restrict__ od,
+                                                           int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    ms_item<PAIR, SCV, FULL, false>(layer_pl, s, work, work_n, entries, aq, ad, oq, od, os, D, F, (int)blockIdx.y,
+                                    (int)blockIdx.x, smem, GdArgs());
+}
+
+// Gate/up and down of the one-tile items in one launch: blocks [0, gxg wmax)
+// are the gate/up blocks (item b / gxg, row tile b % gxg), the rest the down
+// blocks.  Blocks are dispatched in order of their id on each XCD, so every
+// gate/up block has been dispatched (and runs without waiting) before a down
+// block of the same XCD takes a slot; a down block's wait ends once the
+// gate/up blocks of its item, on whichever XCD, have stored h.  The down
+// blocks then fill the slots the gate/up launch's last round leaves idle.
+template <bool SCVG, bool FULLG>
+__global__ __launch_bounds__(MS_NW * 64) void k_mfma_small_gd(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                              const int32_t *__restrict__ work,
+                                                              const int32_t *__restrict__ work_n,
+                                                              const int32_t *__restrict__ entries,
+                                                              const int8_t *__restrict__ xq,
+                                                              const float *__restrict__ xd, int8_t *hq, float *hd,
+                                                              int *hs, float *__restrict__ D, GdArgs G, int gxg,
+                                                              int gxd, int wmax) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int b = (int)blockIdx.x, ng = gxg * wmax;
+    if (b < ng) {
+        ms_item<true, SCVG, FULLG, true>(layer_pl, s, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, FuseArgs(),
+                                         b / gxg, b % gxg, smem, G);
+    } else {
+        const int d = b - ng;
+        ms_item<false, true, true, true>(layer_pl, s, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D,
+                                         FuseArgs(), d / gxd, d % gxd, smem, G);
     }
 }
 
@@ -1371,6 +1466,45 @@ hipError_t launch_down_mfma(const uint8_t *layer_pl, const Shape &s, int mt, int
     if (mt == 2) return mf_go<2, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr,
                                         D, st);
     return mf_go<4, false>(layer_pl, s, wmax, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, st);
+}
+
+bool gd_fuses(const Shape &s, int mt) {
+    const char *v = getenv("TG_FUSE_GD");
+    const bool on = !(v && v[0] == '0');
+    return on && mt == 1 && mfma_shape_ok(s) && s.nbI % MF_KC == 0 && s.nbI <= MS_FC * MF_KC;
+}
+
+template <bool SCVG, bool FULLG>
+static hipError_t gd_go(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                        const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd, int8_t *hq,
+                        float *hd, int *hs, float *D, const GdArgs &G, int gxg, int gxd, hipStream_t st) {
+    const size_t lds = ms_full_lds_bytes();
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_small_gd<SCVG, FULLG>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    TG_LAUNCH((k_mfma_small_gd<SCVG, FULLG>), dim3((unsigned)((gxg + gxd) * wmax)), dim3(MS_NW * 64), lds, st,
+              layer_pl, s, work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, wmax);
+    return hipGetLastError();
+}
+
+hipError_t launch_gu_down_ms(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                             const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                             int8_t *hq, float *hd, int *hs, float *D, const GdArgs &G0, hipStream_t st) {
+    if (!gd_fuses(s, 1) || !G0.rdy || !G0.err || G0.spin == 0) return hipErrorInvalidValue;
+    const int gxg = (int)mf_cdiv((size_t)s.I, 32 * (MS_NW / 2)), gxd = (int)mf_cdiv((size_t)s.H, 32 * MS_NW);
+    if ((size_t)(gxg + gxd) * (size_t)wmax >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    GdArgs G = G0;
+    G.need = gxg;
+    const int nbH = s.nbH;
+    if (nbH % MF_KC == 0 && nbH <= MS_FC * MF_KC)
+        return gd_go<true, true>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, st);
+    if (nbH % MF_KC == 0)
+        return gd_go<true, false>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, st);
+    return gd_go<false, false>(layer_pl, s, wmax, work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, st);
 }
 
 }  // namespace tg

@@ -585,6 +585,8 @@ static uint32_t g_fault_spin = 0;
 static int g_fault_drop = -1;
 
 static uint32_t fault_spin_limit() { return g_fault_spin ? g_fault_spin : RD_SPIN_LIMIT; }
+uint32_t poll_spin_limit() { return fault_spin_limit(); }
+int poll_drop() { return g_fault_drop; }
 
 void set_fault_injection(uint32_t spin_limit, int drop_line) {
     g_fault_spin = spin_limit;
@@ -2228,9 +2230,12 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
                                                       int wmax, int32_t *__restrict__ counts,
                                                       int32_t *__restrict__ offsets, int32_t *__restrict__ entries,
                                                       int32_t *__restrict__ work, int32_t *__restrict__ work_n,
-                                                      int32_t *__restrict__ ecnt, int cap) {
+                                                      int32_t *__restrict__ ecnt, int cap,
+                                                      int32_t *__restrict__ rdy) {
     __shared__ int cnt[MAX_E], off[MAX_E + 1], fill[MAX_E], tmp9[4 * 9], cls_tot[8];
     const int tid = threadIdx.x;
+    if (rdy)  // the fused gate/up + down launch's per-item counts
+        for (int i = tid; i < wmax; i += GR_THREADS) rdy[i] = 0;
     for (int e = tid; e < E; e += GR_THREADS) {
         cnt[e] = 0;
         fill[e] = 0;
@@ -2912,40 +2917,43 @@ int group_work_max(const Shape &s, int n) {
 
 template <bool SORT>
 static hipError_t group_go(const int32_t *idx, int n, int E, int ch, int chd, int wmax, int32_t *counts,
-                           int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
+                           int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, int32_t *rdy,
+                           hipStream_t st) {
     const size_t lds = n <= GR_LDS_ENTRIES ? 4 * (size_t)n : 0;
     hipError_t e = allow_lds((const void *)k_group<SORT>, lds);
     if (e != hipSuccess) return e;
     TG_LAUNCH(k_group<SORT>, dim3(1), dim3(GR_THREADS), lds, st, idx, n, E, ch, chd, wmax, counts, offsets, entries,
-              work, work_n, nullptr, 0);
+              work, work_n, nullptr, 0, rdy);
     return hipGetLastError();
 }
 
 hipError_t launch_group(const Shape &s, const int32_t *idx, int n, int32_t *counts, int32_t *offsets,
                         int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
     return group_go<false>(idx, n, s.E, gu_chunk(s.nbH), dn_chunk(s.nbI, s.I), group_work_max(s, n), counts,
-                           offsets, entries, work, work_n, st);
+                           offsets, entries, work, work_n, nullptr, st);
 }
 
 hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *ecnt, int32_t *counts,
-                               int32_t *offsets, int32_t *work, int32_t *work_n, hipStream_t st) {
+                               int32_t *offsets, int32_t *work, int32_t *work_n, int32_t *rdy, hipStream_t st) {
     const int wmax = group_work_max(s, n, ch);
     if (ch > 32)  // items of several M-tiles: largest first
         TG_LAUNCH((k_group<true, true>), dim3(1), dim3(GR_THREADS), 0, st, nullptr, n, s.E, ch, ch, wmax, counts,
-                  offsets, nullptr, work, work_n, ecnt, cap);
+                  offsets, nullptr, work, work_n, ecnt, cap, rdy);
     else
         TG_LAUNCH((k_group<false, true>), dim3(1), dim3(GR_THREADS), 0, st, nullptr, n, s.E, ch, ch, wmax, counts,
-                  offsets, nullptr, work, work_n, ecnt, cap);
+                  offsets, nullptr, work, work_n, ecnt, cap, rdy);
     return hipGetLastError();
 }
 
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
-                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, hipStream_t st) {
+                                int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, int32_t *rdy,
+                                hipStream_t st) {
     // items of several M-tiles: largest first (one-tile items are all alike)
     if (ch > 32)
         return group_go<true>(idx, n, s.E, ch, ch, group_work_max(s, n, ch), counts, offsets, entries, work, work_n,
-                              st);
-    return group_go<false>(idx, n, s.E, ch, ch, group_work_max(s, n, ch), counts, offsets, entries, work, work_n, st);
+                              rdy, st);
+    return group_go<false>(idx, n, s.E, ch, ch, group_work_max(s, n, ch), counts, offsets, entries, work, work_n,
+                           rdy, st);
 }
 
 template <int NT, int UNR>
