@@ -200,7 +200,7 @@ struct Scratch {
     float *dec_part = nullptr;
     uint64_t *dec_ow = nullptr;
     uint32_t *fc_cnt = nullptr;   // arrival counts of the combine in the down launch (zero between calls)
-    int32_t *ecnt = nullptr;      // E: entries placed per expert by route_q8 (zero between calls)
+    int32_t *ecnt = nullptr;      // E: entries placed per expert by route_q8, then its arrival count (zero between calls)
     int32_t *ent_cap = nullptr;   // E * T: per-expert entry lists of capacity T (chains path: over raw, unused there)
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
@@ -241,7 +241,7 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     c.dec_part = reinterpret_cast<float *>(take(4 * tg::dec_part_floats(s)));
     c.dec_ow = reinterpret_cast<uint64_t *>(take(8 * tg::dec_ow_words(s)));
     c.fc_cnt = reinterpret_cast<uint32_t *>(take(4 * tg::fuse_count_words(s, T)));
-    c.ecnt = reinterpret_cast<int32_t *>(take(4 * (size_t)s.E));
+    c.ecnt = reinterpret_cast<int32_t *>(take(4 * ((size_t)s.E + 1)));  // + route_q8's arrival count
     c.dec = dec0;
     c.dec_bytes = off;
     c.dec_lw = reinterpret_cast<uint64_t *>(dec0);
@@ -557,21 +557,37 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
     // expert per 128 tokens on one counter, cost more than the grouping kernel
     // saves: 2048 tokens, route_q8 10.6 -> 32.4 us for group 12.6 -> 7.1 us)
     const bool mfma = mfma_usable(a, T), placed = mfma && chains;
+    const int n = T * s.k;
+    const int mt = mfma ? tg::mfma_tiles(s, T) : 0, ch = mfma ? tg::mfma_item_entries(s, mt) : 0;
+    const int wmax = mfma ? tg::group_work_max(s, n, ch) : 0;
+    // gate/up and down in one launch where the one-tile kernels take it
+    // (the combine stays a launch of its own)
+    const bool gd = mfma && tg::gd_fuses(s, mt) && !tg::down_fuses(s, mt, T) && wmax <= tg::group_work_max(s, n);
+    int32_t *rdy = gd ? c.rdy : nullptr;
+    // one-tile items over the placed lists: the last route_q8 block builds
+    // the work items (no grouping launch)
+    tg::RouteGroup rg;
+    const bool q8_groups = placed && ch <= 32 && tg::route_groups_on();
+    if (q8_groups) {
+        rg.counts = c.counts;
+        rg.offsets = c.offsets;
+        rg.work = c.work;
+        rg.work_n = c.work_n;
+        rg.rdy = rdy;
+        rg.arrive = reinterpret_cast<uint32_t *>(c.ecnt + s.E);
+        rg.ch = ch;
+        rg.wmax = wmax;
+    }
     PROFILED("route_q8", st,
              tg::launch_route_q8(c.raw, chains ? c.D : nullptr, x, norm_of(a, layer), T, s.E, s.H, s.k, eps, c.idx,
-                                 c.w, c.xq, c.xd, c.xs, placed ? c.ecnt : nullptr, placed ? c.ent_cap : nullptr, st));
-    const int n = T * s.k;
+                                 c.w, c.xq, c.xd, c.xs, placed ? c.ecnt : nullptr, placed ? c.ent_cap : nullptr, rg,
+                                 st));
     if (mfma) {
-        const int mt = tg::mfma_tiles(s, T), ch = tg::mfma_item_entries(s, mt), wmax = tg::group_work_max(s, n, ch);
         int32_t *ent = placed ? c.ent_cap : c.entries;
-        // gate/up and down in one launch where the one-tile kernels take it
-        // (the combine stays a launch of its own)
-        const bool gd = tg::gd_fuses(s, mt) && !tg::down_fuses(s, mt, T) && wmax <= tg::group_work_max(s, n);
-        int32_t *rdy = gd ? c.rdy : nullptr;
-        if (placed)
+        if (!q8_groups && placed)
             PROFILED("group", st,
                      tg::launch_group_placed(s, n, ch, T, c.ecnt, c.counts, c.offsets, c.work, c.work_n, rdy, st));
-        else
+        else if (!q8_groups)
             PROFILED("group", st,
                      tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
                                               rdy, st));

@@ -262,9 +262,22 @@ bool grouped_shape_ok(const Shape &s);
 // raw [T][E] router dots, or chains [H/32][T][E] (non-null: summed first)
 // ent_cap non-null: each token's k entries also go into per-expert lists
 // ent_cap[e * T + i] (i from the atomic count ecnt[e], zero before the call)
+// G.arrive non-null (with ent_cap): the last block to finish also builds the
+// work items of the placed lists (items of at most G.ch entries, both lists
+// alike, at most G.wmax each), clears ecnt and G.rdy (may be null) and sets
+// *G.arrive (one word, zero between calls) back to zero: the grouping
+// kernel's work in the same launch.
+struct RouteGroup {
+    int32_t *counts = nullptr, *offsets = nullptr, *work = nullptr, *work_n = nullptr, *rdy = nullptr;
+    uint32_t *arrive = nullptr;
+    int ch = 0, wmax = 0;
+};
 hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                           int32_t *ecnt, int32_t *ent_cap, hipStream_t st);
+                           int32_t *ecnt, int32_t *ent_cap, const RouteGroup &G, hipStream_t st);
+// TG_ROUTE_GROUP not 0 (read per call): route_q8 builds the placed lists'
+// one-tile work items itself
+bool route_groups_on();
 // Few tokens: the router's per-group fma chains [H/32][T][E], for
 // launch_route_q8 to add (T < 128, E <= 128 and a multiple of 32).
 bool route_chains_usable(int T, int E, int H);

@@ -2104,6 +2104,46 @@ __global__ __launch_bounds__(256) void k_dec_part(const float *__restrict__ Wr, 
 // token in its own slot order, so every output is deterministic and equal
 // to the per-token path bit for bit.
 
+template <int N>
+TG_DEV void scan_256_n(int (&v)[N], int n, int *tmp);
+
+// The work items of the placed lists (k_group<false, true>'s, built by the
+// last k_route_q8 block): thread e < E takes expert e's count (from the
+// device-scope counts every block added to), clears it, and lists its items
+// of at most G.ch entries from e * T in both lists.  Every thread calls it.
+TG_DEV void route_group_items(const RouteGroup &G, int E, int T, int32_t *ecnt, int *tmp) {
+    const int tid = threadIdx.x, ch = G.ch;
+    if (G.rdy)
+        for (int i = tid; i < G.wmax; i += RO_THREADS) G.rdy[i] = 0;
+    int c = 0;
+    if (tid < E) {
+        const int v = __hip_atomic_load(ecnt + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c = v < T ? v : T;  // never past the list
+        __hip_atomic_store(ecnt + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    int sv[2] = {c, (c + ch - 1) / ch};
+    scan_256_n<2>(sv, E, tmp);
+    if (tid < E) {
+        const int o = sv[0], bg = sv[1], ng = (c + ch - 1) / ch, ob = tid * T;
+        G.offsets[tid] = o;
+        G.counts[tid] = c;
+        for (int i = 0; i < ng && bg + i < G.wmax; i++) {
+            const int it3[3] = {tid, ob + i * ch, c - i * ch < ch ? c - i * ch : ch};
+#pragma unroll
+            for (int q = 0; q < 3; q++) {
+                G.work[3 * (size_t)(bg + i) + q] = it3[q];
+                G.work[3 * ((size_t)G.wmax + bg + i) + q] = it3[q];
+            }
+        }
+        if (tid == E - 1) {
+            G.offsets[E] = o + c;
+            const int nw = bg + ng < G.wmax ? bg + ng : G.wmax;
+            G.work_n[0] = nw;
+            G.work_n[1] = nw;
+        }
+    }
+}
+
 // raw: the router dots [T][E], or (chains != null) the group chains of
 // k_route_chains [G][T][E], which thread e adds in ascending group order
 // first (the same sums as k_route's).
@@ -2114,7 +2154,8 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
                                                          int32_t *__restrict__ idx,
                                                          float *__restrict__ w, int8_t *__restrict__ xq,
                                                          float *__restrict__ xd, int *__restrict__ xs,
-                                                         int32_t *__restrict__ ecnt, int32_t *__restrict__ ent_cap) {
+                                                         int32_t *__restrict__ ecnt, int32_t *__restrict__ ent_cap,
+                                                         RouteGroup G) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float rsum[RO_THREADS];
     RouteLds L = route_lds(smem, H);
@@ -2175,6 +2216,19 @@ __global__ __launch_bounds__(RO_THREADS) void k_route_q8(const float *__restrict
 #pragma unroll
             for (int c = 0; c < 8; c++) v[c] = (xv[ps][c] * sc) * g8[c];
             q8_group8(v, i0 < H, i0, xq + (size_t)t * H, xd + (size_t)t * nbH, xs + (size_t)t * nbH);
+        }
+    }
+    if (G.arrive) {  // uniform: the last block to finish builds the work items
+        __shared__ int last;
+        __shared__ int tmp[4 * 2];
+        __syncthreads();  // this block's placements are done (their atomics returned)
+        if (tid == 0)
+            last = __hip_atomic_fetch_add(G.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(T - 1);
+        __syncthreads();
+        if (last) {
+            if (tid == 0) __hip_atomic_store(G.arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            route_group_items(G, E, T, ecnt, tmp);
         }
     }
 }
@@ -2870,7 +2924,10 @@ bool grouped_shape_ok(const Shape &s) {
 
 hipError_t launch_route_q8(const float *raw, const float *chains, const float *x, const float *gn, int T, int E,
                            int H, int k, float eps, int32_t *idx, float *w, int8_t *xq, float *xd, int *xs,
-                           int32_t *ecnt, int32_t *ent_cap, hipStream_t st) {
+                           int32_t *ecnt, int32_t *ent_cap, const RouteGroup &G, hipStream_t st) {
+    if (G.arrive && (!ent_cap || !ecnt || G.ch <= 0 || G.wmax <= 0 || E > RO_THREADS || !G.counts || !G.offsets ||
+                     !G.work || !G.work_n))
+        return hipErrorInvalidValue;
     // x in registers: NP passes of 8 x 256 elements.  The raw-dot form (many
     // tokens, one block each) takes as few passes as H needs, so its blocks
     // need fewer registers and more of them are resident (H 2048: 52 VGPRs,
@@ -2883,13 +2940,18 @@ hipError_t launch_route_q8(const float *raw, const float *chains, const float *x
         hipError_t e = allow_lds((const void *)kern, lds);
         if (e != hipSuccess) return e;
         TG_LAUNCH(kern, dim3(T), dim3(RO_THREADS), lds, st, raw, chains, T, x, gn, E, H, k, eps, idx, w, xq, xd, xs,
-                  ecnt, ent_cap);
+                  ecnt, ent_cap, G);
         return hipGetLastError();
     };
     if (chains) return go(k_route_q8<true, RO_MAXPASS>);
     if (np == 1) return go(k_route_q8<false, 1>);
     if (np == 2) return go(k_route_q8<false, 2>);
     return go(k_route_q8<false, RO_MAXPASS>);
+}
+
+bool route_groups_on() {
+    const char *v = getenv("TG_ROUTE_GROUP");
+    return !(v && v[0] == '0');
 }
 
 bool route_chains_usable(int T, int E, int H) { return T < 128 && route_chains_ok(E, H); }
