@@ -829,11 +829,17 @@ def prefill_leg(args, torch, call, arena, L, K=20, W=2):
         blk.step(xb)
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
-    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "combine")
+    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
-    n_gu, ms_gu = kern["gateup_mfma"]
-    gu_ops = 2 * T * K_TOP * 2 * H * I
+    if "gu_down_mfma" in kern:  # gate/up and down in one launch: the roofline covers both products
+        n_gu, ms_gu = kern["gu_down_mfma"]
+        gu_ops = 2 * T * K_TOP * 3 * H * I
+        roof_kernel, roof_traffic = "k_mfma16_gd (gate/up + down)", profiled_traffic("k_mfma16_gd")
+    else:
+        n_gu, ms_gu = kern["gateup_mfma"]
+        gu_ops = 2 * T * K_TOP * 2 * H * I
+        roof_kernel, roof_traffic = "k_mfma16<true> (gate/up)", profiled_traffic("k_mfma16/gate_up")
     achieved = gu_ops / (ms_gu / n_gu * 1e-3)
     layer_us = sum(kern_us.values())
 
@@ -862,10 +868,9 @@ def prefill_leg(args, torch, call, arena, L, K=20, W=2):
         "mfma_frac": round(tops * 1e12 / MFMA_INT8_PEAK, 4),
         "kernel_avg_us": kern_us,
         "layer_kernel_us": round(layer_us, 2),
-        "roofline": {"bound": "mfma", "kernel": "k_mfma16<true> (gate/up)", "ops_per_launch": gu_ops,
+        "roofline": {"bound": "mfma", "kernel": roof_kernel, "ops_per_launch": gu_ops,
                      "achieved": round(achieved / 1e12, 1), "peak": MFMA_INT8_PEAK / 1e12, "unit": "TOPS",
-                     "frac": round(achieved / MFMA_INT8_PEAK, 4),
-                     "traffic": profiled_traffic("k_mfma16/gate_up")},
+                     "frac": round(achieved / MFMA_INT8_PEAK, 4), "traffic": roof_traffic},
         "cpu_baseline": cpu,
     }
 

@@ -196,3 +196,49 @@ def test_fused_gate_up_down_wait_failure(O, tglib, inject):
         else:
             os.environ["TG_FUSE_GD"] = old
         a.close()
+
+
+def test_fused_x16_wait_failure(O, tglib, inject):
+    """The fused gate/up + down launch of the 16 x 16 items (about 250
+    entries per expert): with the hook, item 0's gate/up blocks never count
+    in, so its down blocks' waits run out: some rows come back NaN, the host
+    call returns TG_E_HIP, and the next call on the same arena equals the
+    oracle again."""
+    import os
+    from tinygiant_amd.arena import HBMExpertArena
+    H, I, E, k, T = 512, 256, 32, 8, 1000
+    lb, r = O.synth_layer(97, 0, H, I, E)
+    a = HBMExpertArena(1, E, H, I, k)
+    old = os.environ.get("TG_FUSE_GD16")
+    os.environ["TG_FUSE_GD16"] = "1"
+    try:
+        a.load_layer(0, lb)
+        a.load_router(0, r)
+        x = O.synth_normal(97, O.stream_id(0, 7, 4), 1.0, T * H).reshape(T, H)
+        ref, _, _, _ = O.moe_layer(lb, r, H, I, E, k, x)
+        gpu_note("fused 16 x 16 gate/up + down: clean call")
+        rc, out = host_layer(tglib, a, 0, x)
+        assert rc == 0 and np.array_equal(bits(out), bits(ref))
+
+        gpu_note("fused 16 x 16 gate/up + down: item 0 never counted in, 4096 tries per wait")
+        inject(4096, 0)
+        rc, bad = host_layer(tglib, a, 0, x)
+        assert rc == TG_E_HIP
+        assert "ran out of tries" in tglib.tg_last_error().decode()
+        nan_rows = np.isnan(bad).any(axis=1)
+        assert 0 < nan_rows.sum() < T
+        assert np.array_equal(bits(bad[~nan_rows]), bits(ref[~nan_rows]))
+
+        gpu_note("fused 16 x 16 gate/up + down: hook cleared")
+        tglib.tg_debug_fault_inject(0, -1)
+        for rep in range(2):
+            rc, out = host_layer(tglib, a, 0, x)
+            assert rc == 0 and np.array_equal(bits(out), bits(ref)), f"rep {rep}"
+        assert tglib.tg_arena_status(a.handle) == 0
+    finally:
+        tglib.tg_debug_fault_inject(0, -1)
+        if old is None:
+            os.environ.pop("TG_FUSE_GD16", None)
+        else:
+            os.environ["TG_FUSE_GD16"] = old
+        a.close()

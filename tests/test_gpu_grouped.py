@@ -243,21 +243,24 @@ def test_fused_combine_counts_across_calls(O, tglib):
         a.close()
 
 
-# (H, I, E, k, token counts): gate/up K of 8 chunks (activations staged once)
-# and of 16 (staged per chunk); the placed-entry grouping below 128 tokens and
-# the listing one from 128
+# (H, I, E, k, token counts): one-tile items with a gate/up K of 8 chunks
+# (activations staged once) and of 16 (staged per chunk), the placed-entry
+# grouping below 128 tokens and the listing one from 128; 16 x 16 items
+# (about 250 and 160 entries per expert: whole items, and experts split over
+# two items)
 @pytest.mark.parametrize("H,I,E,k,Ts", [(512, 256, 32, 8, (40, 9, 64)), (2048, 768, 128, 8, (64, 200, 3)),
-                                        (4096, 1536, 128, 8, (32, 5))])
+                                        (4096, 1536, 128, 8, (32, 5)), (512, 256, 32, 8, (1000, 640, 1000))])
 def test_fused_gate_up_down_across_calls(O, tglib, H, I, E, k, Ts):
-    """One-tile work items run gate/up and down in one launch (down blocks
-    wait, bounded, for their item's gate/up blocks to store h; the grouping
-    kernel clears the per-item counts for every call).  Calls of different
-    sizes on one arena, each made with the fused launch and with the two
-    launches (TG_FUSE_GD=0, read per call), all equal the oracle bit for bit."""
+    """Gate/up and down of the one-tile and the 16 x 16 work items run in one
+    launch (down blocks wait, bounded, for their item's gate/up blocks to
+    store h; the grouping kernel clears the per-item counts for every call).
+    Calls of different sizes on one arena, each made with the fused launches
+    and with the two launches (TG_FUSE_GD=0 and TG_FUSE_GD16=0, read per
+    call), all equal the oracle bit for bit."""
     import os
     from tinygiant_amd.moe import MoEBlock
     a, layers, routers = make_arena(O, 1, H, I, E, k, seed=41)
-    old = os.environ.get("TG_FUSE_GD")
+    old = {v: os.environ.get(v) for v in ("TG_FUSE_GD", "TG_FUSE_GD16")}
     try:
         blk = MoEBlock(a)
         for i, T in enumerate(Ts):
@@ -266,14 +269,16 @@ def test_fused_gate_up_down_across_calls(O, tglib, H, I, E, k, Ts):
             xd = dev(x)
             for mode in ("1", "0", "1"):
                 os.environ["TG_FUSE_GD"] = mode
-                gpu_note(f"fused gate/up + down H={H} T={T} TG_FUSE_GD={mode}")
+                os.environ["TG_FUSE_GD16"] = mode
+                gpu_note(f"fused gate/up + down H={H} T={T} fused={mode}")
                 got = host(blk.forward(0, xd))
                 assert np.array_equal(bits(got), bits(ref)), \
                     f"T={T} mode {mode}: max |diff| {np.max(np.abs(got - ref)):.3e}"
         assert tglib.tg_arena_status(a.handle) == 0
     finally:
-        if old is None:
-            os.environ.pop("TG_FUSE_GD", None)
-        else:
-            os.environ["TG_FUSE_GD"] = old
+        for v, val in old.items():
+            if val is None:
+                os.environ.pop(v, None)
+            else:
+                os.environ[v] = val
         a.close()

@@ -563,7 +563,9 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
     // gate/up and down in one launch where the one-tile kernels take it
     // (the combine stays a launch of its own)
     const bool gd = mfma && tg::gd_fuses(s, mt) && !tg::down_fuses(s, mt, T) && wmax <= tg::group_work_max(s, n);
-    int32_t *rdy = gd ? c.rdy : nullptr;
+    const bool gd16 =
+        mfma && !gd && tg::gd16_fuses(s, mt) && !tg::down_fuses(s, mt, T) && wmax <= tg::group_work_max(s, n);
+    int32_t *rdy = gd || gd16 ? c.rdy : nullptr;
     // one-tile items over the placed lists: the last route_q8 block builds
     // the work items (no grouping launch)
     tg::RouteGroup rg;
@@ -591,15 +593,20 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
             PROFILED("group", st,
                      tg::launch_group_chunked(s, c.idx, n, ch, c.counts, c.offsets, c.entries, c.work, c.work_n,
                                               rdy, st));
-        if (gd) {
+        if (gd || gd16) {
             tg::GdArgs G;
             G.rdy = c.rdy;
             G.err = c.dec_err;
             G.spin = tg::poll_spin_limit();
             G.drop = tg::poll_drop();
-            PROFILED("gu_down_mfma", st,
-                     tg::launch_gu_down_ms(lp, s, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.hq, c.hd, c.hs, c.D, G,
-                                           st));
+            if (gd)
+                PROFILED("gu_down_mfma", st,
+                         tg::launch_gu_down_ms(lp, s, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.hq, c.hd, c.hs, c.D,
+                                               G, st));
+            else
+                PROFILED("gu_down_mfma", st,
+                         tg::launch_gu_down_x16(lp, s, wmax, c.work, c.work_n, ent, c.xq, c.xd, c.hq, c.hd, c.hs,
+                                                c.D, G, st));
             PROFILED("combine", st, tg::launch_combine(c.D, c.w, T, s.H, s.k, resid, out, st));
             return TG_OK;
         }

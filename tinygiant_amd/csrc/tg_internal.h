@@ -332,6 +332,12 @@ bool gd_fuses(const Shape &s, int mt);
 hipError_t launch_gu_down_ms(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
                              const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
                              int8_t *hq, float *hd, int *hs, float *D, const GdArgs &G, hipStream_t st);
+// The same for the 16 x 16 items (mt == 4 with items of more than 128
+// entries: prefill and large batches); TG_FUSE_GD16 not 0 (read per call)
+bool gd16_fuses(const Shape &s, int mt);
+hipError_t launch_gu_down_x16(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                              const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                              int8_t *hq, float *hd, int *hs, float *D, const GdArgs &G, hipStream_t st);
 // the poll bound and the withheld line / item of the failure-channel hook
 uint32_t poll_spin_limit();
 int poll_drop();

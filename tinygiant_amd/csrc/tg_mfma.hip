@@ -500,14 +500,17 @@ TG_DEV int half_sum(int v) {
 // at rdy[wi]; a down block waits (bounded) until all `need` gate/up blocks of
 // its item have, then stages h at agent scope.
 template <bool PAIR, bool SCV, bool FULL, bool GD>
-TG_DEV __attribute__((always_inline)) void ms_item(const uint8_t *__restrict__ layer_pl, const Shape &s,
+TG_DEV __attribute__((always_inline)) void ms_item(const uint8_t *__restrict__ layer_pl, const Shape s,
                                                    const int32_t *__restrict__ work,
                                                    const int32_t *__restrict__ work_n,
                                                    const int32_t *__restrict__ entries,
                                                    const int8_t *__restrict__ aq, const float *__restrict__ ad,
                                                    int8_t *__restrict__ oq, float *__restrict__ od,
-                                                   int *__restrict__ os, float *__restrict__ D, const FuseArgs &F,
-                                                   int wi, int bx, uint8_t *smem, const GdArgs &G) {
+                                                   int *__restrict__ os, float *__restrict__ D, const FuseArgs F,
+                                                   int wi, int bx, const GdArgs G) {
+    // the launch's dynamic LDS, named here so its addresses stay LDS
+    // addresses (through a generic pointer each cast to LDS adds a null test)
+    extern __shared__ __align__(16) uint8_t smem[];
     constexpr int M = 32, NW = MS_NW, NT = NW * 64, TP = 2 * MF_KC;
     constexpr int NTP = M * TP / NT, NDX = M * MF_KC / NT;
     static_assert(NT % TP == 0 && NT % MF_KC == 0 && MF_KC == 8 && NTP >= 1 && NDX >= 1, "staging map");
@@ -871,9 +874,8 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small(const uint8_t *__rest
                                                            const int8_t *__restrict__ aq, const float *__restrict__ ad,
                                                            int8_t *__restrict__ oq, float *__restrict__ od,
                                                            int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
-    extern __shared__ __align__(16) uint8_t smem[];
     ms_item<PAIR, SCV, FULL, false>(layer_pl, s, work, work_n, entries, aq, ad, oq, od, os, D, F, (int)blockIdx.y,
-                                    (int)blockIdx.x, smem, GdArgs());
+                                    (int)blockIdx.x, GdArgs());
 }
 
 // Gate/up and down of the one-tile items in one launch: blocks [0, gxg wmax)
@@ -892,15 +894,14 @@ __global__ __launch_bounds__(MS_NW * 64) void k_mfma_small_gd(const uint8_t *__r
                                                               const float *__restrict__ xd, int8_t *hq, float *hd,
                                                               int *hs, float *__restrict__ D, GdArgs G, int gxg,
                                                               int gxd, int wmax) {
-    extern __shared__ __align__(16) uint8_t smem[];
     const int b = (int)blockIdx.x, ng = gxg * wmax;
     if (b < ng) {
         ms_item<true, SCVG, FULLG, true>(layer_pl, s, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, FuseArgs(),
-                                         b / gxg, b % gxg, smem, G);
+                                         b / gxg, b % gxg, G);
     } else {
         const int d = b - ng;
         ms_item<false, true, true, true>(layer_pl, s, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D,
-                                         FuseArgs(), d / gxd, d % gxd, smem, G);
+                                         FuseArgs(), d / gxd, d % gxd, G);
     }
 }
 
@@ -970,24 +971,27 @@ TG_DEV long xt_unpack(uint2 w, int sh) {
     return (long)(((uint64_t)hi << 32) | lo);
 }
 
-template <bool PAIR>
-__global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict__ layer_pl, Shape s,
-                                                       const int32_t *__restrict__ work,
-                                                       const int32_t *__restrict__ work_n,
-                                                       const int32_t *__restrict__ entries,
-                                                       const int8_t *__restrict__ aq, const float *__restrict__ ad,
-                                                       int8_t *__restrict__ oq, float *__restrict__ od,
-                                                       int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
+// One block of the 16 x 16 kernels: item wi, row tile bx.  GD: gate/up and
+// down blocks of the same launch (k_mfma16_gd), as in the one-tile kernels:
+// a gate/up block stores h at agent scope and counts itself in at rdy[wi]
+// once the stores are acknowledged; a down block waits (bounded) for all
+// `need` gate/up blocks of its item and stages h at agent scope.
+template <bool PAIR, bool GD>
+TG_DEV __attribute__((always_inline)) void x16_item(const uint8_t *__restrict__ layer_pl, const Shape s,
+                                                    const int32_t *__restrict__ work,
+                                                    const int32_t *__restrict__ work_n,
+                                                    const int32_t *__restrict__ entries,
+                                                    const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                    int8_t *__restrict__ oq, float *__restrict__ od,
+                                                    int *__restrict__ os, float *__restrict__ D, const FuseArgs F,
+                                                    int wi, int bx, const GdArgs G) {
+    // the launch's dynamic LDS, named here so its addresses stay LDS
+    // addresses (through a generic pointer each cast to LDS adds a null test)
+    extern __shared__ __align__(16) uint8_t smem[];
     constexpr int NW = XT_NW, ROWS = XtLds::ROWS;
     constexpr int NACT = ROWS * XT_NP / 64;          // activation load instructions per chunk (full item)
     constexpr int NAXS = XT_KC * 16 * XT_CS / 64;    // activation-scale load instructions per chunk
     static_assert(NACT % NW == 0 && NAXS % NW == 0, "staging split");
-    extern __shared__ __align__(16) uint8_t smem[];
-    // blocks are dealt to the 8 XCDs in turn (block b on XCD b % 8): the gx
-    // blocks of one item get ids 8 apart, so they share one XCD's L2 (the
-    // item's activations are fetched into one L2, not eight)
-    const int gx = PAIR ? s.I / (32 * (NW / 2)) : s.H / (32 * NW), bid = (int)blockIdx.x, rest = bid >> 3;
-    const int bx = rest % gx, wi = (rest / gx) * 8 + (bid & 7);
     if (wi >= work_n[0]) return;  // uniform over the block
     const int e = work[3 * wi], o = work[3 * wi + 1], c = work[3 * wi + 2];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, cl = lane & 15;
@@ -1028,19 +1032,30 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
     const int woff1 = (wr0 + 16) * nb * 16 + xt_wslot(wsl, wr0 + 16) * 16;
     const int soffw = (lane >> 1) * nb * 2 + (lane & 1) * 4;
 
-    // activations and their scales: one chunk ahead, two buffers
+    // activations and their scales: one chunk ahead, two buffers (GD down
+    // blocks: h of this launch, at agent scope)
+    constexpr bool COH = GD && !PAIR;
     auto stage_act = [&](int ch) {
         const int q = ch & 1;
 #pragma unroll
         for (int u = 0; u < NACT / NW; u++) {
             const int j = u * NW + wave;
-            if (j * 64 < ct_n * 16 * XT_NP)  // rows of column tiles in use (uniform per instruction)
-                lds_dma16(aq + aoff[u] + ch * XT_RB, lds_addr(smem, XtLds::ACT + q * ROWS * XT_RB + j * 1024));
+            if (j * 64 < ct_n * 16 * XT_NP) {  // rows of column tiles in use (uniform per instruction)
+                const uint32_t m0 = lds_addr(smem, XtLds::ACT + q * ROWS * XT_RB + j * 1024);
+                if constexpr (COH)
+                    lds_dma16_coh(aq + aoff[u] + ch * XT_RB, m0);
+                else
+                    lds_dma16(aq + aoff[u] + ch * XT_RB, m0);
+            }
         }
 #pragma unroll
         for (int u = 0; u < NAXS / NW; u++) {
             const int j = u * NW + wave;
-            lds_dma4(ad + soff[u] + ch * XT_KC, lds_addr(smem, XtLds::AXS + (q * XT_KC * 16 * XT_CS + j * 64) * 4));
+            const uint32_t m0 = lds_addr(smem, XtLds::AXS + (q * XT_KC * 16 * XT_CS + j * 64) * 4);
+            if constexpr (COH)
+                lds_dma4_coh(ad + soff[u] + ch * XT_KC, m0);
+            else
+                lds_dma4(ad + soff[u] + ch * XT_KC, m0);
         }
     };
     // the wave's weight rows and their scales (streamed from HBM): two
@@ -1068,10 +1083,36 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
     float *tab = reinterpret_cast<float *>(smem + XtLds::TAB) + wave * XT_KC * 2 * 2 * 16;
     const int sh = g < 2 ? 4 : 0;  // low nibbles for elements 0..15, high for 16..31
 
-    // issue order: w(0), act(0), w(1); then per chunk ch: act(ch + 1), w(ch + 2)
-    stage_w(0);
-    stage_act(0);
-    if (nch > 1) stage_w(1);
+    // GD down block: every gate/up block of the item has counted in
+    // (bounded; when the wait runs out the rows are stored as NaN and *err
+    // set).  Its first weight chunk is in flight meanwhile.
+    bool gd_bad = false;
+    if constexpr (COH) {
+        __shared__ int gd_flag;
+        stage_w(0);
+        if (tid == 0) {
+            uint32_t tries = 0;
+            int bad = 0;
+            while (__hip_atomic_load(G.rdy + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G.need) {
+                if (++tries >= G.spin) {
+                    bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            gd_flag = bad;
+            if (bad) __hip_atomic_store(G.err, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        gd_bad = gd_flag != 0;
+        stage_act(0);
+        if (nch > 1) stage_w(1);
+    } else {
+        // issue order: w(0), act(0), w(1); then per chunk ch: act(ch + 1), w(ch + 2)
+        stage_w(0);
+        stage_act(0);
+        if (nch > 1) stage_w(1);
+    }
     auto run = [&](auto ctv) {
         constexpr int CT = decltype(ctv)::value;
         for (int ch = 0; ch < nch; ch++) {
@@ -1249,17 +1290,33 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
             if (on) {
                 const int ent = entries[o + t];
                 int8_t *dst = oq + (size_t)ent * s.I + rb + 4 * g;
+                const size_t si = (size_t)ent * s.nbI + nt;
 #pragma unroll
                 for (int rt = 0; rt < 2; rt++) {
                     const uint32_t w = (uint32_t)(qv[rt][0] & 0xFF) | ((uint32_t)(qv[rt][1] & 0xFF) << 8) |
                                        ((uint32_t)(qv[rt][2] & 0xFF) << 16) | ((uint32_t)(qv[rt][3] & 0xFF) << 24);
-                    *reinterpret_cast<uint32_t *>(dst + 16 * rt) = w;
+                    uint32_t *wp = reinterpret_cast<uint32_t *>(dst + 16 * rt);
+                    if constexpr (GD)  // read by down blocks of this launch
+                        __hip_atomic_store(wp, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        *wp = w;
                 }
                 if (g == 0) {
-                    od[(size_t)ent * s.nbI + nt] = h2f(f2h(d));
-                    os[(size_t)ent * s.nbI + nt] = sum;
+                    if constexpr (GD) {
+                        st_coh(od + si, h2f(f2h(d)));
+                        __hip_atomic_store(os + si, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        od[si] = h2f(f2h(d));
+                        os[si] = sum;
+                    }
                 }
             }
+        }
+        if constexpr (GD) {
+            __builtin_amdgcn_s_waitcnt(VMCNT0);  // this thread's h stores acknowledged
+            __syncthreads();                     // ... every thread's
+            if (tid == 0 && wi != G.drop)
+                __hip_atomic_fetch_add(G.rdy + wi, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     } else {
         const bool coh = F.cnt != nullptr;  // uniform
@@ -1270,18 +1327,67 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict
                 float *dst = D + (size_t)entries[o + t] * s.H + rb + 4 * g;
 #pragma unroll
                 for (int rt = 0; rt < 2; rt++) {
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) v[r] = gd_bad ? __builtin_nanf("") : acc[rt][ct][r];
                     if (coh) {
-                        st_coh2(dst + 16 * rt, acc[rt][ct][0], acc[rt][ct][1]);
-                        st_coh2(dst + 16 * rt + 2, acc[rt][ct][2], acc[rt][ct][3]);
+                        st_coh2(dst + 16 * rt, v[0], v[1]);
+                        st_coh2(dst + 16 * rt + 2, v[2], v[3]);
                     } else {
-                        *reinterpret_cast<float4 *>(dst + 16 * rt) =
-                            make_float4(acc[rt][ct][0], acc[rt][ct][1], acc[rt][ct][2], acc[rt][ct][3]);
+                        *reinterpret_cast<float4 *>(dst + 16 * rt) = make_float4(v[0], v[1], v[2], v[3]);
                     }
                 }
             }
         }
         // NW * 32 == FC_ROWS: the block's rows are output tile bx
         if (F.cnt) fused_combine<XT_NW * 64>(F, s, entries, o, c, bx, D, smem);
+    }
+}
+
+// blocks are dealt to the 8 XCDs in turn (block b on XCD b % 8): the gx
+// blocks of one item get ids 8 apart, so they share one XCD's L2 (the
+// item's activations are fetched into one L2, not eight)
+TG_DEV void x16_place(int bid, int gx, int &wi, int &bx) {
+    const int rest = bid >> 3;
+    bx = rest % gx;
+    wi = (rest / gx) * 8 + (bid & 7);
+}
+
+template <bool PAIR>
+__global__ __launch_bounds__(XT_NW * 64) void k_mfma16(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                       const int32_t *__restrict__ work,
+                                                       const int32_t *__restrict__ work_n,
+                                                       const int32_t *__restrict__ entries,
+                                                       const int8_t *__restrict__ aq, const float *__restrict__ ad,
+                                                       int8_t *__restrict__ oq, float *__restrict__ od,
+                                                       int *__restrict__ os, float *__restrict__ D, FuseArgs F) {
+    const int gx = PAIR ? s.I / (32 * (XT_NW / 2)) : s.H / (32 * XT_NW);
+    int wi, bx;
+    x16_place((int)blockIdx.x, gx, wi, bx);
+    x16_item<PAIR, false>(layer_pl, s, work, work_n, entries, aq, ad, oq, od, os, D, F, wi, bx, GdArgs());
+}
+
+// Gate/up and down of the 16 x 16 items in one launch: blocks [0, gxg wm8)
+// are the gate/up blocks, the rest the down blocks (each part placed as in
+// k_mfma16).  Blocks are dispatched in id order on each XCD and gate/up
+// blocks never wait, so the down blocks' waits end (as in k_mfma_small_gd);
+// the down blocks of the items done first fill the gate/up launch's tail.
+__global__ __launch_bounds__(XT_NW * 64) void k_mfma16_gd(const uint8_t *__restrict__ layer_pl, Shape s,
+                                                          const int32_t *__restrict__ work,
+                                                          const int32_t *__restrict__ work_n,
+                                                          const int32_t *__restrict__ entries,
+                                                          const int8_t *__restrict__ xq, const float *__restrict__ xd,
+                                                          int8_t *hq, float *hd, int *hs, float *__restrict__ D,
+                                                          GdArgs G, int gxg, int gxd, int wm8) {
+    const int b = (int)blockIdx.x, ng = gxg * wm8;
+    int wi, bx;
+    if (b < ng) {
+        x16_place(b, gxg, wi, bx);
+        x16_item<true, true>(layer_pl, s, work, work_n, entries, xq, xd, hq, hd, hs, nullptr, FuseArgs(), wi, bx, G);
+    } else {
+        x16_place(b - ng, gxd, wi, bx);
+        x16_item<false, true>(layer_pl, s, work, work_n, entries, hq, hd, nullptr, nullptr, nullptr, D, FuseArgs(),
+                              wi, bx, G);
     }
 }
 
@@ -1472,6 +1578,33 @@ bool gd_fuses(const Shape &s, int mt) {
     const char *v = getenv("TG_FUSE_GD");
     const bool on = !(v && v[0] == '0');
     return on && mt == 1 && mfma_shape_ok(s) && s.nbI % MF_KC == 0 && s.nbI <= MS_FC * MF_KC;
+}
+
+bool gd16_fuses(const Shape &s, int mt) {
+    const char *v = getenv("TG_FUSE_GD16");
+    const bool on = !(v && v[0] == '0');
+    return on && mt == 4 && mfma_shape_ok(s) && mfma_item_entries(s, mt) > 128 && x16_ok(s, true) &&
+           x16_ok(s, false);
+}
+
+hipError_t launch_gu_down_x16(const uint8_t *layer_pl, const Shape &s, int wmax, const int32_t *work,
+                              const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd,
+                              int8_t *hq, float *hd, int *hs, float *D, const GdArgs &G0, hipStream_t st) {
+    if (!gd16_fuses(s, 4) || !G0.rdy || !G0.err || G0.spin == 0) return hipErrorInvalidValue;
+    const int gxg = s.I / (32 * (XT_NW / 2)), gxd = s.H / (32 * XT_NW), wm8 = (wmax + 7) / 8 * 8;
+    if ((size_t)(gxg + gxd) * (size_t)wm8 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    GdArgs G = G0;
+    G.need = gxg;
+    static bool attr = false;
+    if (!attr && XtLds::BYTES > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma16_gd),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, XtLds::BYTES);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    TG_LAUNCH(k_mfma16_gd, dim3((unsigned)((gxg + gxd) * wm8)), dim3(XT_NW * 64), XtLds::BYTES, st, layer_pl, s,
+              work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, wm8);
+    return hipGetLastError();
 }
 
 template <bool SCVG, bool FULLG>
