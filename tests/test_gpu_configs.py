@@ -256,3 +256,44 @@ def test_config5_decode_stack_94_layers_zipf(O, tglib):
         assert np.array_equal(bits(got), bits(x)), f"max |diff| {np.max(np.abs(got - x)):.3e}"
     finally:
         a.close()
+
+
+def test_config5_batched_stack_94_layers_zipf(O, tglib):
+    """32 tokens through all 94 layers of the 235B-shaped stack with
+    Zipf-skewed routers on the grouped path (one-tile items: the routing
+    launch builds the work items, gate/up and down run in one launch).  After
+    every layer all 32 rows equal the oracle's stack bit for bit (the oracle
+    reads each layer back from the arena); 1e-3 at the end."""
+    gpu_note("config 5: 32 tokens x 94 layers H=4096 I=1536, Zipf routers, grouped path")
+    from tinygiant_amd.arena import HBMExpertArena
+    from tinygiant_amd.moe import MoEBlock
+    H, I, E, k, L, T = 4096, 1536, 128, 8, 94, 32
+    seed = 503
+    rng = np.random.default_rng(seed)
+    routers, shift = zipf_stack_routers(rng, L, E, H)
+    a = HBMExpertArena(L, E, H, I, k)
+    try:
+        for l in range(L):
+            a.synth_layer(l, seed)
+            a.load_router(l, routers[l])
+        a.set_batch_path(a.BATCH_GROUPED)
+        x0 = (O.synth_normal(seed, O.stream_id(0, 0, 4), 1.0, T * H).reshape(T, H) + shift).astype(np.float32)
+        xd = dev(x0)
+        blk = MoEBlock(a)
+        xs = x0.copy()
+        uniq = []
+        for l in range(L):
+            blk.step(xd, l, 1)
+            got = host(xd)
+            a.status()
+            xs, tr = O.moe_stack([a.read_layer(l)], [routers[l]], H, I, E, k, xs)
+            uniq.append(len(np.unique(tr[0])))
+            assert np.array_equal(bits(got), bits(xs)), \
+                f"layer {l}: {int(np.sum(bits(got) != bits(xs)))} values differ, max |diff| {np.max(np.abs(got - xs)):.3e}"
+            if l % 16 == 15:
+                gpu_note(f"  layer {l} bit-exact ({uniq[-1]} distinct experts)")
+        err = rel_err(got, xs)
+        gpu_note(f"  94 layers bit-exact, {np.mean(uniq):.1f} distinct experts per layer, rel err {err:.2e}")
+        assert err <= 1e-3
+    finally:
+        a.close()
