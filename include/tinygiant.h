@@ -268,7 +268,8 @@ int tg_moe_stack_q40_trace_dev(tg_arena *a, float *x, int layer0,
                                float *topk_w, void *stream);
 /* Decode path of one-token calls: ROUTED (one launch per layer that also
  * routes, from router partial sums the layer before it leaves; stack
- * calls add one small prologue launch and replay as a HIP graph), FUSED
+ * calls add one small prologue launch and launch layer by layer, or replay
+ * as a HIP graph after tg_arena_set_graphs(a, 1)), FUSED
  * (per layer a routing kernel and one launch for gate/up and down),
  * PER_LAYER (routing, gate/up and down as three kernels per layer), AUTO
  * (ROUTED where the shape allows it, else FUSED, else PER_LAYER).  Value 1
