@@ -485,7 +485,7 @@ def batched_leg(args, torch, call, arena, LR=16, K=256, W=16, T=64):
         blk.forward(i % LR, X[i])
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
-    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "gateup_grouped",
+    names = ("route", "route_q8", "place", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "gateup_grouped",
              "down_grouped", "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
@@ -829,7 +829,7 @@ def prefill_leg(args, torch, call, arena, L, K=20, W=2):
         blk.step(xb)
     torch.cuda.synchronize()
     call("tg_prof_enable", 0)
-    names = ("route", "route_q8", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "combine")
+    names = ("route", "route_q8", "place", "group", "gateup_mfma", "down_mfma", "gu_down_mfma", "combine")
     kern = kernel_times(call, names)
     kern_us = {k: round(v[1] / max(v[0], 1) * 1e3, 3) for k, v in kern.items()}
     if "gu_down_mfma" in kern:  # gate/up and down in one launch: the roofline covers both products

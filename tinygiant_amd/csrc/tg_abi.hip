@@ -200,7 +200,8 @@ struct Scratch {
     float *dec_part = nullptr;
     uint64_t *dec_ow = nullptr;
     uint32_t *fc_cnt = nullptr;   // arrival counts of the combine in the down launch (zero between calls)
-    int32_t *ecnt = nullptr;      // E: entries placed per expert by route_q8, then its arrival count (zero between calls)
+    int32_t *ecnt = nullptr;      // E: entries placed per expert, then the arrival counts of route_q8 and of the
+                                  // placing launch (zero between calls)
     int32_t *ent_cap = nullptr;   // E * T: per-expert entry lists of capacity T (chains path: over raw, unused there)
     int32_t *idx = nullptr;       // T * k
     float *w = nullptr;           // T * k
@@ -241,7 +242,8 @@ static size_t scratch_layout(const Shape &s, int T, uint8_t *base, Scratch *sc) 
     c.dec_part = reinterpret_cast<float *>(take(4 * tg::dec_part_floats(s)));
     c.dec_ow = reinterpret_cast<uint64_t *>(take(8 * tg::dec_ow_words(s)));
     c.fc_cnt = reinterpret_cast<uint32_t *>(take(4 * tg::fuse_count_words(s, T)));
-    c.ecnt = reinterpret_cast<int32_t *>(take(4 * ((size_t)s.E + 1)));  // + route_q8's arrival count
+    // + the arrival counts of route_q8 and of the placing launch
+    c.ecnt = reinterpret_cast<int32_t *>(take(4 * ((size_t)s.E + 2)));
     c.dec = dec0;
     c.dec_bytes = off;
     c.dec_lw = reinterpret_cast<uint64_t *>(dec0);
@@ -585,8 +587,22 @@ static int layer_kernels_grouped(tg_arena *a, const Scratch &c, int layer, const
                                  c.w, c.xq, c.xd, c.xs, placed ? c.ecnt : nullptr, placed ? c.ent_cap : nullptr, rg,
                                  st));
     if (mfma) {
-        int32_t *ent = placed ? c.ent_cap : c.entries;
-        if (!q8_groups && placed)
+        // many entries: placed by many blocks into the lists over the
+        // router-dot buffer (route_q8 has read it), then only the work items
+        const bool par = !placed && tg::place_par_on();
+        int32_t *ent = placed || par ? c.ent_cap : c.entries;
+        if (par) {
+            tg::RouteGroup pg;
+            pg.counts = c.counts;
+            pg.offsets = c.offsets;
+            pg.work = c.work;
+            pg.work_n = c.work_n;
+            pg.rdy = rdy;
+            pg.arrive = reinterpret_cast<uint32_t *>(c.ecnt + s.E + 1);
+            pg.ch = ch;
+            pg.wmax = wmax;
+            PROFILED("group", st, tg::launch_place(c.idx, n, s.E, T, c.ecnt, c.ent_cap, pg, st));
+        } else if (!q8_groups && placed)
             PROFILED("group", st,
                      tg::launch_group_placed(s, n, ch, T, c.ecnt, c.counts, c.offsets, c.work, c.work_n, rdy, st));
         else if (!q8_groups)

@@ -289,6 +289,14 @@ int group_work_max(const Shape &s, int n, int ch);
 hipError_t launch_group_chunked(const Shape &s, const int32_t *idx, int n, int ch, int32_t *counts,
                                 int32_t *offsets, int32_t *entries, int32_t *work, int32_t *work_n, int32_t *rdy,
                                 hipStream_t st);
+// Many entries: idx[n] placed into per-expert lists ent_cap[e * cap + i] by
+// many blocks (counts in ecnt, zero before the call); the last block builds
+// the work items of both lists (chunks of G.ch entries, largest first),
+// clears ecnt and G.rdy (may be null) and sets *G.arrive (zero between calls)
+// back to zero.  TG_GROUP_PAR not 0 (read per call)
+bool place_par_on();
+hipError_t launch_place(const int32_t *idx, int n, int E, int cap, int32_t *ecnt, int32_t *ent_cap,
+                        const RouteGroup &G, hipStream_t st);
 // work items over entries placed by launch_route_q8 (lists of capacity cap);
 // clears ecnt for the next call
 hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *ecnt, int32_t *counts,

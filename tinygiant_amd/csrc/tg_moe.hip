@@ -2279,6 +2279,72 @@ TG_DEV void scan_256_n(int (&v)[N], int n, int *tmp) {
 // (entries[e * cap + i], placed by k_route_q8) and ecnt[e] holds their
 // counts: only the work items are built (items of expert e start at e * cap)
 // and ecnt is cleared for the next layer.
+// Work items of both lists (chunks of ch entries for gate/up, chd for down)
+// listed by size class, largest first: full chunks, then the remainders of
+// more than half, more than a quarter, the rest (blocks are dispatched in
+// item order, so the short ones fill the tail of the grid).  Thread e < E
+// holds expert e's count c.  Items of expert e start at its offset among all
+// entries, or (cap > 0: lists of capacity cap) at e * cap.  Writes counts,
+// offsets, the items and work_n; returns the thread's offset.  Every thread
+// of the block calls it (threads 0..255 take part in the scans).
+TG_DEV int group_items_sorted(int c, int E, int ch, int chd, int wmax, int cap, int32_t *__restrict__ counts,
+                              int32_t *__restrict__ offsets, int32_t *__restrict__ work,
+                              int32_t *__restrict__ work_n, int *tmp9, int *cls_tot) {
+    const int tid = threadIdx.x;
+    // per list (chunk size): full chunks, then the remainder in its class;
+    // the counts and the class flags of both lists in one scan
+    int nf[2], rr[2], cl[2];
+    for (int lst = 0; lst < 2; lst++) {
+        const int chk = lst ? chd : ch;
+        nf[lst] = c / chk;
+        rr[lst] = c - nf[lst] * chk;
+        cl[lst] = rr[lst] == 0 ? -1 : (4 * rr[lst] > 2 * chk ? 0 : (4 * rr[lst] > chk ? 1 : 2));
+    }
+    int sv[9] = {c, nf[0], cl[0] == 0, cl[0] == 1, cl[0] == 2, nf[1], cl[1] == 0, cl[1] == 1, cl[1] == 2};
+    int sc[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) sc[j] = sv[j];
+    scan_256_n<9>(sc, E, tmp9);
+    const int o = sc[0], ob = cap > 0 ? tid * cap : o;  // ob: the expert's first entry
+    if (tid < E) {
+        offsets[tid] = o;
+        counts[tid] = c;
+        if (tid == E - 1) {
+            offsets[E] = o + c;
+            // class totals (exclusive scan + own value)
+            for (int j = 0; j < 8; j++) cls_tot[j] = sc[1 + j] + sv[1 + j];
+        }
+    }
+    __syncthreads();
+    for (int lst = 0; lst < 2; lst++) {
+        const int chk = lst ? chd : ch, nfull = nf[lst], r = rr[lst], cls = cl[lst];
+        const int *tot4 = cls_tot + 4 * lst;
+        const int bf = sc[1 + 4 * lst], b0 = sc[2 + 4 * lst], b1 = sc[3 + 4 * lst], b2 = sc[4 + 4 * lst];
+        const int base_r = cls == 0 ? tot4[0] + b0 : cls == 1 ? tot4[0] + tot4[1] + b1 : tot4[0] + tot4[1] + tot4[2] + b2;
+        int32_t *wl = work + 3 * (size_t)(lst ? wmax : 0);
+        if (tid < E) {
+            for (int i = 0; i < nfull && bf + i < wmax; i++) {
+                int32_t *it = wl + 3 * (size_t)(bf + i);
+                it[0] = tid;
+                it[1] = ob + i * chk;
+                it[2] = chk;
+            }
+            if (cls >= 0 && base_r < wmax) {
+                int32_t *it = wl + 3 * (size_t)base_r;
+                it[0] = tid;
+                it[1] = ob + nfull * chk;
+                it[2] = r;
+            }
+        }
+        if (tid == 0) {
+            const int tot = tot4[0] + tot4[1] + tot4[2] + tot4[3];
+            work_n[lst] = tot < wmax ? tot : wmax;
+        }
+    }
+    __syncthreads();
+    return o;
+}
+
 template <bool SORT, bool PLACED = false>
 __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict__ idx, int n, int E, int ch, int chd,
                                                       int wmax, int32_t *__restrict__ counts,
@@ -2354,58 +2420,10 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         }
         __syncthreads();
     } else {
-    // per list (chunk size): full chunks, then the remainder in its class;
-    // the counts and the class flags of both lists in one scan
-    int nf[2], rr[2], cl[2];
-    for (int lst = 0; lst < 2; lst++) {
-        const int chk = lst ? chd : ch;
-        nf[lst] = c / chk;
-        rr[lst] = c - nf[lst] * chk;
-        cl[lst] = rr[lst] == 0 ? -1 : (4 * rr[lst] > 2 * chk ? 0 : (4 * rr[lst] > chk ? 1 : 2));
-    }
-    int sv[9] = {c, nf[0], cl[0] == 0, cl[0] == 1, cl[0] == 2, nf[1], cl[1] == 0, cl[1] == 1, cl[1] == 2};
-    int sc[9];
-#pragma unroll
-    for (int j = 0; j < 9; j++) sc[j] = sv[j];
-    scan_256_n<9>(sc, E, tmp9);
-    const int o = sc[0], ob = PLACED ? tid * cap : o;  // ob: the expert's first entry
-    if (tid < E) {
-        off[tid] = o;
-        offsets[tid] = o;
-        counts[tid] = c;
-        if (tid == E - 1) {
-            offsets[E] = o + c;
-            // class totals (exclusive scan + own value)
-            for (int j = 0; j < 8; j++) cls_tot[j] = sc[1 + j] + sv[1 + j];
-        }
-    }
-    __syncthreads();
-    for (int lst = 0; lst < 2; lst++) {
-        const int chk = lst ? chd : ch, nfull = nf[lst], r = rr[lst], cls = cl[lst];
-        const int *tot4 = cls_tot + 4 * lst;
-        const int bf = sc[1 + 4 * lst], b0 = sc[2 + 4 * lst], b1 = sc[3 + 4 * lst], b2 = sc[4 + 4 * lst];
-        const int base_r = cls == 0 ? tot4[0] + b0 : cls == 1 ? tot4[0] + tot4[1] + b1 : tot4[0] + tot4[1] + tot4[2] + b2;
-        int32_t *wl = work + 3 * (size_t)(lst ? wmax : 0);
-        if (tid < E) {
-            for (int i = 0; i < nfull && bf + i < wmax; i++) {
-                int32_t *it = wl + 3 * (size_t)(bf + i);
-                it[0] = tid;
-                it[1] = ob + i * chk;
-                it[2] = chk;
-            }
-            if (cls >= 0 && base_r < wmax) {
-                int32_t *it = wl + 3 * (size_t)base_r;
-                it[0] = tid;
-                it[1] = ob + nfull * chk;
-                it[2] = r;
-            }
-        }
-        if (tid == 0) {
-            const int tot = tot4[0] + tot4[1] + tot4[2] + tot4[3];
-            work_n[lst] = tot < wmax ? tot : wmax;
-        }
-    }
-    __syncthreads();
+        const int o = group_items_sorted(c, E, ch, chd, wmax, PLACED ? cap : 0, counts, offsets, work, work_n, tmp9,
+                                         cls_tot);
+        if (tid < E) off[tid] = o;
+        __syncthreads();
     }
     // entry lists: built in LDS when they fit (the dynamic buffer holds n
     // ints), then written out in order, coalesced; scattered 4-byte stores
@@ -2436,6 +2454,64 @@ __global__ __launch_bounds__(GR_THREADS) void k_group(const int32_t *__restrict_
         __syncthreads();
         for (int i = tid; i < n; i += GR_THREADS) entries[i] = ent_l[i];
     }
+}
+
+// Many entries (prefill): the entries are placed in per-expert lists of
+// capacity cap by many blocks (the role of k_route_q8's placement below 128
+// tokens, without its contention): each block counts its PL_THREADS * PL_PER
+// entries per expert in LDS, reserves each expert's range with one
+// device-scope atomic on ecnt[e] and writes its entries there; the last
+// block to finish (one arrival count, G.arrive) builds the work items of
+// both lists in k_group's size order from the counts and clears them.
+// Positions inside a list depend on the order of the atomics, as in k_group.
+constexpr int PL_THREADS = 256, PL_PER = 4;
+
+__global__ __launch_bounds__(PL_THREADS) void k_place(const int32_t *__restrict__ idx, int n, int E, int cap,
+                                                      int32_t *__restrict__ ecnt, int32_t *__restrict__ ent_cap,
+                                                      RouteGroup G) {
+    __shared__ int lcnt[MAX_E], lbase[MAX_E];
+    const int tid = threadIdx.x, b0 = (int)blockIdx.x * PL_THREADS * PL_PER;
+    for (int e = tid; e < E; e += PL_THREADS) lcnt[e] = 0;
+    int ev[PL_PER], lp[PL_PER];
+#pragma unroll
+    for (int u = 0; u < PL_PER; u++) {
+        const int i = b0 + u * PL_THREADS + tid;
+        const int v = i < n ? idx[i] : -1;
+        ev[u] = i < n ? (v < 0 ? 0 : (v >= E ? E - 1 : v)) : -1;  // never index outside the table
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PL_PER; u++)
+        if (ev[u] >= 0) lp[u] = atomicAdd(&lcnt[ev[u]], 1);
+    __syncthreads();
+    for (int e = tid; e < E; e += PL_THREADS)
+        if (lcnt[e]) lbase[e] = atomicAdd(ecnt + e, lcnt[e]);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PL_PER; u++) {
+        if (ev[u] >= 0) {
+            const int pos = lbase[ev[u]] + lp[u];
+            // at most cap entries per expert when the counts started at zero
+            // (a call cut short could leave them nonzero: never write past the list)
+            if (pos < cap) ent_cap[(size_t)ev[u] * cap + pos] = b0 + u * PL_THREADS + tid;
+        }
+    }
+    __shared__ int last, tmp9[4 * 9], cls_tot[8];
+    __syncthreads();  // this block's reservations are done (their atomics returned)
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(G.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;  // uniform over the block
+    if (tid == 0) __hip_atomic_store(G.arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (G.rdy)
+        for (int i = tid; i < G.wmax; i += PL_THREADS) G.rdy[i] = 0;
+    int c = 0;
+    if (tid < E) {
+        const int v = __hip_atomic_load(ecnt + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c = v < cap ? v : cap;  // never past the list
+        __hip_atomic_store(ecnt + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    group_items_sorted(c, E, G.ch, G.ch, G.wmax, cap, G.counts, G.offsets, G.work, G.work_n, tmp9, cls_tot);
 }
 
 // Tokens (entries) per chunk of the grouped kernels, from an LDS budget.
@@ -3004,6 +3080,21 @@ hipError_t launch_group_placed(const Shape &s, int n, int ch, int cap, int32_t *
     else
         TG_LAUNCH((k_group<false, true>), dim3(1), dim3(GR_THREADS), 0, st, nullptr, n, s.E, ch, ch, wmax, counts,
                   offsets, nullptr, work, work_n, ecnt, cap, rdy);
+    return hipGetLastError();
+}
+
+bool place_par_on() {
+    const char *v = getenv("TG_GROUP_PAR");
+    return !(v && v[0] == '0');
+}
+
+hipError_t launch_place(const int32_t *idx, int n, int E, int cap, int32_t *ecnt, int32_t *ent_cap,
+                        const RouteGroup &G, hipStream_t st) {
+    if (n <= 0 || E > PL_THREADS || E > MAX_E || cap <= 0 || !G.arrive || G.ch <= 0 || G.wmax <= 0 || !G.counts ||
+        !G.offsets || !G.work || !G.work_n)
+        return hipErrorInvalidValue;
+    const unsigned nb = (unsigned)((n + PL_THREADS * PL_PER - 1) / (PL_THREADS * PL_PER));
+    TG_LAUNCH(k_place, dim3(nb), dim3(PL_THREADS), 0, st, idx, n, E, cap, ecnt, ent_cap, G);
     return hipGetLastError();
 }
 
