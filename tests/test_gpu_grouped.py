@@ -253,14 +253,17 @@ def test_fused_combine_counts_across_calls(O, tglib):
 def test_fused_gate_up_down_across_calls(O, tglib, H, I, E, k, Ts):
     """Gate/up and down of the one-tile and the 16 x 16 work items run in one
     launch (down blocks wait, bounded, for their item's gate/up blocks to
-    store h; the grouping kernel clears the per-item counts for every call).
-    Calls of different sizes on one arena, each made with the fused launches
-    and with the two launches (TG_FUSE_GD=0 and TG_FUSE_GD16=0, read per
-    call), all equal the oracle bit for bit."""
+    store h; the kernel that builds the work items clears the per-item counts
+    for every call).  Calls of different sizes on one arena, each made with
+    the default launches and with every alternative switched on (TG_FUSE_GD=0
+    and TG_FUSE_GD16=0: the two launches; TG_ROUTE_GROUP=0 and TG_GROUP_PAR=0:
+    the grouping kernel, building the entry lists itself from 128 tokens; all
+    read per call), equal the oracle bit for bit."""
     import os
     from tinygiant_amd.moe import MoEBlock
     a, layers, routers = make_arena(O, 1, H, I, E, k, seed=41)
-    old = {v: os.environ.get(v) for v in ("TG_FUSE_GD", "TG_FUSE_GD16")}
+    switches = ("TG_FUSE_GD", "TG_FUSE_GD16", "TG_ROUTE_GROUP", "TG_GROUP_PAR")
+    old = {v: os.environ.get(v) for v in switches}
     try:
         blk = MoEBlock(a)
         for i, T in enumerate(Ts):
@@ -268,9 +271,9 @@ def test_fused_gate_up_down_across_calls(O, tglib, H, I, E, k, Ts):
             ref, _, _, _ = O.moe_layer(layers[0], routers[0], H, I, E, k, x)
             xd = dev(x)
             for mode in ("1", "0", "1"):
-                os.environ["TG_FUSE_GD"] = mode
-                os.environ["TG_FUSE_GD16"] = mode
-                gpu_note(f"fused gate/up + down H={H} T={T} fused={mode}")
+                for v in switches:
+                    os.environ[v] = mode
+                gpu_note(f"fused gate/up + down H={H} T={T} defaults={mode}")
                 got = host(blk.forward(0, xd))
                 assert np.array_equal(bits(got), bits(ref)), \
                     f"T={T} mode {mode}: max |diff| {np.max(np.abs(got - ref)):.3e}"
