@@ -30,6 +30,8 @@
 // Gate/up then applies SwiGLU and Q8_0 per (entry, 32 rows): the 32 values
 // of one entry sit in lanes n and n + 32, 16 registers each.  Down writes
 // fp32 rows per entry for the combine.
+#include <atomic>
+
 #include "tg_device.h"
 #include "tg_internal.h"
 
@@ -1394,6 +1396,20 @@ __global__ __launch_bounds__(XT_NW * 64) void k_mfma16_gd(const uint8_t *__restr
 // ================================================================ launchers
 static inline unsigned mf_cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// The dynamic-LDS limit of kernel fn raised to `bytes` (above 64 KB) on the
+// current device, once per (kernel, device): `done` holds a bit per device.
+static hipError_t lds_attr(const void *fn, size_t bytes, std::atomic<uint64_t> &done) {
+    if (bytes <= 65536) return hipSuccess;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+    if (bit && (done.load(std::memory_order_relaxed) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_relaxed);
+    return e;
+}
+
 static bool x16_ok(const Shape &s, bool pair);
 
 // entries per work item of the MFMA path at mt M-tiles: the 16 x 16 kernels
@@ -1482,13 +1498,9 @@ static hipError_t ms_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
     }();
     if (full_on && nb % MF_KC == 0 && nb <= MS_FC * MF_KC) {
         const size_t lds = ms_full_lds_bytes();
-        static bool attr = false;
-        if (!attr) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_small<PAIR, true, true>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-            attr = true;
-        }
+        static std::atomic<uint64_t> attr{0};
+        hipError_t e = lds_attr(reinterpret_cast<const void *>(&k_mfma_small<PAIR, true, true>), lds, attr);
+        if (e != hipSuccess) return e;
         TG_LAUNCH((k_mfma_small<PAIR, true, true>), dim3(gx, wmax), dim3(MS_NW * 64), lds, st, layer_pl, s, work,
                   work_n, entries, aq, ad, oq, od, os, D, F);
         return hipGetLastError();
@@ -1519,13 +1531,9 @@ static hipError_t x16_go(const uint8_t *layer_pl, const Shape &s, int wmax, cons
                          const int32_t *work_n, const int32_t *entries, const int8_t *aq, const float *ad, int8_t *oq,
                          float *od, int *os, float *D, const FuseArgs &F, hipStream_t st) {
     const unsigned gx = PAIR ? (unsigned)(s.I / (32 * (XT_NW / 2))) : (unsigned)(s.H / (32 * XT_NW));
-    static bool attr = false;
-    if (!attr && XtLds::BYTES > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma16<PAIR>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, XtLds::BYTES);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    hipError_t e = lds_attr(reinterpret_cast<const void *>(&k_mfma16<PAIR>), XtLds::BYTES, attr);
+    if (e != hipSuccess) return e;
     // one dimension: gx blocks for each of wmax items, wmax rounded up to 8
     const unsigned wm8 = (unsigned)((wmax + 7) / 8 * 8);
     TG_LAUNCH((k_mfma16<PAIR>), dim3(gx * wm8), dim3(XT_NW * 64), XtLds::BYTES, st, layer_pl, s, work, work_n,
@@ -1595,13 +1603,9 @@ hipError_t launch_gu_down_x16(const uint8_t *layer_pl, const Shape &s, int wmax,
     if ((size_t)(gxg + gxd) * (size_t)wm8 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
     GdArgs G = G0;
     G.need = gxg;
-    static bool attr = false;
-    if (!attr && XtLds::BYTES > 65536) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma16_gd),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, XtLds::BYTES);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    hipError_t e = lds_attr(reinterpret_cast<const void *>(&k_mfma16_gd), XtLds::BYTES, attr);
+    if (e != hipSuccess) return e;
     TG_LAUNCH(k_mfma16_gd, dim3((unsigned)((gxg + gxd) * wm8)), dim3(XT_NW * 64), XtLds::BYTES, st, layer_pl, s,
               work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, wm8);
     return hipGetLastError();
@@ -1612,13 +1616,9 @@ static hipError_t gd_go(const uint8_t *layer_pl, const Shape &s, int wmax, const
                         const int32_t *work_n, const int32_t *entries, const int8_t *xq, const float *xd, int8_t *hq,
                         float *hd, int *hs, float *D, const GdArgs &G, int gxg, int gxd, hipStream_t st) {
     const size_t lds = ms_full_lds_bytes();
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_small_gd<SCVG, FULLG>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<uint64_t> attr{0};
+    hipError_t e = lds_attr(reinterpret_cast<const void *>(&k_mfma_small_gd<SCVG, FULLG>), lds, attr);
+    if (e != hipSuccess) return e;
     TG_LAUNCH((k_mfma_small_gd<SCVG, FULLG>), dim3((unsigned)((gxg + gxd) * wmax)), dim3(MS_NW * 64), lds, st,
               layer_pl, s, work, work_n, entries, xq, xd, hq, hd, hs, D, G, gxg, gxd, wmax);
     return hipGetLastError();
