@@ -60,8 +60,9 @@ int tg_device_sync(void);
 const char *tg_version(void);
 /* Kernel timing.  While enabled, the MoE entry points bracket every kernel
  * launch with HIP events recorded on the launching stream; tg_prof_read
- * waits for them and returns, for one kernel name ("route", "gateup",
- * "down"), the number of launches and their summed duration in ms.
+ * waits for them and returns, for one launch role ("dec_part", "layer",
+ * "route", "route_q8", "group", "gu_down_mfma", "gateup_mfma", "down_mfma",
+ * "combine", ...), the number of launches and their summed duration in ms.
  * tg_prof_enable(1) also discards earlier records. */
 int tg_prof_enable(int on);
 int tg_prof_read(const char *kernel, int *launches, double *total_ms);
