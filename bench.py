@@ -1456,7 +1456,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures a single GPU (one MI355X); --gpus must be 1. "
-              "The multi-GPU expert-parallel design is described in DESIGN.md but not built.",
+              "Expert-parallel sharding over several GPUs is designed but not built.",
               file=sys.stderr)
         return 2
 
